@@ -1,0 +1,242 @@
+"""Benchmark: Gated DeltaNet recurrence forward + backward, tokens/s per layer at the Qwen3.5-4B layer shape.
+
+One step = one forward (qb_gdn_fwd, writing the 64-token checkpoints) and one backward (qb_gdn_bwd) over the
+workload's tokens, inputs resident in HBM before the timed region. value = tokens / (wall time per step), the best
+design's. Each kernel's duration comes from HIP events the library records on its launch stream (the descriptor's
+trace_events); the roofline object is for the kernel with the most time per step, its algorithmic work per launch
+divided by its mean duration. cpu_baseline times the oracle (the CPU restatement, float32, OpenMP) on the host on
+the same inputs.
+
+python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--design auto|1|2] [--workload qwen35_4b] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "Gated DeltaNet fwd+bwd tokens/s per layer @4B shape; % HBM/MFMA roofline"
+HBM_PEAK_GBS = 8000.0      # MI355X HBM3E, published
+FP32_PEAK_TFLOPS = 157.3   # MI355X FP32 vector, published
+BF16_MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense BF16 MFMA, published
+
+
+class Hip:
+    """The few HIP event calls the timer needs, from the runtime torch already loaded."""
+
+    def __init__(self):
+        self.lib = ctypes.CDLL("libamdhip64.so")
+        self.lib.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+        self.lib.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+        self.lib.hipEventDestroy.argtypes = [ctypes.c_void_p]
+
+    def event(self):
+        e = ctypes.c_void_p()
+        if self.lib.hipEventCreate(ctypes.byref(e)) != 0:
+            raise RuntimeError("hipEventCreate failed")
+        return e.value
+
+    def elapsed_ms(self, a, b):
+        ms = ctypes.c_float()
+        if self.lib.hipEventElapsedTime(ctypes.byref(ms), ctypes.c_void_p(a), ctypes.c_void_p(b)) != 0:
+            raise RuntimeError("hipEventElapsedTime failed")
+        return ms.value
+
+
+def algorithmic_work(w, kernel, nc, design):
+    """(kind, amount per launch) for a kernel: "bytes" of compulsory HBM traffic or "flops" of the recurrent
+    algorithm (7 Dk Dv per token and value head forward, 15 backward; recompute not credited)."""
+    BT, Hk, Hv, Dk, Dv = w.B * w.T, w.Hk, w.Hv, w.Dk, w.Dv
+    io = 2 if w.dtype == "bf16" else 4
+    qk = 2 * BT * Hk * Dk * io
+    vv = BT * Hv * Dv * io
+    scal = BT * Hv * (4 + io)
+    states = nc * Hv * Dv * Dk * 4
+    s0 = (w.n_states * Hv * Dv * Dk * 4) if w.s0_std > 0 else 0
+    if kernel == "rec_fwd":
+        return "flops", 7.0 * Dk * Dv * BT * Hv
+    if kernel == "rec_bwd":
+        return "flops", 15.0 * Dk * Dv * BT * Hv
+    if kernel == "rec_reduce":
+        nblk = (Dv + 15) // 16
+        return "bytes", 2 * BT * Hv * nblk * (Dk + 1) * 4 + qk + BT * Hv * (4 + io)
+    raise KeyError(kernel)
+
+
+def roofline_of(kind, amount, ms):
+    if kind == "bytes":
+        achieved = amount / (ms * 1e-3) / 1e9
+        return {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": achieved / HBM_PEAK_GBS}
+    achieved = amount / (ms * 1e-3) / 1e12
+    return {"bound": "valu", "achieved": achieved, "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": achieved / FP32_PEAK_TFLOPS}
+
+
+def run_design(torch, hip, lib, w, dev, design, steps, warmup):
+    """Times `steps` fwd+bwd steps after `warmup`; returns wall ms/step and per-kernel mean ms."""
+    B, T, Hk, Hv, Dk, Dv = w.B, w.T, w.Hk, w.Hv, w.Dk, w.Dv
+    cu = w.cu_seqlens
+    dt = lib.BF16 if w.dtype == "bf16" else lib.F32
+    desc_f, keep_f = lib.make_desc(B, T, Hk, Hv, Dk, Dv, dtype=dt, design=design, cu_seqlens=cu)
+    desc_b, keep_b = lib.make_desc(B, T, Hk, Hv, Dk, Dv, dtype=dt, design=design, cu_seqlens=cu)
+    why = lib.validate(desc_f)
+    if why:
+        return None, why
+    fnames, bnames = lib.launches(desc_f, 0), lib.launches(desc_b, 1)
+    N = w.n_states
+    tdt = torch.bfloat16 if w.dtype == "bf16" else torch.float32
+    y = torch.empty(B, T, Hv, Dv, dtype=tdt, device="cuda")
+    s_out = torch.empty(N, Hv, Dv, Dk, dtype=torch.float32, device="cuda")
+    ckpt = torch.empty(lib.ckpt_bytes(desc_f) // 4, dtype=torch.float32, device="cuda")
+    ws = torch.empty(max(lib.workspace_bytes(desc_f), 1), dtype=torch.uint8, device="cuda")
+    dq, dk = torch.empty_like(dev["q"]), torch.empty_like(dev["k"])
+    dv, dbeta = torch.empty_like(dev["v"]), torch.empty_like(dev["beta"])
+    dg = torch.empty_like(dev["g"])
+    ds0 = torch.empty(N, Hv, Dv, Dk, dtype=torch.float32, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+    p = lambda t: None if t is None else t.data_ptr()  # noqa: E731
+
+    nf, nb = len(fnames) + 1, len(bnames) + 1
+    evs = [[hip.event() for _ in range(nf + nb)] for _ in range(steps)]
+
+    def step(i=None):
+        if i is not None:
+            keep1 = lib.set_trace(desc_f, evs[i][:nf])
+            keep2 = lib.set_trace(desc_b, evs[i][nf:])
+        else:
+            desc_f.trace_events, desc_f.n_trace_events = None, 0
+            desc_b.trace_events, desc_b.n_trace_events = None, 0
+        lib.fwd(desc_f, p(dev["q"]), p(dev["k"]), p(dev["v"]), p(dev["g"]), p(dev["beta"]), p(dev["s0"]), p(y),
+                p(s_out), p(ckpt), p(ws), stream)
+        lib.bwd(desc_b, p(dev["q"]), p(dev["k"]), p(dev["v"]), p(dev["g"]), p(dev["beta"]), p(ckpt), p(dev["dy"]),
+                p(dev["ds_out"]), p(dq), p(dk), p(dv), p(dg), p(dbeta), p(ds0), p(ws), stream)
+        if i is not None:
+            del keep1, keep2
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        step(i)
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / steps
+    per = {}
+    for i in range(steps):
+        e = evs[i]
+        for j, n in enumerate(fnames):
+            per.setdefault(n, []).append(hip.elapsed_ms(e[j], e[j + 1]))
+        for j, n in enumerate(bnames):
+            per.setdefault(n, []).append(hip.elapsed_ms(e[nf + j], e[nf + j + 1]))
+    fwd_ms = sum(hip.elapsed_ms(evs[i][0], evs[i][nf - 1]) for i in range(steps)) / steps
+    bwd_ms = sum(hip.elapsed_ms(evs[i][nf], evs[i][nf + nb - 1]) for i in range(steps)) / steps
+    for row in evs:
+        for e in row:
+            hip.lib.hipEventDestroy(ctypes.c_void_p(e))
+    del keep_f, keep_b
+    kernels = {n: sum(v) / len(v) for n, v in per.items()}
+    return {"ms_per_step": wall_ms, "fwd_ms": fwd_ms, "bwd_ms": bwd_ms, "kernels_ms": kernels,
+            "nc": lib.num_chunks(desc_f)}, None
+
+
+def cpu_baseline(w, inp, budget_s=12.0, max_reps=5):
+    """The oracle's float32 forward + backward on the host cores, repeated until about budget_s."""
+    from oracle import gdn_ref
+
+    f = inp.f32
+    reps, total = 0, 0.0
+    while reps < max_reps and (reps == 0 or total < budget_s):
+        t0 = time.perf_counter()
+        y, s, ck = gdn_ref.fwd(f["q"], f["k"], f["v"], f["g"], f["beta"], f["s0"], cu_seqlens=w.cu_seqlens,
+                               dtype="float32")
+        gdn_ref.bwd(f["q"], f["k"], f["v"], f["g"], f["beta"], ck, f["dy"], f["ds_out"], cu_seqlens=w.cu_seqlens,
+                    dtype="float32")
+        total += time.perf_counter() - t0
+        reps += 1
+    per = total / reps
+    return {"value": w.tokens / per, "unit": "tokens/s", "cores": gdn_ref.threads(), "kind": "port",
+            "sample": f"the full {w.name} workload ({w.tokens} tokens), float32 forward + backward, "
+                      f"{reps} run(s), {per:.2f} s each"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--design", default="auto")
+    ap.add_argument("--workload", default="qwen35_4b")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported (the recurrence shards "
+              "by key-head groups with no exchange, so per-GPU work is the one-GPU run at Hk/N, Hv/N).",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from quotebound_amd import _lib as lib
+    from quotebound_amd.synthetic import make_inputs, to_device, workload
+
+    w = workload(args.workload)
+    inp = make_inputs(w)
+    dev = to_device(inp, "cuda")
+    torch.cuda.synchronize()
+    hip = Hip()
+    designs = [lib.RECURRENT, lib.CHUNKED] if args.design == "auto" else [int(args.design)]
+    results = {}
+    for d in designs:
+        r, why = run_design(torch, hip, lib, w, dev, d, args.steps, args.warmup)
+        name = {lib.RECURRENT: "recurrent", lib.CHUNKED: "chunked"}[d]
+        if r is None:
+            results[name] = {"unavailable": why}
+            continue
+        r["tokens_per_s"] = w.tokens / (r["ms_per_step"] * 1e-3)
+        results[name] = r
+    ok = {k: v for k, v in results.items() if "ms_per_step" in v}
+    if not ok:
+        print(json.dumps({"metric": METRIC, "error": results}))
+        sys.exit(1)
+    best = max(ok, key=lambda k: ok[k]["tokens_per_s"])
+    r = ok[best]
+    dom = max(r["kernels_ms"], key=r["kernels_ms"].get)
+    kind, amount = algorithmic_work(w, dom, r["nc"], best)
+    roof = roofline_of(kind, amount, r["kernels_ms"][dom])
+    roof.update({"kernel": dom, "mean_ms": r["kernels_ms"][dom], "algorithmic_" + kind + "_per_launch": amount,
+                 "traffic": None})
+    out = {
+        "metric": METRIC,
+        "value": r["tokens_per_s"],
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": r["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded numpy: unit-norm q/k, N(0,1) v, log-decay -softplus(N) clipped to [-8,0], "
+                "beta sigmoid(N), dy N(0,1))",
+        "config": {"workload": f"{w.name}: B={w.B} T={w.T} Hk={w.Hk} Hv={w.Hv} Dk={w.Dk} Dv={w.Dv}, "
+                               f"{w.dtype} I/O, fp32 state, 64-token checkpoints, fwd+bwd",
+                   "design": best, "io_dtype": w.dtype},
+        "roofline": roof,
+        "designs": {k: ({kk: vv for kk, vv in v.items() if kk != "nc"} if "ms_per_step" in v else v)
+                    for k, v in results.items()},
+    }
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_baseline(w, inp)
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,109 @@
+/*
+ * qb_gdn: the gated delta rule (Qwen3.5's Gated DeltaNet recurrence), forward and backward, as HIP kernels for
+ * MI355X (gfx950) behind a C ABI.
+ *
+ * It replaces, on device buffers, the recurrence the reference runs through MLX and Metal:
+ *   gated_delta(q, k, v, g, beta, state, train)          reference src/deltanet.h:17-19, src/deltanet.cpp:49-61
+ *   gated_delta_trainable(q, k, v, g, beta, state)       reference src/delta_grad.h:14-16, src/delta_grad.cpp:201-212
+ *   gated_delta_vjp(primals, dy, dstate)                 reference src/delta_grad.h:19-20, src/delta_grad.cpp:155-199
+ * qb_gdn_fwd is the forward (mx::fast::gated_delta_update plus the chunk-start states the reference's vjp rebuilds
+ * at src/delta_grad.cpp:172-181); qb_gdn_bwd is the vjp (the Metal kernel at :23-145 and the reductions at :194-198).
+ * The C++ adapters with the reference's own signatures are in qb/deltanet.h and qb/delta_grad.h.
+ *
+ * Conventions (those of the reference's C library, src/constrain_capi.h:8-9): every call that can fail returns -1
+ * and writes why into err (cut to errlen, NUL-terminated); nothing throws across the ABI. All data pointers are
+ * caller-owned DEVICE buffers, row-major, in the layouts below. Work is queued on `stream` (a hipStream_t; NULL is
+ * the default stream) and the calls return without waiting for it. The library keeps no mutable global state:
+ * calls on different streams may overlap as long as they do not share output or workspace buffers.
+ *
+ * Layouts (N = B, or n_seqs with cu_seqlens; NC = chunk slots, see qb_gdn_num_chunks):
+ *   q, k            [B, T, Hk, Dk]     dtype          key head of value head hv: hv / (Hv / Hk)
+ *   v               [B, T, Hv, Dv]     dtype
+ *   y, dy           [B, T, Hv, Dv]     out dtype      (dtype, or float32 with out_f32)
+ *   g               [B, T, Hv]         float32        decay factor, or log-decay when g_is_log
+ *   beta            [B, T, Hv]         dtype
+ *   s0, s_out, ...  [N, Hv, Dv, Dk]    float32        state S (row = value index), as the reference's [B,Hv,Dv,Dk]
+ *   ckpt            qb_gdn_ckpt_bytes  float32        starts with the chunk-start states [NC, Hv, Dv, Dk]
+ *   dq, dk          [B, T, Hk, Dk]     out dtype; dv [B, T, Hv, Dv] out dtype; dbeta [B, T, Hv] out dtype
+ *   dg              [B, T, Hv]         float32
+ * Pointers to q, k and ckpt must be 16-byte aligned, the others aligned to their element size.
+ *
+ * Semantics per value head and step (reference tests/gated_delta_ref.h:110-118):
+ *   S~ = g_t S;  u = S~ k_t;  delta = beta_t (v_t - u);  S = S~ + delta k_t^T;  y_t = S q_t
+ * Arithmetic is float32 throughout; bf16 is an input/output format only.
+ */
+#ifndef QB_GDN_H
+#define QB_GDN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define QB_GDN_MAX_SEQS 255 /* packed sequences per call */
+
+typedef enum qb_dtype { QB_DTYPE_F32 = 0, QB_DTYPE_BF16 = 1 } qb_dtype;
+
+typedef enum qb_gdn_design {
+  QB_GDN_RECURRENT = 1, /* per state row: fp32 state in registers, wave-level reductions over Dk */
+  QB_GDN_CHUNKED = 2    /* 64-token chunks in WY/UT form on bf16 MFMA with fp32 accumulation */
+} qb_gdn_design;
+
+typedef struct qb_gdn_desc {
+  int32_t B, T, Hk, Hv, Dk, Dv;
+  int32_t chunk;              /* checkpoint stride in steps: 64, the reference's kChunk (src/delta_grad.cpp:11) */
+  int32_t dtype;              /* qb_dtype of q, k, v, beta (and of the outputs unless out_f32) */
+  int32_t g_is_log;           /* 0: g is the decay factor and dg = dL/dg (the reference's convention);
+                                 1: g is the log-decay a, g_t = exp(a_t), and dg = dL/da */
+  int32_t design;             /* qb_gdn_design */
+  int32_t out_f32;            /* 0: y, dy, dq, dk, dv, dbeta are in dtype (the reference returns y in q's dtype,
+                                 src/deltanet.cpp:57, 60); 1: they are float32 whatever dtype is */
+  const int32_t* cu_seqlens;  /* HOST array of n_seqs + 1 token offsets (0 .. T), or NULL. With it B must be 1 and
+                                 the T tokens are n_seqs sequences, each with its own initial/final state and the
+                                 state reset at each boundary: equal to one call per sequence. */
+  int32_t n_seqs;
+  void** trace_events;        /* Instrumentation, no reference counterpart; NULL for none. Caller-owned hipEvent_t
+                                 handles: a call records trace_events[i] on its stream before its kernel launch i
+                                 and trace_events[n] after its last launch (n = qb_gdn_launches), so the caller
+                                 can time each kernel with hipEventElapsedTime. */
+  int32_t n_trace_events;     /* at least qb_gdn_launches(...) + 1 when trace_events is set */
+} qb_gdn_desc;
+
+/* The library's version string. */
+const char* qb_gdn_version(void);
+
+/* 0 when the library supports desc, else -1 with the reason in err. Checks what qb_gdn_fwd / qb_gdn_bwd check. */
+int qb_gdn_validate(const qb_gdn_desc* desc, char* err, int errlen);
+
+/* Chunk slots: ceil(T / chunk) per sequence, summed. -1 on an invalid desc. */
+int64_t qb_gdn_num_chunks(const qb_gdn_desc* desc);
+
+/* Bytes of the residual buffer the forward writes and the backward reads (the chunk-start states, then what the
+ * design keeps for its backward). 0 on an invalid desc. */
+size_t qb_gdn_ckpt_bytes(const qb_gdn_desc* desc);
+
+/* Bytes of scratch the forward and the backward need (may be 0; the pointer may then be NULL). The contents do
+ * not need to survive between calls. 0 on an invalid desc. */
+size_t qb_gdn_workspace_bytes(const qb_gdn_desc* desc);
+
+/* The kernels a call launches, in order: their count is returned and their names written comma-separated into
+ * names (cut to len; may be NULL). which: 0 for qb_gdn_fwd, 1 for qb_gdn_bwd. -1 on an invalid desc. */
+int qb_gdn_launches(const qb_gdn_desc* desc, int which, char* names, int len);
+
+/* Forward. s0 may be NULL (zero initial state); s_out may be NULL; ckpt may be NULL when no backward follows. */
+int qb_gdn_fwd(const qb_gdn_desc* desc, const void* q, const void* k, const void* v, const float* g, const void* beta,
+               const float* s0, void* y, float* s_out, float* ckpt, void* workspace, void* stream, char* err,
+               int errlen);
+
+/* Backward from the forward's ckpt: the cotangents of (q, k, v, g, beta, s0) given dy and ds_out (the cotangent of
+ * the final state; NULL is zero). ds0 may be NULL. Deterministic: sums run in a fixed order, no atomics. */
+int qb_gdn_bwd(const qb_gdn_desc* desc, const void* q, const void* k, const void* v, const float* g,
+               const void* beta, const float* ckpt, const void* dy, const float* ds_out, void* dq, void* dk, void* dv,
+               float* dg, void* dbeta, float* ds0, void* workspace, void* stream, char* err, int errlen);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

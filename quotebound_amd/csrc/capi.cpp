@@ -1,0 +1,272 @@
+// The C ABI of include/qb_gdn.h: validates a descriptor, resolves it into a Problem and dispatches to the design's
+// kernels. Every entry point catches everything; failures return -1 with the reason in err (the convention of
+// reference src/constrain_capi.h:8-9). No mutable global state.
+#include "qb_gdn.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+#include <exception>
+#include <string>
+
+#include "gdn_kernels.h"
+
+namespace {
+
+using qbgdn::Problem;
+
+void set_err(char* err, int errlen, const std::string& what) {
+  if (!err || errlen <= 0) return;
+  std::strncpy(err, what.c_str(), size_t(errlen) - 1);
+  err[errlen - 1] = '\0';
+}
+
+template <class F>
+int guarded(char* err, int errlen, F&& f) {
+  try {
+    return f();
+  } catch (const std::exception& e) {
+    set_err(err, errlen, e.what());
+  } catch (...) {
+    set_err(err, errlen, "unknown error");
+  }
+  return -1;
+}
+
+std::string shape_of(const qb_gdn_desc& d) {
+  char buf[160];
+  std::snprintf(buf, sizeof buf, "(B %d, T %d, Hk %d, Hv %d, Dk %d, Dv %d, chunk %d)", d.B, d.T, d.Hk, d.Hv, d.Dk,
+                d.Dv, d.chunk);
+  return buf;
+}
+
+// Resolves and checks desc; returns an empty string when usable, else the reason.
+std::string resolve(const qb_gdn_desc* d, Problem& p) {
+  if (!d) return "gated delta: null descriptor";
+  const std::string sh = shape_of(*d);
+  if (d->B < 1 || d->T < 0 || d->Hk < 1 || d->Hv < 1 || d->Dk < 1 || d->Dv < 1)
+    return "gated delta: sizes must be positive " + sh;
+  if (d->Hv % d->Hk)
+    return "gated delta: value heads must be a multiple of key heads " + sh;
+  if (d->Dk % 32) return "gated delta: needs Dk a multiple of 32 " + sh;
+  if (d->chunk != qbgdn::kChunk) return "gated delta: the checkpoint stride must be 64 " + sh;
+  if (d->dtype != QB_DTYPE_F32 && d->dtype != QB_DTYPE_BF16) return "gated delta: dtype must be f32 or bf16";
+  if (d->g_is_log != 0 && d->g_is_log != 1) return "gated delta: g_is_log must be 0 or 1";
+  if (d->design != QB_GDN_RECURRENT && d->design != QB_GDN_CHUNKED)
+    return "gated delta: design must be 1 (recurrent) or 2 (chunked)";
+  if (d->out_f32 != 0 && d->out_f32 != 1) return "gated delta: out_f32 must be 0 or 1";
+  const int64_t BT = int64_t(d->B) * d->T;
+  // Element counts must fit the kernels' 64-bit offsets with room; token counts a 32-bit grid dimension.
+  if (BT > (int64_t(1) << 31) || int64_t(d->Hv) * d->Dv * d->Dk > (int64_t(1) << 31))
+    return "gated delta: problem too large " + sh;
+  p = Problem{};
+  p.B = d->B, p.T = d->T, p.Hk = d->Hk, p.Hv = d->Hv, p.Dk = d->Dk, p.Dv = d->Dv;
+  p.in_bf16 = d->dtype == QB_DTYPE_BF16;
+  p.out_bf16 = p.in_bf16 && !d->out_f32;
+  p.g_is_log = d->g_is_log;
+  p.BT = BT;
+  const int64_t per = (d->T + qbgdn::kChunk - 1) / qbgdn::kChunk;
+  if (d->cu_seqlens) {
+    if (d->B != 1) return "gated delta: packed sequences need B == 1 " + sh;
+    if (d->n_seqs < 1 || d->n_seqs > QB_GDN_MAX_SEQS)
+      return "gated delta: n_seqs must be in [1, " + std::to_string(QB_GDN_MAX_SEQS) + "], got " +
+             std::to_string(d->n_seqs);
+    const int32_t* cu = d->cu_seqlens;
+    if (cu[0] != 0 || cu[d->n_seqs] != d->T)
+      return "gated delta: cu_seqlens must run from 0 to T " + sh;
+    p.tab.n = d->n_seqs;
+    int64_t slots = 0;
+    for (int i = 0; i < d->n_seqs; ++i) {
+      if (cu[i + 1] < cu[i]) return "gated delta: cu_seqlens must not decrease";
+      p.tab.tok0[i] = cu[i];
+      p.tab.slot0[i] = int32_t(slots);
+      slots += (cu[i + 1] - cu[i] + qbgdn::kChunk - 1) / qbgdn::kChunk;
+    }
+    p.tab.tok0[d->n_seqs] = cu[d->n_seqs];
+    p.tab.slot0[d->n_seqs] = int32_t(slots);
+    p.N = d->n_seqs;
+    p.NC = slots;
+  } else {
+    p.tab.n = 0;
+    p.tab.T = d->T;
+    p.tab.nc = int32_t(per);
+    p.N = d->B;
+    p.NC = per * d->B;
+  }
+  const char* why = d->design == QB_GDN_RECURRENT ? qbgdn::rec_supports(p) : qbgdn::chunk_supports(p);
+  if (why) return std::string("gated delta: ") + why + " " + sh;
+  return {};
+}
+
+bool aligned(const void* ptr, size_t a) { return (reinterpret_cast<uintptr_t>(ptr) % a) == 0; }
+
+std::string check_ptr(const char* name, const void* ptr, bool required, size_t align) {
+  if (!ptr) return required ? std::string("gated delta: ") + name + " is null" : std::string();
+  if (!aligned(ptr, align))
+    return std::string("gated delta: ") + name + " must be " + std::to_string(align) + "-byte aligned";
+  return {};
+}
+
+size_t ckpt_bytes(const qb_gdn_desc* d, const Problem& p) {
+  return d->design == QB_GDN_RECURRENT ? qbgdn::rec_ckpt_bytes(p) : qbgdn::chunk_ckpt_bytes(p);
+}
+
+size_t ws_bytes(const qb_gdn_desc* d, const Problem& p) {
+  return d->design == QB_GDN_RECURRENT ? qbgdn::rec_workspace_bytes(p) : qbgdn::chunk_workspace_bytes(p);
+}
+
+qbgdn::Tracer tracer_of(const qb_gdn_desc* d, hipStream_t s) {
+  qbgdn::Tracer t;
+  t.ev = d->trace_events;
+  t.n = d->trace_events ? d->n_trace_events : 0;
+  t.s = s;
+  return t;
+}
+
+int count_names(const char* names) {
+  if (!*names) return 0;
+  int n = 1;
+  for (const char* c = names; *c; ++c) n += *c == ',';
+  return n;
+}
+
+std::string hip_fail(const char* what, hipError_t e) {
+  return std::string("gated delta: ") + what + " failed: " + hipGetErrorString(e);
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* qb_gdn_version(void) { return "qb_gdn 0.1 (gfx950)"; }
+
+int qb_gdn_validate(const qb_gdn_desc* desc, char* err, int errlen) {
+  return guarded(err, errlen, [&] {
+    Problem p;
+    const std::string why = resolve(desc, p);
+    if (!why.empty()) {
+      set_err(err, errlen, why);
+      return -1;
+    }
+    return 0;
+  });
+}
+
+int qb_gdn_launches(const qb_gdn_desc* desc, int which, char* names, int len) {
+  try {
+    Problem p;
+    if (!resolve(desc, p).empty() || (which != 0 && which != 1)) return -1;
+    const bool rec = desc->design == QB_GDN_RECURRENT;
+    const char* list = which == 0 ? (rec ? qbgdn::kRecFwdLaunches : qbgdn::kChunkFwdLaunches)
+                                  : (rec ? qbgdn::kRecBwdLaunches : qbgdn::kChunkBwdLaunches);
+    set_err(names, len, list);
+    return count_names(list);
+  } catch (...) {
+    return -1;
+  }
+}
+
+int64_t qb_gdn_num_chunks(const qb_gdn_desc* desc) {
+  try {
+    Problem p;
+    return resolve(desc, p).empty() ? p.NC : -1;
+  } catch (...) {
+    return -1;
+  }
+}
+
+size_t qb_gdn_ckpt_bytes(const qb_gdn_desc* desc) {
+  try {
+    Problem p;
+    return resolve(desc, p).empty() ? ckpt_bytes(desc, p) : 0;
+  } catch (...) {
+    return 0;
+  }
+}
+
+size_t qb_gdn_workspace_bytes(const qb_gdn_desc* desc) {
+  try {
+    Problem p;
+    return resolve(desc, p).empty() ? ws_bytes(desc, p) : 0;
+  } catch (...) {
+    return 0;
+  }
+}
+
+int qb_gdn_fwd(const qb_gdn_desc* desc, const void* q, const void* k, const void* v, const float* g, const void* beta,
+               const float* s0, void* y, float* s_out, float* ckpt, void* workspace, void* stream, char* err,
+               int errlen) {
+  return guarded(err, errlen, [&] {
+    Problem p;
+    std::string why = resolve(desc, p);
+    const size_t el = p.in_bf16 ? 2 : 4, eo = p.out_bf16 ? 2 : 4;
+    const bool any = p.BT > 0;
+    const struct {
+      const char* name;
+      const void* ptr;
+      bool req;
+      size_t align;
+    } ptrs[] = {{"q", q, any, 16},           {"k", k, any, 16},         {"v", v, any, el},
+                {"g", g, any, 4},            {"beta", beta, any, el},   {"s0", s0, false, 4},
+                {"y", y, any, eo},           {"s_out", s_out, false, 4}, {"ckpt", ckpt, false, 16},
+                {"workspace", workspace, why.empty() && any && ws_bytes(desc, p) > 0, 16}};
+    for (const auto& c : ptrs)
+      if (why.empty()) why = check_ptr(c.name, c.ptr, c.req, c.align);
+    if (!why.empty()) {
+      set_err(err, errlen, why);
+      return -1;
+    }
+    const qbgdn::FwdPtrs a{q, k, v, g, beta, s0, y, s_out, ckpt};
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    qbgdn::Tracer tr = tracer_of(desc, s);
+    const hipError_t e = desc->design == QB_GDN_RECURRENT ? qbgdn::rec_fwd(p, a, workspace, s, tr)
+                                                          : qbgdn::chunk_fwd(p, a, workspace, s, tr);
+    if (e != hipSuccess) {
+      set_err(err, errlen, hip_fail("forward launch", e));
+      return -1;
+    }
+    return 0;
+  });
+}
+
+int qb_gdn_bwd(const qb_gdn_desc* desc, const void* q, const void* k, const void* v, const float* g,
+               const void* beta, const float* ckpt, const void* dy, const float* ds_out, void* dq, void* dk, void* dv,
+               float* dg, void* dbeta, float* ds0, void* workspace, void* stream, char* err, int errlen) {
+  return guarded(err, errlen, [&] {
+    Problem p;
+    std::string why = resolve(desc, p);
+    const size_t el = p.in_bf16 ? 2 : 4, eo = p.out_bf16 ? 2 : 4;
+    const bool any = p.BT > 0;
+    const struct {
+      const char* name;
+      const void* ptr;
+      bool req;
+      size_t align;
+    } ptrs[] = {{"q", q, any, 16},         {"k", k, any, 16},           {"v", v, any, el},
+                {"g", g, any, 4},          {"beta", beta, any, el},     {"ckpt", ckpt, any, 16},
+                {"dy", dy, any, eo},       {"ds_out", ds_out, false, 4}, {"dq", dq, any, eo},
+                {"dk", dk, any, eo},       {"dv", dv, any, eo},         {"dg", dg, any, 4},
+                {"dbeta", dbeta, any, eo}, {"ds0", ds0, false, 4},
+                {"workspace", workspace, why.empty() && any && ws_bytes(desc, p) > 0, 16}};
+    for (const auto& c : ptrs)
+      if (why.empty()) why = check_ptr(c.name, c.ptr, c.req, c.align);
+    if (!why.empty()) {
+      set_err(err, errlen, why);
+      return -1;
+    }
+    const qbgdn::BwdPtrs a{q, k, v, g, beta, ckpt, dy, ds_out, dq, dk, dv, dg, dbeta, ds0};
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    qbgdn::Tracer tr = tracer_of(desc, s);
+    const hipError_t e = desc->design == QB_GDN_RECURRENT ? qbgdn::rec_bwd(p, a, workspace, s, tr)
+                                                          : qbgdn::chunk_bwd(p, a, workspace, s, tr);
+    if (e != hipSuccess) {
+      set_err(err, errlen, hip_fail("backward launch", e));
+      return -1;
+    }
+    return 0;
+  });
+}
+
+}  // extern "C"

@@ -1,0 +1,92 @@
+// Device-side pieces shared by both designs: element I/O for float32 and bfloat16, wave64 lane reductions, and the
+// table that maps a (sequence, step) to its token and chunk slot.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace qbgdn {
+
+constexpr int kChunk = 64;     // checkpoint stride, the reference's kChunk (src/delta_grad.cpp:11)
+constexpr int kMaxSeqs = 255;  // packed sequences per call
+
+// bfloat16 is carried as its bit pattern.
+typedef uint16_t bf16_t;
+
+__device__ __forceinline__ float bf16_to_f32(bf16_t b) { return __uint_as_float(uint32_t(b) << 16); }
+
+// Round to nearest even; NaN stays NaN.
+__device__ __forceinline__ bf16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return bf16_t((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return bf16_t(u >> 16);
+}
+
+template <typename T>
+struct IO;
+template <>
+struct IO<float> {
+  static __device__ __forceinline__ float ld(const float* p, int64_t i) { return p[i]; }
+  static __device__ __forceinline__ void st(float* p, int64_t i, float x) { p[i] = x; }
+  // 8 consecutive elements from a 16-byte aligned address.
+  static __device__ __forceinline__ void ld8(const float* p, float* o) {
+    const float4 a = reinterpret_cast<const float4*>(p)[0], b = reinterpret_cast<const float4*>(p)[1];
+    o[0] = a.x, o[1] = a.y, o[2] = a.z, o[3] = a.w, o[4] = b.x, o[5] = b.y, o[6] = b.z, o[7] = b.w;
+  }
+};
+template <>
+struct IO<bf16_t> {
+  static __device__ __forceinline__ float ld(const bf16_t* p, int64_t i) { return bf16_to_f32(p[i]); }
+  static __device__ __forceinline__ void st(bf16_t* p, int64_t i, float x) { p[i] = f32_to_bf16(x); }
+  static __device__ __forceinline__ void ld8(const bf16_t* p, float* o) {
+    const uint4 r = *reinterpret_cast<const uint4*>(p);
+    const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      o[2 * i] = __uint_as_float(w[i] << 16);
+      o[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    }
+  }
+};
+
+// ---- lane reductions ------------------------------------------------------------------------------------------
+// DPP controls (gfx9 encoding): quad_perm, row_mirror, row_half_mirror.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, false));
+}
+
+// Sum over each 16-lane row of the wave; every lane of the row gets the same bits (each stage pairs lanes
+// symmetrically, and a + b == b + a).
+__device__ __forceinline__ float sum16(float x) {
+  x += dpp_mov<0xb1>(x);   // quad_perm [1,0,3,2]
+  x += dpp_mov<0x4e>(x);   // quad_perm [2,3,0,1]
+  x += dpp_mov<0x141>(x);  // row_half_mirror: quad q pairs with quad q^1
+  x += dpp_mov<0x140>(x);  // row_mirror: half-row h pairs with h^1
+  return x;
+}
+
+// ---- packed sequences ------------------------------------------------------------------------------------------
+// Passed by value as a kernel argument. n == 0: batch mode, sequence i is batch row i (T tokens, nc chunk slots
+// each). n > 0: tok0[i] is the first token of sequence i (tok0[n] == total tokens) and slot0[i] its first chunk
+// slot (slot0[n] == total slots).
+struct SeqTable {
+  int32_t n;
+  int32_t T;
+  int32_t nc;
+  int32_t tok0[kMaxSeqs + 1];
+  int32_t slot0[kMaxSeqs + 1];
+};
+
+struct Seq {
+  int64_t tok0;  // flattened index of the first token in [B * T]
+  int32_t len;   // steps
+  int64_t slot0; // first chunk slot
+};
+
+__device__ __forceinline__ Seq seq_of(const SeqTable& tab, int i) {
+  if (tab.n == 0) return Seq{int64_t(i) * tab.T, tab.T, int64_t(i) * tab.nc};
+  return Seq{tab.tok0[i], tab.tok0[i + 1] - tab.tok0[i], tab.slot0[i]};
+}
+
+}  // namespace qbgdn

@@ -1,0 +1,92 @@
+// Host-side entry points of the kernels, shared between the C ABI (capi.cpp) and the kernel sources.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "gdn_common.h"
+
+namespace qbgdn {
+
+// A validated call: the descriptor resolved into sizes and the packed-sequence table.
+struct Problem {
+  int B, T, Hk, Hv, Dk, Dv;
+  int in_bf16;   // 1: q, k, v, beta are bfloat16; 0: float32
+  int out_bf16;  // 1: y, dy, dq, dk, dv, dbeta are bfloat16; 0: float32
+  int g_is_log;
+  int N;         // state count: B, or the number of packed sequences
+  int64_t BT;    // tokens
+  int64_t NC;    // chunk slots
+  SeqTable tab;
+};
+
+// Forward pointers (device). s0, s_out, ckpt may be null.
+struct FwdPtrs {
+  const void* q;
+  const void* k;
+  const void* v;
+  const float* g;
+  const void* beta;
+  const float* s0;
+  void* y;
+  float* s_out;
+  float* ckpt;
+};
+
+// Backward pointers (device). ds_out, ds0 may be null.
+struct BwdPtrs {
+  const void* q;
+  const void* k;
+  const void* v;
+  const float* g;
+  const void* beta;
+  const float* ckpt;
+  const void* dy;
+  const float* ds_out;
+  void* dq;
+  void* dk;
+  void* dv;
+  float* dg;
+  void* dbeta;
+  float* ds0;
+};
+
+// Optional per-launch events (qb_gdn_desc.trace_events): mark() before each kernel launch and once after the last.
+struct Tracer {
+  void** ev = nullptr;
+  int n = 0;
+  int i = 0;
+  hipStream_t s = nullptr;
+  void mark() {
+    if (ev && i < n) (void)hipEventRecord(static_cast<hipEvent_t>(ev[i++]), s);
+  }
+};
+
+// Design 1: recurrent, one state row per 16 lanes.
+const char* rec_supports(const Problem& p);  // null when supported, else why not
+size_t rec_ckpt_bytes(const Problem& p);
+size_t rec_workspace_bytes(const Problem& p);
+extern const char* const kRecFwdLaunches;  // comma-separated kernel names, in launch order
+extern const char* const kRecBwdLaunches;
+hipError_t rec_fwd(const Problem& p, const FwdPtrs& a, void* ws, hipStream_t s, Tracer& tr);
+hipError_t rec_bwd(const Problem& p, const BwdPtrs& a, void* ws, hipStream_t s, Tracer& tr);
+
+// Design 2: chunkwise WY/UT form on MFMA.
+const char* chunk_supports(const Problem& p);
+size_t chunk_ckpt_bytes(const Problem& p);
+size_t chunk_workspace_bytes(const Problem& p);
+extern const char* const kChunkFwdLaunches;
+extern const char* const kChunkBwdLaunches;
+hipError_t chunk_fwd(const Problem& p, const FwdPtrs& a, void* ws, hipStream_t s, Tracer& tr);
+hipError_t chunk_bwd(const Problem& p, const BwdPtrs& a, void* ws, hipStream_t s, Tracer& tr);
+
+// Blocks are dispatched round-robin over the MI355X's 8 XCDs (block id runs on XCD id % 8), each with its own
+// L2. This gives XCD x a contiguous range of work items, so neighbouring items (which read the same key head)
+// share an L2. A bijection on [0, n).
+__device__ __forceinline__ int xcd_remap(int id, int n) {
+  const int per = n >> 3, rem = n & 7;
+  const int x = id & 7, s = id >> 3;
+  return x * per + (x < rem ? x : rem) + s;
+}
+
+}  // namespace qbgdn

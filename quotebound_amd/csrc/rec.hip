@@ -1,0 +1,495 @@
+// Design 1: the recurrent form. Rows of the state S [Dv, Dk] evolve independently (reference
+// src/delta_grad.cpp:13-18), so each row is owned by 16 lanes of a wave (one DPP row), each lane holding Dk/16
+// columns in VGPRs for all T steps. The two mat-vecs per step are 16-lane DPP reductions. A block is 4 waves =
+// 16 state rows of one value head; the chunk's keys, queries and scalars are staged in LDS once per 64 steps and
+// read by all 16 rows.
+//
+// Forward (per row, per step), the same recurrence as reference tests/gated_delta_ref.h:46-67 but with both dot
+// products taken on the previous state, so one reduction latency per step sits on the dependency chain:
+//   a = S_prev k, b = S_prev q;  u = g a;  delta = beta (v - u);  y = g b + delta (k.q);  S = g S_prev + delta k^T
+// The chunk-start states (the reference's ckpt, src/delta_grad.cpp:172-181) are written as the forward passes them.
+//
+// Backward: reference src/delta_grad.cpp:23-145 re-derived for this layout. Per chunk in reverse: pass A replays
+// the chunk from its checkpoint (one reduction per step) keeping delta and v - u per step in LDS and the state at
+// every 8th step in registers; pass B re-forms 8 states at a time from those without reductions and runs the reverse
+// steps. dq and dk sum over rows: over a wave's 4 rows with lane shuffles, over the block's 4 waves in LDS, over the
+// Dv/16 row blocks and the GQA group in rec_reduce_kernel, always in the same order (no atomics).
+#include "gdn_common.h"
+#include "gdn_kernels.h"
+
+namespace qbgdn {
+namespace {
+
+constexpr int kWaves = 4;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kRows = 4 * kWaves;  // state rows per block
+constexpr int kSub = 8;            // states re-formed at a time in the backward
+constexpr int kNSub = kChunk / kSub;
+
+struct RecFwdArgs {
+  FwdPtrs p;
+  int Hk, Hv, Dv, g_is_log, nblk, total;
+  SeqTable tab;
+};
+
+struct RecBwdArgs {
+  BwdPtrs p;
+  int Hk, Hv, Dv, g_is_log, nblk, total;
+  float* dq_part;  // [BT, Hv, nblk, Dk]
+  float* dk_part;
+  float* dg_part;  // [BT, Hv, nblk]
+  float* db_part;
+  SeqTable tab;
+};
+
+// Work item -> (row block, value head, sequence), row block fastest, placed by xcd_remap.
+struct Item {
+  int blk, hv, n;
+};
+__device__ __forceinline__ Item item_of(int nblk, int Hv, int total) {
+  const int w = xcd_remap(blockIdx.x, total);
+  return Item{w % nblk, (w / nblk) % Hv, w / (nblk * Hv)};
+}
+
+// Stages rows [t0, t0 + L) of the key head's k and q into LDS as float32, 8 elements per access.
+template <int Dk, typename InT>
+__device__ __forceinline__ void stage_kq(float (*Ks)[Dk], float (*Qs)[Dk], const InT* k, const InT* q,
+                                         int64_t tok, int Hk, int hk, int L) {
+  constexpr int V8 = Dk / 8;
+  for (int e = threadIdx.x; e < kChunk * V8; e += kThreads) {
+    const int tt = e / V8, c8 = (e % V8) * 8;
+    if (tt < L) {
+      const int64_t off = ((tok + tt) * Hk + hk) * Dk + c8;
+      IO<InT>::ld8(k + off, &Ks[tt][c8]);
+      IO<InT>::ld8(q + off, &Qs[tt][c8]);
+    }
+  }
+}
+
+// Stages a [T, Hv, Dv] tensor's 16-row slice of rows [t0, t0 + L) (zeros past Dv).
+template <typename InT>
+__device__ __forceinline__ void stage_rows(float (*Xs)[kRows], const InT* x, int64_t tok, int Hv, int hv, int Dv,
+                                           int row0, int L) {
+  for (int e = threadIdx.x; e < kChunk * kRows; e += kThreads) {
+    const int tt = e / kRows, j = e % kRows;
+    if (tt < L) Xs[tt][j] = (row0 + j < Dv) ? IO<InT>::ld(x, ((tok + tt) * Hv + hv) * Dv + row0 + j) : 0.f;
+  }
+}
+
+// Per-step scalars: the decay factor (exp of the log-decay when g_is_log) and beta.
+template <typename InT>
+__device__ __forceinline__ void stage_scalars(float* Gs, float* Bs, const float* g, const InT* beta, int64_t tok,
+                                              int Hv, int hv, int L, int g_is_log) {
+  for (int tt = threadIdx.x; tt < L; tt += kThreads) {
+    const int64_t i = (tok + tt) * Hv + hv;
+    const float gv = g[i];
+    Gs[tt] = g_is_log ? expf(gv) : gv;
+    Bs[tt] = IO<InT>::ld(beta, i);
+  }
+}
+
+template <int NPT, typename InT, typename OutT>
+__global__ __launch_bounds__(kThreads) void rec_fwd_kernel(RecFwdArgs a) {
+  constexpr int Dk = 16 * NPT;
+  __shared__ float Ks[kChunk][Dk];
+  __shared__ float Qs[kChunk][Dk];
+  __shared__ float Vs[kChunk][kRows];
+  __shared__ float Ys[kChunk][kRows];
+  __shared__ float Gs[kChunk], Bs[kChunk], KQs[kChunk];
+
+  const Item it = item_of(a.nblk, a.Hv, a.total);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int cl = lane & 15, rl = (tid >> 6) * 4 + (lane >> 4);
+  const int row0 = it.blk * kRows, row = row0 + rl;
+  const bool live = row < a.Dv;
+  const int hv = it.hv, hk = hv / (a.Hv / a.Hk);
+  const Seq sq = seq_of(a.tab, it.n);
+  const InT* q = static_cast<const InT*>(a.p.q);
+  const InT* k = static_cast<const InT*>(a.p.k);
+  const InT* v = static_cast<const InT*>(a.p.v);
+  const InT* beta = static_cast<const InT*>(a.p.beta);
+  OutT* y = static_cast<OutT*>(a.p.y);
+  const int64_t SS = int64_t(a.Dv) * Dk;
+  const int64_t srow = (int64_t(it.n) * a.Hv + hv) * SS + int64_t(row) * Dk + cl * NPT;
+
+  float s[NPT];
+#pragma unroll
+  for (int i = 0; i < NPT; ++i) s[i] = (live && a.p.s0) ? a.p.s0[srow + i] : 0.f;
+
+  const int nch = (sq.len + kChunk - 1) / kChunk;
+  for (int c = 0; c < nch; ++c) {
+    const int t0 = c * kChunk, L = min(kChunk, sq.len - t0);
+    const int64_t tok = sq.tok0 + t0;
+    if (a.p.ckpt && live) {
+      float* dst = a.p.ckpt + ((sq.slot0 + c) * a.Hv + hv) * SS + int64_t(row) * Dk + cl * NPT;
+#pragma unroll
+      for (int i = 0; i < NPT; ++i) dst[i] = s[i];
+    }
+    __syncthreads();  // the previous chunk's LDS readers are done
+    stage_kq<Dk>(Ks, Qs, (const InT*)k, (const InT*)q, tok, a.Hk, hk, L);
+    stage_rows(Vs, v, tok, a.Hv, hv, a.Dv, row0, L);
+    stage_scalars(Gs, Bs, a.p.g, beta, tok, a.Hv, hv, L, a.g_is_log);
+    __syncthreads();
+    // k.q per step: 16 row groups of 16 lanes, 4 steps each.
+    for (int tt = tid >> 4; tt < kChunk; tt += kThreads / 16) {
+      float kq = 0.f;
+#pragma unroll
+      for (int i = 0; i < NPT; ++i) kq += Ks[tt][cl * NPT + i] * Qs[tt][cl * NPT + i];
+      kq = sum16(kq);
+      if (cl == 0) KQs[tt] = kq;
+    }
+    __syncthreads();
+    for (int tt = 0; tt < L; ++tt) {
+      float kk[NPT], qq[NPT];
+#pragma unroll
+      for (int i = 0; i < NPT; ++i) kk[i] = Ks[tt][cl * NPT + i], qq[i] = Qs[tt][cl * NPT + i];
+      float pa = 0.f, pb = 0.f;
+#pragma unroll
+      for (int i = 0; i < NPT; ++i) pa += s[i] * kk[i], pb += s[i] * qq[i];
+      pa = sum16(pa);
+      pb = sum16(pb);
+      const float gt = Gs[tt], bt = Bs[tt];
+      const float d = bt * (Vs[tt][rl] - gt * pa);
+      const float yv = gt * pb + d * KQs[tt];
+#pragma unroll
+      for (int i = 0; i < NPT; ++i) s[i] = gt * s[i] + d * kk[i];
+      if (cl == 0) Ys[tt][rl] = yv;
+    }
+    __syncthreads();
+    for (int e = tid; e < L * kRows; e += kThreads) {
+      const int tt = e / kRows, j = e % kRows;
+      if (row0 + j < a.Dv) IO<OutT>::st(y, ((tok + tt) * a.Hv + hv) * a.Dv + row0 + j, Ys[tt][j]);
+    }
+  }
+  if (a.p.s_out && live) {
+#pragma unroll
+    for (int i = 0; i < NPT; ++i) a.p.s_out[srow + i] = s[i];
+  }
+}
+
+// Sums NPT per-lane column values over the wave's 4 row groups (lanes l, l^16, l^32, l^48 hold the same columns of
+// different rows) and writes each column's sum once into dst[0, Dk). With NPT >= 4 the values are halved at each
+// exchange so each lane ends with NPT/4 finished columns; with NPT == 2 a plain butterfly is used.
+template <int NPT>
+__device__ __forceinline__ void wave_rows_sum(const float* p, float* dst, int lane) {
+  const int cl = lane & 15;
+  if constexpr (NPT >= 4) {
+    constexpr int H = NPT / 2, Q = NPT / 4;
+    const bool h32 = lane & 32, h16 = lane & 16;
+    float w[H], x[Q];
+#pragma unroll
+    for (int j = 0; j < H; ++j) {
+      const float send = h32 ? p[j] : p[j + H], keep = h32 ? p[j + H] : p[j];
+      w[j] = keep + __shfl_xor(send, 32);
+    }
+#pragma unroll
+    for (int j = 0; j < Q; ++j) {
+      const float send = h16 ? w[j] : w[j + Q], keep = h16 ? w[j + Q] : w[j];
+      x[j] = keep + __shfl_xor(send, 16);
+    }
+    const int base = cl * NPT + (h16 ? Q : 0) + (h32 ? H : 0);
+#pragma unroll
+    for (int j = 0; j < Q; ++j) dst[base + j] = x[j];
+  } else {
+#pragma unroll
+    for (int j = 0; j < NPT; ++j) {
+      float x = p[j];
+      x += __shfl_xor(x, 32);
+      x += __shfl_xor(x, 16);
+      if (lane < 16) dst[cl * NPT + j] = x;
+    }
+  }
+}
+
+template <int NPT, typename InT, typename OutT>
+__global__ __launch_bounds__(kThreads) void rec_bwd_kernel(RecBwdArgs a) {
+  constexpr int Dk = 16 * NPT;
+  __shared__ float Ks[kChunk][Dk];
+  __shared__ float Qs[kChunk][Dk];
+  __shared__ float Vs[kChunk][kRows], DYs[kChunk][kRows], Ds[kChunk][kRows], Es[kChunk][kRows];
+  __shared__ float Gs[kChunk], Bs[kChunk];
+  __shared__ float red[kSub][kWaves][2 * Dk];  // per step and wave: column sums of (dq | dk) over the wave's rows
+  __shared__ float rowv[kSub][3][kRows];       // per step and row: dv, dbeta, dg (factor)
+
+  const Item it = item_of(a.nblk, a.Hv, a.total);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int cl = lane & 15, rl = wave * 4 + (lane >> 4);
+  const int row0 = it.blk * kRows, row = row0 + rl;
+  const bool live = row < a.Dv;
+  const int hv = it.hv, hk = hv / (a.Hv / a.Hk);
+  const Seq sq = seq_of(a.tab, it.n);
+  const InT* q = static_cast<const InT*>(a.p.q);
+  const InT* k = static_cast<const InT*>(a.p.k);
+  const InT* v = static_cast<const InT*>(a.p.v);
+  const OutT* dy = static_cast<const OutT*>(a.p.dy);
+  const InT* beta = static_cast<const InT*>(a.p.beta);
+  OutT* dv = static_cast<OutT*>(a.p.dv);
+  const int64_t SS = int64_t(a.Dv) * Dk;
+  const int64_t srow = (int64_t(it.n) * a.Hv + hv) * SS + int64_t(row) * Dk + cl * NPT;
+
+  float ds[NPT];
+#pragma unroll
+  for (int i = 0; i < NPT; ++i) ds[i] = (live && a.p.ds_out) ? a.p.ds_out[srow + i] : 0.f;
+
+  const int nch = (sq.len + kChunk - 1) / kChunk;
+  for (int c = nch - 1; c >= 0; --c) {
+    const int t0 = c * kChunk, L = min(kChunk, sq.len - t0);
+    const int64_t tok = sq.tok0 + t0;
+    __syncthreads();
+    stage_kq<Dk>(Ks, Qs, k, q, tok, a.Hk, hk, L);
+    stage_rows(Vs, v, tok, a.Hv, hv, a.Dv, row0, L);
+    stage_rows(DYs, dy, tok, a.Hv, hv, a.Dv, row0, L);
+    stage_scalars(Gs, Bs, a.p.g, beta, tok, a.Hv, hv, L, a.g_is_log);
+    float st[NPT];
+    {
+      const float* src = a.p.ckpt + ((sq.slot0 + c) * a.Hv + hv) * SS + int64_t(row) * Dk + cl * NPT;
+#pragma unroll
+      for (int i = 0; i < NPT; ++i) st[i] = live ? src[i] : 0.f;
+    }
+    __syncthreads();
+
+    // Pass A: replay the chunk, keeping delta and v - u per step and every kSub-th state.
+    float sub[kNSub][NPT];
+    for (int m = 0; m < kNSub; ++m) {
+#pragma unroll
+      for (int mm = 0; mm < kNSub; ++mm)
+        if (mm == m) {
+#pragma unroll
+          for (int i = 0; i < NPT; ++i) sub[mm][i] = st[i];
+        }
+#pragma unroll
+      for (int j = 0; j < kSub; ++j) {
+        const int tt = m * kSub + j;
+        if (tt < L) {
+          float kk[NPT];
+#pragma unroll
+          for (int i = 0; i < NPT; ++i) kk[i] = Ks[tt][cl * NPT + i];
+          float pa = 0.f;
+#pragma unroll
+          for (int i = 0; i < NPT; ++i) pa += st[i] * kk[i];
+          pa = sum16(pa);
+          const float gt = Gs[tt];
+          const float e = Vs[tt][rl] - gt * pa;
+          const float d = Bs[tt] * e;
+#pragma unroll
+          for (int i = 0; i < NPT; ++i) st[i] = gt * st[i] + d * kk[i];
+          if (cl == 0) Ds[tt][rl] = d, Es[tt][rl] = e;
+        }
+      }
+    }
+    __syncthreads();
+
+    // Pass B: 8 states at a time from the kept starts, then the reverse steps (reference :97-141).
+    for (int m = kNSub - 1; m >= 0; --m) {
+      const int ts = m * kSub;
+      if (ts >= L) continue;  // uniform over the block
+      float S[kSub + 1][NPT];
+#pragma unroll
+      for (int i = 0; i < NPT; ++i) S[0][i] = 0.f;
+#pragma unroll
+      for (int mm = 0; mm < kNSub; ++mm)
+        if (mm == m) {
+#pragma unroll
+          for (int i = 0; i < NPT; ++i) S[0][i] = sub[mm][i];
+        }
+#pragma unroll
+      for (int j = 0; j < kSub; ++j) {
+        const int tt = ts + j;
+        if (tt < L) {
+          const float gt = Gs[tt], d = Ds[tt][rl];
+#pragma unroll
+          for (int i = 0; i < NPT; ++i) S[j + 1][i] = gt * S[j][i] + d * Ks[tt][cl * NPT + i];
+        } else {
+#pragma unroll
+          for (int i = 0; i < NPT; ++i) S[j + 1][i] = S[j][i];
+        }
+      }
+#pragma unroll
+      for (int j = kSub - 1; j >= 0; --j) {
+        const int tt = ts + j;
+        if (tt >= L) continue;
+        float kk[NPT], qq[NPT], pq[NPT], pk[NPT];
+#pragma unroll
+        for (int i = 0; i < NPT; ++i) kk[i] = Ks[tt][cl * NPT + i], qq[i] = Qs[tt][cl * NPT + i];
+        const float gt = Gs[tt], bt = Bs[tt], dyt = DYs[tt][rl], d = Ds[tt][rl], e = Es[tt][rl];
+        float dd = 0.f;
+#pragma unroll
+        for (int i = 0; i < NPT; ++i) {
+          ds[i] += dyt * qq[i];
+          pq[i] = dyt * S[j + 1][i];
+          dd += ds[i] * kk[i];
+        }
+        dd = sum16(dd);
+        const float du = -bt * dd;
+        float dg = 0.f;
+#pragma unroll
+        for (int i = 0; i < NPT; ++i) {
+          pk[i] = ds[i] * d + du * (gt * S[j][i]);
+          ds[i] += du * kk[i];
+          dg += ds[i] * S[j][i];
+          ds[i] *= gt;
+        }
+        dg = sum16(dg);
+        if (cl == 0) rowv[j][0][rl] = bt * dd, rowv[j][1][rl] = dd * e, rowv[j][2][rl] = dg;
+        wave_rows_sum<NPT>(pq, red[j][wave], lane);
+        wave_rows_sum<NPT>(pk, red[j][wave] + Dk, lane);
+      }
+      __syncthreads();
+      const int Ls = min(kSub, L - ts);
+      for (int e = tid; e < Ls * 2 * Dk; e += kThreads) {
+        const int j = e / (2 * Dk), col = e % (2 * Dk);
+        float acc = 0.f;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) acc += red[j][w][col];
+        const int64_t at = (((tok + ts + j) * a.Hv + hv) * a.nblk + it.blk) * Dk;
+        if (col < Dk)
+          a.dq_part[at + col] = acc;
+        else
+          a.dk_part[at + col - Dk] = acc;
+      }
+      for (int e = tid; e < Ls * kRows; e += kThreads) {
+        const int j = e / kRows, r = e % kRows;
+        if (row0 + r < a.Dv) IO<OutT>::st(dv, ((tok + ts + j) * a.Hv + hv) * a.Dv + row0 + r, rowv[j][0][r]);
+      }
+      if (tid < 2 * Ls) {
+        const int j = tid >> 1, which = tid & 1;  // 0: dbeta, 1: dg
+        float acc = 0.f;
+        for (int r = 0; r < kRows; ++r) acc += rowv[j][1 + which][r];
+        const int64_t at = ((tok + ts + j) * a.Hv + hv) * a.nblk + it.blk;
+        (which ? a.dg_part : a.db_part)[at] = acc;
+      }
+      __syncthreads();
+    }
+  }
+  if (a.p.ds0 && live) {
+#pragma unroll
+    for (int i = 0; i < NPT; ++i) a.p.ds0[srow + i] = ds[i];
+  }
+}
+
+// dq, dk [BT, Hk, Dk] = sum over the group's value heads, then over row blocks, of the partials (reference
+// src/delta_grad.cpp:194-198 sums row blocks first; both orders are fixed). dg, dbeta [BT, Hv] likewise over row
+// blocks; dg becomes d/d(log-decay) when g_is_log.
+template <typename OutT>
+__global__ __launch_bounds__(128) void rec_reduce_kernel(const float* dq_part, const float* dk_part,
+                                                         const float* dg_part, const float* db_part, const float* g,
+                                                         OutT* dq, OutT* dk, float* dg, OutT* dbeta, int Hk, int Hv,
+                                                         int Dk, int nblk, int g_is_log) {
+  const int64_t tok = blockIdx.x;
+  const int hk = blockIdx.y, grp = Hv / Hk;
+  for (int col = threadIdx.x; col < Dk; col += blockDim.x) {
+    float aq = 0.f, ak = 0.f;
+    for (int h = 0; h < grp; ++h)
+      for (int b = 0; b < nblk; ++b) {
+        const int64_t at = ((tok * Hv + hk * grp + h) * nblk + b) * Dk + col;
+        aq += dq_part[at];
+        ak += dk_part[at];
+      }
+    IO<OutT>::st(dq, (tok * Hk + hk) * Dk + col, aq);
+    IO<OutT>::st(dk, (tok * Hk + hk) * Dk + col, ak);
+  }
+  if (threadIdx.x < grp) {
+    const int hv = hk * grp + threadIdx.x;
+    float ag = 0.f, ab = 0.f;
+    for (int b = 0; b < nblk; ++b) {
+      ag += dg_part[(tok * Hv + hv) * nblk + b];
+      ab += db_part[(tok * Hv + hv) * nblk + b];
+    }
+    const float gv = g[tok * Hv + hv];
+    dg[tok * Hv + hv] = g_is_log ? ag * expf(gv) : ag;
+    IO<OutT>::st(dbeta, tok * Hv + hv, ab);
+  }
+}
+
+template <typename InT, typename OutT>
+hipError_t launch_fwd(const Problem& p, const FwdPtrs& ptrs, hipStream_t s, Tracer& tr) {
+  RecFwdArgs a;
+  a.p = ptrs;
+  a.Hk = p.Hk, a.Hv = p.Hv, a.Dv = p.Dv, a.g_is_log = p.g_is_log;
+  a.nblk = (p.Dv + kRows - 1) / kRows;
+  a.total = a.nblk * p.Hv * p.N;
+  a.tab = p.tab;
+  const dim3 grid(a.total), block(kThreads);
+  tr.mark();
+  switch (p.Dk) {
+    case 32: hipLaunchKernelGGL((rec_fwd_kernel<2, InT, OutT>), grid, block, 0, s, a); break;
+    case 64: hipLaunchKernelGGL((rec_fwd_kernel<4, InT, OutT>), grid, block, 0, s, a); break;
+    case 128: hipLaunchKernelGGL((rec_fwd_kernel<8, InT, OutT>), grid, block, 0, s, a); break;
+    default: return hipErrorInvalidValue;
+  }
+  tr.mark();
+  return hipGetLastError();
+}
+
+struct BwdWs {
+  float *dq_part, *dk_part, *dg_part, *db_part;
+};
+
+BwdWs carve(const Problem& p, void* ws) {
+  const int64_t nblk = (p.Dv + kRows - 1) / kRows;
+  const int64_t big = p.BT * p.Hv * nblk * p.Dk, small = p.BT * p.Hv * nblk;
+  float* f = static_cast<float*>(ws);
+  return BwdWs{f, f + big, f + 2 * big, f + 2 * big + small};
+}
+
+template <typename InT, typename OutT>
+hipError_t launch_bwd(const Problem& p, const BwdPtrs& ptrs, void* ws, hipStream_t s, Tracer& tr) {
+  RecBwdArgs a;
+  a.p = ptrs;
+  a.Hk = p.Hk, a.Hv = p.Hv, a.Dv = p.Dv, a.g_is_log = p.g_is_log;
+  a.nblk = (p.Dv + kRows - 1) / kRows;
+  a.total = a.nblk * p.Hv * p.N;
+  const BwdWs w = carve(p, ws);
+  a.dq_part = w.dq_part, a.dk_part = w.dk_part, a.dg_part = w.dg_part, a.db_part = w.db_part;
+  a.tab = p.tab;
+  const dim3 grid(a.total), block(kThreads);
+  tr.mark();
+  switch (p.Dk) {
+    case 32: hipLaunchKernelGGL((rec_bwd_kernel<2, InT, OutT>), grid, block, 0, s, a); break;
+    case 64: hipLaunchKernelGGL((rec_bwd_kernel<4, InT, OutT>), grid, block, 0, s, a); break;
+    case 128: hipLaunchKernelGGL((rec_bwd_kernel<8, InT, OutT>), grid, block, 0, s, a); break;
+    default: return hipErrorInvalidValue;
+  }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  tr.mark();
+  if (p.BT == 0) {
+    tr.mark();
+    return hipSuccess;
+  }
+  const dim3 rgrid(static_cast<unsigned>(p.BT), p.Hk);
+  hipLaunchKernelGGL((rec_reduce_kernel<OutT>), rgrid, dim3(128), 0, s, w.dq_part, w.dk_part, w.dg_part, w.db_part,
+                     ptrs.g, static_cast<OutT*>(ptrs.dq), static_cast<OutT*>(ptrs.dk), ptrs.dg,
+                     static_cast<OutT*>(ptrs.dbeta), p.Hk, p.Hv, p.Dk, a.nblk, p.g_is_log);
+  tr.mark();
+  return hipGetLastError();
+}
+
+}  // namespace
+
+const char* rec_supports(const Problem& p) {
+  if (p.Dk != 32 && p.Dk != 64 && p.Dk != 128) return "the recurrent design needs Dk of 32, 64 or 128";
+  return nullptr;
+}
+
+size_t rec_ckpt_bytes(const Problem& p) { return size_t(p.NC) * p.Hv * p.Dv * p.Dk * sizeof(float); }
+
+size_t rec_workspace_bytes(const Problem& p) {
+  const size_t nblk = (p.Dv + kRows - 1) / kRows;
+  return (2 * size_t(p.BT) * p.Hv * nblk * p.Dk + 2 * size_t(p.BT) * p.Hv * nblk) * sizeof(float);
+}
+
+const char* const kRecFwdLaunches = "rec_fwd";
+const char* const kRecBwdLaunches = "rec_bwd,rec_reduce";
+
+hipError_t rec_fwd(const Problem& p, const FwdPtrs& a, void*, hipStream_t s, Tracer& tr) {
+  if (!p.in_bf16) return launch_fwd<float, float>(p, a, s, tr);
+  return p.out_bf16 ? launch_fwd<bf16_t, bf16_t>(p, a, s, tr) : launch_fwd<bf16_t, float>(p, a, s, tr);
+}
+
+hipError_t rec_bwd(const Problem& p, const BwdPtrs& a, void* ws, hipStream_t s, Tracer& tr) {
+  if (!p.in_bf16) return launch_bwd<float, float>(p, a, ws, s, tr);
+  return p.out_bf16 ? launch_bwd<bf16_t, bf16_t>(p, a, ws, s, tr) : launch_bwd<bf16_t, float>(p, a, ws, s, tr);
+}
+
+}  // namespace qbgdn

@@ -1,0 +1,153 @@
+"""The reference's recurrence interface on torch device tensors, running the HIP kernels through the C ABI.
+
+  gated_delta(q, k, v, g, beta, state, train=False)      reference src/deltanet.h:17-19, src/deltanet.cpp:49-61
+  gated_delta_trainable(q, k, v, g, beta, state)         reference src/delta_grad.h:14-16, src/delta_grad.cpp:201-212
+  gated_delta_vjp(primals, dy, dstate)                   reference src/delta_grad.h:19-20, src/delta_grad.cpp:155-199
+
+Shapes and meaning follow the reference: q, k [B, T, Hk, Dk]; v [B, T, Hv, Dv]; g, beta [B, T, Hv]; state
+[B, Hv, Dv, Dk] float32; y comes back in q's dtype and the state in float32. g is the decay factor unless
+log_decay=True, in which case it is the log-decay and its cotangent is d/d(log-decay). Errors are raised as
+RuntimeError carrying the library's message (the reference throws std::runtime_error, src/delta_grad.cpp:164-170).
+torch provides device memory and the stream only; all arithmetic runs in the library's HIP kernels, and there is
+no CPU or eager fallback.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+DEFAULT_DESIGN = _lib.RECURRENT
+
+
+def _dev_ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+def _stream(device):
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _io_dtype(*ts):
+    """bf16 when every activation is bf16, else float32 (the reference computes in float32 either way)."""
+    return torch.bfloat16 if all(t.dtype == torch.bfloat16 for t in ts) else torch.float32
+
+
+def _prep(q, k, v, g, beta, dtype):
+    if not q.is_cuda:
+        raise RuntimeError("gated delta: tensors must be on a HIP device (there is no CPU path)")
+    c = lambda t: t.to(dtype).contiguous()  # noqa: E731
+    return c(q), c(k), c(v), g.to(torch.float32).contiguous(), c(beta)
+
+
+def _desc(q, v, dtype, g_is_log, design, cu_seqlens, out_f32):
+    B, T, Hk, Dk = q.shape
+    Hv, Dv = v.shape[2], v.shape[3]
+    return _lib.make_desc(B, T, Hk, Hv, Dk, Dv, dtype=_lib.BF16 if dtype == torch.bfloat16 else _lib.F32,
+                          g_is_log=g_is_log, design=design, cu_seqlens=cu_seqlens, out_f32=out_f32)
+
+
+def _workspace(desc, device):
+    n = _lib.workspace_bytes(desc)
+    return torch.empty(max(n, 1), dtype=torch.uint8, device=device)
+
+
+def forward(q, k, v, g, beta, state=None, *, log_decay=False, design=DEFAULT_DESIGN, cu_seqlens=None,
+            save_ckpt=True, out_f32=False):
+    """Returns (y, s_out, ckpt); ckpt is the residual buffer the backward reads (None unless save_ckpt).
+    y is in the inputs' dtype, or float32 with out_f32."""
+    dtype = _io_dtype(q, k, v, beta)
+    q, k, v, g, beta = _prep(q, k, v, g, beta, dtype)
+    desc, keep = _desc(q, v, dtype, log_decay, design, cu_seqlens, out_f32)
+    odt = torch.float32 if out_f32 else dtype
+    why = _lib.validate(desc)
+    if why:
+        raise RuntimeError(why)
+    N = q.shape[0] if cu_seqlens is None else len(cu_seqlens) - 1
+    dev = q.device
+    Hv, Dv, Dk = v.shape[2], v.shape[3], q.shape[3]
+    s0 = None if state is None else state.to(torch.float32).contiguous()
+    y = torch.empty(v.shape, dtype=odt, device=dev)
+    s_out = torch.empty(N, Hv, Dv, Dk, dtype=torch.float32, device=dev)
+    ckpt = None
+    if save_ckpt:
+        ckpt = torch.empty(max(_lib.ckpt_bytes(desc) // 4, 1), dtype=torch.float32, device=dev)
+    ws = _workspace(desc, dev)
+    _lib.fwd(desc, _dev_ptr(q), _dev_ptr(k), _dev_ptr(v), _dev_ptr(g), _dev_ptr(beta), _dev_ptr(s0), _dev_ptr(y),
+             _dev_ptr(s_out), _dev_ptr(ckpt), _dev_ptr(ws), _stream(dev))
+    del keep
+    return y, s_out, ckpt
+
+
+def backward(q, k, v, g, beta, ckpt, dy, ds_out=None, *, log_decay=False, design=DEFAULT_DESIGN, cu_seqlens=None,
+             want_ds0=True, out_f32=False):
+    """Returns (dq, dk, dv, dg, dbeta, ds0): dg and ds0 float32, the others in the inputs' dtype (float32 with
+    out_f32, in which case dy is taken as float32 too)."""
+    dtype = _io_dtype(q, k, v, beta)
+    q, k, v, g, beta = _prep(q, k, v, g, beta, dtype)
+    odt = torch.float32 if out_f32 else dtype
+    dy = dy.to(odt).contiguous()
+    desc, keep = _desc(q, v, dtype, log_decay, design, cu_seqlens, out_f32)
+    why = _lib.validate(desc)
+    if why:
+        raise RuntimeError(why)
+    N = q.shape[0] if cu_seqlens is None else len(cu_seqlens) - 1
+    dev = q.device
+    Hv, Dv, Dk = v.shape[2], v.shape[3], q.shape[3]
+    dso = None if ds_out is None else ds_out.to(torch.float32).contiguous()
+    dq, dk = torch.empty(q.shape, dtype=odt, device=dev), torch.empty(k.shape, dtype=odt, device=dev)
+    dv, dbeta = torch.empty(v.shape, dtype=odt, device=dev), torch.empty(beta.shape, dtype=odt, device=dev)
+    dg = torch.empty_like(g)
+    ds0 = torch.empty(N, Hv, Dv, Dk, dtype=torch.float32, device=dev) if want_ds0 else None
+    ws = _workspace(desc, dev)
+    _lib.bwd(desc, _dev_ptr(q), _dev_ptr(k), _dev_ptr(v), _dev_ptr(g), _dev_ptr(beta), _dev_ptr(ckpt), _dev_ptr(dy),
+             _dev_ptr(dso), _dev_ptr(dq), _dev_ptr(dk), _dev_ptr(dv), _dev_ptr(dg), _dev_ptr(dbeta), _dev_ptr(ds0),
+             _dev_ptr(ws), _stream(dev))
+    del keep
+    return dq, dk, dv, dg, dbeta, ds0
+
+
+class _GatedDelta(torch.autograd.Function):
+    """custom_vjp of the recurrence: the forward keeps the chunk-start states, the backward is gated_delta_vjp
+    (reference src/delta_grad.cpp:204-211, which saves only the primals and rebuilds the states instead)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, g, beta, state, log_decay, design):
+        y, s_out, ckpt = forward(q, k, v, g, beta, state, log_decay=log_decay, design=design)
+        ctx.save_for_backward(q, k, v, g, beta, ckpt)
+        ctx.state_meta = (state is not None, None if state is None else state.dtype)
+        ctx.opts = (log_decay, design)
+        return y.to(q.dtype), s_out
+
+    @staticmethod
+    def backward(ctx, dy, dstate):
+        q, k, v, g, beta, ckpt = ctx.saved_tensors
+        log_decay, design = ctx.opts
+        if dy is None:
+            dy = torch.zeros(v.shape, dtype=q.dtype, device=q.device)
+        dq, dk, dv, dg, dbeta, ds0 = backward(q, k, v, g, beta, ckpt, dy, dstate, log_decay=log_decay, design=design)
+        has_state, sdt = ctx.state_meta
+        return (dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), dg.to(g.dtype), dbeta.to(beta.dtype),
+                ds0.to(sdt) if has_state else None, None, None)
+
+
+def gated_delta_trainable(q, k, v, g, beta, state, *, log_decay=False, design=DEFAULT_DESIGN):
+    """(y, new_state) with gated_delta_vjp as the backward."""
+    return _GatedDelta.apply(q, k, v, g, beta, state, log_decay, design)
+
+
+def gated_delta(q, k, v, g, beta, state, train=False, *, log_decay=False, design=DEFAULT_DESIGN):
+    """(y in q's dtype, new float32 state). With train, the trainable form (reference src/deltanet.cpp:55-58)."""
+    if train:
+        return gated_delta_trainable(q, k, v, g, beta, state, log_decay=log_decay, design=design)
+    y, s_out, _ = forward(q, k, v, g, beta, state, log_decay=log_decay, design=design, save_ckpt=False)
+    return y.to(q.dtype), s_out
+
+
+def gated_delta_vjp(primals, dy, dstate, *, log_decay=False, design=DEFAULT_DESIGN):
+    """Cotangents [dq, dk, dv, dg, dbeta, dstate0] of primals (q, k, v, g, beta, state) given those of y and the
+    final state (reference src/delta_grad.cpp:155-199). Runs the forward once to get the chunk-start states."""
+    q, k, v, g, beta, state = primals
+    _, _, ckpt = forward(q, k, v, g, beta, state, log_decay=log_decay, design=design)
+    dq, dk, dv, dg, dbeta, ds0 = backward(q, k, v, g, beta, ckpt, dy, dstate, log_decay=log_decay, design=design)
+    return [dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), dg.to(g.dtype), dbeta.to(beta.dtype), ds0]

@@ -132,3 +132,20 @@ def workload(name: str) -> Workload:
 
 
 WORKLOADS = ("tiny", "qwen35_4b", "qwen35_9b", "qwen35_4b_varlen")
+
+
+def to_device(inp: Inputs, device="cuda"):
+    """torch tensors on device: bf16 inputs from their exact bit patterns, g and states in float32."""
+    import torch
+
+    out = {}
+    for name in ("q", "k", "v", "beta", "dy"):
+        if name in inp.bits:
+            t = torch.from_numpy(inp.bits[name].view(np.int16).reshape(inp.f32[name].shape))
+            out[name] = t.view(torch.bfloat16).to(device)
+        else:
+            out[name] = torch.from_numpy(inp.f32[name]).to(device)
+    for name in ("g", "s0", "ds_out"):
+        x = inp.f32.get(name)
+        out[name] = None if x is None else torch.from_numpy(np.ascontiguousarray(x, dtype=np.float32)).to(device)
+    return out

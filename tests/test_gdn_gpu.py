@@ -1,0 +1,184 @@
+"""Parity of the HIP kernels with the oracle, on the GPU, through the C ABI.
+
+Criterion (the reference's normwise metric, reference tests/test_deltanet.cpp:93-94, 127-128):
+max|x - ref| / max|ref| per output tensor, against the oracle run on the same inputs (bf16 inputs rounded once,
+the oracle in float32 on their exact values):
+  * bf16 I/O, fp32 state (the layer shapes and the packed batch):     <= 2e-3 for y, s_out and every gradient;
+  * float32 I/O (the tiny workload, the golden vectors and the reference's gradient cases): <= 1e-5, the reference's
+    own criterion for its float32 backward.
+"""
+import os
+
+import numpy as np
+import pytest
+
+from helpers import GRAD_NAMES, normwise, reference_case
+from quotebound_amd import _lib
+
+pytestmark = pytest.mark.gpu
+
+OUT_NAMES = ("y", "s_out") + GRAD_NAMES
+DESIGNS = [_lib.RECURRENT]
+DESIGN_IDS = {_lib.RECURRENT: "recurrent", _lib.CHUNKED: "chunked"}
+BF16_TOL = 2e-3
+F32_TOL = 1e-5
+
+
+@pytest.fixture(scope="module")
+def torch_dev():
+    import torch
+
+    if not torch.cuda.is_available():
+        pytest.skip("needs a GPU")
+    _lib.load()  # raises when the library is missing: there is no fallback
+    return torch
+
+
+def run(torch, d, design, *, log_decay=True, cu=None, need_s0_grad=True, out_f32=False):
+    from quotebound_amd import gdn
+
+    y, s_out, ckpt = gdn.forward(d["q"], d["k"], d["v"], d["g"], d["beta"], d.get("s0"), log_decay=log_decay,
+                                 design=design, cu_seqlens=cu, out_f32=out_f32)
+    grads = gdn.backward(d["q"], d["k"], d["v"], d["g"], d["beta"], ckpt, d["dy"], d.get("ds_out"),
+                         log_decay=log_decay, design=design, cu_seqlens=cu, want_ds0=need_s0_grad,
+                         out_f32=out_f32)
+    torch.cuda.synchronize()
+    out = {"y": y, "s_out": s_out, "ckpt": ckpt}
+    out.update(zip(GRAD_NAMES, grads))
+    return {k: (None if v is None else v.float().cpu().numpy()) for k, v in out.items()}
+
+
+def host_to_dev(torch, arrays, dtype):
+    out = {}
+    for k, x in arrays.items():
+        if x is None:
+            continue
+        t = torch.tensor(np.asarray(x, dtype=np.float32))
+        if k in ("q", "k", "v", "beta", "dy"):
+            t = t.to(dtype)
+        out[k] = t.cuda()
+    return out
+
+
+def assert_close(got, ref, tol, names=OUT_NAMES, label=""):
+    errs = {n: normwise(got[n], ref[n]) for n in names}
+    report = "; ".join(f"{n} {errs[n]:.2e} (max-abs {np.max(np.abs(got[n] - ref[n])):.2e})" for n in names)
+    print(label, report)
+    for n in names:
+        assert errs[n] <= tol, f"{label}: {n} normwise error {errs[n]:.3g} > {tol}; {report}"
+
+
+def bf16_half_ulp(x):
+    """Half the bf16 spacing at |x| (x in [2^(e-1), 2^e) has spacing 2^(e-8)): the most that rounding to nearest
+    can move it."""
+    return np.ldexp(1.0, np.frexp(np.asarray(x, np.float64))[1] - 9)
+
+
+def _golden(name):
+    z = np.load(os.path.join(os.path.dirname(__file__), "golden", name + ".npz"))
+    inp = {k[3:]: z[k] for k in z.files if k.startswith("in_")}
+    out = {k[4:]: z[k] for k in z.files if k.startswith("out_")}
+    return inp, out
+
+
+@pytest.mark.parametrize("design", DESIGNS, ids=DESIGN_IDS.get)
+@pytest.mark.parametrize("name", ["tiny_fp32", "tiny_fp32_s0"])
+def test_golden_vectors(torch_dev, design, name):
+    torch = torch_dev
+    inp, exp = _golden(name)
+    got = run(torch, host_to_dev(torch, inp, torch.float32), design)
+    assert_close(got, exp, F32_TOL, label=f"{name} design {design}")
+
+
+@pytest.mark.parametrize("design", DESIGNS, ids=DESIGN_IDS.get)
+@pytest.mark.parametrize("case", [  # reference tests/test_deltanet.cpp:266-275
+    (1, 19, 16, 32, 128, 128, 0.5), (1, 64, 16, 32, 128, 128, 0.9), (2, 150, 16, 32, 128, 128, 0.99),
+    (1, 129, 16, 32, 128, 128, 0.9), (1, 70, 2, 8, 32, 32, 0.9), (2, 33, 4, 4, 64, 64, 0.99),
+    (1, 70, 2, 4, 128, 4, 0.9), (1, 40, 2, 4, 256, 64, 0.9)], ids=lambda c: "B%dT%dHk%dHv%dDk%dDv%d" % c[:6])
+def test_reference_gradient_cases(torch_dev, oracle, design, case):
+    torch = torch_dev
+    B, T, Hk, Hv, Dk, Dv, g_lo = case
+    inp = reference_case(B, T, Hk, Hv, Dk, Dv, g_lo, seed=100 + T)
+    d, _ = _lib.make_desc(B, T, Hk, Hv, Dk, Dv, dtype=_lib.F32, g_is_log=False, design=design)
+    why = _lib.validate(d)
+    if why is not None:  # a shape the design does not take must be refused with a reason, never run
+        with pytest.raises(RuntimeError, match="gated delta"):
+            run(torch, host_to_dev(torch, inp, torch.float32), design, log_decay=False)
+        return
+    y, s, ck = oracle.fwd(inp["q"], inp["k"], inp["v"], inp["g"], inp["beta"], inp["s0"], g_is_log=False)
+    grads = oracle.bwd(inp["q"], inp["k"], inp["v"], inp["g"], inp["beta"], ck, inp["dy"], inp["ds_out"],
+                       g_is_log=False)
+    exp = {"y": y, "s_out": s, **dict(zip(GRAD_NAMES, grads))}
+    got = run(torch, host_to_dev(torch, inp, torch.float32), design, log_decay=False)
+    assert_close(got, exp, F32_TOL, label=f"case {case} design {design}")
+
+
+@pytest.mark.parametrize("design", DESIGNS, ids=DESIGN_IDS.get)
+@pytest.mark.parametrize("wname", ["qwen35_4b", "qwen35_9b", "qwen35_4b_varlen"])
+def test_layer_shapes_bf16(torch_dev, oracle, design, wname):
+    """The benchmark workloads at full size: B=1, T=4096, Dk=Dv=128, Hk=16, Hv=32 (4B) or 48 (9B, nonzero initial
+    state, dS0 returned), and 8 packed sequences at the 4B shape."""
+    torch = torch_dev
+    from quotebound_amd.synthetic import make_inputs, to_device, workload
+
+    from quotebound_amd.synthetic import round_bf16
+
+    w = workload(wname)
+    inp = make_inputs(w)
+    cu = w.cu_seqlens
+    exp = oracle.fwd_bwd(inp.f32, cu_seqlens=cu, dtype=np.float32)
+    d = to_device(inp)
+    # The kernels' float32 results (bf16 inputs, float32 outputs): the 2e-3 criterion on every output.
+    d32 = dict(d, dy=d["dy"].float())
+    got32 = run(torch, d32, design, cu=cu, out_f32=True)
+    assert_close(got32, exp, BF16_TOL, label=f"{wname} design {design} (f32 out)")
+    nc = exp["ckpt"].size
+    assert normwise(got32["ckpt"][:nc].reshape(exp["ckpt"].shape), exp["ckpt"]) <= BF16_TOL
+    # bf16 outputs are those float32 results rounded once to nearest even, and nothing else changes.
+    got16 = run(torch, d, design, cu=cu)
+    for n in ("y", "dq", "dk", "dv", "dbeta"):
+        assert np.array_equal(got16[n], round_bf16(got32[n].astype(np.float32))), n
+    for n in ("s_out", "dg", "ds0"):
+        assert np.array_equal(got16[n], got32[n]), n
+    # Against the oracle, the bf16 outputs miss by at most the criterion plus their own half-ulp rounding.
+    for n in ("y", "dq", "dk", "dv", "dbeta"):
+        slack = np.abs(got16[n] - exp[n]) - bf16_half_ulp(np.maximum(np.abs(exp[n]), np.abs(got32[n])))
+        assert slack.max() <= BF16_TOL * np.max(np.abs(exp[n])), n
+
+
+@pytest.mark.parametrize("design", DESIGNS, ids=DESIGN_IDS.get)
+def test_deterministic(torch_dev, design):
+    """Same inputs, same bits: every sum runs in a fixed order (the reference's resume bit-identity relies on it,
+    reference src/delta_grad.cpp:19-22)."""
+    torch = torch_dev
+    from quotebound_amd.synthetic import Workload, make_inputs, to_device
+
+    w = Workload("det", 1, 700, 4, 8, 128, 128, seed=21, s0_std=0.02, ds_out=True)
+    d = to_device(make_inputs(w))
+    a = run(torch, d, design)
+    b = run(torch, d, design)
+    for n in OUT_NAMES:
+        assert np.array_equal(a[n], b[n]), n
+
+
+@pytest.mark.parametrize("design", DESIGNS, ids=DESIGN_IDS.get)
+def test_trainable_autograd_matches_vjp(torch_dev, design):
+    """gated_delta_trainable under torch autograd gives gated_delta_vjp's cotangents (reference
+    src/delta_grad.cpp:201-212), with the decay factor as input as the reference's gated_delta takes it."""
+    torch = torch_dev
+    from quotebound_amd import gdn
+
+    B, T, Hk, Hv, D = 1, 130, 2, 4, 64
+    inp = reference_case(B, T, Hk, Hv, D, D, 0.9, seed=31)
+    d = host_to_dev(torch, inp, torch.bfloat16)
+    leaves = {k: d[k].clone().requires_grad_(True) for k in ("q", "k", "v", "g", "beta", "s0")}
+    y, s = gdn.gated_delta(leaves["q"], leaves["k"], leaves["v"], leaves["g"], leaves["beta"], leaves["s0"],
+                           train=True, design=design)
+    assert y.dtype == torch.bfloat16 and s.dtype == torch.float32
+    ((y.float() * d["dy"].float()).sum() + (s * d["ds_out"]).sum()).backward()
+    vjp = gdn.gated_delta_vjp([d[k] for k in ("q", "k", "v", "g", "beta", "s0")], d["dy"], d["ds_out"],
+                              design=design)
+    for name, got in zip(("q", "k", "v", "g", "beta", "s0"), vjp):
+        assert torch.equal(leaves[name].grad, got), name
+    y2, s2 = gdn.gated_delta(d["q"], d["k"], d["v"], d["g"], d["beta"], d["s0"], design=design)
+    assert torch.equal(y2, y.detach()) and torch.equal(s2, s.detach())

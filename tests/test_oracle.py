@@ -204,7 +204,6 @@ def test_zero_decay_cuts_the_gradient(oracle):
     """With g_t = 0 the state is wiped at t: inputs before t get no gradient from cotangents at or after t."""
     inp = small_case(1, 40, 1, 2, 8, 4, seed=12, s0=True, ds_out=True, log_decay=False)
     inp["g"][0, 25, :] = 0.0
-    a = oracle.fwd_bwd(inp, chunk=16) if False else None  # noqa: F841
     y, s, ck = oracle.fwd(inp["q"], inp["k"], inp["v"], inp["g"], inp["beta"], inp["s0"], chunk=16, g_is_log=False)
     base = oracle.bwd(inp["q"], inp["k"], inp["v"], inp["g"], inp["beta"], ck, inp["dy"], inp["ds_out"], chunk=16,
                       g_is_log=False)
