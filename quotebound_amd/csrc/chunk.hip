@@ -1,14 +1,101 @@
-// Design 2: the chunkwise WY/UT form on MFMA. Not built yet: every call is rejected with a clear error.
+// Chunked design: the host side. The forward is prep (T, G per chunk) then the sequential state pass (states,
+// y, final state); the backward is the reverse state pass (dv, ds0 and each chunk's end-state cotangent) then the
+// per-chunk gradient kernel (dq, dk, dg, dbeta).
+#include "chunk_kernels.h"
 #include "gdn_kernels.h"
 
 namespace qbgdn {
+namespace {
 
-const char* chunk_supports(const Problem&) { return "the chunked design is not available in this build"; }
-size_t chunk_ckpt_bytes(const Problem&) { return 0; }
-size_t chunk_workspace_bytes(const Problem&) { return 0; }
-const char* const kChunkFwdLaunches = "";
-const char* const kChunkBwdLaunches = "";
-hipError_t chunk_fwd(const Problem&, const FwdPtrs&, void*, hipStream_t, Tracer&) { return hipErrorNotSupported; }
-hipError_t chunk_bwd(const Problem&, const BwdPtrs&, void*, hipStream_t, Tracer&) { return hipErrorNotSupported; }
+ChunkLayout layout_of(const Problem& p) { return ChunkLayout{p.NC, p.Hv, p.Dv, p.Dk}; }
+
+size_t extras_bytes(const Problem& p) { return size_t(p.NC) * p.Hv * (kC * kC * 4 + kC * 8); }
+size_t dsend_bytes(const Problem& p) { return size_t(p.NC) * p.Hv * p.Dv * p.Dk * 4; }
+
+ChunkArgs base_args(const Problem& p) {
+  ChunkArgs a{};
+  a.lay = layout_of(p);
+  a.Hk = p.Hk, a.Hv = p.Hv, a.Dv = p.Dv, a.g_is_log = p.g_is_log;
+  a.nblk = p.Dv / 16;
+  a.N = p.N;
+  a.tab = p.tab;
+  return a;
+}
+
+// T and G sit after the states in ckpt, or at the start of the workspace when there is no ckpt.
+void place_extras(const Problem& p, ChunkArgs& a, float* ckpt, void* ws) {
+  float* base = ckpt ? ckpt + a.lay.states_elems() : static_cast<float*>(ws);
+  a.Tall = base;
+  a.Gall = reinterpret_cast<double*>(base + p.NC * p.Hv * int64_t(kC * kC));
+}
+
+}  // namespace
+
+const char* const kChunkFwdLaunches = "chunk_prep,chunk_fwd";
+const char* const kChunkBwdLaunches = "chunk_bwd_state,chunk_bwd_grads";
+
+const char* chunk_supports(const Problem& p) {
+  if (!p.in_bf16) return "the chunked design needs bf16 inputs (use the recurrent design for float32)";
+  if (p.Dk != 128) return "the chunked design needs Dk of 128";
+  if (p.Dv % 32) return "the chunked design needs Dv a multiple of 32";
+  if (p.NC * p.Hv > (int64_t(1) << 30) || int64_t(p.N) * p.Hv * (p.Dv / 16) > (int64_t(1) << 30))
+    return "problem too large for the chunked design's grid";
+  return nullptr;
+}
+
+size_t chunk_ckpt_bytes(const Problem& p) { return layout_of(p).bytes(); }
+
+size_t chunk_workspace_bytes(const Problem& p) {
+  const size_t a = dsend_bytes(p), b = extras_bytes(p);
+  return a > b ? a : b;
+}
+
+hipError_t chunk_fwd(const Problem& p, const FwdPtrs& f, void* ws, hipStream_t s, Tracer& tr) {
+  ChunkArgs a = base_args(p);
+  a.q = static_cast<const bf16_t*>(f.q);
+  a.k = static_cast<const bf16_t*>(f.k);
+  a.v = static_cast<const bf16_t*>(f.v);
+  a.beta = static_cast<const bf16_t*>(f.beta);
+  a.g = f.g;
+  a.s0 = f.s0;
+  a.y = f.y;
+  a.s_out = f.s_out;
+  a.ckpt = f.ckpt;
+  place_extras(p, a, f.ckpt, ws);
+  tr.mark();
+  hipError_t e = launch_chunk_prep(a, s);
+  if (e != hipSuccess) return e;
+  tr.mark();
+  e = launch_chunk_fwd(a, p.out_bf16, s);
+  tr.mark();
+  return e;
+}
+
+hipError_t chunk_bwd(const Problem& p, const BwdPtrs& b, void* ws, hipStream_t s, Tracer& tr) {
+  ChunkArgs a = base_args(p);
+  a.q = static_cast<const bf16_t*>(b.q);
+  a.k = static_cast<const bf16_t*>(b.k);
+  a.v = static_cast<const bf16_t*>(b.v);
+  a.beta = static_cast<const bf16_t*>(b.beta);
+  a.g = b.g;
+  a.ckpt = const_cast<float*>(b.ckpt);
+  place_extras(p, a, a.ckpt, nullptr);
+  a.dy = b.dy;
+  a.ds_out = b.ds_out;
+  a.dq = b.dq;
+  a.dk = b.dk;
+  a.dv = b.dv;
+  a.dg = b.dg;
+  a.dbeta = b.dbeta;
+  a.ds0 = b.ds0;
+  a.dsend = static_cast<float*>(ws);
+  tr.mark();
+  hipError_t e = launch_chunk_bwd_state(a, p.out_bf16, s);
+  if (e != hipSuccess) return e;
+  tr.mark();
+  e = launch_chunk_bwd_grads(a, p.out_bf16, s);
+  tr.mark();
+  return e;
+}
 
 }  // namespace qbgdn

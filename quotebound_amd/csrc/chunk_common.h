@@ -1,0 +1,85 @@
+// Shared pieces of the chunked design: buffer layouts, the chunk-slot -> (sequence, chunk) map, and staging.
+//
+// Residuals (the ckpt buffer), per chunk slot s and value head h:
+//   states  [NC][Hv][Dv][Dk]  f32   state at the chunk's start (the reference's ckpt, src/delta_grad.cpp:172-181)
+//   T       [NC][Hv][64][64]  f32   (I + A)^-1 of the chunk (row i, col j), A = strict_lower(diag(beta)(E * K K^T))
+//   Gam     [NC][Hv][64]      f64   G_i = sum_{j <= i} a_j within the chunk (0-padded past its end)
+// Workspace: dSend [NC][Hv][Dv][Dk] f32, the cotangent of the state at each chunk's end.
+#pragma once
+#include "gdn_common.h"
+#include "mfma.h"
+
+namespace qbgdn {
+
+constexpr int kC = kChunk;  // 64 positions per chunk
+constexpr int kPadB = 8;    // bf16 row padding in LDS (keeps 16-byte alignment, staggers banks)
+
+struct ChunkLayout {
+  int64_t NC;
+  int Hv, Dv, Dk;
+  __host__ __device__ int64_t states_elems() const { return NC * Hv * int64_t(Dv) * Dk; }
+  __host__ __device__ float* T(float* ckpt) const { return ckpt + states_elems(); }
+  __host__ __device__ const float* T(const float* ckpt) const { return ckpt + states_elems(); }
+  __host__ __device__ double* Gam(float* ckpt) const {
+    return reinterpret_cast<double*>(ckpt + states_elems() + NC * Hv * int64_t(kC * kC));
+  }
+  __host__ __device__ const double* Gam(const float* ckpt) const {
+    return reinterpret_cast<const double*>(ckpt + states_elems() + NC * Hv * int64_t(kC * kC));
+  }
+  __host__ __device__ size_t bytes() const {
+    return size_t(states_elems()) * 4 + size_t(NC) * Hv * (kC * kC * 4 + kC * 8);
+  }
+};
+
+// The sequence and chunk of a chunk slot (slots of sequence n are [slot0[n], slot0[n + 1])).
+struct SlotPos {
+  int n, c;
+  int64_t tok;  // first token of the chunk
+  int L;        // valid positions
+};
+
+__device__ __forceinline__ SlotPos slot_pos(const SeqTable& tab, int64_t slot) {
+  int n, c;
+  if (tab.n == 0) {
+    n = int(slot / tab.nc);
+    c = int(slot - int64_t(n) * tab.nc);
+  } else {  // largest n with slot0[n] <= slot (empty sequences share a slot0 with their successor)
+    int lo = 0, hi = tab.n - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (tab.slot0[mid] <= slot) lo = mid; else hi = mid - 1;
+    }
+    n = lo;
+    c = int(slot - tab.slot0[n]);
+  }
+  const Seq sq = seq_of(tab, n);
+  const int t0 = c * kC;
+  return SlotPos{n, c, sq.tok0 + t0, min(kC, sq.len - t0)};
+}
+
+// Copies rows [0, L) of a [tokens, H, D] bf16 tensor's head h into LDS rows of length D (stride ld), zero rows past
+// L. 8 elements per access.
+template <int D>
+__device__ __forceinline__ void stage_rows_bf16(__bf16* dst, int ld, const bf16_t* src, int64_t tok, int H, int h,
+                                                int L, int nthreads) {
+  constexpr int V8 = D / 8;
+  for (int e = threadIdx.x; e < kC * V8; e += nthreads) {
+    const int t = e / V8, c8 = (e % V8) * 8;
+    bf16x8 v;
+    if (t < L) {
+      v = gld8(src + ((tok + t) * H + h) * int64_t(D) + c8);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = (__bf16)0.f;
+    }
+    *reinterpret_cast<bf16x8*>(dst + t * ld + c8) = v;
+  }
+}
+
+// The decay factor's log: the input itself (g_is_log) or log of the factor.
+__device__ __forceinline__ double log_decay(const float* g, int64_t i, int g_is_log) {
+  const float x = g[i];
+  return g_is_log ? double(x) : log(double(x));
+}
+
+}  // namespace qbgdn

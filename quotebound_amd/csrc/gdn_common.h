@@ -66,6 +66,15 @@ __device__ __forceinline__ float sum16(float x) {
   return x;
 }
 
+// Blocks are dispatched round-robin over the MI355X's 8 XCDs (block id runs on XCD id % 8), each with its own
+// L2. This gives XCD x a contiguous range of work items, so neighbouring items (which read the same key head)
+// share an L2. A bijection on [0, n).
+__device__ __forceinline__ int xcd_remap(int id, int n) {
+  const int per = n >> 3, rem = n & 7;
+  const int x = id & 7, s = id >> 3;
+  return x * per + (x < rem ? x : rem) + s;
+}
+
 // ---- packed sequences ------------------------------------------------------------------------------------------
 // Passed by value as a kernel argument. n == 0: batch mode, sequence i is batch row i (T tokens, nc chunk slots
 // each). n > 0: tok0[i] is the first token of sequence i (tok0[n] == total tokens) and slot0[i] its first chunk

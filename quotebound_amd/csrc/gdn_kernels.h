@@ -80,13 +80,4 @@ extern const char* const kChunkBwdLaunches;
 hipError_t chunk_fwd(const Problem& p, const FwdPtrs& a, void* ws, hipStream_t s, Tracer& tr);
 hipError_t chunk_bwd(const Problem& p, const BwdPtrs& a, void* ws, hipStream_t s, Tracer& tr);
 
-// Blocks are dispatched round-robin over the MI355X's 8 XCDs (block id runs on XCD id % 8), each with its own
-// L2. This gives XCD x a contiguous range of work items, so neighbouring items (which read the same key head)
-// share an L2. A bijection on [0, n).
-__device__ __forceinline__ int xcd_remap(int id, int n) {
-  const int per = n >> 3, rem = n & 7;
-  const int x = id & 7, s = id >> 3;
-  return x * per + (x < rem ? x : rem) + s;
-}
-
 }  // namespace qbgdn

@@ -1,0 +1,84 @@
+// MFMA building blocks for the chunked design: v_mfma_f32_16x16x32_bf16 (gfx950) with float32 operands split
+// into a bf16 pair (hi = rne(x), lo = rne(x - hi)) so products of float32 values keep ~2^-16 relative accuracy:
+//   x * y ~= hi(x) hi(y) + hi(x) lo(y) + lo(x) hi(y)        (three MFMAs; two when one side is exact in bf16).
+//
+// Lane layouts of v_mfma_f32_16x16x32_bf16 (wave64, lane l, g = l / 16):
+//   A [16 x 32]: lane l holds row l % 16, k = 8 g + 0..7
+//   B [32 x 16]: lane l holds col l % 16, k = 8 g + 0..7
+//   C [16 x 16]: lane l holds col l % 16, rows 4 g + 0..3
+// The contraction index k may be permuted freely as long as A and B use the same permutation. Two stacked C tiles
+// (rows 0-15 and 16-31 of a 32-row block) therefore feed a later product directly as its k = 32 operand with
+// k order {4g + 0..3, 16 + 4g + 0..3}: a C result can be used, without moving it, as the operand that contracts
+// over C's row index. kperm() gives that order.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include "gdn_common.h"
+
+namespace qbgdn {
+
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
+
+__device__ __forceinline__ f32x4 mma(f32x4 c, bf16x8 a, bf16x8 b) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+struct Split8 {
+  bf16x8 hi, lo;
+};
+
+__device__ __forceinline__ Split8 split8(const float* x) {
+  Split8 s;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const __bf16 h = (__bf16)x[j];
+    s.hi[j] = h;
+    s.lo[j] = (__bf16)(x[j] - (float)h);
+  }
+  return s;
+}
+
+__device__ __forceinline__ bf16x8 round8(const float* x) {
+  bf16x8 r;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) r[j] = (__bf16)x[j];
+  return r;
+}
+
+// acc += A * B for split operands (three MFMAs).
+__device__ __forceinline__ f32x4 mma3(f32x4 c, const Split8& a, const Split8& b) {
+  c = mma(c, a.hi, b.hi);
+  c = mma(c, a.hi, b.lo);
+  return mma(c, a.lo, b.hi);
+}
+// acc += A * B with B exact in bf16 (two MFMAs).
+__device__ __forceinline__ f32x4 mma2(f32x4 c, const Split8& a, bf16x8 b) {
+  c = mma(c, a.hi, b);
+  return mma(c, a.lo, b);
+}
+__device__ __forceinline__ f32x4 mma2(f32x4 c, bf16x8 a, const Split8& b) {
+  c = mma(c, a, b.hi);
+  return mma(c, a, b.lo);
+}
+
+__device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
+
+// Position of element j (0..7) of a lane in k group g under the stacked-C order: {4g + 0..3, 16 + 4g + 0..3}.
+__device__ __forceinline__ int kperm(int g, int j) { return (j < 4 ? 4 * g + j : 16 + 4 * g + (j - 4)); }
+
+// Loads 8 consecutive bf16 from LDS (16-byte aligned).
+__device__ __forceinline__ bf16x8 lds8(const __bf16* p) { return *reinterpret_cast<const bf16x8*>(p); }
+
+// Loads 4 + 4 bf16 (two 8-byte runs) from LDS: p[0..3] and p[16..19], the stacked-C k order.
+__device__ __forceinline__ bf16x8 lds4x2(const __bf16* p) {
+  typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4;
+  const bf16x4 a = *reinterpret_cast<const bf16x4*>(p);
+  const bf16x4 b = *reinterpret_cast<const bf16x4*>(p + 16);
+  return bf16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+}
+
+// Global bf16 bits -> bf16x8 (16-byte aligned).
+__device__ __forceinline__ bf16x8 gld8(const bf16_t* p) { return *reinterpret_cast<const bf16x8*>(p); }
+
+}  // namespace qbgdn

@@ -17,7 +17,7 @@ import torch
 
 from . import _lib
 
-DEFAULT_DESIGN = _lib.RECURRENT
+DEFAULT_DESIGN = _lib.CHUNKED
 
 
 def _dev_ptr(t):

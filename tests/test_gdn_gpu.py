@@ -18,7 +18,7 @@ from quotebound_amd import _lib
 pytestmark = pytest.mark.gpu
 
 OUT_NAMES = ("y", "s_out") + GRAD_NAMES
-DESIGNS = [_lib.RECURRENT]
+DESIGNS = [_lib.RECURRENT, _lib.CHUNKED]
 DESIGN_IDS = {_lib.RECURRENT: "recurrent", _lib.CHUNKED: "chunked"}
 BF16_TOL = 2e-3
 F32_TOL = 1e-5
@@ -81,7 +81,7 @@ def _golden(name):
     return inp, out
 
 
-@pytest.mark.parametrize("design", DESIGNS, ids=DESIGN_IDS.get)
+@pytest.mark.parametrize("design", [_lib.RECURRENT], ids=DESIGN_IDS.get)
 @pytest.mark.parametrize("name", ["tiny_fp32", "tiny_fp32_s0"])
 def test_golden_vectors(torch_dev, design, name):
     torch = torch_dev
@@ -111,6 +111,54 @@ def test_reference_gradient_cases(torch_dev, oracle, design, case):
     exp = {"y": y, "s_out": s, **dict(zip(GRAD_NAMES, grads))}
     got = run(torch, host_to_dev(torch, inp, torch.float32), design, log_decay=False)
     assert_close(got, exp, F32_TOL, label=f"case {case} design {design}")
+
+
+REF_SHAPES_BF16 = [c for c in [  # the reference's gradient cases, bf16 inputs (reference tests/test_deltanet.cpp:266-275)
+    (1, 19, 16, 32, 128, 128, 0.5), (1, 64, 16, 32, 128, 128, 0.9), (2, 150, 16, 32, 128, 128, 0.99),
+    (1, 129, 16, 32, 128, 128, 0.9)]]
+
+
+@pytest.mark.parametrize("design", DESIGNS, ids=DESIGN_IDS.get)
+@pytest.mark.parametrize("case", REF_SHAPES_BF16, ids=lambda c: "B%dT%dHk%dHv%dDk%dDv%d" % c[:6])
+def test_reference_cases_bf16_inputs(torch_dev, oracle, design, case):
+    """The reference's gradient cases with the inputs rounded to bf16: the kernels' float32 outputs against the oracle
+    on the same rounded inputs (decay factor input, cotangents on y and the final state, nonzero initial state)."""
+    torch = torch_dev
+    from quotebound_amd.synthetic import round_bf16
+
+    B, T, Hk, Hv, Dk, Dv, g_lo = case
+    inp = reference_case(B, T, Hk, Hv, Dk, Dv, g_lo, seed=100 + T)
+    for n in ("q", "k", "v", "beta", "dy"):
+        inp[n] = round_bf16(np.asarray(inp[n], np.float32)).astype(np.float64)
+    y, s, ck = oracle.fwd(inp["q"], inp["k"], inp["v"], inp["g"], inp["beta"], inp["s0"], g_is_log=False)
+    grads = oracle.bwd(inp["q"], inp["k"], inp["v"], inp["g"], inp["beta"], ck, inp["dy"], inp["ds_out"],
+                       g_is_log=False)
+    exp = {"y": y, "s_out": s, **dict(zip(GRAD_NAMES, grads))}
+    d = host_to_dev(torch, inp, torch.bfloat16)
+    d["dy"] = d["dy"].float()
+    got = run(torch, d, design, log_decay=False, out_f32=True)
+    assert_close(got, exp, BF16_TOL, label=f"bf16 case {case} design {design}")
+
+
+@pytest.mark.parametrize("design", DESIGNS, ids=DESIGN_IDS.get)
+def test_forward_only(torch_dev, oracle, design):
+    """The forward alone at the 4B layer shape: y, the final state and the chunk-start states."""
+    torch = torch_dev
+    from quotebound_amd import gdn
+    from quotebound_amd.synthetic import make_inputs, to_device, workload
+
+    w = workload("qwen35_4b")
+    inp = make_inputs(w)
+    y, s, ck = oracle.fwd(inp.f32["q"], inp.f32["k"], inp.f32["v"], inp.f32["g"], inp.f32["beta"], None,
+                          dtype=np.float32)
+    d = to_device(inp)
+    gy, gs, gck = gdn.forward(d["q"], d["k"], d["v"], d["g"], d["beta"], None, log_decay=True, design=design,
+                              out_f32=True)
+    torch.cuda.synchronize()
+    got = {"y": gy.cpu().numpy(), "s_out": gs.cpu().numpy(),
+           "ckpt": gck[:ck.size].cpu().numpy().reshape(ck.shape)}
+    assert_close(got, {"y": y, "s_out": s, "ckpt": ck}, BF16_TOL, names=("y", "s_out", "ckpt"),
+                 label=f"forward design {design}")
 
 
 @pytest.mark.parametrize("design", DESIGNS, ids=DESIGN_IDS.get)
@@ -168,7 +216,7 @@ def test_trainable_autograd_matches_vjp(torch_dev, design):
     torch = torch_dev
     from quotebound_amd import gdn
 
-    B, T, Hk, Hv, D = 1, 130, 2, 4, 64
+    B, T, Hk, Hv, D = 1, 130, 2, 4, 128
     inp = reference_case(B, T, Hk, Hv, D, D, 0.9, seed=31)
     d = host_to_dev(torch, inp, torch.bfloat16)
     leaves = {k: d[k].clone().requires_grad_(True) for k in ("q", "k", "v", "g", "beta", "s0")}
