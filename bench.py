@@ -50,15 +50,26 @@ class Hip:
 
 
 def algorithmic_work(w, kernel, nc, design):
-    """(kind, amount per launch) for a kernel: "bytes" of compulsory HBM traffic or "flops" of the recurrent
-    algorithm (7 Dk Dv per token and value head forward, 15 backward; recompute not credited)."""
+    """(kind, amount per launch) for a kernel: "bytes" of the HBM traffic the kernel cannot avoid (each input read
+    once, each output written once, at their storage types), or "flops" of the recurrent algorithm (7 Dk Dv per
+    token and value head forward, 15 backward; recompute not credited)."""
     BT, Hk, Hv, Dk, Dv = w.B * w.T, w.Hk, w.Hv, w.Dk, w.Dv
     io = 2 if w.dtype == "bf16" else 4
     qk = 2 * BT * Hk * Dk * io
     vv = BT * Hv * Dv * io
     scal = BT * Hv * (4 + io)
     states = nc * Hv * Dv * Dk * 4
-    s0 = (w.n_states * Hv * Dv * Dk * 4) if w.s0_std > 0 else 0
+    tg = nc * Hv * (64 * 64 * 4 + 64 * 8)
+    fin = w.n_states * Hv * Dv * Dk * 4
+    s0 = fin if w.s0_std > 0 else 0
+    if kernel == "chunk_prep":
+        return "bytes", qk / 2 + scal + tg
+    if kernel == "chunk_fwd":
+        return "bytes", qk + vv + BT * Hv * io + tg + vv + states + s0 + fin
+    if kernel == "chunk_bwd_state":
+        return "bytes", qk + vv + BT * Hv * io + tg + states + vv + fin
+    if kernel == "chunk_bwd_grads":
+        return "bytes", qk + 2 * vv + scal + tg + 2 * states + qk + BT * Hv * (4 + io)
     if kernel == "rec_fwd":
         return "flops", 7.0 * Dk * Dv * BT * Hv
     if kernel == "rec_bwd":
@@ -67,6 +78,23 @@ def algorithmic_work(w, kernel, nc, design):
         nblk = (Dv + 15) // 16
         return "bytes", 2 * BT * Hv * nblk * (Dk + 1) * 4 + qk + BT * Hv * (4 + io)
     raise KeyError(kernel)
+
+
+def step_roof_us(w, nc):
+    """The whole fwd+bwd step's roofline time: max(bytes_alg / HBM peak, flops_alg / MFMA peak), bytes_alg = the
+    compulsory bf16/f32 I/O plus the 64-token fp32 checkpoints written once and read once, flops_alg = 22 Dk Dv per
+    token and value head."""
+    BT, Hk, Hv, Dk, Dv = w.B * w.T, w.Hk, w.Hv, w.Dk, w.Dv
+    io = 2 if w.dtype == "bf16" else 4
+    fin = w.n_states * Hv * Dv * Dk * 4
+    s0 = fin if w.s0_std > 0 else 0
+    fwd = 2 * BT * Hk * Dk * io + BT * Hv * Dv * io + BT * Hv * (4 + io) + s0 + BT * Hv * Dv * io + fin
+    bwd = 2 * BT * Hk * Dk * io + BT * Hv * Dv * io + BT * Hv * (4 + io) + BT * Hv * Dv * io \
+        + 2 * BT * Hk * Dk * io + BT * Hv * Dv * io + BT * Hv * (4 + io) + s0
+    ckpt = (nc - w.n_states) * Hv * Dv * Dk * 4 + nc * Hv * Dv * Dk * 4
+    nbytes = fwd + bwd + ckpt
+    flops = 22.0 * Dk * Dv * BT * Hv
+    return max(nbytes / (HBM_PEAK_GBS * 1e9), flops / (BF16_MFMA_PEAK_TFLOPS * 1e12)) * 1e6, nbytes, flops
 
 
 def roofline_of(kind, amount, ms):
@@ -212,6 +240,7 @@ def main():
     roof = roofline_of(kind, amount, r["kernels_ms"][dom])
     roof.update({"kernel": dom, "mean_ms": r["kernels_ms"][dom], "algorithmic_" + kind + "_per_launch": amount,
                  "traffic": None})
+    t_roof, nbytes, nflops = step_roof_us(w, r["nc"])
     out = {
         "metric": METRIC,
         "value": r["tokens_per_s"],
@@ -223,13 +252,15 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": "f32" if best == "recurrent" else "bf16x3-mfma/f32",
         "data": "synthetic (seeded numpy: unit-norm q/k, N(0,1) v, log-decay -softplus(N) clipped to [-8,0], "
                 "beta sigmoid(N), dy N(0,1))",
         "config": {"workload": f"{w.name}: B={w.B} T={w.T} Hk={w.Hk} Hv={w.Hv} Dk={w.Dk} Dv={w.Dv}, "
                                f"{w.dtype} I/O, fp32 state, 64-token checkpoints, fwd+bwd",
                    "design": best, "io_dtype": w.dtype},
         "roofline": roof,
+        "step_roofline": {"t_roof_us": t_roof, "bytes_alg": nbytes, "flops_alg": nflops,
+                          "t_step_us": r["ms_per_step"] * 1e3, "frac": t_roof / (r["ms_per_step"] * 1e3)},
         "designs": {k: ({kk: vv for kk, vv in v.items() if kk != "nc"} if "ms_per_step" in v else v)
                     for k, v in results.items()},
     }
