@@ -9,7 +9,7 @@ namespace {
 
 ChunkLayout layout_of(const Problem& p) { return ChunkLayout{p.NC, p.Hv, p.Dv, p.Dk}; }
 
-size_t extras_bytes(const Problem& p) { return size_t(p.NC) * p.Hv * (kC * kC * 4 + kC * 8); }
+size_t extras_bytes(const Problem& p) { return layout_of(p).tiles_bytes(); }
 size_t dsend_bytes(const Problem& p) { return size_t(p.NC) * p.Hv * p.Dv * p.Dk * 4; }
 
 ChunkArgs base_args(const Problem& p) {
@@ -22,11 +22,9 @@ ChunkArgs base_args(const Problem& p) {
   return a;
 }
 
-// T and G sit after the states in ckpt, or at the start of the workspace when there is no ckpt.
-void place_extras(const Problem& p, ChunkArgs& a, float* ckpt, void* ws) {
-  float* base = ckpt ? ckpt + a.lay.states_elems() : static_cast<float*>(ws);
-  a.Tall = base;
-  a.Gall = reinterpret_cast<double*>(base + p.NC * p.Hv * int64_t(kC * kC));
+// The tiles sit after the states in ckpt, or at the start of the workspace when there is no ckpt.
+void place_extras(const Problem&, ChunkArgs& a, float* ckpt, void* ws) {
+  a.tiles = reinterpret_cast<Tile*>(ckpt ? ckpt + a.lay.states_elems() : static_cast<float*>(ws));
 }
 
 }  // namespace

@@ -1,9 +1,9 @@
-// Chunked design, kernel 4: the per-chunk gradients. One block (4 waves) per (chunk slot, key head); the value heads
+// Chunked design, kernel 4: the per-chunk gradients. One block (8 waves) per (chunk slot, key head); the value heads
 // of the key head's GQA group run in order and their dq, dk contributions add up in registers, so the sums over
 // value heads have a fixed order (reference src/delta_grad.cpp:194-198) and need no atomics.
 //
 // Per value head, with S0 the chunk's start state (checkpoint), dS its end-state cotangent (from the backward state
-// pass) and the chunk's T, G (from prep), the state rows are streamed in blocks of 32:
+// pass) and the chunk's tile (Tb, P, T, exp G, D from prep), the state rows are streamed in blocks of 32:
 //   KS = K S0^T, R = V - diag(exp G) KS, Delta = Tb R, KdS = K dS^T,
 //   dDelta = P^T dY + D KdS, dR = Tb^T dDelta                          (Tb = T diag(beta), D = diag(exp(G_63 - G)))
 //   dP^T += Delta dY^T, dTb^T += R dDelta^T, dQ_inter += dY S0, dK += -diag(exp G) dR S0 + D Delta dS
@@ -12,7 +12,8 @@
 //   dA = -T^T (dTb diag(beta)) T^T,  dKK = strict_lower(diag(beta) dA * E)
 //   dbeta_j = sum_i dTb_ij T_ij + sum_m dA_jm E_jm (K K^T)_jm,  dG from every exp(.) factor, dg = reverse cumsum
 // (tests/chunk_math.py restates these equations and checks them against the oracle.) Wave w owns positions
-// 16w..16w+15 of every position-indexed result. MFMA with split float32 operands as in the forward.
+// 16 (w % 4) .. + 15 and, within each product, the half w / 4 of the other index (state rows of a 32-row block,
+// key-position tiles, or 64 of the 128 columns). MFMA with split float32 operands as in the forward.
 #include <type_traits>
 
 #include "chunk_common.h"
@@ -21,7 +22,8 @@
 namespace qbgdn {
 namespace {
 
-constexpr int kThreads = 256;
+constexpr int kThreads = 512;
+constexpr int Dk_ = 128;
 constexpr int kLDK = 128 + kPadB;  // bf16 [.][128] rows
 constexpr int kLDC = kC + kPadB;   // bf16 [.][64] rows
 constexpr int kLDR = 40;           // bf16 [.][32] rows, padded
@@ -42,10 +44,11 @@ constexpr int odDth = oDDml + kC * kLDN, odDtl = odDth + 32 * kLDC;
 constexpr int odDmh = odDtl + 32 * kLDC, odDml = odDmh + kC * kLDN;
 constexpr int oGdRh = odDml + kC * kLDN, oGdRl = oGdRh + kC * kLDN;
 constexpr int kLoopBytes = (oGdRl + kC * kLDN) * 2;
-// End-phase region (aliases the block-loop region): bf16 K, Q then f32 64 x 64 matrices.
-constexpr int eKb = 0, eQb = kC * kLDK;                    // bf16 offsets
-constexpr int eF = (2 * kC * kLDK * 2) / 4;                // first f32 offset
-constexpr int edPM = eF, eQK = edPM + kC * kLDF, edTb = eQK + kC * kLDF, eT = edTb + kC * kLDF;
+// End-phase region (aliases the block-loop region): bf16 K (rows), K^T and Q^T ([column][position]) then f32
+// 64 x 64 matrices.
+constexpr int eKb = 0, eKt = kC * kLDK, eQt = eKt + Dk_ * kLDC;  // bf16 offsets
+constexpr int eF = (eQt + Dk_ * kLDC) / 2;                       // first f32 offset
+constexpr int edP = eF, edTb = edP + kC * kLDF, eT = edTb + kC * kLDF;
 constexpr int eKK = eT + kC * kLDF, eZt = eKK + kC * kLDF;
 constexpr int kEndBytes = (eZt + kC * kLDF) * 4;
 constexpr int kSmemBytes = kLoopBytes > kEndBytes ? kLoopBytes : kEndBytes;
@@ -56,14 +59,16 @@ __device__ __forceinline__ void put_split(__bf16* hi, __bf16* lo, int at, float 
   lo[at] = (__bf16)(x - (float)h);
 }
 
+__device__ __forceinline__ __bf16 as_bf(bf16_t b) { return __builtin_bit_cast(__bf16, b); }
+
 template <typename OutT>
 __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) {
   constexpr int Dk = 128;
   constexpr bool kExactDy = std::is_same<OutT, bf16_t>::value;
   __shared__ __align__(16) unsigned char smem[kSmemBytes];
-  __shared__ double Gd[kC];
-  __shared__ float gam[kC], Dd[kC], Bs[kC], dGpos[kC], hDtot[kC], x1r[kC], x1c[kC], x2r[kC], x2c[kC];
-  __shared__ float dbT[kC], dbA[kC], dGt[kC], red[kThreads];
+  __shared__ float gam[kC], dec[kC], bet[kC], Gf[kC];
+  __shared__ float gpos[2][kC], hpos[2][kC], tpos[2][kC];
+  __shared__ float x1r[kC], x1c[kC], x2r[kC], x2c[kC], dbT[kC], dbA[kC], dGt[kC], red[kThreads];
   __shared__ float SdS_total;
   __bf16* sb = reinterpret_cast<__bf16*>(smem);
   float* sf = reinterpret_cast<float*>(smem);
@@ -76,85 +81,62 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
   const int L = sp.L;
   const int64_t tok = sp.tok;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 4, li = lane & 15;
+  const int pw = w & 3, hw = w >> 2;  // position tile, half
+  const int ip = 16 * pw + li;        // the lane's position as an A-operand row
   const OutT* dy = static_cast<const OutT*>(a.dy);
+  const int sk = a.Hk * Dk, sv = a.Hv * a.Dv;  // token strides of k/q/dq/dk and v/dy
+  const bf16_t* kbase = a.k + tok * sk + hk * Dk;
+  const bf16_t* qbase = a.q + tok * sk + hk * Dk;
 
-  // K and Q rows of the wave's positions (A operands), and Q K^T with lane -> column j = 16w + li, rows i.
-  stage_rows_bf16<Dk>(sb + eKb, kLDK, a.k, tok, a.Hk, hk, L, kThreads);
-  stage_rows_bf16<Dk>(sb + eQb, kLDK, a.q, tok, a.Hk, hk, L, kThreads);
-  __syncthreads();
-  bf16x8 Kf[4], Qf[4];
+  // K rows of the wave's positions (A operands of K S0^T, K dS^T, K K^T).
+  bf16x8 Kf[4];
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
-    Kf[s] = lds8(sb + eKb + (16 * w + li) * kLDK + 32 * s + 8 * g);
-    Qf[s] = lds8(sb + eQb + (16 * w + li) * kLDK + 32 * s + 8 * g);
-  }
-  f32x4 qk[4];
+    if (ip < L) {
+      Kf[s] = gld8(kbase + ip * sk + 32 * s + 8 * g);
+    } else {
 #pragma unroll
-  for (int m = 0; m < 4; ++m) {
-    qk[m] = zero4();
-    if (m >= w) {
-#pragma unroll
-      for (int s = 0; s < 4; ++s) qk[m] = mma(qk[m], lds8(sb + eQb + (16 * m + li) * kLDK + 32 * s + 8 * g), Kf[s]);
+      for (int j = 0; j < 8; ++j) Kf[s][j] = (__bf16)0.f;
     }
   }
-  f32x4 dQ[8], dK[8];
+  f32x4 dQ[4], dK[4];  // columns 16 (4 hw + t) + li, rows 16 pw + 4 g + jj
 #pragma unroll
-  for (int t = 0; t < 8; ++t) dQ[t] = zero4(), dK[t] = zero4();
+  for (int t = 0; t < 4; ++t) dQ[t] = zero4(), dK[t] = zero4();
 
   for (int e = 0; e < grp; ++e) {
     const int hv = hk * grp + e;
     const int64_t sh = slot * a.Hv + hv;
+    const Tile* tl = a.tiles + sh;
     __syncthreads();
-    if (tid < kC) {
-      const double* G = a.Gall + sh * kC;
-      const double gt = G[tid], gl = G[kC - 1];
-      Gd[tid] = gt;
-      gam[tid] = expf(float(gt));
-      Dd[tid] = expf(float(gl - gt));
-      Bs[tid] = tid < L ? bf16_to_f32(a.beta[(tok + tid) * a.Hv + hv]) : 0.f;
-    }
-    __syncthreads();
-    const float* T = a.Tall + sh * int64_t(kC * kC);
-    Split8 TbA[2], TbtA[2], PA[2];
-    {
-      const int i = 16 * w + li;
+    if (tid < kC) gam[tid] = tl->gam[tid], dec[tid] = tl->dec[tid], bet[tid] = tl->beta[tid], Gf[tid] = tl->G[tid];
+    f32x4 dPt[2], dTbt[2], dQi[4];  // dPt, dTbt: key tiles m = 2 hw + mi; lane -> column i = ip, rows j
 #pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        float x[8], y[8], p[8];
+    for (int t = 0; t < 2; ++t) dPt[t] = zero4(), dTbt[t] = zero4();
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const int jj = 32 * s + 8 * g + j;
-          x[j] = T[i * kC + jj] * Bs[jj];
-          y[j] = T[jj * kC + i] * Bs[i];
-        }
-        // P^T row j = i (k = query positions in the stacked order of qk[2s], qk[2s + 1])
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-          const int q0 = 32 * s + 4 * g + jj, q1 = q0 + 16;
-          p[jj] = q0 >= i ? qk[2 * s][jj] * expf(float(Gd[q0] - Gd[i])) : 0.f;
-          p[4 + jj] = q1 >= i ? qk[2 * s + 1][jj] * expf(float(Gd[q1] - Gd[i])) : 0.f;
-        }
-        TbA[s] = split8(x);
-        TbtA[s] = split8(y);
-        PA[s] = split8(p);
-      }
-    }
-    f32x4 dPt[4], dTbt[4], dQi[8];
-#pragma unroll
-    for (int t = 0; t < 4; ++t) dPt[t] = zero4(), dTbt[t] = zero4();
-#pragma unroll
-    for (int t = 0; t < 8; ++t) dQi[t] = zero4();
+    for (int t = 0; t < 4; ++t) dQi[t] = zero4();
     float gpart[4] = {0.f, 0.f, 0.f, 0.f}, hD[4] = {0.f, 0.f, 0.f, 0.f}, sds = 0.f;
+    __syncthreads();
 
     for (int r0 = 0; r0 < a.Dv; r0 += 32) {
+      // Lane indices re-derived from an opaque copy, so their many address expressions are recomputed here instead
+      // of being hoisted out of both loops and held (spilled) for the whole kernel.
+      int lt = tid;
+      asm volatile("" : "+v"(lt));
+      const int g = (lt >> 4) & 3, li = lt & 15, pw = (lt >> 6) & 3, hw = lt >> 8, ip = 16 * pw + li;
       __syncthreads();
-      {  // S0 and dS rows r0..r0+31: thread -> row tid / 8, columns 16 (tid % 8) ..
-        const int r = tid >> 3, c0 = (tid & 7) * 16;
-        const int64_t at = (sh * a.Dv + r0 + r) * Dk + c0;
-        const float* s0p = a.ckpt + at;
-        const float* dsp = a.dsend + at;
+      // Uniform bases of this block's rows; lanes add 32-bit offsets.
+      const int64_t rows0 = (sh * a.Dv + r0) * Dk;
+      const float* s0b = a.ckpt + rows0;
+      const float* dsb = a.dsend + rows0;
+      const OutT* dyb = dy + (tok * a.Hv + hv) * a.Dv + r0;
+      const bf16_t* vb = a.v + (tok * a.Hv + hv) * a.Dv + r0;
+      {  // S0 and dS rows r0..r0+31: thread -> row tid / 16, columns 8 (tid % 16) ..
+        const int r = tid >> 4, c0 = (tid & 15) * 8;
+        const uint32_t at = uint32_t(r * Dk + c0);
+        const float* s0p = s0b + at;
+        const float* dsp = dsb + at;
 #pragma unroll
-        for (int q4 = 0; q4 < 4; ++q4) {
+        for (int q4 = 0; q4 < 2; ++q4) {
           const float4 x4 = *reinterpret_cast<const float4*>(s0p + 4 * q4);
           const float4 y4 = *reinterpret_cast<const float4*>(dsp + 4 * q4);
           const float xs[4] = {x4.x, x4.y, x4.z, x4.w}, ys[4] = {y4.x, y4.y, y4.z, y4.w};
@@ -169,91 +151,98 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
           }
         }
       }
-      {  // dY^T [r][i]: thread -> position tid / 4, rows 8 (tid % 4) ..
-        const int i = tid >> 2, r8 = (tid & 3) * 8;
+      {  // dY^T [r][i]: thread -> position tid / 8, rows 4 (tid % 8) ..
+        const int i = tid >> 3, r4 = (tid & 7) * 4;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const float x = i < L ? IO<OutT>::ld(dy, ((tok + i) * a.Hv + hv) * a.Dv + r0 + r8 + j) : 0.f;
-          put_split(sb + odYth, sb + odYtl, (r8 + j) * kLDC + i, x);
+        for (int j = 0; j < 4; ++j) {
+          const float x = i < L ? IO<OutT>::ld(dyb, uint32_t(i * sv + r4 + j)) : 0.f;
+          put_split(sb + odYth, sb + odYtl, (r4 + j) * kLDC + i, x);
         }
       }
-      // The wave's own dY rows (i = 16w + li, k = r = 8g..): A of dY S0, B of Delta dY^T.
+      // The wave's own dY rows (i = ip, k = r = 8g..): A of dY S0, B of Delta dY^T.
       Split8 dYo;
       {
-        const int i = 16 * w + li;
         float x[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) x[j] = i < L ? IO<OutT>::ld(dy, ((tok + i) * a.Hv + hv) * a.Dv + r0 + 8 * g + j) : 0.f;
+        for (int j = 0; j < 8; ++j)
+          x[j] = ip < L ? IO<OutT>::ld(dyb, uint32_t(ip * sv + 8 * g + j)) : 0.f;
         dYo = split8(x);
       }
-      __syncthreads();
-
-      // Phase 1: KS, QS, KdS for positions 16w.. (lane -> column r = 16nt + li, rows i = 16w + 4g + jj).
-      f32x4 ks[2], qs[2], kds[2];
-      float gks[2][4];
+      // A operands from the tile for this block (reloaded per block from L2 to keep them out of the loop-carried
+      // registers): Tb rows ip (k = j), Tb^T rows ip (k = j) and P^T rows ip (k = i).
+      Split8 TbA[2], TbtA[2], PA[2];
+      {
+        const Tile* tb = tl;
+        asm volatile("" : "+s"(tb));  // the loads stay inside the loop
+        const int ar = ip * kC + 8 * g;
 #pragma unroll
-      for (int nt = 0; nt < 2; ++nt) {
-        ks[nt] = qs[nt] = kds[nt] = zero4();
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          const int at = (16 * nt + li) * kLDK + 32 * s + 8 * g;
-          const bf16x8 bh = lds8(sb + oS0h + at), bl = lds8(sb + oS0l + at);
-          ks[nt] = mma(mma(ks[nt], Kf[s], bh), Kf[s], bl);
-          qs[nt] = mma(mma(qs[nt], Qf[s], bh), Qf[s], bl);
-          kds[nt] = mma(mma(kds[nt], Kf[s], lds8(sb + odSh + at)), Kf[s], lds8(sb + odSl + at));
+        for (int s = 0; s < 2; ++s) {
+          TbA[s] = Split8{gld8(tb->tb_hi + ar + 32 * s), gld8(tb->tb_lo + ar + 32 * s)};
+          TbtA[s] = Split8{gld8(tb->tbt_hi + ar + 32 * s), gld8(tb->tbt_lo + ar + 32 * s)};
+          PA[s] = Split8{gld8(tb->pt_hi + ar + 32 * s), gld8(tb->pt_lo + ar + 32 * s)};
         }
+      }
+      // v at the wave's accumulator positions (rows i = 16 pw + 4g + jj, column r = 16 hw + li).
+      float vv[4];
 #pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-          const int i = 16 * w + 4 * g + jj, r = 16 * nt + li;
-          const float vv = i < L ? bf16_to_f32(a.v[((tok + i) * a.Hv + hv) * a.Dv + r0 + r]) : 0.f;
-          gks[nt][jj] = gam[i] * ks[nt][jj];
-          const float R = vv - gks[nt][jj];
-          const float dyv = (float)sb[odYth + r * kLDC + i] + (float)sb[odYtl + r * kLDC + i];
-          gpart[jj] += gam[i] * dyv * qs[nt][jj];
-          put_split(sb + oRth, sb + oRtl, r * kLDC + i, R);
-          put_split(sb + oRmh, sb + oRml, i * kLDN + r, R);
-        }
+      for (int jj = 0; jj < 4; ++jj) {
+        const int i = 16 * pw + 4 * g + jj;
+        vv[jj] = i < L ? bf16_to_f32(vb[uint32_t(i * sv + 16 * hw + li)]) : 0.f;
       }
       __syncthreads();
 
-      // Phase 2: Delta = Tb R and dDelta = P^T dY + D KdS for positions 16w..
+      // Phase 1: KS and KdS for positions 16 pw.., state rows r = 16 hw + li.
+      const int r = 16 * hw + li;
+      f32x4 ks = zero4(), kds = zero4();
 #pragma unroll
-      for (int nt = 0; nt < 2; ++nt) {
-        const int r = 16 * nt + li;
-        f32x4 dl = zero4(), dd;
+      for (int s = 0; s < 4; ++s) {
+        const int at = r * kLDK + 32 * s + 8 * g;
+        ks = mma(mma(ks, Kf[s], lds8(sb + oS0h + at)), Kf[s], lds8(sb + oS0l + at));
+        kds = mma(mma(kds, Kf[s], lds8(sb + odSh + at)), Kf[s], lds8(sb + odSl + at));
+      }
+      float gks[4];
 #pragma unroll
-        for (int s = 0; s < 2; ++s) {
+      for (int jj = 0; jj < 4; ++jj) {
+        const int i = 16 * pw + 4 * g + jj;
+        gks[jj] = gam[i] * ks[jj];
+        const float R = vv[jj] - gks[jj];
+        put_split(sb + oRth, sb + oRtl, r * kLDC + i, R);
+        put_split(sb + oRmh, sb + oRml, i * kLDN + r, R);
+      }
+      __syncthreads();
+
+      // Phase 2: Delta = Tb R and dDelta = P^T dY + D KdS.
+      f32x4 dl = zero4(), dd;
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        const int at = r * kLDC + 32 * s + 8 * g;
+        dl = mma3(dl, TbA[s], Split8{lds8(sb + oRth + at), lds8(sb + oRtl + at)});
+      }
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) dd[jj] = dec[16 * pw + 4 * g + jj] * kds[jj];
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        if (32 * s + 31 >= 16 * pw) {
           const int at = r * kLDC + 32 * s + 8 * g;
-          dl = mma3(dl, TbA[s], Split8{lds8(sb + oRth + at), lds8(sb + oRtl + at)});
+          if constexpr (kExactDy)
+            dd = mma2(dd, PA[s], lds8(sb + odYth + at));
+          else
+            dd = mma3(dd, PA[s], Split8{lds8(sb + odYth + at), lds8(sb + odYtl + at)});
         }
+      }
 #pragma unroll
-        for (int jj = 0; jj < 4; ++jj) dd[jj] = Dd[16 * w + 4 * g + jj] * kds[nt][jj];
-#pragma unroll
-        for (int s = 0; s < 2; ++s) {
-          if (2 * s + 1 >= w) {
-            const int at = r * kLDC + 32 * s + 4 * g;
-            if constexpr (kExactDy)
-              dd = mma2(dd, PA[s], lds4x2(sb + odYth + at));
-            else
-              dd = mma3(dd, PA[s], Split8{lds4x2(sb + odYth + at), lds4x2(sb + odYtl + at)});
-          }
-        }
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-          const int i = 16 * w + 4 * g + jj;
-          hD[jj] += Dd[i] * dl[jj] * kds[nt][jj];
-          put_split(sb + oDmh, sb + oDml, i * kLDN + r, dl[jj]);
-          put_split(sb + oDDmh, sb + oDDml, i * kLDN + r, Dd[i] * dl[jj]);
-          put_split(sb + odDth, sb + odDtl, r * kLDC + i, dd[jj]);
-          put_split(sb + odDmh, sb + odDml, i * kLDN + r, dd[jj]);
-        }
+      for (int jj = 0; jj < 4; ++jj) {
+        const int i = 16 * pw + 4 * g + jj;
+        hD[jj] += dec[i] * dl[jj] * kds[jj];
+        put_split(sb + oDmh, sb + oDml, i * kLDN + r, dl[jj]);
+        put_split(sb + oDDmh, sb + oDDml, i * kLDN + r, dec[i] * dl[jj]);
+        put_split(sb + odDth, sb + odDtl, r * kLDC + i, dd[jj]);
+        put_split(sb + odDmh, sb + odDml, i * kLDN + r, dd[jj]);
       }
       __syncthreads();
 
-      // Phase 3: dR = Tb^T dDelta; dP^T += Delta dY^T and dTb^T += R dDelta^T (rows j, columns i = own).
-#pragma unroll
-      for (int nt = 0; nt < 2; ++nt) {
-        const int r = 16 * nt + li;
+      // Phase 3: dR = Tb^T dDelta; dP^T += Delta dY^T and dTb^T += R dDelta^T over this half's key tiles.
+      {
         f32x4 dr = zero4();
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
@@ -262,37 +251,38 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
         }
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) {
-          const int i = 16 * w + 4 * g + jj;
-          gpart[jj] -= dr[jj] * gks[nt][jj];
+          const int i = 16 * pw + 4 * g + jj;
+          gpart[jj] -= dr[jj] * gks[jj];
           put_split(sb + oGdRh, sb + oGdRl, i * kLDN + r, -gam[i] * dr[jj]);
         }
       }
       {
-        const int atn = (16 * w + li) * kLDN + 8 * g;
+        const int atn = ip * kLDN + 8 * g;
         const Split8 BdD{lds8(sb + odDmh + atn), lds8(sb + odDml + atn)};
 #pragma unroll
-        for (int m = 0; m < 4; ++m) {
-          if (m <= w) {
+        for (int mi = 0; mi < 2; ++mi) {
+          const int m = 2 * hw + mi;
+          if (m <= pw) {
             const int at = (16 * m + li) * kLDN + 8 * g;
             const Split8 AD{lds8(sb + oDmh + at), lds8(sb + oDml + at)};
             if constexpr (kExactDy)
-              dPt[m] = mma2(dPt[m], AD, dYo.hi);
+              dPt[mi] = mma2(dPt[mi], AD, dYo.hi);
             else
-              dPt[m] = mma3(dPt[m], AD, dYo);
-            dTbt[m] = mma3(dTbt[m], Split8{lds8(sb + oRmh + at), lds8(sb + oRml + at)}, BdD);
+              dPt[mi] = mma3(dPt[mi], AD, dYo);
+            dTbt[mi] = mma3(dTbt[mi], Split8{lds8(sb + oRmh + at), lds8(sb + oRml + at)}, BdD);
           }
         }
       }
       __syncthreads();
 
-      // Phase 4: dQ_inter += dY S0; dK += -diag(exp G) dR S0 + D Delta dS (rows i = own, columns c).
+      // Phase 4: dQ_inter += dY S0; dK += -diag(exp G) dR S0 + D Delta dS (columns of this half).
       {
-        const int at = (16 * w + li) * kLDN + 8 * g;
+        const int at = ip * kLDN + 8 * g;
         const Split8 AGdR{lds8(sb + oGdRh + at), lds8(sb + oGdRl + at)};
         const Split8 ADD{lds8(sb + oDDmh + at), lds8(sb + oDDml + at)};
 #pragma unroll
-        for (int t = 0; t < 8; ++t) {
-          const int bt = (16 * t + li) * kLDR + 8 * g;
+        for (int t = 0; t < 4; ++t) {
+          const int bt = (16 * (4 * hw + t) + li) * kLDR + 8 * g;
           const Split8 B0{lds8(sb + oS0th + bt), lds8(sb + oS0tl + bt)};
           const Split8 B1{lds8(sb + odSth + bt), lds8(sb + odStl + bt)};
           if constexpr (kExactDy)
@@ -304,54 +294,74 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
         }
       }
     }
-    // End of the state rows for this value head.
-#pragma unroll
-    for (int t = 0; t < 8; ++t)
-#pragma unroll
-      for (int jj = 0; jj < 4; ++jj) dQ[t][jj] += gam[16 * w + 4 * g + jj] * dQi[t][jj];
+
+    // End of the state rows for this value head: per-position partials, then the 64 x 64 part.
+    int lt = tid;
+    asm volatile("" : "+v"(lt));
+    const int g = (lt >> 4) & 3, li = lt & 15, pw = (lt >> 6) & 3, hw = lt >> 8, ip = 16 * pw + li;
 #pragma unroll
     for (int jj = 0; jj < 4; ++jj) {
       const float v = sum16(gpart[jj]), h = sum16(hD[jj]);
-      if (li == 0) {
-        dGpos[16 * w + 4 * g + jj] = v - h;
-        hDtot[16 * w + 4 * g + jj] = h;
-      }
+      if (li == 0) gpos[hw][16 * pw + 4 * g + jj] = v, hpos[hw][16 * pw + 4 * g + jj] = h;
     }
     red[tid] = sds;
     __syncthreads();
 
-    // E1: K, Q, T, dP * M, dTb, Q K^T into the end-phase region.
-    stage_rows_bf16<Dk>(sb + eKb, kLDK, a.k, tok, a.Hk, hk, L, kThreads);
-    stage_rows_bf16<Dk>(sb + eQb, kLDK, a.q, tok, a.Hk, hk, L, kThreads);
-    for (int q = tid; q < kC * kC; q += kThreads) sf[eT + (q >> 6) * kLDF + (q & 63)] = T[q];
-    {
-      const int i = 16 * w + li;
+    // E1: K, K^T, Q^T, T, dP (unmasked, j <= i) and dTb into the end-phase region.
+    for (int e = tid; e < kC * 16; e += kThreads) {
+      const int t = e >> 4, c8 = (e & 15) * 8;
+      bf16x8 kv, qv;
+      if (t < L) {
+        kv = gld8(kbase + t * sk + c8);
+        qv = gld8(qbase + t * sk + c8);
+      } else {
 #pragma unroll
-      for (int m = 0; m < 4; ++m)
+        for (int j = 0; j < 8; ++j) kv[j] = qv[j] = (__bf16)0.f;
+      }
+      *reinterpret_cast<bf16x8*>(sb + eKb + t * kLDK + c8) = kv;
 #pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-          const int j = 16 * m + 4 * g + jj;
-          sf[edPM + i * kLDF + j] = j <= i ? dPt[m][jj] * expf(float(Gd[i] - Gd[j])) : 0.f;
-          sf[edTb + i * kLDF + j] = j <= i ? dTbt[m][jj] : 0.f;
-          // qk: lane -> column j' = 16w + li, rows i' = 16m + 4g + jj
-          const int jq = 16 * w + li, iq = 16 * m + 4 * g + jj;
-          sf[eQK + iq * kLDF + jq] = iq >= jq ? qk[m][jj] : 0.f;
-        }
+      for (int j = 0; j < 8; ++j) {
+        sb[eKt + (c8 + j) * kLDC + t] = kv[j];
+        sb[eQt + (c8 + j) * kLDC + t] = qv[j];
+      }
     }
+    for (int q = tid; q < kC * kC; q += kThreads) sf[eT + (q >> 6) * kLDF + (q & 63)] = tl->t[q];
+#pragma unroll
+    for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        const int j = 16 * (2 * hw + mi) + 4 * g + jj;
+        sf[edP + ip * kLDF + j] = j <= ip ? dPt[mi][jj] : 0.f;
+        sf[edTb + ip * kLDF + j] = j <= ip ? dTbt[mi][jj] : 0.f;
+      }
     __syncthreads();
 
-    // E2: K K^T rows p = own; dQ += (dP * M) K; dK += (dP * M)^T Q; Z = (dTb diag(beta)) T^T.
+    // E2: dQ += diag(exp G) dQ_inter and its dG term; K K^T; dQ += (dP * M) K; dK += (dP * M)^T Q; Z = dT T^T.
     {
-      const int p = 16 * w + li;
+      float tq[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt) {
-        f32x4 kk = zero4();
-        if (mt <= w) {
+      for (int t = 0; t < 4; ++t)
 #pragma unroll
-          for (int s = 0; s < 4; ++s) kk = mma(kk, Kf[s], lds8(sb + eKb + (16 * mt + li) * kLDK + 32 * s + 8 * g));
+        for (int jj = 0; jj < 4; ++jj) {
+          const int i = 16 * pw + 4 * g + jj, c = 16 * (4 * hw + t) + li;
+          tq[jj] += (float)sb[eQt + c * kLDC + i] * dQi[t][jj];
+          dQ[t][jj] += gam[i] * dQi[t][jj];
         }
 #pragma unroll
-        for (int jj = 0; jj < 4; ++jj) sf[eKK + (16 * w + 4 * g + jj) * kLDF + 16 * mt + li] = kk[jj];
+      for (int jj = 0; jj < 4; ++jj) {
+        const float v = sum16(tq[jj]);
+        if (li == 0) tpos[hw][16 * pw + 4 * g + jj] = v;
+      }
+#pragma unroll
+      for (int mi = 0; mi < 2; ++mi) {
+        const int m = 2 * hw + mi;
+        f32x4 kk = zero4();
+        if (m <= pw) {
+#pragma unroll
+          for (int s = 0; s < 4; ++s) kk = mma(kk, Kf[s], lds8(sb + eKb + (16 * m + li) * kLDK + 32 * s + 8 * g));
+        }
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) sf[eKK + (16 * pw + 4 * g + jj) * kLDF + 16 * m + li] = kk[jj];
       }
       Split8 AdPM[2], AdPMt[2], AdT[2];
 #pragma unroll
@@ -360,40 +370,37 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
           const int jj = 32 * s + 8 * g + j;
-          x[j] = sf[edPM + p * kLDF + jj];
-          y[j] = sf[edPM + jj * kLDF + p];
-          z[j] = sf[edTb + p * kLDF + jj] * Bs[jj];
+          // M_ij = exp(G_i - G_j) only where j <= i (elsewhere the exponent is positive and may overflow)
+          x[j] = jj <= ip ? sf[edP + ip * kLDF + jj] * __expf(Gf[ip] - Gf[jj]) : 0.f;
+          y[j] = jj >= ip ? sf[edP + jj * kLDF + ip] * __expf(Gf[jj] - Gf[ip]) : 0.f;
+          z[j] = sf[edTb + ip * kLDF + jj] * bet[jj];
         }
         AdPM[s] = split8(x);
         AdPMt[s] = split8(y);
         AdT[s] = split8(z);
       }
 #pragma unroll
-      for (int t = 0; t < 8; ++t) {
+      for (int t = 0; t < 4; ++t) {
+        const int c = 16 * (4 * hw + t) + li;
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
-          bf16x8 bk, bq;
-#pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            bk[j] = sb[eKb + (32 * s + 8 * g + j) * kLDK + 16 * t + li];
-            bq[j] = sb[eQb + (32 * s + 8 * g + j) * kLDK + 16 * t + li];
-          }
-          dQ[t] = mma2(dQ[t], AdPM[s], bk);
-          dK[t] = mma2(dK[t], AdPMt[s], bq);
+          dQ[t] = mma2(dQ[t], AdPM[s], lds8(sb + eKt + c * kLDC + 32 * s + 8 * g));
+          dK[t] = mma2(dK[t], AdPMt[s], lds8(sb + eQt + c * kLDC + 32 * s + 8 * g));
         }
       }
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt) {
+      for (int mi = 0; mi < 2; ++mi) {
+        const int m = 2 * hw + mi;
         f32x4 z = zero4();
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
           float tv[8];
 #pragma unroll
-          for (int j = 0; j < 8; ++j) tv[j] = sf[eT + (16 * mt + li) * kLDF + 32 * s + 8 * g + j];
+          for (int j = 0; j < 8; ++j) tv[j] = sf[eT + (16 * m + li) * kLDF + 32 * s + 8 * g + j];
           z = mma3(z, AdT[s], split8(tv));
         }
 #pragma unroll
-        for (int jj = 0; jj < 4; ++jj) sf[eZt + (16 * mt + li) * kLDF + 16 * w + 4 * g + jj] = z[jj];
+        for (int jj = 0; jj < 4; ++jj) sf[eZt + (16 * m + li) * kLDF + 16 * pw + 4 * g + jj] = z[jj];
       }
     }
     if (tid < kC) {
@@ -401,15 +408,17 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
       float acc = 0.f;
       for (int i = j; i < kC; ++i) acc += sf[edTb + i * kLDF + j] * sf[eT + i * kLDF + j];
       dbT[j] = acc;
-    } else if (tid < 2 * kC) {
+    } else if (tid < 2 * kC) {  // P row i from the tile
       const int i = tid - kC;
       float acc = 0.f;
-      for (int j = 0; j <= i; ++j) acc += sf[edPM + i * kLDF + j] * sf[eQK + i * kLDF + j];
+      for (int j = 0; j <= i; ++j)
+        acc += sf[edP + i * kLDF + j] * ((float)as_bf(tl->p_hi[i * kC + j]) + (float)as_bf(tl->p_lo[i * kC + j]));
       x2r[i] = acc;
-    } else if (tid < 3 * kC) {
+    } else if (tid < 3 * kC) {  // P column j: row j of P^T
       const int j = tid - 2 * kC;
       float acc = 0.f;
-      for (int i = j; i < kC; ++i) acc += sf[edPM + i * kLDF + j] * sf[eQK + i * kLDF + j];
+      for (int i = j; i < kC; ++i)
+        acc += sf[edP + i * kLDF + j] * ((float)as_bf(tl->pt_hi[j * kC + i]) + (float)as_bf(tl->pt_lo[j * kC + i]));
       x2c[j] = acc;
     } else if (tid == 3 * kC) {
       float acc = 0.f;
@@ -418,36 +427,36 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
     }
     __syncthreads();
 
-    // E3: dA = -T^T Z (strict lower), rows p = own, into the dP * M slot.
+    // E3: dA = -T^T Z (strict lower) for rows p = ip, this half's column tiles, into the dP slot.
     {
-      const int p = 16 * w + li;
       Split8 AT[2];
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
         float x[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) x[j] = sf[eT + (32 * s + 8 * g + j) * kLDF + p];
+        for (int j = 0; j < 8; ++j) x[j] = sf[eT + (32 * s + 8 * g + j) * kLDF + ip];
         AT[s] = split8(x);
       }
-      f32x4 da[4];
+      f32x4 da[2];
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt) {
-        da[mt] = zero4();
+      for (int mi = 0; mi < 2; ++mi) {
+        const int m = 2 * hw + mi;
+        da[mi] = zero4();
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
           float zv[8];
 #pragma unroll
-          for (int j = 0; j < 8; ++j) zv[j] = sf[eZt + (16 * mt + li) * kLDF + 32 * s + 8 * g + j];
-          da[mt] = mma3(da[mt], AT[s], split8(zv));
+          for (int j = 0; j < 8; ++j) zv[j] = sf[eZt + (16 * m + li) * kLDF + 32 * s + 8 * g + j];
+          da[mi] = mma3(da[mi], AT[s], split8(zv));
         }
       }
-      __syncthreads();  // every wave has read dP * M (E2) and Z before dA overwrites the slot
+      __syncthreads();  // every wave has read dP and Z before dA overwrites the dP slot
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt)
+      for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) {
-          const int pr = 16 * w + 4 * g + jj, m = 16 * mt + li;
-          sf[edPM + pr * kLDF + m] = m < pr ? -da[mt][jj] : 0.f;
+          const int p = 16 * pw + 4 * g + jj, m = 16 * (2 * hw + mi) + li;
+          sf[edP + p * kLDF + m] = m < p ? -da[mi][jj] : 0.f;
         }
     }
     __syncthreads();
@@ -456,26 +465,24 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
     if (tid < kC) {
       const int p = tid;
       float acc = 0.f;
-      for (int m = 0; m < p; ++m)
-        acc += sf[edPM + p * kLDF + m] * expf(float(Gd[p] - Gd[m])) * sf[eKK + p * kLDF + m];
+      for (int m = 0; m < p; ++m) acc += sf[edP + p * kLDF + m] * __expf(Gf[p] - Gf[m]) * sf[eKK + p * kLDF + m];
       dbA[p] = acc;
-      x1r[p] = Bs[p] * acc;
+      x1r[p] = bet[p] * acc;
     } else if (tid < 2 * kC) {
       const int m = tid - kC;
       float acc = 0.f;
       for (int p = m + 1; p < kC; ++p)
-        acc += Bs[p] * sf[edPM + p * kLDF + m] * expf(float(Gd[p] - Gd[m])) * sf[eKK + p * kLDF + m];
+        acc += bet[p] * sf[edP + p * kLDF + m] * __expf(Gf[p] - Gf[m]) * sf[eKK + p * kLDF + m];
       x1c[m] = acc;
     }
     for (int q = tid; q < kC * kC; q += kThreads) {
       const int p = q >> 6, m = q & 63;
-      sf[edTb + p * kLDF + m] = m < p ? Bs[p] * sf[edPM + p * kLDF + m] * expf(float(Gd[p] - Gd[m])) : 0.f;
+      sf[edTb + p * kLDF + m] = m < p ? bet[p] * sf[edP + p * kLDF + m] * __expf(Gf[p] - Gf[m]) : 0.f;
     }
     __syncthreads();
 
-    // E5: dK += (dKK + dKK^T) K for rows j = own.
+    // E5: dK += (dKK + dKK^T) K for rows j = ip, this half's columns.
     {
-      const int j0 = 16 * w + li;
       Split8 A[2];
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
@@ -483,27 +490,25 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
           const int m = 32 * s + 8 * g + j;
-          x[j] = sf[edTb + j0 * kLDF + m] + sf[edTb + m * kLDF + j0];
+          x[j] = sf[edTb + ip * kLDF + m] + sf[edTb + m * kLDF + ip];
         }
         A[s] = split8(x);
       }
 #pragma unroll
-      for (int t = 0; t < 8; ++t)
+      for (int t = 0; t < 4; ++t) {
+        const int c = 16 * (4 * hw + t) + li;
 #pragma unroll
-        for (int s = 0; s < 2; ++s) {
-          bf16x8 bk;
-#pragma unroll
-          for (int j = 0; j < 8; ++j) bk[j] = sb[eKb + (32 * s + 8 * g + j) * kLDK + 16 * t + li];
-          dK[t] = mma2(dK[t], A[s], bk);
-        }
+        for (int s = 0; s < 2; ++s) dK[t] = mma2(dK[t], A[s], lds8(sb + eKt + c * kLDC + 32 * s + 8 * g));
+      }
     }
     // E6: dG per position, then dg = reverse cumsum and dbeta.
     if (tid < kC) {
       const int t = tid;
-      float v = dGpos[t] + x1r[t] - x1c[t] + x2r[t] - x2c[t];
+      float v = gam[t] * (tpos[0][t] + tpos[1][t]) + gpos[0][t] + gpos[1][t] - hpos[0][t] - hpos[1][t] + x1r[t] -
+                x1c[t] + x2r[t] - x2c[t];
       if (t == kC - 1) {
         float hsum = 0.f;
-        for (int i = 0; i < kC; ++i) hsum += hDtot[i];
+        for (int i = 0; i < kC; ++i) hsum += hpos[0][i] + hpos[1][i];
         v += hsum + gam[kC - 1] * SdS_total;
       }
       dGt[t] = v;
@@ -513,22 +518,23 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
       const int t = tid;
       float da = 0.f;
       for (int i = kC - 1; i >= t; --i) da += dGt[i];
-      const int64_t gi = (tok + t) * a.Hv + hv;
-      a.dg[gi] = a.g_is_log ? da : da / a.g[gi];
-      IO<OutT>::st(static_cast<OutT*>(a.dbeta), gi, dbT[t] + dbA[t]);
+      const int64_t g0 = tok * a.Hv + hv;
+      const uint32_t gi = uint32_t(t * a.Hv);
+      a.dg[g0 + gi] = a.g_is_log ? da : da / a.g[g0 + gi];
+      IO<OutT>::st(static_cast<OutT*>(a.dbeta) + g0, gi, dbT[t] + dbA[t]);
     }
   }
 
-  // dq, dk for the wave's positions (lane -> column c = 16t + li, rows i = 16w + 4g + jj).
-  OutT* dq = static_cast<OutT*>(a.dq);
-  OutT* dk = static_cast<OutT*>(a.dk);
+  // dq, dk for the wave's positions and columns (lane -> column 16 (4 hw + t) + li, rows 16 pw + 4g + jj).
+  OutT* dq = static_cast<OutT*>(a.dq) + (tok * a.Hk + hk) * Dk;
+  OutT* dk = static_cast<OutT*>(a.dk) + (tok * a.Hk + hk) * Dk;
 #pragma unroll
-  for (int t = 0; t < 8; ++t)
+  for (int t = 0; t < 4; ++t)
 #pragma unroll
     for (int jj = 0; jj < 4; ++jj) {
-      const int i = 16 * w + 4 * g + jj;
+      const int i = 16 * pw + 4 * g + jj;
       if (i < L) {
-        const int64_t at = ((tok + i) * a.Hk + hk) * Dk + 16 * t + li;
+        const uint32_t at = uint32_t(i * sk + 16 * (4 * hw + t) + li);
         IO<OutT>::st(dq, at, dQ[t][jj]);
         IO<OutT>::st(dk, at, dK[t][jj]);
       }

@@ -3,11 +3,12 @@
 // last chunk), per chunk:
 //   store dS (the gradient kernel needs it)
 //   dDelta = P^T dY + D K dS^T,  D = diag(exp(G_63 - G))                 wave w: positions 16w..16w+15
-//   dR = (T diag(beta))^T dDelta;   dv = dR
+//   dR = Tb^T dDelta;   dv = dR
 //   dS <- exp(G_63) dS + (diag(exp G) dY)^T Q - (diag(exp G) dR)^T K      wave w: state columns 32w..32w+31
 // This is the adjoint of the forward state pass; together with the gradient kernel it reproduces the reference's
-// backward (src/delta_grad.cpp:14-18). dS0 is what remains after the first chunk. MFMA with split float32 operands
-// as in the forward.
+// backward (src/delta_grad.cpp:14-18). dS0 is what remains after the first chunk. Tb and P come ready from the prep
+// kernel; MFMA with split float32 operands as in the forward; the previous chunk's tiles (in the reverse sweep) are
+// loaded into registers while the current one computes.
 #include <type_traits>
 
 #include "chunk_common.h"
@@ -25,14 +26,12 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_state_kernel(ChunkArgs a) 
   constexpr int Dk = 128;
   constexpr bool kExactDy = std::is_same<OutT, bf16_t>::value;  // bf16 cotangents enter MFMA exactly
   __shared__ __bf16 Kb[kC][kLDK], Qb[kC][kLDK];
-  __shared__ __bf16 Tbth[kC][kLDC], Tbtl[kC][kLDC];  // (T diag(beta))^T, row i, column j
   __shared__ __bf16 dSh[16][kLDK], dSl[16][kLDK];
   __shared__ __bf16 dYth[16][kLDC], dYtl[16][kLDC];   // dY^T [r][i]
   __shared__ __bf16 GdYth[16][kLDC], GdYtl[16][kLDC]; // (diag(exp G) dY)^T
   __shared__ __bf16 dDth[16][kLDC], dDtl[16][kLDC];   // dDelta^T [r][j]
   __shared__ __bf16 GdRth[16][kLDC], GdRtl[16][kLDC]; // -(diag(exp G) dR)^T
-  __shared__ double Gd[kC];
-  __shared__ float gam[kC], Dd[kC], Bs[kC];
+  __shared__ float gam[kC], dec[kC];
 
   const int total = a.nblk * a.Hv * a.N;
   const int wid = xcd_remap(blockIdx.x, total);
@@ -43,6 +42,7 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_state_kernel(ChunkArgs a) 
   const int nch = (sq.len + kC - 1) / kC;
   const OutT* dy = static_cast<const OutT*>(a.dy);
   OutT* dv = static_cast<OutT*>(a.dv);
+  const int sk = a.Hk * Dk, sv = a.Hv * a.Dv;
 
   f32x4 dS[2];  // wave w: rows 4g + jj, columns 32w + 16nt + li
 #pragma unroll
@@ -52,6 +52,39 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_state_kernel(ChunkArgs a) 
       dS[nt][jj] = a.ds_out
                        ? a.ds_out[((int64_t(n) * a.Hv + hv) * a.Dv + row0 + 4 * g + jj) * Dk + 32 * w + 16 * nt + li]
                        : 0.f;
+
+  // Registers holding the previous chunk: k, q rows, dy, exp G, D, and the wave's A operands Tb^T rows 16w + li
+  // and P^T rows 16w + li (k = 8g.., two k steps, hi and lo).
+  bf16x8 fk[4], fq[4], ft[4], fp[4], ct[4], cp[4];
+  float fdy[4], fgt[4], fgam = 0.f, fdec = 0.f;
+  auto prefetch = [&](int c) {
+    const int64_t slot = sq.slot0 + c, tok = sq.tok0 + int64_t(c) * kC;
+    const int L = min(kC, sq.len - c * kC);
+    const bf16_t* kb = a.k + tok * sk + hk * Dk;
+    const bf16_t* qb = a.q + tok * sk + hk * Dk;
+    const OutT* yb = dy + tok * sv + hv * a.Dv + row0;
+    const Tile* tl = a.tiles + (slot * a.Hv + hv);
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4) {
+      const int e = tid + kThreads * q4, t = e >> 4, c8 = (e & 15) * 8;
+      if (t < L) {
+        fk[q4] = gld8(kb + t * sk + c8);
+        fq[q4] = gld8(qb + t * sk + c8);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) fk[q4][j] = fq[q4][j] = (__bf16)0.f;
+      }
+      fdy[q4] = t < L ? IO<OutT>::ld(yb, int64_t(t) * sv + (e & 15)) : 0.f;
+      fgt[q4] = tl->gam[t];
+    }
+    const int ar = (16 * w + li) * kC + 8 * g;
+    ft[0] = gld8(tl->tbt_hi + ar), ft[1] = gld8(tl->tbt_lo + ar), ft[2] = gld8(tl->tbt_hi + ar + 32),
+    ft[3] = gld8(tl->tbt_lo + ar + 32);
+    fp[0] = gld8(tl->pt_hi + ar), fp[1] = gld8(tl->pt_lo + ar), fp[2] = gld8(tl->pt_hi + ar + 32),
+    fp[3] = gld8(tl->pt_lo + ar + 32);
+    if (tid < kC) fgam = tl->gam[tid], fdec = tl->dec[tid];
+  };
+  if (nch > 0) prefetch(nch - 1);
 
   for (int c = nch - 1; c >= 0; --c) {
     const int64_t slot = sq.slot0 + c, tok = sq.tok0 + int64_t(c) * kC;
@@ -71,46 +104,25 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_state_kernel(ChunkArgs a) 
           dSl[r][col] = (__bf16)(x - (float)h);
         }
     }
-    stage_rows_bf16<Dk>(&Kb[0][0], kLDK, a.k, tok, a.Hk, hk, L, kThreads);
-    stage_rows_bf16<Dk>(&Qb[0][0], kLDK, a.q, tok, a.Hk, hk, L, kThreads);
-    if (tid < kC) {
-      const double* G = a.Gall + (slot * a.Hv + hv) * kC;
-      const double gt = G[tid], gl = G[kC - 1];
-      Gd[tid] = gt;
-      gam[tid] = expf(float(gt));
-      Dd[tid] = expf(float(gl - gt));
-      Bs[tid] = tid < L ? bf16_to_f32(a.beta[(tok + tid) * a.Hv + hv]) : 0.f;
-    }
-    __syncthreads();
-    for (int e = tid; e < kC * 16; e += kThreads) {
-      const int t = e >> 4, r = e & 15;
-      const float x = t < L ? IO<OutT>::ld(dy, ((tok + t) * a.Hv + hv) * a.Dv + row0 + r) : 0.f;
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4) {
+      const int e = tid + kThreads * q4, t = e >> 4, r = e & 15, c8 = (e & 15) * 8;
+      *reinterpret_cast<bf16x8*>(&Kb[t][c8]) = fk[q4];
+      *reinterpret_cast<bf16x8*>(&Qb[t][c8]) = fq[q4];
+      const float x = fdy[q4];
       const __bf16 h = (__bf16)x;
       dYth[r][t] = h;
       dYtl[r][t] = (__bf16)(x - (float)h);
-      const float gx = gam[t] * x;
+      const float gx = fgt[q4] * x;
       const __bf16 gh = (__bf16)gx;
       GdYth[r][t] = gh;
       GdYtl[r][t] = (__bf16)(gx - (float)gh);
     }
-    {  // (T diag(beta))^T: Tbt[i][j] = T[j][i] beta_i; thread -> row j = tid / 4 of T, columns 16 (tid % 4) ..
-      const float* T = a.Tall + (slot * a.Hv + hv) * int64_t(kC * kC);
-      const int j = tid >> 2, i0 = (tid & 3) * 16;
 #pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4) {
-        const float4 t4 = *reinterpret_cast<const float4*>(T + j * kC + i0 + 4 * q4);
-        const float tv[4] = {t4.x, t4.y, t4.z, t4.w};
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const int i = i0 + 4 * q4 + u;
-          const float x = tv[u] * Bs[i];
-          const __bf16 h = (__bf16)x;
-          Tbth[i][j] = h;
-          Tbtl[i][j] = (__bf16)(x - (float)h);
-        }
-      }
-    }
+    for (int u = 0; u < 4; ++u) ct[u] = ft[u], cp[u] = fp[u];
+    if (tid < kC) gam[tid] = fgam, dec[tid] = fdec;
     __syncthreads();
+    if (c > 0) prefetch(c - 1);
 
     // K dS^T for positions j = 16w..: lane -> column r = li, rows j = 16w + 4g + jj.
     f32x4 kds = zero4();
@@ -119,37 +131,18 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_state_kernel(ChunkArgs a) 
       const bf16x8 ak = lds8(&Kb[16 * w + li][32 * s + 8 * g]);
       kds = mma(mma(kds, ak, lds8(&dSh[li][32 * s + 8 * g])), ak, lds8(&dSl[li][32 * s + 8 * g]));
     }
-    // P^T rows j = 16w + li (k = i): tiles of P = Q K^T with lane -> column j, rows i = 16m + 4g + jj.
-    f32x4 pq[4];
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      pq[m] = zero4();
-      if (m >= w) {
-#pragma unroll
-        for (int s = 0; s < 4; ++s)
-          pq[m] = mma(pq[m], lds8(&Qb[16 * m + li][32 * s + 8 * g]), lds8(&Kb[16 * w + li][32 * s + 8 * g]));
-        const int j = 16 * w + li;
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-          const int i = 16 * m + 4 * g + jj;
-          pq[m][jj] = i >= j ? pq[m][jj] * expf(float(Gd[i] - Gd[j])) : 0.f;
-        }
-      }
-    }
+    // dDelta rows j = 16w.. = D KdS + P^T dY (A = P^T rows j, k = i).
     f32x4 dd;
 #pragma unroll
-    for (int jj = 0; jj < 4; ++jj) dd[jj] = Dd[16 * w + 4 * g + jj] * kds[jj];
+    for (int jj = 0; jj < 4; ++jj) dd[jj] = dec[16 * w + 4 * g + jj] * kds[jj];
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
-      if (2 * s + 1 >= w) {
-        float pv[8];
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj) pv[jj] = pq[2 * s][jj], pv[4 + jj] = pq[2 * s + 1][jj];
-        const Split8 A = split8(pv);
+      if (32 * s + 31 >= 16 * w) {
+        const Split8 A{cp[2 * s], cp[2 * s + 1]};
         if constexpr (kExactDy) {
-          dd = mma2(dd, A, lds4x2(&dYth[li][32 * s + 4 * g]));
+          dd = mma2(dd, A, lds8(&dYth[li][32 * s + 8 * g]));
         } else {
-          dd = mma3(dd, A, Split8{lds4x2(&dYth[li][32 * s + 4 * g]), lds4x2(&dYtl[li][32 * s + 4 * g])});
+          dd = mma3(dd, A, Split8{lds8(&dYth[li][32 * s + 8 * g]), lds8(&dYtl[li][32 * s + 8 * g])});
         }
       }
     }
@@ -162,18 +155,17 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_state_kernel(ChunkArgs a) 
     }
     __syncthreads();
 
-    // dR = (T diag(beta))^T dDelta for positions i = 16w..; dv = dR.
+    // dR = Tb^T dDelta for positions i = 16w.. (A = Tb^T rows i, k = j); dv = dR.
     f32x4 dr = zero4();
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
-      const Split8 A{lds8(&Tbth[16 * w + li][32 * s + 8 * g]), lds8(&Tbtl[16 * w + li][32 * s + 8 * g])};
-      const Split8 B{lds8(&dDth[li][32 * s + 8 * g]), lds8(&dDtl[li][32 * s + 8 * g])};
-      dr = mma3(dr, A, B);
+      dr = mma3(dr, Split8{ct[2 * s], ct[2 * s + 1]}, Split8{lds8(&dDth[li][32 * s + 8 * g]), lds8(&dDtl[li][32 * s + 8 * g])});
     }
+    OutT* dvb = dv + tok * sv + hv * a.Dv + row0 + li;
 #pragma unroll
     for (int jj = 0; jj < 4; ++jj) {
       const int i = 16 * w + 4 * g + jj;
-      if (i < L) IO<OutT>::st(dv, ((tok + i) * a.Hv + hv) * a.Dv + row0 + li, dr[jj]);
+      if (i < L) IO<OutT>::st(dvb, int64_t(i) * sv, dr[jj]);
       const float x = -gam[i] * dr[jj];
       const __bf16 h = (__bf16)x;
       GdRth[li][i] = h;

@@ -1,9 +1,9 @@
 // Shared pieces of the chunked design: buffer layouts, the chunk-slot -> (sequence, chunk) map, and staging.
 //
-// Residuals (the ckpt buffer), per chunk slot s and value head h:
+// Residuals (the ckpt buffer): the chunk-start states, then per chunk slot s and value head h a Tile record that
+// the prep kernel writes and the other three kernels read:
 //   states  [NC][Hv][Dv][Dk]  f32   state at the chunk's start (the reference's ckpt, src/delta_grad.cpp:172-181)
-//   T       [NC][Hv][64][64]  f32   (I + A)^-1 of the chunk (row i, col j), A = strict_lower(diag(beta)(E * K K^T))
-//   Gam     [NC][Hv][64]      f64   G_i = sum_{j <= i} a_j within the chunk (0-padded past its end)
+//   tiles   [NC][Hv] Tile
 // Workspace: dSend [NC][Hv][Dv][Dk] f32, the cotangent of the state at each chunk's end.
 #pragma once
 #include "gdn_common.h"
@@ -14,21 +14,29 @@ namespace qbgdn {
 constexpr int kC = kChunk;  // 64 positions per chunk
 constexpr int kPadB = 8;    // bf16 row padding in LDS (keeps 16-byte alignment, staggers banks)
 
+// Everything about a (chunk, value head) that does not depend on the state, as MFMA-ready bf16 hi/lo pairs:
+//   Tb = T diag(beta), T = (I + A)^-1, A = strict_lower(diag(beta) (E * K K^T)), E_ij = exp(G_i - G_j)
+//   P  = lower_incl(E * Q K^T)
+// and the per-position vectors. Positions past the chunk's end are padded (beta 0, log-decay 0, k = q = 0).
+struct Tile {
+  bf16_t tb_hi[kC * kC], tb_lo[kC * kC];    // Tb, row i, column j
+  bf16_t tbt_hi[kC * kC], tbt_lo[kC * kC];  // Tb^T, row j, column i
+  bf16_t p_hi[kC * kC], p_lo[kC * kC];      // P, row i (query), column j (key)
+  bf16_t pt_hi[kC * kC], pt_lo[kC * kC];    // P^T, row j (key), column i (query)
+  float t[kC * kC];                         // T, row i, column j
+  float beta[kC];
+  float gam[kC];  // exp(G_i)
+  float dec[kC];  // exp(G_63 - G_i)
+  float G[kC];    // G_i = sum_{j <= i} a_j within the chunk
+};
+static_assert(sizeof(Tile) % 16 == 0, "Tile records stay 16-byte aligned");
+
 struct ChunkLayout {
   int64_t NC;
   int Hv, Dv, Dk;
   __host__ __device__ int64_t states_elems() const { return NC * Hv * int64_t(Dv) * Dk; }
-  __host__ __device__ float* T(float* ckpt) const { return ckpt + states_elems(); }
-  __host__ __device__ const float* T(const float* ckpt) const { return ckpt + states_elems(); }
-  __host__ __device__ double* Gam(float* ckpt) const {
-    return reinterpret_cast<double*>(ckpt + states_elems() + NC * Hv * int64_t(kC * kC));
-  }
-  __host__ __device__ const double* Gam(const float* ckpt) const {
-    return reinterpret_cast<const double*>(ckpt + states_elems() + NC * Hv * int64_t(kC * kC));
-  }
-  __host__ __device__ size_t bytes() const {
-    return size_t(states_elems()) * 4 + size_t(NC) * Hv * (kC * kC * 4 + kC * 8);
-  }
+  __host__ __device__ size_t tiles_bytes() const { return size_t(NC) * Hv * sizeof(Tile); }
+  __host__ __device__ size_t bytes() const { return size_t(states_elems()) * 4 + tiles_bytes(); }
 };
 
 // The sequence and chunk of a chunk slot (slots of sequence n are [slot0[n], slot0[n + 1])).

@@ -3,11 +3,12 @@
 // so a 16-row block needs no other block. Per chunk, with S the block's rows of the state at the chunk start:
 //   write S to the chunk's checkpoint slot (the reference's ckpt, src/delta_grad.cpp:172-181)
 //   KS = K S^T, QS = Q S^T                        [64 x 16]   wave w: positions 16w..16w+15
-//   R = V - diag(exp G) KS;  Delta = T diag(beta) R
+//   R = V - diag(exp G) KS;  Delta = Tb R
 //   S <- exp(G_63) S + (diag(exp(G_63 - G)) Delta)^T K        wave w: state columns 32w..32w+31
-//   Y = diag(exp G) QS + P Delta,  P = lower_incl(exp(G_i - G_j) q_i . k_j)
-// All products run on v_mfma_f32_16x16x32_bf16; float32 operands (S, T diag(beta), R, Delta, P) are split into
-// bf16 hi + lo pairs so the state keeps float32 accuracy, and k, q, v enter exactly (they are bf16).
+//   Y = diag(exp G) QS + P Delta
+// Tb and P come ready from the prep kernel (each wave loads its rows as MFMA A operands). All products run on v_mfma_f32_16x16x32_bf16; float32 operands (S, R,
+// Delta, Tb, P) are split into bf16 hi + lo pairs so the state keeps float32 accuracy, while k, q, v enter exactly.
+// The next chunk's tiles are loaded into registers while the current chunk computes.
 #include "chunk_common.h"
 #include "chunk_kernels.h"
 
@@ -22,12 +23,10 @@ template <typename OutT>
 __global__ __launch_bounds__(kThreads) void chunk_fwd_kernel(ChunkArgs a) {
   constexpr int Dk = 128;
   __shared__ __bf16 Kb[kC][kLDK], Qb[kC][kLDK];
-  __shared__ __bf16 Tbh[kC][kLDC], Tbl[kC][kLDC];
   __shared__ __bf16 Sh[16][kLDK], Sl[16][kLDK];
   __shared__ __bf16 Rth[16][kLDC], Rtl[16][kLDC], Dth[16][kLDC], Dtl[16][kLDC], DDth[16][kLDC], DDtl[16][kLDC];
   __shared__ float Vs[kC][16];
-  __shared__ double Gd[kC];
-  __shared__ float gam[kC], Dd[kC], Bs[kC];
+  __shared__ float gam[kC], dec[kC];
 
   const int total = a.nblk * a.Hv * a.N;
   const int wid = xcd_remap(blockIdx.x, total);
@@ -37,6 +36,7 @@ __global__ __launch_bounds__(kThreads) void chunk_fwd_kernel(ChunkArgs a) {
   const Seq sq = seq_of(a.tab, n);
   const int nch = (sq.len + kC - 1) / kC;
   OutT* y = static_cast<OutT*>(a.y);
+  const int sk = a.Hk * Dk, sv = a.Hv * a.Dv;  // token strides of k/q and v/y
 
   // State block: wave w holds rows 4g + jj, columns 32w + 16nt + li.
   f32x4 S[2];
@@ -46,6 +46,39 @@ __global__ __launch_bounds__(kThreads) void chunk_fwd_kernel(ChunkArgs a) {
     for (int jj = 0; jj < 4; ++jj)
       S[nt][jj] = a.s0 ? a.s0[((int64_t(n) * a.Hv + hv) * a.Dv + row0 + 4 * g + jj) * Dk + 32 * w + 16 * nt + li]
                        : 0.f;
+
+  // Registers holding the next chunk: k and q rows (thread e of [0, 1024) in steps of 256 covers row e / 16,
+  // columns 8 (e % 16)), v, exp G, D, and the wave's A operands: Tb rows 16w + li and P rows 16w + li (k = 8g..,
+  // two k steps, hi and lo).
+  bf16x8 fk[4], fq[4], ft[4], fp[4], ct[4], cp[4];
+  float fv[4], fgam = 0.f, fdec = 0.f;
+  auto prefetch = [&](int c) {
+    const int64_t slot = sq.slot0 + c, tok = sq.tok0 + int64_t(c) * kC;
+    const int L = min(kC, sq.len - c * kC);
+    const bf16_t* kb = a.k + tok * sk + hk * Dk;
+    const bf16_t* qb = a.q + tok * sk + hk * Dk;
+    const bf16_t* vb = a.v + tok * sv + hv * a.Dv + row0;
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4) {
+      const int e = tid + kThreads * q4, t = e >> 4, c8 = (e & 15) * 8;
+      if (t < L) {
+        fk[q4] = gld8(kb + t * sk + c8);
+        fq[q4] = gld8(qb + t * sk + c8);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) fk[q4][j] = fq[q4][j] = (__bf16)0.f;
+      }
+      fv[q4] = t < L ? bf16_to_f32(vb[t * sv + (e & 15)]) : 0.f;
+    }
+    const Tile* tl = a.tiles + (slot * a.Hv + hv);
+    const int ar = (16 * w + li) * kC + 8 * g;
+    ft[0] = gld8(tl->tb_hi + ar), ft[1] = gld8(tl->tb_lo + ar), ft[2] = gld8(tl->tb_hi + ar + 32),
+    ft[3] = gld8(tl->tb_lo + ar + 32);
+    fp[0] = gld8(tl->p_hi + ar), fp[1] = gld8(tl->p_lo + ar), fp[2] = gld8(tl->p_hi + ar + 32),
+    fp[3] = gld8(tl->p_lo + ar + 32);
+    if (tid < kC) fgam = tl->gam[tid], fdec = tl->dec[tid];
+  };
+  if (nch > 0) prefetch(0);
 
   for (int c = 0; c < nch; ++c) {
     const int64_t slot = sq.slot0 + c, tok = sq.tok0 + int64_t(c) * kC;
@@ -65,39 +98,18 @@ __global__ __launch_bounds__(kThreads) void chunk_fwd_kernel(ChunkArgs a) {
           Sl[r][col] = (__bf16)(x - (float)h);
         }
     }
-    stage_rows_bf16<Dk>(&Kb[0][0], kLDK, a.k, tok, a.Hk, hk, L, kThreads);
-    stage_rows_bf16<Dk>(&Qb[0][0], kLDK, a.q, tok, a.Hk, hk, L, kThreads);
-    for (int e = tid; e < kC * 16; e += kThreads) {
-      const int t = e >> 4, r = e & 15;
-      Vs[t][r] = t < L ? bf16_to_f32(a.v[((tok + t) * a.Hv + hv) * a.Dv + row0 + r]) : 0.f;
-    }
-    if (tid < kC) {
-      const double* G = a.Gall + (slot * a.Hv + hv) * kC;
-      const double gt = G[tid], gl = G[kC - 1];
-      Gd[tid] = gt;
-      gam[tid] = expf(float(gt));
-      Dd[tid] = expf(float(gl - gt));
-      Bs[tid] = tid < L ? bf16_to_f32(a.beta[(tok + tid) * a.Hv + hv]) : 0.f;
-    }
-    __syncthreads();
-    {  // T diag(beta), split: thread -> row tid / 4, columns 16 (tid % 4) .. + 16
-      const float* T = a.Tall + (slot * a.Hv + hv) * int64_t(kC * kC);
-      const int i = tid >> 2, j0 = (tid & 3) * 16;
 #pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4) {
-        const float4 t4 = *reinterpret_cast<const float4*>(T + i * kC + j0 + 4 * q4);
-        const float tv[4] = {t4.x, t4.y, t4.z, t4.w};
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const int j = j0 + 4 * q4 + u;
-          const float x = tv[u] * Bs[j];
-          const __bf16 h = (__bf16)x;
-          Tbh[i][j] = h;
-          Tbl[i][j] = (__bf16)(x - (float)h);
-        }
-      }
+    for (int q4 = 0; q4 < 4; ++q4) {
+      const int e = tid + kThreads * q4, t = e >> 4, c8 = (e & 15) * 8;
+      *reinterpret_cast<bf16x8*>(&Kb[t][c8]) = fk[q4];
+      *reinterpret_cast<bf16x8*>(&Qb[t][c8]) = fq[q4];
+      Vs[t][e & 15] = fv[q4];
     }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) ct[u] = ft[u], cp[u] = fp[u];
+    if (tid < kC) gam[tid] = fgam, dec[tid] = fdec;
     __syncthreads();
+    if (c + 1 < nch) prefetch(c + 1);
 
     // KS, QS for positions 16w..: lane -> column r = li, rows i = 16w + 4g + jj.
     f32x4 ks = zero4(), qs = zero4();
@@ -118,18 +130,17 @@ __global__ __launch_bounds__(kThreads) void chunk_fwd_kernel(ChunkArgs a) {
     }
     __syncthreads();
 
-    // Delta = T diag(beta) R for positions 16w..
+    // Delta = Tb R for positions 16w..
     f32x4 dl = zero4();
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
-      const Split8 A{lds8(&Tbh[16 * w + li][32 * s + 8 * g]), lds8(&Tbl[16 * w + li][32 * s + 8 * g])};
       const Split8 B{lds8(&Rth[li][32 * s + 8 * g]), lds8(&Rtl[li][32 * s + 8 * g])};
-      dl = mma3(dl, A, B);
+      dl = mma3(dl, Split8{ct[2 * s], ct[2 * s + 1]}, B);
     }
 #pragma unroll
     for (int jj = 0; jj < 4; ++jj) {
       const int i = 16 * w + 4 * g + jj;
-      const float x = dl[jj], xd = Dd[i] * dl[jj];
+      const float x = dl[jj], xd = dec[i] * dl[jj];
       const __bf16 h = (__bf16)x, hd = (__bf16)xd;
       Dth[li][i] = h;
       Dtl[li][i] = (__bf16)(x - (float)h);
@@ -155,46 +166,22 @@ __global__ __launch_bounds__(kThreads) void chunk_fwd_kernel(ChunkArgs a) {
       }
     }
 
-    // Y = diag(exp G) QS + P Delta for positions i = 16w.. (P as the A operand: lane -> row i, k = j in the
-    // stacked-C order of the P^T tiles below).
-    f32x4 pt[4];
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      pt[m] = zero4();
-      if (m <= w) {
-#pragma unroll
-        for (int s = 0; s < 4; ++s)
-          pt[m] = mma(pt[m], lds8(&Kb[16 * m + li][32 * s + 8 * g]), lds8(&Qb[16 * w + li][32 * s + 8 * g]));
-      }
-    }
-    {
-      const int i = 16 * w + li;
-#pragma unroll
-      for (int m = 0; m < 4; ++m)
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-          const int j = 16 * m + 4 * g + jj;
-          pt[m][jj] = j <= i ? pt[m][jj] * expf(float(Gd[i] - Gd[j])) : 0.f;
-        }
-    }
+    // Y = diag(exp G) QS + P Delta for positions i = 16w.. (P rows from the tile; zero above the diagonal).
     f32x4 yacc;
 #pragma unroll
     for (int jj = 0; jj < 4; ++jj) yacc[jj] = gam[16 * w + 4 * g + jj] * qs[jj];
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
       if (32 * s <= 16 * w + 15) {
-        float pv[8];
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj) pv[jj] = pt[2 * s][jj], pv[4 + jj] = pt[2 * s + 1][jj];
-        const Split8 A = split8(pv);
-        const Split8 B{lds4x2(&Dth[li][32 * s + 4 * g]), lds4x2(&Dtl[li][32 * s + 4 * g])};
-        yacc = mma3(yacc, A, B);
+        const Split8 B{lds8(&Dth[li][32 * s + 8 * g]), lds8(&Dtl[li][32 * s + 8 * g])};
+        yacc = mma3(yacc, Split8{cp[2 * s], cp[2 * s + 1]}, B);
       }
     }
+    OutT* yb = y + tok * sv + hv * a.Dv + row0 + li;
 #pragma unroll
     for (int jj = 0; jj < 4; ++jj) {
       const int i = 16 * w + 4 * g + jj;
-      if (i < L) IO<OutT>::st(y, ((tok + i) * a.Hv + hv) * a.Dv + row0 + li, yacc[jj]);
+      if (i < L) IO<OutT>::st(yb, int64_t(i) * sv, yacc[jj]);
     }
   }
   if (a.s_out) {

@@ -14,9 +14,8 @@ struct ChunkArgs {
   const float* s0;
   void* y;
   float* s_out;
-  float* ckpt;  // chunk-start states (may be null in a forward without backward)
-  float* Tall;  // T per (slot, value head), inside ckpt after the states, or in the workspace
-  double* Gall; // G per (slot, value head)
+  float* ckpt;   // chunk-start states (may be null in a forward without backward)
+  Tile* tiles;   // per (slot, value head): inside ckpt after the states, or in the workspace
   const void* dy;
   const float* ds_out;
   void* dq;
