@@ -68,7 +68,7 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
   __shared__ __align__(16) unsigned char smem[kSmemBytes];
   __shared__ float gam[kC], dec[kC], bet[kC], Gf[kC];
   __shared__ float gpos[2][kC], hpos[2][kC], tpos[2][kC];
-  __shared__ float x1r[kC], x1c[kC], x2r[kC], x2c[kC], dbT[kC], dbA[kC], dGt[kC], red[kThreads];
+  __shared__ float x1r[kC], x1c[kC], x2r[2][kC], x2c[4][kC], dbT[kC], dbA[kC], dGt[kC], red[kThreads / 64];
   __shared__ float SdS_total;
   __bf16* sb = reinterpret_cast<__bf16*>(smem);
   float* sf = reinterpret_cast<float*>(smem);
@@ -87,18 +87,13 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
   const int sk = a.Hk * Dk, sv = a.Hv * a.Dv;  // token strides of k/q/dq/dk and v/dy
   const bf16_t* kbase = a.k + tok * sk + hk * Dk;
   const bf16_t* qbase = a.q + tok * sk + hk * Dk;
+  // Rows past the chunk's last row read as zeros.
+  const auto krs = buffer_rsrc(kbase, uint32_t(L * sk) * 2u), qrs = buffer_rsrc(qbase, uint32_t(L * sk) * 2u);
 
   // K rows of the wave's positions (A operands of K S0^T, K dS^T, K K^T).
   bf16x8 Kf[4];
 #pragma unroll
-  for (int s = 0; s < 4; ++s) {
-    if (ip < L) {
-      Kf[s] = gld8(kbase + ip * sk + 32 * s + 8 * g);
-    } else {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) Kf[s][j] = (__bf16)0.f;
-    }
-  }
+  for (int s = 0; s < 4; ++s) Kf[s] = __builtin_bit_cast(bf16x8, buf_ld16(krs, uint32_t(ip * sk + 32 * s + 8 * g) * 2));
   f32x4 dQ[4], dK[4];  // columns 16 (4 hw + t) + li, rows 16 pw + 4 g + jj
 #pragma unroll
   for (int t = 0; t < 4; ++t) dQ[t] = zero4(), dK[t] = zero4();
@@ -124,50 +119,34 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
       asm volatile("" : "+v"(lt));
       const int g = (lt >> 4) & 3, li = lt & 15, pw = (lt >> 6) & 3, hw = lt >> 8, ip = 16 * pw + li;
       __syncthreads();
-      // Uniform bases of this block's rows; lanes add 32-bit offsets.
+      // All of this block's global reads are issued together before any is used. dy and v go through buffer
+      // resources that end at the chunk's last row, so rows past it read as zeros without a branch.
       const int64_t rows0 = (sh * a.Dv + r0) * Dk;
       const float* s0b = a.ckpt + rows0;
       const float* dsb = a.dsend + rows0;
-      const OutT* dyb = dy + (tok * a.Hv + hv) * a.Dv + r0;
-      const bf16_t* vb = a.v + (tok * a.Hv + hv) * a.Dv + r0;
-      {  // S0 and dS rows r0..r0+31: thread -> row tid / 16, columns 8 (tid % 16) ..
-        const int r = tid >> 4, c0 = (tid & 15) * 8;
-        const uint32_t at = uint32_t(r * Dk + c0);
-        const float* s0p = s0b + at;
-        const float* dsp = dsb + at;
+      const auto yr = buffer_rsrc(dy + (tok * a.Hv + hv) * a.Dv + r0, uint32_t(L * sv) * uint32_t(sizeof(OutT)));
+      const auto vr = buffer_rsrc(a.v + (tok * a.Hv + hv) * a.Dv + r0, uint32_t(L * sv) * 2u);
+      // S0 and dS: thread -> column c = tid % 128, rows 8 (tid / 128) .. + 7.
+      const int cc = lt & 127, rg = 8 * (lt >> 7);
+      float xs[8], ys[8];
 #pragma unroll
-        for (int q4 = 0; q4 < 2; ++q4) {
-          const float4 x4 = *reinterpret_cast<const float4*>(s0p + 4 * q4);
-          const float4 y4 = *reinterpret_cast<const float4*>(dsp + 4 * q4);
-          const float xs[4] = {x4.x, x4.y, x4.z, x4.w}, ys[4] = {y4.x, y4.y, y4.z, y4.w};
-#pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            const int c = c0 + 4 * q4 + u;
-            sds += xs[u] * ys[u];
-            put_split(sb + oS0h, sb + oS0l, r * kLDK + c, xs[u]);
-            put_split(sb + oS0th, sb + oS0tl, c * kLDR + r, xs[u]);
-            put_split(sb + odSh, sb + odSl, r * kLDK + c, ys[u]);
-            put_split(sb + odSth, sb + odStl, c * kLDR + r, ys[u]);
-          }
-        }
+      for (int u = 0; u < 8; ++u) xs[u] = s0b[(rg + u) * Dk + cc], ys[u] = dsb[(rg + u) * Dk + cc];
+      // dY^T: thread -> position tid / 8, rows 4 (tid % 8) ..; the wave's own dY rows (i = ip, r = 8g..).
+      const int iy = lt >> 3, r4 = (lt & 7) * 4;
+      uint4 yT, yo[2];
+      if constexpr (kExactDy) {
+        const auto t2 = __builtin_amdgcn_raw_buffer_load_b64(yr, int(uint32_t(iy * sv + r4) * 2), 0, 0);
+        yT = uint4{t2[0], t2[1], 0u, 0u};
+        yo[0] = buf_ld16(yr, uint32_t(ip * sv + 8 * g) * 2);
+      } else {
+        yT = buf_ld16(yr, uint32_t(iy * sv + r4) * 4);
+        yo[0] = buf_ld16(yr, uint32_t(ip * sv + 8 * g) * 4);
+        yo[1] = buf_ld16(yr, uint32_t(ip * sv + 8 * g) * 4 + 16);
       }
-      {  // dY^T [r][i]: thread -> position tid / 8, rows 4 (tid % 8) ..
-        const int i = tid >> 3, r4 = (tid & 7) * 4;
+      // v at the wave's accumulator positions (rows i = 16 pw + 4g + jj, column r = 16 hw + li).
+      uint16_t vraw[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const float x = i < L ? IO<OutT>::ld(dyb, uint32_t(i * sv + r4 + j)) : 0.f;
-          put_split(sb + odYth, sb + odYtl, (r4 + j) * kLDC + i, x);
-        }
-      }
-      // The wave's own dY rows (i = ip, k = r = 8g..): A of dY S0, B of Delta dY^T.
-      Split8 dYo;
-      {
-        float x[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-          x[j] = ip < L ? IO<OutT>::ld(dyb, uint32_t(ip * sv + 8 * g + j)) : 0.f;
-        dYo = split8(x);
-      }
+      for (int jj = 0; jj < 4; ++jj) vraw[jj] = buf_ld2(vr, uint32_t((16 * pw + 4 * g + jj) * sv + 16 * hw + li) * 2);
       // A operands from the tile for this block (reloaded per block from L2 to keep them out of the loop-carried
       // registers): Tb rows ip (k = j), Tb^T rows ip (k = j) and P^T rows ip (k = i).
       Split8 TbA[2], TbtA[2], PA[2];
@@ -182,13 +161,49 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
           PA[s] = Split8{gld8(tb->pt_hi + ar + 32 * s), gld8(tb->pt_lo + ar + 32 * s)};
         }
       }
-      // v at the wave's accumulator positions (rows i = 16 pw + 4g + jj, column r = 16 hw + li).
+      __syncthreads();  // the previous block's readers of LDS are done
+
+      {  // S0, dS row-major [r][c] (scalar) and transposed [c][r] (one 16-byte vector per split half).
+        bf16x8 th, tl8, uh, ul;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          sds += xs[u] * ys[u];
+          const __bf16 xh = (__bf16)xs[u], xl = (__bf16)(xs[u] - (float)xh);
+          const __bf16 yh = (__bf16)ys[u], yl = (__bf16)(ys[u] - (float)yh);
+          sb[oS0h + (rg + u) * kLDK + cc] = xh, sb[oS0l + (rg + u) * kLDK + cc] = xl;
+          sb[odSh + (rg + u) * kLDK + cc] = yh, sb[odSl + (rg + u) * kLDK + cc] = yl;
+          th[u] = xh, tl8[u] = xl, uh[u] = yh, ul[u] = yl;
+        }
+        *reinterpret_cast<bf16x8*>(sb + oS0th + cc * kLDR + rg) = th;
+        *reinterpret_cast<bf16x8*>(sb + oS0tl + cc * kLDR + rg) = tl8;
+        *reinterpret_cast<bf16x8*>(sb + odSth + cc * kLDR + rg) = uh;
+        *reinterpret_cast<bf16x8*>(sb + odStl + cc * kLDR + rg) = ul;
+      }
+      {  // dY^T [r][i]
+        const uint32_t wv[4] = {yT.x, yT.y, yT.z, yT.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float x = kExactDy ? (j & 1 ? __uint_as_float(wv[j >> 1] & 0xffff0000u) : __uint_as_float(wv[j >> 1] << 16))
+                                   : __uint_as_float(wv[j]);
+          put_split(sb + odYth, sb + odYtl, (r4 + j) * kLDC + iy, x);
+        }
+      }
+      Split8 dYo;
+      {
+        float x[8];
+        const uint32_t w0[4] = {yo[0].x, yo[0].y, yo[0].z, yo[0].w}, w1[4] = {yo[1].x, yo[1].y, yo[1].z, yo[1].w};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          if constexpr (kExactDy)
+            x[j] = j & 1 ? __uint_as_float(w0[j >> 1] & 0xffff0000u) : __uint_as_float(w0[j >> 1] << 16);
+          else
+            x[j] = __uint_as_float(j < 4 ? w0[j] : w1[j - 4]);
+        }
+        dYo = split8(x);
+      }
       float vv[4];
 #pragma unroll
-      for (int jj = 0; jj < 4; ++jj) {
-        const int i = 16 * pw + 4 * g + jj;
-        vv[jj] = i < L ? bf16_to_f32(vb[uint32_t(i * sv + 16 * hw + li)]) : 0.f;
-      }
+      for (int jj = 0; jj < 4; ++jj) vv[jj] = bf16_to_f32(vraw[jj]);
       __syncthreads();
 
       // Phase 1: KS and KdS for positions 16 pw.., state rows r = 16 hw + li.
@@ -304,20 +319,19 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
       const float v = sum16(gpart[jj]), h = sum16(hD[jj]);
       if (li == 0) gpos[hw][16 * pw + 4 * g + jj] = v, hpos[hw][16 * pw + 4 * g + jj] = h;
     }
-    red[tid] = sds;
+    {
+      float v = sum16(sds);
+      v += __shfl_xor(v, 16);
+      v += __shfl_xor(v, 32);
+      if ((tid & 63) == 0) red[tid >> 6] = v;
+    }
     __syncthreads();
 
     // E1: K, K^T, Q^T, T, dP (unmasked, j <= i) and dTb into the end-phase region.
     for (int e = tid; e < kC * 16; e += kThreads) {
       const int t = e >> 4, c8 = (e & 15) * 8;
-      bf16x8 kv, qv;
-      if (t < L) {
-        kv = gld8(kbase + t * sk + c8);
-        qv = gld8(qbase + t * sk + c8);
-      } else {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) kv[j] = qv[j] = (__bf16)0.f;
-      }
+      const bf16x8 kv = __builtin_bit_cast(bf16x8, buf_ld16(krs, uint32_t(t * sk + c8) * 2));
+      const bf16x8 qv = __builtin_bit_cast(bf16x8, buf_ld16(qrs, uint32_t(t * sk + c8) * 2));
       *reinterpret_cast<bf16x8*>(sb + eKb + t * kLDK + c8) = kv;
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
@@ -326,14 +340,36 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
       }
     }
     for (int q = tid; q < kC * kC; q += kThreads) sf[eT + (q >> 6) * kLDF + (q & 63)] = tl->t[q];
+    {
+      // With the masked dP entries of the lane (i = ip, j = 16 (2 hw + mi) + 4g + jj) and P_ij from the tile: the
+      // row sums sum_j dP_ij P_ij (over g here, over hw in dG) and column sums sum_i dP_ij P_ij (over li here,
+      // over pw in dG).
+      float prow = 0.f;
 #pragma unroll
-    for (int mi = 0; mi < 2; ++mi)
+      for (int mi = 0; mi < 2; ++mi) {
+        const int j0 = 16 * (2 * hw + mi) + 4 * g;
+        const uint2 ph = *reinterpret_cast<const uint2*>(tl->p_hi + ip * kC + j0);
+        const uint2 pl = *reinterpret_cast<const uint2*>(tl->p_lo + ip * kC + j0);
+        const uint32_t hw4[2] = {ph.x, ph.y}, lw4[2] = {pl.x, pl.y};
 #pragma unroll
-      for (int jj = 0; jj < 4; ++jj) {
-        const int j = 16 * (2 * hw + mi) + 4 * g + jj;
-        sf[edP + ip * kLDF + j] = j <= ip ? dPt[mi][jj] : 0.f;
-        sf[edTb + ip * kLDF + j] = j <= ip ? dTbt[mi][jj] : 0.f;
+        for (int jj = 0; jj < 4; ++jj) {
+          const int j = j0 + jj;
+          const float dp = j <= ip ? dPt[mi][jj] : 0.f;
+          sf[edP + ip * kLDF + j] = dp;
+          sf[edTb + ip * kLDF + j] = j <= ip ? dTbt[mi][jj] : 0.f;
+          const uint32_t hb = hw4[jj >> 1], lb = lw4[jj >> 1];
+          const float pv = jj & 1 ? __uint_as_float(hb & 0xffff0000u) + __uint_as_float(lb & 0xffff0000u)
+                                  : __uint_as_float(hb << 16) + __uint_as_float(lb << 16);
+          const float x = dp * pv;
+          prow += x;
+          const float col = sum16(x);
+          if (li == 0) x2c[pw][j] = col;
+        }
       }
+      prow += __shfl_xor(prow, 16);
+      prow += __shfl_xor(prow, 32);
+      if (g == 0) x2r[hw][ip] = prow;
+    }
     __syncthreads();
 
     // E2: dQ += diag(exp G) dQ_inter and its dG term; K K^T; dQ += (dP * M) K; dK += (dP * M)^T Q; Z = dT T^T.
@@ -408,21 +444,9 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
       float acc = 0.f;
       for (int i = j; i < kC; ++i) acc += sf[edTb + i * kLDF + j] * sf[eT + i * kLDF + j];
       dbT[j] = acc;
-    } else if (tid < 2 * kC) {  // P row i from the tile
-      const int i = tid - kC;
+    } else if (tid == kC) {
       float acc = 0.f;
-      for (int j = 0; j <= i; ++j)
-        acc += sf[edP + i * kLDF + j] * ((float)as_bf(tl->p_hi[i * kC + j]) + (float)as_bf(tl->p_lo[i * kC + j]));
-      x2r[i] = acc;
-    } else if (tid < 3 * kC) {  // P column j: row j of P^T
-      const int j = tid - 2 * kC;
-      float acc = 0.f;
-      for (int i = j; i < kC; ++i)
-        acc += sf[edP + i * kLDF + j] * ((float)as_bf(tl->pt_hi[j * kC + i]) + (float)as_bf(tl->pt_lo[j * kC + i]));
-      x2c[j] = acc;
-    } else if (tid == 3 * kC) {
-      float acc = 0.f;
-      for (int t = 0; t < kThreads; ++t) acc += red[t];
+      for (int t = 0; t < kThreads / 64; ++t) acc += red[t];
       SdS_total = acc;
     }
     __syncthreads();
@@ -505,7 +529,7 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
     if (tid < kC) {
       const int t = tid;
       float v = gam[t] * (tpos[0][t] + tpos[1][t]) + gpos[0][t] + gpos[1][t] - hpos[0][t] - hpos[1][t] + x1r[t] -
-                x1c[t] + x2r[t] - x2c[t];
+                x1c[t] + x2r[0][t] + x2r[1][t] - (x2c[0][t] + x2c[1][t] + x2c[2][t] + x2c[3][t]);
       if (t == kC - 1) {
         float hsum = 0.f;
         for (int i = 0; i < kC; ++i) hsum += hpos[0][i] + hpos[1][i];

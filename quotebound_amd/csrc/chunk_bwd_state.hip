@@ -53,76 +53,95 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_state_kernel(ChunkArgs a) 
                        ? a.ds_out[((int64_t(n) * a.Hv + hv) * a.Dv + row0 + 4 * g + jj) * Dk + 32 * w + 16 * nt + li]
                        : 0.f;
 
-  // Registers holding the previous chunk: k, q rows, dy, exp G, D, and the wave's A operands Tb^T rows 16w + li
-  // and P^T rows 16w + li (k = 8g.., two k steps, hi and lo).
-  bf16x8 fk[4], fq[4], ft[4], fp[4], ct[4], cp[4];
-  float fdy[4], fgt[4], fgam = 0.f, fdec = 0.f;
-  auto prefetch = [&](int c) {
+  // One chunk's inputs, loaded into registers a chunk ahead (in the reverse sweep): k and q rows (thread e of
+  // [0, 1024) in steps of 256 covers row e / 16, columns 8 (e % 16)), dy (row e / 16, state row e % 16) with its
+  // exp G, the chunk's exp G and D, and the wave's A operands Tb^T rows 16w + li and P^T rows 16w + li (k = 8g..,
+  // two k steps, hi and lo). k, q, dy are read through buffer resources that end at the sequence's last row, so rows
+  // past it read as zeros without a branch.
+  struct Pre {
+    uint4 k[4], q[4];
+    bf16x8 t[4], p[4];
+    uint32_t dy[4];  // raw bits (bf16 in the low half, or float32)
+    float gt[4];
+    float gam, dec;
+  };
+  auto prefetch = [&](Pre& f, int c) {
     const int64_t slot = sq.slot0 + c, tok = sq.tok0 + int64_t(c) * kC;
-    const int L = min(kC, sq.len - c * kC);
-    const bf16_t* kb = a.k + tok * sk + hk * Dk;
-    const bf16_t* qb = a.q + tok * sk + hk * Dk;
-    const OutT* yb = dy + tok * sv + hv * a.Dv + row0;
+    const uint32_t L = uint32_t(min(kC, sq.len - c * kC));
+    const auto kr = buffer_rsrc(a.k + tok * sk + hk * Dk, L * sk * 2);
+    const auto qr = buffer_rsrc(a.q + tok * sk + hk * Dk, L * sk * 2);
+    const auto yr = buffer_rsrc(dy + tok * sv + hv * a.Dv + row0, L * sv * uint32_t(sizeof(OutT)));
     const Tile* tl = a.tiles + (slot * a.Hv + hv);
+    f.gam = tl->gam[tid & (kC - 1)], f.dec = tl->dec[tid & (kC - 1)];
 #pragma unroll
     for (int q4 = 0; q4 < 4; ++q4) {
       const int e = tid + kThreads * q4, t = e >> 4, c8 = (e & 15) * 8;
-      if (t < L) {
-        fk[q4] = gld8(kb + t * sk + c8);
-        fq[q4] = gld8(qb + t * sk + c8);
-      } else {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) fk[q4][j] = fq[q4][j] = (__bf16)0.f;
-      }
-      fdy[q4] = t < L ? IO<OutT>::ld(yb, int64_t(t) * sv + (e & 15)) : 0.f;
-      fgt[q4] = tl->gam[t];
+      f.k[q4] = buf_ld16(kr, uint32_t(t * sk + c8) * 2);
+      f.q[q4] = buf_ld16(qr, uint32_t(t * sk + c8) * 2);
+      const uint32_t yo = uint32_t(t * sv + (e & 15));
+      if constexpr (kExactDy)
+        f.dy[q4] = buf_ld2(yr, yo * 2);
+      else
+        f.dy[q4] = __float_as_uint(buf_ld4(yr, yo * 4));
+      f.gt[q4] = tl->gam[t];
     }
     const int ar = (16 * w + li) * kC + 8 * g;
-    ft[0] = gld8(tl->tbt_hi + ar), ft[1] = gld8(tl->tbt_lo + ar), ft[2] = gld8(tl->tbt_hi + ar + 32),
-    ft[3] = gld8(tl->tbt_lo + ar + 32);
-    fp[0] = gld8(tl->pt_hi + ar), fp[1] = gld8(tl->pt_lo + ar), fp[2] = gld8(tl->pt_hi + ar + 32),
-    fp[3] = gld8(tl->pt_lo + ar + 32);
-    if (tid < kC) fgam = tl->gam[tid], fdec = tl->dec[tid];
+    f.t[0] = gld8(tl->tbt_hi + ar), f.t[1] = gld8(tl->tbt_lo + ar), f.t[2] = gld8(tl->tbt_hi + ar + 32),
+    f.t[3] = gld8(tl->tbt_lo + ar + 32);
+    f.p[0] = gld8(tl->pt_hi + ar), f.p[1] = gld8(tl->pt_lo + ar), f.p[2] = gld8(tl->pt_hi + ar + 32),
+    f.p[3] = gld8(tl->pt_lo + ar + 32);
   };
-  if (nch > 0) prefetch(nch - 1);
 
-  for (int c = nch - 1; c >= 0; --c) {
-    const int64_t slot = sq.slot0 + c, tok = sq.tok0 + int64_t(c) * kC;
-    const int L = min(kC, sq.len - c * kC);
+  // dv of a chunk is stored during the chunk processed after it (after that chunk's inputs are staged), so no wait
+  // for the staged loads ever covers these stores.
+  auto store_dv = [&](int c, const f32x4& dr) {
+    const int64_t tok = sq.tok0 + int64_t(c) * kC;
+    const uint32_t L = uint32_t(min(kC, sq.len - c * kC));
+    // Rows i >= L fall past the resource and are dropped.
+    const auto vr = buffer_rsrc(dv + tok * sv + hv * a.Dv + row0, L * sv * uint32_t(sizeof(OutT)));
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) BufIO<OutT>::st(vr, uint32_t((16 * w + 4 * g + jj) * sv + li), dr[jj]);
+  };
+
+  auto step = [&](int c, Pre& f, Pre& nxt, f32x4& dr) {
+    const int64_t slot = sq.slot0 + c;
     __syncthreads();
+    // Stage the chunk first: the waits for its loads then come before this chunk's own stores.
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4) {
+      const int e = tid + kThreads * q4, t = e >> 4, r = e & 15, c8 = (e & 15) * 8;
+      *reinterpret_cast<uint4*>(&Kb[t][c8]) = f.k[q4];
+      *reinterpret_cast<uint4*>(&Qb[t][c8]) = f.q[q4];
+      const float x = kExactDy ? __uint_as_float(f.dy[q4] << 16) : __uint_as_float(f.dy[q4]);
+      const __bf16 h = (__bf16)x;
+      dYth[r][t] = h;
+      dYtl[r][t] = (__bf16)(x - (float)h);
+      const float gx = f.gt[q4] * x;
+      const __bf16 gh = (__bf16)gx;
+      GdYth[r][t] = gh;
+      GdYtl[r][t] = (__bf16)(gx - (float)gh);
+    }
+    if (tid < kC) gam[tid] = f.gam, dec[tid] = f.dec;
+    // The A operands are consumed later in the step: take them here, so their waits are here too.
+#pragma unroll
+    for (int u = 0; u < 4; ++u) asm volatile("" : "+v"(f.t[u]), "+v"(f.p[u]));
+    if (c + 1 < nch) store_dv(c + 1, dr);
     {
-      float* out = a.dsend + ((slot * a.Hv + hv) * a.Dv + row0) * Dk;
+      const auto out = buffer_rsrc(a.dsend + ((slot * a.Hv + hv) * a.Dv + row0) * Dk, 16 * Dk * 4);
 #pragma unroll
       for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) {
           const int r = 4 * g + jj, col = 32 * w + 16 * nt + li;
           const float x = dS[nt][jj];
-          out[r * Dk + col] = x;
+          BufIO<float>::st(out, uint32_t(r * Dk + col), x);
           const __bf16 h = (__bf16)x;
           dSh[r][col] = h;
           dSl[r][col] = (__bf16)(x - (float)h);
         }
     }
-#pragma unroll
-    for (int q4 = 0; q4 < 4; ++q4) {
-      const int e = tid + kThreads * q4, t = e >> 4, r = e & 15, c8 = (e & 15) * 8;
-      *reinterpret_cast<bf16x8*>(&Kb[t][c8]) = fk[q4];
-      *reinterpret_cast<bf16x8*>(&Qb[t][c8]) = fq[q4];
-      const float x = fdy[q4];
-      const __bf16 h = (__bf16)x;
-      dYth[r][t] = h;
-      dYtl[r][t] = (__bf16)(x - (float)h);
-      const float gx = fgt[q4] * x;
-      const __bf16 gh = (__bf16)gx;
-      GdYth[r][t] = gh;
-      GdYtl[r][t] = (__bf16)(gx - (float)gh);
-    }
-#pragma unroll
-    for (int u = 0; u < 4; ++u) ct[u] = ft[u], cp[u] = fp[u];
-    if (tid < kC) gam[tid] = fgam, dec[tid] = fdec;
     __syncthreads();
-    if (c > 0) prefetch(c - 1);
+    if (c > 0) prefetch(nxt, c - 1);
 
     // K dS^T for positions j = 16w..: lane -> column r = li, rows j = 16w + 4g + jj.
     f32x4 kds = zero4();
@@ -138,7 +157,7 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_state_kernel(ChunkArgs a) 
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
       if (32 * s + 31 >= 16 * w) {
-        const Split8 A{cp[2 * s], cp[2 * s + 1]};
+        const Split8 A{f.p[2 * s], f.p[2 * s + 1]};
         if constexpr (kExactDy) {
           dd = mma2(dd, A, lds8(&dYth[li][32 * s + 8 * g]));
         } else {
@@ -156,16 +175,14 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_state_kernel(ChunkArgs a) 
     __syncthreads();
 
     // dR = Tb^T dDelta for positions i = 16w.. (A = Tb^T rows i, k = j); dv = dR.
-    f32x4 dr = zero4();
+    dr = zero4();
 #pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      dr = mma3(dr, Split8{ct[2 * s], ct[2 * s + 1]}, Split8{lds8(&dDth[li][32 * s + 8 * g]), lds8(&dDtl[li][32 * s + 8 * g])});
-    }
-    OutT* dvb = dv + tok * sv + hv * a.Dv + row0 + li;
+    for (int s = 0; s < 2; ++s)
+      dr = mma3(dr, Split8{f.t[2 * s], f.t[2 * s + 1]},
+                Split8{lds8(&dDth[li][32 * s + 8 * g]), lds8(&dDtl[li][32 * s + 8 * g])});
 #pragma unroll
     for (int jj = 0; jj < 4; ++jj) {
       const int i = 16 * w + 4 * g + jj;
-      if (i < L) IO<OutT>::st(dvb, int64_t(i) * sv, dr[jj]);
       const float x = -gam[i] * dr[jj];
       const __bf16 h = (__bf16)x;
       GdRth[li][i] = h;
@@ -189,7 +206,17 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_state_kernel(ChunkArgs a) 
         dS[nt] = mma2(dS[nt], Split8{lds8(&GdRth[li][32 * s + 8 * g]), lds8(&GdRtl[li][32 * s + 8 * g])}, bk);
       }
     }
+  };
+
+  // Two register sets in turn: chunk c computes from one while chunk c - 1 loads into the other.
+  Pre pa, pb;
+  f32x4 dr = zero4();
+  if (nch > 0) prefetch(pa, nch - 1);
+  for (int c = nch - 1; c >= 0; c -= 2) {
+    step(c, pa, pb, dr);
+    if (c > 0) step(c - 1, pb, pa, dr);
   }
+  if (nch > 0) store_dv(0, dr);
   if (a.ds0) {
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt)

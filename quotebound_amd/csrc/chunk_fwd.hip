@@ -8,7 +8,7 @@
 //   Y = diag(exp G) QS + P Delta
 // Tb and P come ready from the prep kernel (each wave loads its rows as MFMA A operands). All products run on v_mfma_f32_16x16x32_bf16; float32 operands (S, R,
 // Delta, Tb, P) are split into bf16 hi + lo pairs so the state keeps float32 accuracy, while k, q, v enter exactly.
-// The next chunk's tiles are loaded into registers while the current chunk computes.
+// The next chunk's inputs are loaded into registers while the current chunk computes.
 #include "chunk_common.h"
 #include "chunk_kernels.h"
 
@@ -47,69 +47,82 @@ __global__ __launch_bounds__(kThreads) void chunk_fwd_kernel(ChunkArgs a) {
       S[nt][jj] = a.s0 ? a.s0[((int64_t(n) * a.Hv + hv) * a.Dv + row0 + 4 * g + jj) * Dk + 32 * w + 16 * nt + li]
                        : 0.f;
 
-  // Registers holding the next chunk: k and q rows (thread e of [0, 1024) in steps of 256 covers row e / 16,
-  // columns 8 (e % 16)), v, exp G, D, and the wave's A operands: Tb rows 16w + li and P rows 16w + li (k = 8g..,
-  // two k steps, hi and lo).
-  bf16x8 fk[4], fq[4], ft[4], fp[4], ct[4], cp[4];
-  float fv[4], fgam = 0.f, fdec = 0.f;
-  auto prefetch = [&](int c) {
+  // One chunk's inputs, loaded into registers a chunk ahead: k and q rows (thread e of [0, 1024) in steps of 256
+  // covers row e / 16, columns 8 (e % 16)), v (row e / 16, state row e % 16), exp G, D, and the wave's A operands,
+  // Tb rows 16w + li and P rows 16w + li (k = 8g.., two k steps, hi and lo). k, q, v are read through buffer
+  // resources that end at the sequence's last row, so rows past it read as zeros without a branch.
+  struct Pre {
+    uint4 k[4], q[4];
+    bf16x8 t[4], p[4];
+    uint16_t v[4];
+    float gam, dec;
+  };
+  auto prefetch = [&](Pre& f, int c) {
     const int64_t slot = sq.slot0 + c, tok = sq.tok0 + int64_t(c) * kC;
-    const int L = min(kC, sq.len - c * kC);
-    const bf16_t* kb = a.k + tok * sk + hk * Dk;
-    const bf16_t* qb = a.q + tok * sk + hk * Dk;
-    const bf16_t* vb = a.v + tok * sv + hv * a.Dv + row0;
+    const uint32_t L = uint32_t(min(kC, sq.len - c * kC));
+    const auto kr = buffer_rsrc(a.k + tok * sk + hk * Dk, L * sk * 2);
+    const auto qr = buffer_rsrc(a.q + tok * sk + hk * Dk, L * sk * 2);
+    const auto vr = buffer_rsrc(a.v + tok * sv + hv * a.Dv + row0, L * sv * 2);
+    const Tile* tl = a.tiles + (slot * a.Hv + hv);
+    f.gam = tl->gam[tid & (kC - 1)], f.dec = tl->dec[tid & (kC - 1)];
 #pragma unroll
     for (int q4 = 0; q4 < 4; ++q4) {
       const int e = tid + kThreads * q4, t = e >> 4, c8 = (e & 15) * 8;
-      if (t < L) {
-        fk[q4] = gld8(kb + t * sk + c8);
-        fq[q4] = gld8(qb + t * sk + c8);
-      } else {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) fk[q4][j] = fq[q4][j] = (__bf16)0.f;
-      }
-      fv[q4] = t < L ? bf16_to_f32(vb[t * sv + (e & 15)]) : 0.f;
+      f.k[q4] = buf_ld16(kr, uint32_t(t * sk + c8) * 2);
+      f.q[q4] = buf_ld16(qr, uint32_t(t * sk + c8) * 2);
+      f.v[q4] = buf_ld2(vr, uint32_t(t * sv + (e & 15)) * 2);
     }
-    const Tile* tl = a.tiles + (slot * a.Hv + hv);
     const int ar = (16 * w + li) * kC + 8 * g;
-    ft[0] = gld8(tl->tb_hi + ar), ft[1] = gld8(tl->tb_lo + ar), ft[2] = gld8(tl->tb_hi + ar + 32),
-    ft[3] = gld8(tl->tb_lo + ar + 32);
-    fp[0] = gld8(tl->p_hi + ar), fp[1] = gld8(tl->p_lo + ar), fp[2] = gld8(tl->p_hi + ar + 32),
-    fp[3] = gld8(tl->p_lo + ar + 32);
-    if (tid < kC) fgam = tl->gam[tid], fdec = tl->dec[tid];
+    f.t[0] = gld8(tl->tb_hi + ar), f.t[1] = gld8(tl->tb_lo + ar), f.t[2] = gld8(tl->tb_hi + ar + 32),
+    f.t[3] = gld8(tl->tb_lo + ar + 32);
+    f.p[0] = gld8(tl->p_hi + ar), f.p[1] = gld8(tl->p_lo + ar), f.p[2] = gld8(tl->p_hi + ar + 32),
+    f.p[3] = gld8(tl->p_lo + ar + 32);
   };
-  if (nch > 0) prefetch(0);
 
-  for (int c = 0; c < nch; ++c) {
-    const int64_t slot = sq.slot0 + c, tok = sq.tok0 + int64_t(c) * kC;
-    const int L = min(kC, sq.len - c * kC);
+  // y of a chunk is stored during the next chunk (after that chunk's inputs are staged), so no wait for the
+  // staged loads ever covers these stores.
+  auto store_y = [&](int c, const f32x4& yacc) {
+    const int64_t tok = sq.tok0 + int64_t(c) * kC;
+    const uint32_t L = uint32_t(min(kC, sq.len - c * kC));
+    // Rows i >= L fall past the resource and are dropped.
+    const auto yr = buffer_rsrc(y + tok * sv + hv * a.Dv + row0, L * sv * uint32_t(sizeof(OutT)));
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) BufIO<OutT>::st(yr, uint32_t((16 * w + 4 * g + jj) * sv + li), yacc[jj]);
+  };
+
+  auto step = [&](int c, Pre& f, Pre& nxt, f32x4& yacc) {
+    const int64_t slot = sq.slot0 + c;
     __syncthreads();  // the previous chunk's readers of LDS are done
+    // Stage the chunk first: the waits for its loads then come before this chunk's own stores.
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4) {
+      const int e = tid + kThreads * q4, t = e >> 4, c8 = (e & 15) * 8;
+      *reinterpret_cast<uint4*>(&Kb[t][c8]) = f.k[q4];
+      *reinterpret_cast<uint4*>(&Qb[t][c8]) = f.q[q4];
+      Vs[t][e & 15] = bf16_to_f32(f.v[q4]);
+    }
+    if (tid < kC) gam[tid] = f.gam, dec[tid] = f.dec;
+    // The A operands are consumed later in the step: take them here, so their waits are here too.
+#pragma unroll
+    for (int u = 0; u < 4; ++u) asm volatile("" : "+v"(f.t[u]), "+v"(f.p[u]));
+    if (c > 0) store_y(c - 1, yacc);
     {
-      float* ck = a.ckpt ? a.ckpt + ((slot * a.Hv + hv) * a.Dv + row0) * Dk : nullptr;
+      const auto ck = a.ckpt ? buffer_rsrc(a.ckpt + ((slot * a.Hv + hv) * a.Dv + row0) * Dk, 16 * Dk * 4)
+                             : buffer_rsrc(a.s0, 0);
 #pragma unroll
       for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) {
           const int r = 4 * g + jj, col = 32 * w + 16 * nt + li;
           const float x = S[nt][jj];
-          if (ck) ck[r * Dk + col] = x;
+          BufIO<float>::st(ck, uint32_t(r * Dk + col), x);
           const __bf16 h = (__bf16)x;
           Sh[r][col] = h;
           Sl[r][col] = (__bf16)(x - (float)h);
         }
     }
-#pragma unroll
-    for (int q4 = 0; q4 < 4; ++q4) {
-      const int e = tid + kThreads * q4, t = e >> 4, c8 = (e & 15) * 8;
-      *reinterpret_cast<bf16x8*>(&Kb[t][c8]) = fk[q4];
-      *reinterpret_cast<bf16x8*>(&Qb[t][c8]) = fq[q4];
-      Vs[t][e & 15] = fv[q4];
-    }
-#pragma unroll
-    for (int u = 0; u < 4; ++u) ct[u] = ft[u], cp[u] = fp[u];
-    if (tid < kC) gam[tid] = fgam, dec[tid] = fdec;
     __syncthreads();
-    if (c + 1 < nch) prefetch(c + 1);
+    if (c + 1 < nch) prefetch(nxt, c + 1);
 
     // KS, QS for positions 16w..: lane -> column r = li, rows i = 16w + 4g + jj.
     f32x4 ks = zero4(), qs = zero4();
@@ -135,7 +148,7 @@ __global__ __launch_bounds__(kThreads) void chunk_fwd_kernel(ChunkArgs a) {
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
       const Split8 B{lds8(&Rth[li][32 * s + 8 * g]), lds8(&Rtl[li][32 * s + 8 * g])};
-      dl = mma3(dl, Split8{ct[2 * s], ct[2 * s + 1]}, B);
+      dl = mma3(dl, Split8{f.t[2 * s], f.t[2 * s + 1]}, B);
     }
 #pragma unroll
     for (int jj = 0; jj < 4; ++jj) {
@@ -166,24 +179,27 @@ __global__ __launch_bounds__(kThreads) void chunk_fwd_kernel(ChunkArgs a) {
       }
     }
 
-    // Y = diag(exp G) QS + P Delta for positions i = 16w.. (P rows from the tile; zero above the diagonal).
-    f32x4 yacc;
+    // Y = diag(exp G) QS + P Delta for positions i = 16w.. (P is zero above the diagonal).
 #pragma unroll
     for (int jj = 0; jj < 4; ++jj) yacc[jj] = gam[16 * w + 4 * g + jj] * qs[jj];
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
       if (32 * s <= 16 * w + 15) {
         const Split8 B{lds8(&Dth[li][32 * s + 8 * g]), lds8(&Dtl[li][32 * s + 8 * g])};
-        yacc = mma3(yacc, Split8{cp[2 * s], cp[2 * s + 1]}, B);
+        yacc = mma3(yacc, Split8{f.p[2 * s], f.p[2 * s + 1]}, B);
       }
     }
-    OutT* yb = y + tok * sv + hv * a.Dv + row0 + li;
-#pragma unroll
-    for (int jj = 0; jj < 4; ++jj) {
-      const int i = 16 * w + 4 * g + jj;
-      if (i < L) IO<OutT>::st(yb, int64_t(i) * sv, yacc[jj]);
-    }
+  };
+
+  // Two register sets in turn: chunk c computes from one while chunk c + 1 loads into the other.
+  Pre pa, pb;
+  f32x4 yacc = zero4();
+  if (nch > 0) prefetch(pa, 0);
+  for (int c = 0; c < nch; c += 2) {
+    step(c, pa, pb, yacc);
+    if (c + 1 < nch) step(c + 1, pb, pa, yacc);
   }
+  if (nch > 0) store_y(nch - 1, yacc);
   if (a.s_out) {
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt)

@@ -49,6 +49,41 @@ struct IO<bf16_t> {
   }
 };
 
+// ---- buffer stores -----------------------------------------------------------------------------------------------
+// A raw buffer resource over [base, base + bytes): vector stores at byte offsets past the range are dropped by the
+// hardware. Masked stores of a tile's last rows then need no branch, which keeps the compiler's count of outstanding
+// memory operations exact (a branch around a store makes it wait for every load in flight). bytes == 0 drops every
+// store. Word 3 is the untyped-buffer format word of CDNA (32-bit data format).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, int(bytes), 0x00020000);
+}
+// Loads at byte offsets past the range return zeros.
+__device__ __forceinline__ uint4 buf_ld16(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, int(byte_off), 0, 0);
+  return uint4{v[0], v[1], v[2], v[3]};
+}
+__device__ __forceinline__ uint16_t buf_ld2(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+  return __builtin_amdgcn_raw_buffer_load_b16(r, int(byte_off), 0, 0);
+}
+__device__ __forceinline__ float buf_ld4(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+  return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, int(byte_off), 0, 0));
+}
+
+template <typename T>
+struct BufIO;
+template <>
+struct BufIO<float> {
+  static __device__ __forceinline__ void st(__amdgpu_buffer_rsrc_t r, uint32_t i, float x) {
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x), r, int(i * 4), 0, 0);
+  }
+};
+template <>
+struct BufIO<bf16_t> {
+  static __device__ __forceinline__ void st(__amdgpu_buffer_rsrc_t r, uint32_t i, float x) {
+    __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16(x), r, int(i * 2), 0, 0);
+  }
+};
+
 // ---- lane reductions ------------------------------------------------------------------------------------------
 // DPP controls (gfx9 encoding): quad_perm, row_mirror, row_half_mirror.
 template <int CTRL>
