@@ -1,0 +1,18 @@
+// The recurrence dispatcher with the reference's signature (src/deltanet.h:17-19, src/deltanet.cpp:49-61), on
+// qb::array and the HIP kernels of qb_gdn.h.
+//   q, k [B, T, Hk, Dk]; v [B, T, Hv, Dv]; g, beta [B, T, Hv]; state [B, Hv, Dv, Dk] float32.
+// Per value head and step: S~ = g S; u = S~ k; delta = beta (v - u); S = S~ + delta k^T; y = S q. Arithmetic is
+// float32; y comes back in q's dtype and the final state in float32, as in the reference. g is the decay factor
+// and is never rounded to bfloat16. train selects the trainable op, whose forward is the same computation.
+// Throws std::runtime_error naming the offending shapes when the kernels cannot run them.
+#pragma once
+#include <utility>
+
+#include "qb/array.h"
+
+namespace qb {
+
+std::pair<array, array> gated_delta(const array& q, const array& k, const array& v, const array& g,
+                                    const array& beta, const array& state, bool train = false);
+
+}  // namespace qb

@@ -1,0 +1,249 @@
+// The C++ adapters of include/qb: qb::array and the reference's entry points gated_delta (src/deltanet.cpp:49-61),
+// gated_delta_trainable and gated_delta_vjp (src/delta_grad.cpp:155-212) on top of the C ABI of qb_gdn.h.
+// A failed ABI call (-1 and a message) becomes std::runtime_error with that message, as the reference throws.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <stdexcept>
+#include <string>
+
+#include "gdn_common.h"
+#include "qb/delta_grad.h"
+#include "qb/deltanet.h"
+#include "qb_gdn.h"
+
+namespace qb {
+namespace {
+
+void* g_stream = nullptr;
+
+hipStream_t cur() { return static_cast<hipStream_t>(g_stream); }
+
+void check(hipError_t e, const char* what) {
+  if (e != hipSuccess) throw std::runtime_error(std::string("gated delta: ") + what + ": " + hipGetErrorString(e));
+}
+
+void* device_alloc(size_t bytes) {
+  void* p = nullptr;
+  if (bytes) check(hipMalloc(&p, bytes), "hipMalloc");
+  return p;
+}
+
+std::string shape_str(const Shape& s) {
+  std::string r = "[";
+  for (size_t i = 0; i < s.size(); ++i) r += (i ? ", " : "") + std::to_string(s[i]);
+  return r + "]";
+}
+
+__global__ void cast_kernel(const void* src, void* dst, int64_t n, int to_bf16) {
+  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  if (to_bf16)
+    static_cast<qbgdn::bf16_t*>(dst)[i] = qbgdn::f32_to_bf16(static_cast<const float*>(src)[i]);
+  else
+    static_cast<float*>(dst)[i] = qbgdn::bf16_to_f32(static_cast<const qbgdn::bf16_t*>(src)[i]);
+}
+
+// A fill kernel rather than hipMemsetAsync, which must not be recorded into graphs a caller may capture.
+__global__ void zero_kernel(uint32_t* dst, int64_t n) {
+  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n) dst[i] = 0u;
+}
+
+// Scratch device memory for one call, released in stream order.
+struct Scratch {
+  void* p = nullptr;
+  explicit Scratch(size_t bytes) {
+    if (bytes) check(hipMallocAsync(&p, bytes, cur()), "hipMallocAsync");
+  }
+  ~Scratch() {
+    if (p) (void)hipFreeAsync(p, cur());
+  }
+  Scratch(const Scratch&) = delete;
+  Scratch& operator=(const Scratch&) = delete;
+};
+
+// The design the adapters run: the chunked one where the library supports the shape, else the recurrent one.
+int pick_design(qb_gdn_desc d) {
+  char err[16];
+  d.design = QB_GDN_CHUNKED;
+  if (qb_gdn_validate(&d, err, sizeof err) == 0) return QB_GDN_CHUNKED;
+  return QB_GDN_RECURRENT;
+}
+
+// Shapes of one call, checked against each other; the messages name every shape, as the reference's do.
+struct Problem {
+  int B, T, Hk, Dk, Hv, Dv;
+};
+
+Problem check_shapes(const char* who, const array& q, const array& k, const array& v, const array& g,
+                     const array& beta, const array& state) {
+  auto fail = [&](const std::string& why) {
+    throw std::runtime_error(std::string(who) + ": " + why + " (q " + shape_str(q.shape()) + ", k " +
+                             shape_str(k.shape()) + ", v " + shape_str(v.shape()) + ", g " + shape_str(g.shape()) +
+                             ", beta " + shape_str(beta.shape()) + ", state " + shape_str(state.shape()) + ")");
+  };
+  if (q.ndim() != 4 || k.ndim() != 4 || v.ndim() != 4 || g.ndim() != 3 || beta.ndim() != 3 || state.ndim() != 4)
+    fail("q, k, v, state need 4 dimensions and g, beta 3");
+  const Problem p{q.shape(0), q.shape(1), q.shape(2), q.shape(3), v.shape(2), v.shape(3)};
+  if (k.shape() != q.shape()) fail("k must have q's shape");
+  if (v.shape(0) != p.B || v.shape(1) != p.T) fail("v must match q in batch and time");
+  const Shape bth{p.B, p.T, p.Hv};
+  if (g.shape() != bth || beta.shape() != bth) fail("g and beta must be [B, T, Hv]");
+  if (state.shape() != Shape{p.B, p.Hv, p.Dv, p.Dk}) fail("state must be [B, Hv, Dv, Dk]");
+  return p;
+}
+
+qb_gdn_desc make_desc(const Problem& p, Dtype io, bool out_f32) {
+  qb_gdn_desc d{};
+  d.B = p.B, d.T = p.T, d.Hk = p.Hk, d.Hv = p.Hv, d.Dk = p.Dk, d.Dv = p.Dv;
+  d.chunk = 64;
+  d.dtype = int(io);
+  d.g_is_log = 0;  // the reference's decay factor; the library takes logs and returns dL/dg
+  d.out_f32 = out_f32 ? 1 : 0;
+  d.design = pick_design(d);
+  return d;
+}
+
+// The ABI's element type for q, k, v, beta: bfloat16 when all four are, else float32 (the reference computes in
+// float32 whatever it is fed, src/deltanet.cpp:54).
+Dtype io_dtype(const array& q, const array& k, const array& v, const array& beta) {
+  const bool bf = q.dtype() == bfloat16 && k.dtype() == bfloat16 && v.dtype() == bfloat16 &&
+                  beta.dtype() == bfloat16;
+  return bf ? bfloat16 : float32;
+}
+
+// Forward through the ABI; ckpt may be null.
+void run_fwd(const qb_gdn_desc& d, const array& q, const array& k, const array& v, const array& g,
+             const array& beta, const array& s0, array& y, array& s_out, float* ckpt) {
+  Scratch ws(qb_gdn_workspace_bytes(&d));
+  char err[512];
+  if (qb_gdn_fwd(&d, q.data(), k.data(), v.data(), static_cast<const float*>(g.data()), beta.data(),
+                 static_cast<const float*>(s0.data()), y.data(), static_cast<float*>(s_out.data()), ckpt, ws.p,
+                 g_stream, err, sizeof err) != 0)
+    throw std::runtime_error(err);
+}
+
+}  // namespace
+
+size_t size_of(Dtype dtype) { return dtype == bfloat16 ? 2 : 4; }
+
+array::array(Shape shape, Dtype dtype) : shape_(std::move(shape)), dtype_(dtype) {
+  for (int s : shape_)
+    if (s < 0) throw std::runtime_error("qb::array: negative dimension in " + shape_str(shape_));
+  buf_ = std::shared_ptr<void>(device_alloc(std::max<size_t>((nbytes() + 3) / 4 * 4, 4)),
+                               [](void* p) { (void)hipFree(p); });
+}
+
+array array::from_host(const void* data, Shape shape, Dtype dtype) {
+  array a(std::move(shape), dtype);
+  check(hipMemcpyAsync(a.data(), data, a.nbytes(), hipMemcpyHostToDevice, cur()), "hipMemcpyAsync");
+  check(hipStreamSynchronize(cur()), "hipStreamSynchronize");
+  return a;
+}
+
+array array::zeros(Shape shape, Dtype dtype) {
+  array a(std::move(shape), dtype);
+  const int64_t words = int64_t((a.nbytes() + 3) / 4);  // the buffer is at least 4-byte aligned and padded
+  if (words) {
+    hipLaunchKernelGGL(zero_kernel, dim3(unsigned((words + 255) / 256)), dim3(256), 0, cur(),
+                       static_cast<uint32_t*>(a.data()), words);
+    check(hipGetLastError(), "zero kernel");
+  }
+  return a;
+}
+
+void array::to_host(void* dst) const {
+  check(hipMemcpyAsync(dst, data(), nbytes(), hipMemcpyDeviceToHost, cur()), "hipMemcpyAsync");
+  check(hipStreamSynchronize(cur()), "hipStreamSynchronize");
+}
+
+int array::shape(int dim) const {
+  const int n = ndim();
+  if (dim < -n || dim >= n) throw std::runtime_error("qb::array: dimension " + std::to_string(dim) + " of " +
+                                                     shape_str(shape_));
+  return shape_[dim < 0 ? dim + n : dim];
+}
+
+size_t array::size() const {
+  size_t n = 1;
+  for (int s : shape_) n *= size_t(s);
+  return n;
+}
+
+array astype(const array& x, Dtype dtype) {
+  if (x.dtype() == dtype) return x;
+  array r(x.shape(), dtype);
+  const int64_t n = int64_t(x.size());
+  if (n) {
+    hipLaunchKernelGGL(cast_kernel, dim3(unsigned((n + 255) / 256)), dim3(256), 0, cur(), x.data(), r.data(), n,
+                       dtype == bfloat16 ? 1 : 0);
+    check(hipGetLastError(), "cast kernel");
+  }
+  return r;
+}
+
+void set_stream(void* s) { g_stream = s; }
+void* stream() { return g_stream; }
+
+std::pair<array, array> gated_delta_trainable(const array& q, const array& k, const array& v, const array& g,
+                                              const array& beta, const array& state) {
+  const Problem p = check_shapes("gated delta", q, k, v, g, beta, state);
+  const Dtype io = io_dtype(q, k, v, beta);
+  const qb_gdn_desc d = make_desc(p, io, false);
+  array y({p.B, p.T, p.Hv, p.Dv}, io), s_out({p.B, p.Hv, p.Dv, p.Dk}, float32);
+  run_fwd(d, astype(q, io), astype(k, io), astype(v, io), astype(g, float32), astype(beta, io),
+          astype(state, float32), y, s_out, nullptr);
+  return {y, s_out};
+}
+
+std::pair<array, array> gated_delta(const array& q, const array& k, const array& v, const array& g,
+                                    const array& beta, const array& state, bool train) {
+  // The trainable op's forward is the same computation (src/deltanet.cpp:55-60); y returns in q's dtype.
+  (void)train;
+  auto [y, s] = gated_delta_trainable(q, k, v, g, beta, state);
+  return {astype(y, q.dtype()), s};
+}
+
+std::vector<array> gated_delta_vjp(const std::vector<array>& in, const array& dy, const array& dstate) {
+  if (in.size() != 6)
+    throw std::runtime_error("gated delta backward: needs 6 primals (q, k, v, g, beta, state), got " +
+                             std::to_string(in.size()));
+  const array &q = in[0], &k = in[1], &v = in[2], &g = in[3], &beta = in[4], &state = in[5];
+  const Problem p = check_shapes("gated delta backward", q, k, v, g, beta, state);
+  if (dy.shape() != Shape{p.B, p.T, p.Hv, p.Dv})
+    throw std::runtime_error("gated delta backward: dy must be " + shape_str({p.B, p.T, p.Hv, p.Dv}) + ", got " +
+                             shape_str(dy.shape()));
+  if (!dstate.empty() && dstate.shape() != state.shape())
+    throw std::runtime_error("gated delta backward: dstate must be " + shape_str(state.shape()) + ", got " +
+                             shape_str(dstate.shape()));
+  const Dtype io = io_dtype(q, k, v, beta);
+  // Cotangents in float32 unless every tensor of the output side is bfloat16.
+  const bool out_f32 = io == float32 || dy.dtype() == float32;
+  const Dtype od = out_f32 ? float32 : bfloat16;
+  const qb_gdn_desc d = make_desc(p, io, out_f32);
+  const array qi = astype(q, io), ki = astype(k, io), vi = astype(v, io), bi = astype(beta, io);
+  const array gi = astype(g, float32), s0 = astype(state, float32);
+
+  // The chunk-start states from the forward itself (the reference rebuilds them, src/delta_grad.cpp:172-181).
+  Scratch ckpt(qb_gdn_ckpt_bytes(&d));
+  {
+    array y({p.B, p.T, p.Hv, p.Dv}, od), s_out({p.B, p.Hv, p.Dv, p.Dk}, float32);
+    run_fwd(d, qi, ki, vi, gi, bi, s0, y, s_out, static_cast<float*>(ckpt.p));
+  }
+  const array dyi = astype(dy, od);
+  const array dsi = dstate.empty() ? array() : astype(dstate, float32);
+  array dq({p.B, p.T, p.Hk, p.Dk}, od), dk({p.B, p.T, p.Hk, p.Dk}, od), dv({p.B, p.T, p.Hv, p.Dv}, od);
+  array dg({p.B, p.T, p.Hv}, float32), db({p.B, p.T, p.Hv}, od), ds0({p.B, p.Hv, p.Dv, p.Dk}, float32);
+  Scratch ws(qb_gdn_workspace_bytes(&d));
+  char err[512];
+  if (qb_gdn_bwd(&d, qi.data(), ki.data(), vi.data(), static_cast<const float*>(gi.data()), bi.data(),
+                 static_cast<const float*>(ckpt.p), dyi.data(), static_cast<const float*>(dsi.data()), dq.data(),
+                 dk.data(), dv.data(), static_cast<float*>(dg.data()), db.data(), static_cast<float*>(ds0.data()),
+                 ws.p, g_stream, err, sizeof err) != 0)
+    throw std::runtime_error(err);
+  return {astype(dq, q.dtype()), astype(dk, k.dtype()),  astype(dv, v.dtype()),
+          astype(dg, g.dtype()), astype(db, beta.dtype()), astype(ds0, state.dtype())};
+}
+
+}  // namespace qb

@@ -17,7 +17,7 @@ import torch
 
 from . import _lib
 
-DEFAULT_DESIGN = _lib.CHUNKED
+DEFAULT_DESIGN = None  # the chunked design where the library supports the shape, else the recurrent one
 
 
 def _dev_ptr(t):
@@ -43,8 +43,15 @@ def _prep(q, k, v, g, beta, dtype):
 def _desc(q, v, dtype, g_is_log, design, cu_seqlens, out_f32):
     B, T, Hk, Dk = q.shape
     Hv, Dv = v.shape[2], v.shape[3]
-    return _lib.make_desc(B, T, Hk, Hv, Dk, Dv, dtype=_lib.BF16 if dtype == torch.bfloat16 else _lib.F32,
-                          g_is_log=g_is_log, design=design, cu_seqlens=cu_seqlens, out_f32=out_f32)
+    make = lambda d: _lib.make_desc(B, T, Hk, Hv, Dk, Dv,  # noqa: E731
+                                    dtype=_lib.BF16 if dtype == torch.bfloat16 else _lib.F32, g_is_log=g_is_log,
+                                    design=d, cu_seqlens=cu_seqlens, out_f32=out_f32)
+    if design is None:
+        desc, keep = make(_lib.CHUNKED)
+        if not _lib.validate(desc):
+            return desc, keep
+        design = _lib.RECURRENT
+    return make(design)
 
 
 def _workspace(desc, device):
