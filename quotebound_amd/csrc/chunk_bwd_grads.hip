@@ -13,7 +13,9 @@
 //   dbeta_j = sum_i dTb_ij T_ij + sum_m dA_jm E_jm (K K^T)_jm,  dG from every exp(.) factor, dg = reverse cumsum
 // (tests/chunk_math.py restates these equations and checks them against the oracle.) Wave w owns positions
 // 16 (w % 4) .. + 15 and, within each product, the half w / 4 of the other index (state rows of a 32-row block,
-// key-position tiles, or 64 of the 128 columns). MFMA with split float32 operands as in the forward.
+// key-position tiles, or 64 of the 128 columns). MFMA with split float32 operands as in the forward. Each
+// intermediate crosses between waves through LDS once, written as 8-byte vectors and read either directly or with
+// gfx950's transposing LDS read, whichever index the consuming product reduces over.
 #include <type_traits>
 
 #include "chunk_common.h"
@@ -23,43 +25,38 @@ namespace qbgdn {
 namespace {
 
 constexpr int kThreads = 512;
-constexpr int Dk_ = 128;
-constexpr int kLDK = 128 + kPadB;  // bf16 [.][128] rows
-constexpr int kLDC = kC + kPadB;   // bf16 [.][64] rows
-constexpr int kLDR = 40;           // bf16 [.][32] rows, padded
-constexpr int kLDN = 32;           // bf16 [.][32] rows, packed
-constexpr int kLDF = kC + 1;       // f32 [.][64] rows
-
-// Block-loop region (bf16 element offsets).
-constexpr int oS0h = 0, oS0l = oS0h + 32 * kLDK;
-constexpr int oS0th = oS0l + 32 * kLDK, oS0tl = oS0th + 128 * kLDR;
-constexpr int odSh = oS0tl + 128 * kLDR, odSl = odSh + 32 * kLDK;
-constexpr int odSth = odSl + 32 * kLDK, odStl = odSth + 128 * kLDR;
-constexpr int odYth = odStl + 128 * kLDR, odYtl = odYth + 32 * kLDC;
-constexpr int oRth = odYtl + 32 * kLDC, oRtl = oRth + 32 * kLDC;
-constexpr int oRmh = oRtl + 32 * kLDC, oRml = oRmh + kC * kLDN;
-constexpr int oDmh = oRml + kC * kLDN, oDml = oDmh + kC * kLDN;
-constexpr int oDDmh = oDml + kC * kLDN, oDDml = oDDmh + kC * kLDN;
-constexpr int odDth = oDDml + kC * kLDN, odDtl = odDth + 32 * kLDC;
-constexpr int odDmh = odDtl + 32 * kLDC, odDml = odDmh + kC * kLDN;
-constexpr int oGdRh = odDml + kC * kLDN, oGdRl = oGdRh + kC * kLDN;
-constexpr int kLoopBytes = (oGdRl + kC * kLDN) * 2;
-// End-phase region (aliases the block-loop region): bf16 K (rows), K^T and Q^T ([column][position]) then f32
-// 64 x 64 matrices.
-constexpr int eKb = 0, eKt = kC * kLDK, eQt = eKt + Dk_ * kLDC;  // bf16 offsets
-constexpr int eF = (eQt + Dk_ * kLDC) / 2;                       // first f32 offset
+// Block-loop region (bf16 element offsets), one 32-row block of the state at a time. Every matrix is stored once, as
+// hi and lo halves: S0, dS as rows [r][c]; dY as rows [i][r]; the per-position results as [r][i]. Products that
+// reduce over the contiguous index read 16 bytes per lane; those that reduce over the other index use the
+// transposing read (lds_tr8). The row strides put the four rows each transposing read touches, and the eight rows
+// each 16-byte read touches, on distinct banks.
+constexpr int kLS = 144;  // S0, dS [32][128]
+constexpr int kLY = 48;   // dY [64][32]
+constexpr int kLP = 72;   // [32][64]
+constexpr int oS0h = 0, oS0l = oS0h + 32 * kLS, odSh = oS0l + 32 * kLS, odSl = odSh + 32 * kLS;
+constexpr int odYh = odSl + 32 * kLS, odYl = odYh + kC * kLY;
+constexpr int oRh = odYl + kC * kLY, oRl = oRh + 32 * kLP;        // R = V - diag(exp G) K S0^T
+constexpr int oDh = oRl + 32 * kLP, oDl = oDh + 32 * kLP;         // Delta
+constexpr int oDDh = oDl + 32 * kLP, oDDl = oDDh + 32 * kLP;      // D Delta
+constexpr int odDh = oDDl + 32 * kLP, odDl = odDh + 32 * kLP;     // dDelta
+constexpr int oGdRh = odDl + 32 * kLP, oGdRl = oGdRh + 32 * kLP;  // -diag(exp G) dR
+constexpr int kLoopBytes = (oGdRl + 32 * kLP) * 2;
+// End-phase region (aliases the block-loop region): bf16 K and Q rows, then f32 64 x 64 matrices.
+constexpr int kLK = 144;
+constexpr int eKb = 0, eQb = kC * kLK;   // bf16 offsets
+constexpr int eF = (2 * kC * kLK) / 2;  // first f32 offset
+constexpr int kLDF = kC + 1;            // f32 [.][64] rows
 constexpr int edP = eF, edTb = edP + kC * kLDF, eT = edTb + kC * kLDF;
 constexpr int eKK = eT + kC * kLDF, eZt = eKK + kC * kLDF;
 constexpr int kEndBytes = (eZt + kC * kLDF) * 4;
 constexpr int kSmemBytes = kLoopBytes > kEndBytes ? kLoopBytes : kEndBytes;
 
-__device__ __forceinline__ void put_split(__bf16* hi, __bf16* lo, int at, float x) {
-  const __bf16 h = (__bf16)x;
-  hi[at] = h;
-  lo[at] = (__bf16)(x - (float)h);
+// Four consecutive values at element offset at (a multiple of 4) of the hi and lo matrices.
+__device__ __forceinline__ void put4(__bf16* hi, __bf16* lo, int at, float x0, float x1, float x2, float x3) {
+  const Split4 v = split4(x0, x1, x2, x3);
+  *reinterpret_cast<uint2*>(hi + at) = v.hi;
+  *reinterpret_cast<uint2*>(lo + at) = v.lo;
 }
-
-__device__ __forceinline__ __bf16 as_bf(bf16_t b) { return __builtin_bit_cast(__bf16, b); }
 
 template <typename OutT>
 __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) {
@@ -126,22 +123,22 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
       const float* dsb = a.dsend + rows0;
       const auto yr = buffer_rsrc(dy + (tok * a.Hv + hv) * a.Dv + r0, uint32_t(L * sv) * uint32_t(sizeof(OutT)));
       const auto vr = buffer_rsrc(a.v + (tok * a.Hv + hv) * a.Dv + r0, uint32_t(L * sv) * 2u);
-      // S0 and dS: thread -> column c = tid % 128, rows 8 (tid / 128) .. + 7.
-      const int cc = lt & 127, rg = 8 * (lt >> 7);
-      float xs[8], ys[8];
+      // S0 and dS: thread -> row tid / 16, columns 8 (tid % 16) .. + 7.
+      const int sr = lt >> 4, sc = (lt & 15) * 8;
+      float4 xs[2], ys[2];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) xs[u] = s0b[(rg + u) * Dk + cc], ys[u] = dsb[(rg + u) * Dk + cc];
-      // dY^T: thread -> position tid / 8, rows 4 (tid % 8) ..; the wave's own dY rows (i = ip, r = 8g..).
+      for (int q = 0; q < 2; ++q) {
+        xs[q] = *reinterpret_cast<const float4*>(s0b + sr * Dk + sc + 4 * q);
+        ys[q] = *reinterpret_cast<const float4*>(dsb + sr * Dk + sc + 4 * q);
+      }
+      // dY: thread -> position tid / 8, rows 4 (tid % 8) .. + 3.
       const int iy = lt >> 3, r4 = (lt & 7) * 4;
-      uint4 yT, yo[2];
+      uint4 yraw;
       if constexpr (kExactDy) {
         const auto t2 = __builtin_amdgcn_raw_buffer_load_b64(yr, int(uint32_t(iy * sv + r4) * 2), 0, 0);
-        yT = uint4{t2[0], t2[1], 0u, 0u};
-        yo[0] = buf_ld16(yr, uint32_t(ip * sv + 8 * g) * 2);
+        yraw = uint4{t2[0], t2[1], 0u, 0u};
       } else {
-        yT = buf_ld16(yr, uint32_t(iy * sv + r4) * 4);
-        yo[0] = buf_ld16(yr, uint32_t(ip * sv + 8 * g) * 4);
-        yo[1] = buf_ld16(yr, uint32_t(ip * sv + 8 * g) * 4 + 16);
+        yraw = buf_ld16(yr, uint32_t(iy * sv + r4) * 4);
       }
       // v at the wave's accumulator positions (rows i = 16 pw + 4g + jj, column r = 16 hw + li).
       uint16_t vraw[4];
@@ -163,96 +160,81 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
       }
       __syncthreads();  // the previous block's readers of LDS are done
 
-      {  // S0, dS row-major [r][c] (scalar) and transposed [c][r] (one 16-byte vector per split half).
-        bf16x8 th, tl8, uh, ul;
+      {  // Stage S0, dS rows and dY rows as hi / lo.
+        const float x[8] = {xs[0].x, xs[0].y, xs[0].z, xs[0].w, xs[1].x, xs[1].y, xs[1].z, xs[1].w};
+        const float y[8] = {ys[0].x, ys[0].y, ys[0].z, ys[0].w, ys[1].x, ys[1].y, ys[1].z, ys[1].w};
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          sds += xs[u] * ys[u];
-          const __bf16 xh = (__bf16)xs[u], xl = (__bf16)(xs[u] - (float)xh);
-          const __bf16 yh = (__bf16)ys[u], yl = (__bf16)(ys[u] - (float)yh);
-          sb[oS0h + (rg + u) * kLDK + cc] = xh, sb[oS0l + (rg + u) * kLDK + cc] = xl;
-          sb[odSh + (rg + u) * kLDK + cc] = yh, sb[odSl + (rg + u) * kLDK + cc] = yl;
-          th[u] = xh, tl8[u] = xl, uh[u] = yh, ul[u] = yl;
+        for (int u = 0; u < 8; ++u) sds += x[u] * y[u];
+        const Split8 xsp = split8(x), ysp = split8(y);
+        const int at = sr * kLS + sc;
+        *reinterpret_cast<bf16x8*>(sb + oS0h + at) = xsp.hi;
+        *reinterpret_cast<bf16x8*>(sb + oS0l + at) = xsp.lo;
+        *reinterpret_cast<bf16x8*>(sb + odSh + at) = ysp.hi;
+        *reinterpret_cast<bf16x8*>(sb + odSl + at) = ysp.lo;
+        if constexpr (kExactDy) {
+          *reinterpret_cast<uint2*>(sb + odYh + iy * kLY + r4) = uint2{yraw.x, yraw.y};
+        } else {
+          put4(sb + odYh, sb + odYl, iy * kLY + r4, __uint_as_float(yraw.x), __uint_as_float(yraw.y),
+               __uint_as_float(yraw.z), __uint_as_float(yraw.w));
         }
-        *reinterpret_cast<bf16x8*>(sb + oS0th + cc * kLDR + rg) = th;
-        *reinterpret_cast<bf16x8*>(sb + oS0tl + cc * kLDR + rg) = tl8;
-        *reinterpret_cast<bf16x8*>(sb + odSth + cc * kLDR + rg) = uh;
-        *reinterpret_cast<bf16x8*>(sb + odStl + cc * kLDR + rg) = ul;
-      }
-      {  // dY^T [r][i]
-        const uint32_t wv[4] = {yT.x, yT.y, yT.z, yT.w};
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const float x = kExactDy ? (j & 1 ? __uint_as_float(wv[j >> 1] & 0xffff0000u) : __uint_as_float(wv[j >> 1] << 16))
-                                   : __uint_as_float(wv[j]);
-          put_split(sb + odYth, sb + odYtl, (r4 + j) * kLDC + iy, x);
-        }
-      }
-      Split8 dYo;
-      {
-        float x[8];
-        const uint32_t w0[4] = {yo[0].x, yo[0].y, yo[0].z, yo[0].w}, w1[4] = {yo[1].x, yo[1].y, yo[1].z, yo[1].w};
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          if constexpr (kExactDy)
-            x[j] = j & 1 ? __uint_as_float(w0[j >> 1] & 0xffff0000u) : __uint_as_float(w0[j >> 1] << 16);
-          else
-            x[j] = __uint_as_float(j < 4 ? w0[j] : w1[j - 4]);
-        }
-        dYo = split8(x);
       }
       float vv[4];
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj) vv[jj] = bf16_to_f32(vraw[jj]);
       __syncthreads();
 
-      // Phase 1: KS and KdS for positions 16 pw.., state rows r = 16 hw + li.
-      const int r = 16 * hw + li;
+      // The wave's own dY rows (i = ip, k = r = 8g..): A of dY S0, B of Delta dY^T.
+      Split8 dYo;
+      dYo.hi = lds8(sb + odYh + ip * kLY + 8 * g);
+      if constexpr (!kExactDy) dYo.lo = lds8(sb + odYl + ip * kLY + 8 * g);
+
+      // Phase 1: KS and KdS for positions i = 16 pw + 4g + jj, state rows r = 16 hw + li.
+      const int r = 16 * hw + li, i0 = 16 * pw + 4 * g;
       f32x4 ks = zero4(), kds = zero4();
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        const int at = r * kLDK + 32 * s + 8 * g;
+        const int at = r * kLS + 32 * s + 8 * g;
         ks = mma(mma(ks, Kf[s], lds8(sb + oS0h + at)), Kf[s], lds8(sb + oS0l + at));
         kds = mma(mma(kds, Kf[s], lds8(sb + odSh + at)), Kf[s], lds8(sb + odSl + at));
       }
-      float gks[4];
+      float gks[4], rv[4];
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj) {
-        const int i = 16 * pw + 4 * g + jj;
-        gks[jj] = gam[i] * ks[jj];
-        const float R = vv[jj] - gks[jj];
-        put_split(sb + oRth, sb + oRtl, r * kLDC + i, R);
-        put_split(sb + oRmh, sb + oRml, i * kLDN + r, R);
+        gks[jj] = gam[i0 + jj] * ks[jj];
+        rv[jj] = vv[jj] - gks[jj];
       }
+      put4(sb + oRh, sb + oRl, r * kLP + i0, rv[0], rv[1], rv[2], rv[3]);
       __syncthreads();
 
-      // Phase 2: Delta = Tb R and dDelta = P^T dY + D KdS.
+      // Phase 2: Delta = Tb R and dDelta = P^T dY + D KdS (rows: the wave's positions; lane: row r).
       f32x4 dl = zero4(), dd;
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
-        const int at = r * kLDC + 32 * s + 8 * g;
-        dl = mma3(dl, TbA[s], Split8{lds8(sb + oRth + at), lds8(sb + oRtl + at)});
+        const int at = r * kLP + 32 * s + 8 * g;
+        dl = mma3(dl, TbA[s], Split8{lds8(sb + oRh + at), lds8(sb + oRl + at)});
       }
 #pragma unroll
-      for (int jj = 0; jj < 4; ++jj) dd[jj] = dec[16 * pw + 4 * g + jj] * kds[jj];
+      for (int jj = 0; jj < 4; ++jj) dd[jj] = dec[i0 + jj] * kds[jj];
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
-        if (32 * s + 31 >= 16 * pw) {
-          const int at = r * kLDC + 32 * s + 8 * g;
+        if (32 * s + 31 >= 16 * pw) {  // P^T is zero below the diagonal
+          const int at = 32 * s * kLY + 16 * hw;
           if constexpr (kExactDy)
-            dd = mma2(dd, PA[s], lds8(sb + odYth + at));
+            dd = mma2(dd, PA[s], lds_tr8(sb + odYh + at, kLY, lt));
           else
-            dd = mma3(dd, PA[s], Split8{lds8(sb + odYth + at), lds8(sb + odYtl + at)});
+            dd = mma3(dd, PA[s], Split8{lds_tr8(sb + odYh + at, kLY, lt), lds_tr8(sb + odYl + at, kLY, lt)});
         }
       }
+      {
+        float ddl[4];
 #pragma unroll
-      for (int jj = 0; jj < 4; ++jj) {
-        const int i = 16 * pw + 4 * g + jj;
-        hD[jj] += dec[i] * dl[jj] * kds[jj];
-        put_split(sb + oDmh, sb + oDml, i * kLDN + r, dl[jj]);
-        put_split(sb + oDDmh, sb + oDDml, i * kLDN + r, dec[i] * dl[jj]);
-        put_split(sb + odDth, sb + odDtl, r * kLDC + i, dd[jj]);
-        put_split(sb + odDmh, sb + odDml, i * kLDN + r, dd[jj]);
+        for (int jj = 0; jj < 4; ++jj) {
+          hD[jj] += dec[i0 + jj] * dl[jj] * kds[jj];
+          ddl[jj] = dec[i0 + jj] * dl[jj];
+        }
+        put4(sb + oDh, sb + oDl, r * kLP + i0, dl[0], dl[1], dl[2], dl[3]);
+        put4(sb + oDDh, sb + oDDl, r * kLP + i0, ddl[0], ddl[1], ddl[2], ddl[3]);
+        put4(sb + odDh, sb + odDl, r * kLP + i0, dd[0], dd[1], dd[2], dd[3]);
       }
       __syncthreads();
 
@@ -261,30 +243,32 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
         f32x4 dr = zero4();
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
-          const int at = r * kLDC + 32 * s + 8 * g;
-          dr = mma3(dr, TbtA[s], Split8{lds8(sb + odDth + at), lds8(sb + odDtl + at)});
+          const int at = r * kLP + 32 * s + 8 * g;
+          dr = mma3(dr, TbtA[s], Split8{lds8(sb + odDh + at), lds8(sb + odDl + at)});
         }
+        float gdr[4];
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) {
-          const int i = 16 * pw + 4 * g + jj;
           gpart[jj] -= dr[jj] * gks[jj];
-          put_split(sb + oGdRh, sb + oGdRl, i * kLDN + r, -gam[i] * dr[jj]);
+          gdr[jj] = -gam[i0 + jj] * dr[jj];
         }
+        put4(sb + oGdRh, sb + oGdRl, r * kLP + i0, gdr[0], gdr[1], gdr[2], gdr[3]);
       }
       {
-        const int atn = ip * kLDN + 8 * g;
-        const Split8 BdD{lds8(sb + odDmh + atn), lds8(sb + odDml + atn)};
+        // dDelta[i][r] of the wave's positions as B (k = r, n = i).
+        const Split8 BdD{lds_tr8(sb + odDh + 16 * pw, kLP, lt), lds_tr8(sb + odDl + 16 * pw, kLP, lt)};
 #pragma unroll
         for (int mi = 0; mi < 2; ++mi) {
           const int m = 2 * hw + mi;
           if (m <= pw) {
-            const int at = (16 * m + li) * kLDN + 8 * g;
-            const Split8 AD{lds8(sb + oDmh + at), lds8(sb + oDml + at)};
+            // Delta and R rows j of key tile m as A (m = j, k = r).
+            const Split8 AD{lds_tr8(sb + oDh + 16 * m, kLP, lt), lds_tr8(sb + oDl + 16 * m, kLP, lt)};
             if constexpr (kExactDy)
               dPt[mi] = mma2(dPt[mi], AD, dYo.hi);
             else
               dPt[mi] = mma3(dPt[mi], AD, dYo);
-            dTbt[mi] = mma3(dTbt[mi], Split8{lds8(sb + oRmh + at), lds8(sb + oRml + at)}, BdD);
+            const Split8 AR{lds_tr8(sb + oRh + 16 * m, kLP, lt), lds_tr8(sb + oRl + 16 * m, kLP, lt)};
+            dTbt[mi] = mma3(dTbt[mi], AR, BdD);
           }
         }
       }
@@ -292,14 +276,13 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
 
       // Phase 4: dQ_inter += dY S0; dK += -diag(exp G) dR S0 + D Delta dS (columns of this half).
       {
-        const int at = ip * kLDN + 8 * g;
-        const Split8 AGdR{lds8(sb + oGdRh + at), lds8(sb + oGdRl + at)};
-        const Split8 ADD{lds8(sb + oDDmh + at), lds8(sb + oDDml + at)};
+        const Split8 AGdR{lds_tr8(sb + oGdRh + 16 * pw, kLP, lt), lds_tr8(sb + oGdRl + 16 * pw, kLP, lt)};
+        const Split8 ADD{lds_tr8(sb + oDDh + 16 * pw, kLP, lt), lds_tr8(sb + oDDl + 16 * pw, kLP, lt)};
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
-          const int bt = (16 * (4 * hw + t) + li) * kLDR + 8 * g;
-          const Split8 B0{lds8(sb + oS0th + bt), lds8(sb + oS0tl + bt)};
-          const Split8 B1{lds8(sb + odSth + bt), lds8(sb + odStl + bt)};
+          const int c0 = 16 * (4 * hw + t);
+          const Split8 B0{lds_tr8(sb + oS0h + c0, kLS, lt), lds_tr8(sb + oS0l + c0, kLS, lt)};
+          const Split8 B1{lds_tr8(sb + odSh + c0, kLS, lt), lds_tr8(sb + odSl + c0, kLS, lt)};
           if constexpr (kExactDy)
             dQi[t] = mma2(dQi[t], dYo.hi, B0);
           else
@@ -327,17 +310,11 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
     }
     __syncthreads();
 
-    // E1: K, K^T, Q^T, T, dP (unmasked, j <= i) and dTb into the end-phase region.
+    // E1: K, Q rows, T, dP (unmasked, j <= i) and dTb into the end-phase region.
     for (int e = tid; e < kC * 16; e += kThreads) {
       const int t = e >> 4, c8 = (e & 15) * 8;
-      const bf16x8 kv = __builtin_bit_cast(bf16x8, buf_ld16(krs, uint32_t(t * sk + c8) * 2));
-      const bf16x8 qv = __builtin_bit_cast(bf16x8, buf_ld16(qrs, uint32_t(t * sk + c8) * 2));
-      *reinterpret_cast<bf16x8*>(sb + eKb + t * kLDK + c8) = kv;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        sb[eKt + (c8 + j) * kLDC + t] = kv[j];
-        sb[eQt + (c8 + j) * kLDC + t] = qv[j];
-      }
+      *reinterpret_cast<uint4*>(sb + eKb + t * kLK + c8) = buf_ld16(krs, uint32_t(t * sk + c8) * 2);
+      *reinterpret_cast<uint4*>(sb + eQb + t * kLK + c8) = buf_ld16(qrs, uint32_t(t * sk + c8) * 2);
     }
     for (int q = tid; q < kC * kC; q += kThreads) sf[eT + (q >> 6) * kLDF + (q & 63)] = tl->t[q];
     {
@@ -380,7 +357,7 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) {
           const int i = 16 * pw + 4 * g + jj, c = 16 * (4 * hw + t) + li;
-          tq[jj] += (float)sb[eQt + c * kLDC + i] * dQi[t][jj];
+          tq[jj] += (float)sb[eQb + i * kLK + c] * dQi[t][jj];
           dQ[t][jj] += gam[i] * dQi[t][jj];
         }
 #pragma unroll
@@ -394,7 +371,7 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
         f32x4 kk = zero4();
         if (m <= pw) {
 #pragma unroll
-          for (int s = 0; s < 4; ++s) kk = mma(kk, Kf[s], lds8(sb + eKb + (16 * m + li) * kLDK + 32 * s + 8 * g));
+          for (int s = 0; s < 4; ++s) kk = mma(kk, Kf[s], lds8(sb + eKb + (16 * m + li) * kLK + 32 * s + 8 * g));
         }
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) sf[eKK + (16 * pw + 4 * g + jj) * kLDF + 16 * m + li] = kk[jj];
@@ -417,11 +394,10 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
       }
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
-        const int c = 16 * (4 * hw + t) + li;
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
-          dQ[t] = mma2(dQ[t], AdPM[s], lds8(sb + eKt + c * kLDC + 32 * s + 8 * g));
-          dK[t] = mma2(dK[t], AdPMt[s], lds8(sb + eQt + c * kLDC + 32 * s + 8 * g));
+          dQ[t] = mma2(dQ[t], AdPM[s], lds_tr8(sb + eKb + 32 * s * kLK + 16 * (4 * hw + t), kLK, lt));
+          dK[t] = mma2(dK[t], AdPMt[s], lds_tr8(sb + eQb + 32 * s * kLK + 16 * (4 * hw + t), kLK, lt));
         }
       }
 #pragma unroll
@@ -520,9 +496,9 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
       }
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
-        const int c = 16 * (4 * hw + t) + li;
 #pragma unroll
-        for (int s = 0; s < 2; ++s) dK[t] = mma2(dK[t], A[s], lds8(sb + eKt + c * kLDC + 32 * s + 8 * g));
+        for (int s = 0; s < 2; ++s)
+          dK[t] = mma2(dK[t], A[s], lds_tr8(sb + eKb + 32 * s * kLK + 16 * (4 * hw + t), kLK, lt));
       }
     }
     // E6: dG per position, then dg = reverse cumsum and dbeta.

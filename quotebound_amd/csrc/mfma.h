@@ -81,4 +81,37 @@ __device__ __forceinline__ bf16x8 lds4x2(const __bf16* p) {
 // Global bf16 bits -> bf16x8 (16-byte aligned).
 __device__ __forceinline__ bf16x8 gld8(const bf16_t* p) { return *reinterpret_cast<const bf16x8*>(p); }
 
+// An MFMA operand whose k index runs down the rows of a row-major bf16 LDS matrix: lane (g = lane / 16,
+// n = lane % 16) gets M[8g + j][n], j = 0..7, of the matrix M at L (L points at its element [0][0]; ld, the row
+// stride in elements, and the offset of L are multiples of 4). This is the operand for k = rows, n = columns (B), or
+// m = columns, k = rows (A). It uses gfx950's transposing LDS read (ds_read_b64_tr_b16): within each group of 16
+// lanes, lane s supplies the address of row s / 4, columns 4 (s % 4) .. + 3, and lane 4a + b receives element b
+// of the rows supplied by lanes a, 4 + a, 8 + a, 12 + a. Two reads cover k = 8g .. 8g + 3 and 8g + 4 .. 8g + 7.
+__device__ __forceinline__ bf16x8 lds_tr8(const __bf16* L, int ld, int lane) {
+  typedef short s16x4 __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+  const int s = lane & 15, g = (lane >> 4) & 3;
+  const __bf16* p = L + (8 * g + (s >> 2)) * ld + 4 * (s & 3);
+  typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4;
+  const s16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p));
+  const s16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p + 4 * ld));
+  // Whole vectors are bit-cast: a bit cast of a single vector element reads element 0 with this compiler.
+  const bf16x4 x = __builtin_bit_cast(bf16x4, a), y = __builtin_bit_cast(bf16x4, b);
+  return __builtin_shufflevector(x, y, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+// Four consecutive values as bf16 hi and lo halves (x = hi + lo to about 16 bits), each packed into 8 bytes.
+struct Split4 {
+  uint2 hi, lo;
+};
+__device__ __forceinline__ Split4 split4(float x0, float x1, float x2, float x3) {
+  const __bf16 h0 = (__bf16)x0, h1 = (__bf16)x1, h2 = (__bf16)x2, h3 = (__bf16)x3;
+  const __bf16 l0 = (__bf16)(x0 - (float)h0), l1 = (__bf16)(x1 - (float)h1);
+  const __bf16 l2 = (__bf16)(x2 - (float)h2), l3 = (__bf16)(x3 - (float)h3);
+  auto pack = [](__bf16 a, __bf16 b) {
+    return uint32_t(__builtin_bit_cast(uint16_t, a)) | (uint32_t(__builtin_bit_cast(uint16_t, b)) << 16);
+  };
+  return Split4{uint2{pack(h0, h1), pack(h2, h3)}, uint2{pack(l0, l1), pack(l2, l3)}};
+}
+
 }  // namespace qbgdn
