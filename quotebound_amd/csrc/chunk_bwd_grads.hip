@@ -45,10 +45,9 @@ constexpr int kLoopBytes = (oGdRl + 32 * kLP) * 2;
 constexpr int kLK = 144;
 constexpr int eKb = 0, eQb = kC * kLK;   // bf16 offsets
 constexpr int eF = (2 * kC * kLK) / 2;  // first f32 offset
-constexpr int kLDF = kC + 1;            // f32 [.][64] rows
-constexpr int edP = eF, edTb = edP + kC * kLDF, eT = edTb + kC * kLDF;
-constexpr int eKK = eT + kC * kLDF, eZt = eKK + kC * kLDF;
-constexpr int kEndBytes = (eZt + kC * kLDF) * 4;
+constexpr int kLF = kC + 4;             // f32 [.][64] rows
+constexpr int edP = eF, edTb = edP + kC * kLF, eT = edTb + kC * kLF, eZt = eT + kC * kLF;
+constexpr int kEndBytes = (eZt + kC * kLF) * 4;
 constexpr int kSmemBytes = kLoopBytes > kEndBytes ? kLoopBytes : kEndBytes;
 
 // Four consecutive values at element offset at (a multiple of 4) of the hi and lo matrices.
@@ -65,8 +64,7 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
   __shared__ __align__(16) unsigned char smem[kSmemBytes];
   __shared__ float gam[kC], dec[kC], bet[kC], Gf[kC];
   __shared__ float gpos[2][kC], hpos[2][kC], tpos[2][kC];
-  __shared__ float x1r[kC], x1c[kC], x2r[2][kC], x2c[4][kC], dbT[kC], dbA[kC], dGt[kC], red[kThreads / 64];
-  __shared__ float SdS_total;
+  __shared__ float x2r[2][kC], x2c[4][kC], dbTp[4][kC], dbAp[2][kC], x1cp[4][kC], red[kThreads / 64];
   __bf16* sb = reinterpret_cast<__bf16*>(smem);
   float* sf = reinterpret_cast<float*>(smem);
 
@@ -297,10 +295,11 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
     int lt = tid;
     asm volatile("" : "+v"(lt));
     const int g = (lt >> 4) & 3, li = lt & 15, pw = (lt >> 6) & 3, hw = lt >> 8, ip = 16 * pw + li;
+    const int i0 = 16 * pw + 4 * g;  // first of the lane's accumulator rows
 #pragma unroll
     for (int jj = 0; jj < 4; ++jj) {
       const float v = sum16(gpart[jj]), h = sum16(hD[jj]);
-      if (li == 0) gpos[hw][16 * pw + 4 * g + jj] = v, hpos[hw][16 * pw + 4 * g + jj] = h;
+      if (li == 0) gpos[hw][i0 + jj] = v, hpos[hw][i0 + jj] = h;
     }
     {
       float v = sum16(sds);
@@ -310,37 +309,39 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
     }
     __syncthreads();
 
-    // E1: K, Q rows, T, dP (unmasked, j <= i) and dTb into the end-phase region.
+    // E1: K, Q rows, T, and dP, dTb (masked to j <= i) into the end-phase region. From the accumulators: the row and
+    // column sums of dP * P (the P factor's part of dG) and the column sums of dTb * T (dbeta's T part).
     for (int e = tid; e < kC * 16; e += kThreads) {
       const int t = e >> 4, c8 = (e & 15) * 8;
       *reinterpret_cast<uint4*>(sb + eKb + t * kLK + c8) = buf_ld16(krs, uint32_t(t * sk + c8) * 2);
       *reinterpret_cast<uint4*>(sb + eQb + t * kLK + c8) = buf_ld16(qrs, uint32_t(t * sk + c8) * 2);
     }
-    for (int q = tid; q < kC * kC; q += kThreads) sf[eT + (q >> 6) * kLDF + (q & 63)] = tl->t[q];
+    for (int q = tid; q < kC * kC; q += kThreads) sf[eT + (q >> 6) * kLF + (q & 63)] = tl->t[q];
     {
-      // With the masked dP entries of the lane (i = ip, j = 16 (2 hw + mi) + 4g + jj) and P_ij from the tile: the
-      // row sums sum_j dP_ij P_ij (over g here, over hw in dG) and column sums sum_i dP_ij P_ij (over li here,
-      // over pw in dG).
+      // Lane: i = ip, j = 16 (2 hw + mi) + 4g + jj. Row sums (over j) add up over g here and over hw in dG; column
+      // sums (over i) over li here and over pw in dG.
       float prow = 0.f;
 #pragma unroll
       for (int mi = 0; mi < 2; ++mi) {
         const int j0 = 16 * (2 * hw + mi) + 4 * g;
         const uint2 ph = *reinterpret_cast<const uint2*>(tl->p_hi + ip * kC + j0);
         const uint2 pl = *reinterpret_cast<const uint2*>(tl->p_lo + ip * kC + j0);
+        const float4 t4 = *reinterpret_cast<const float4*>(tl->t + ip * kC + j0);
         const uint32_t hw4[2] = {ph.x, ph.y}, lw4[2] = {pl.x, pl.y};
+        const float tv4[4] = {t4.x, t4.y, t4.z, t4.w};
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) {
           const int j = j0 + jj;
-          const float dp = j <= ip ? dPt[mi][jj] : 0.f;
-          sf[edP + ip * kLDF + j] = dp;
-          sf[edTb + ip * kLDF + j] = j <= ip ? dTbt[mi][jj] : 0.f;
+          const float dp = j <= ip ? dPt[mi][jj] : 0.f, db = j <= ip ? dTbt[mi][jj] : 0.f;
+          sf[edP + ip * kLF + j] = dp;
+          sf[edTb + ip * kLF + j] = db;
           const uint32_t hb = hw4[jj >> 1], lb = lw4[jj >> 1];
           const float pv = jj & 1 ? __uint_as_float(hb & 0xffff0000u) + __uint_as_float(lb & 0xffff0000u)
                                   : __uint_as_float(hb << 16) + __uint_as_float(lb << 16);
           const float x = dp * pv;
           prow += x;
-          const float col = sum16(x);
-          if (li == 0) x2c[pw][j] = col;
+          const float col = sum16(x), colb = sum16(db * tv4[jj]);
+          if (li == 0) x2c[pw][j] = col, dbTp[pw][j] = colb;
         }
       }
       prow += __shfl_xor(prow, 16);
@@ -349,32 +350,33 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
     }
     __syncthreads();
 
-    // E2: dQ += diag(exp G) dQ_inter and its dG term; K K^T; dQ += (dP * M) K; dK += (dP * M)^T Q; Z = dT T^T.
+    // E2: dQ += diag(exp G) dQ_inter and its dG term; K K^T (kept in registers); dQ += (dP * M) K;
+    // dK += (dP * M)^T Q; Z = dT T^T.
+    f32x4 kk[2];  // (K K^T)[p][m], rows p = 16 pw + 4g + jj, columns m = 16 (2 hw + mi) + li; zero above tile pw
     {
       float tq[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int t = 0; t < 4; ++t)
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) {
-          const int i = 16 * pw + 4 * g + jj, c = 16 * (4 * hw + t) + li;
+          const int i = i0 + jj, c = 16 * (4 * hw + t) + li;
           tq[jj] += (float)sb[eQb + i * kLK + c] * dQi[t][jj];
           dQ[t][jj] += gam[i] * dQi[t][jj];
         }
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj) {
         const float v = sum16(tq[jj]);
-        if (li == 0) tpos[hw][16 * pw + 4 * g + jj] = v;
+        if (li == 0) tpos[hw][i0 + jj] = v;
       }
 #pragma unroll
       for (int mi = 0; mi < 2; ++mi) {
         const int m = 2 * hw + mi;
-        f32x4 kk = zero4();
+        kk[mi] = zero4();
         if (m <= pw) {
 #pragma unroll
-          for (int s = 0; s < 4; ++s) kk = mma(kk, Kf[s], lds8(sb + eKb + (16 * m + li) * kLK + 32 * s + 8 * g));
+          for (int s = 0; s < 4; ++s)
+            kk[mi] = mma(kk[mi], Kf[s], lds8(sb + eKb + (16 * m + li) * kLK + 32 * s + 8 * g));
         }
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj) sf[eKK + (16 * pw + 4 * g + jj) * kLDF + 16 * m + li] = kk[jj];
       }
       Split8 AdPM[2], AdPMt[2], AdT[2];
 #pragma unroll
@@ -384,9 +386,9 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
         for (int j = 0; j < 8; ++j) {
           const int jj = 32 * s + 8 * g + j;
           // M_ij = exp(G_i - G_j) only where j <= i (elsewhere the exponent is positive and may overflow)
-          x[j] = jj <= ip ? sf[edP + ip * kLDF + jj] * __expf(Gf[ip] - Gf[jj]) : 0.f;
-          y[j] = jj >= ip ? sf[edP + jj * kLDF + ip] * __expf(Gf[jj] - Gf[ip]) : 0.f;
-          z[j] = sf[edTb + ip * kLDF + jj] * bet[jj];
+          x[j] = jj <= ip ? sf[edP + ip * kLF + jj] * __expf(Gf[ip] - Gf[jj]) : 0.f;
+          y[j] = jj >= ip ? sf[edP + jj * kLF + ip] * __expf(Gf[jj] - Gf[ip]) : 0.f;
+          z[j] = sf[edTb + ip * kLF + jj] * bet[jj];
         }
         AdPM[s] = split8(x);
         AdPMt[s] = split8(y);
@@ -408,80 +410,62 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
         for (int s = 0; s < 2; ++s) {
           float tv[8];
 #pragma unroll
-          for (int j = 0; j < 8; ++j) tv[j] = sf[eT + (16 * m + li) * kLDF + 32 * s + 8 * g + j];
+          for (int j = 0; j < 8; ++j) tv[j] = sf[eT + (16 * m + li) * kLF + 32 * s + 8 * g + j];
           z = mma3(z, AdT[s], split8(tv));
         }
 #pragma unroll
-        for (int jj = 0; jj < 4; ++jj) sf[eZt + (16 * m + li) * kLDF + 16 * pw + 4 * g + jj] = z[jj];
+        for (int jj = 0; jj < 4; ++jj) sf[eZt + (16 * m + li) * kLF + i0 + jj] = z[jj];
       }
-    }
-    if (tid < kC) {
-      const int j = tid;
-      float acc = 0.f;
-      for (int i = j; i < kC; ++i) acc += sf[edTb + i * kLDF + j] * sf[eT + i * kLDF + j];
-      dbT[j] = acc;
-    } else if (tid == kC) {
-      float acc = 0.f;
-      for (int t = 0; t < kThreads / 64; ++t) acc += red[t];
-      SdS_total = acc;
     }
     __syncthreads();
 
-    // E3: dA = -T^T Z (strict lower) for rows p = ip, this half's column tiles, into the dP slot.
+    // E3: dA = -T^T Z below the diagonal (rows p = i0 + jj, columns m = 16 (2 hw + mi) + li, as kk), and at once
+    // its products with E = exp(G_p - G_m) and K K^T: the A part of dbeta (row sums), of dG (row and column sums),
+    // and dKK = diag(beta) (dA * E), written over dTb.
     {
       Split8 AT[2];
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
         float x[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) x[j] = sf[eT + (32 * s + 8 * g + j) * kLDF + ip];
+        for (int j = 0; j < 8; ++j) x[j] = sf[eT + (32 * s + 8 * g + j) * kLF + ip];
         AT[s] = split8(x);
       }
-      f32x4 da[2];
+      float rowp[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int mi = 0; mi < 2; ++mi) {
-        const int m = 2 * hw + mi;
-        da[mi] = zero4();
+        const int mt = 2 * hw + mi, mcol = 16 * mt + li;
+        f32x4 da = zero4();
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
           float zv[8];
 #pragma unroll
-          for (int j = 0; j < 8; ++j) zv[j] = sf[eZt + (16 * m + li) * kLDF + 32 * s + 8 * g + j];
-          da[mi] = mma3(da[mi], AT[s], split8(zv));
+          for (int j = 0; j < 8; ++j) zv[j] = sf[eZt + (16 * mt + li) * kLF + 32 * s + 8 * g + j];
+          da = mma3(da, AT[s], split8(zv));
         }
-      }
-      __syncthreads();  // every wave has read dP and Z before dA overwrites the dP slot
-#pragma unroll
-      for (int mi = 0; mi < 2; ++mi)
+        float colp = 0.f;
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) {
-          const int p = 16 * pw + 4 * g + jj, m = 16 * (2 * hw + mi) + li;
-          sf[edP + p * kLDF + m] = m < p ? -da[mi][jj] : 0.f;
+          const int pr = i0 + jj;
+          const float dae = mcol < pr ? -da[jj] * __expf(Gf[pr] - Gf[mcol]) : 0.f;  // dA_pm E_pm
+          const float prod = dae * kk[mi][jj];
+          rowp[jj] += prod;
+          colp += bet[pr] * prod;
+          sf[edTb + pr * kLF + mcol] = bet[pr] * dae;
         }
+        colp += __shfl_xor(colp, 16);
+        colp += __shfl_xor(colp, 32);
+        if (g == 0) x1cp[pw][mcol] = colp;
+      }
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        const float v = sum16(rowp[jj]);
+        if (li == 0) dbAp[hw][i0 + jj] = v;
+      }
     }
     __syncthreads();
 
-    // E4: dbeta (A part), the A-factor terms of dG, and dKK = beta_p dA E into the dTb slot.
-    if (tid < kC) {
-      const int p = tid;
-      float acc = 0.f;
-      for (int m = 0; m < p; ++m) acc += sf[edP + p * kLDF + m] * __expf(Gf[p] - Gf[m]) * sf[eKK + p * kLDF + m];
-      dbA[p] = acc;
-      x1r[p] = bet[p] * acc;
-    } else if (tid < 2 * kC) {
-      const int m = tid - kC;
-      float acc = 0.f;
-      for (int p = m + 1; p < kC; ++p)
-        acc += bet[p] * sf[edP + p * kLDF + m] * __expf(Gf[p] - Gf[m]) * sf[eKK + p * kLDF + m];
-      x1c[m] = acc;
-    }
-    for (int q = tid; q < kC * kC; q += kThreads) {
-      const int p = q >> 6, m = q & 63;
-      sf[edTb + p * kLDF + m] = m < p ? bet[p] * sf[edP + p * kLDF + m] * __expf(Gf[p] - Gf[m]) : 0.f;
-    }
-    __syncthreads();
-
-    // E5: dK += (dKK + dKK^T) K for rows j = ip, this half's columns.
+    // E4: dK += (dKK + dKK^T) K for rows j = ip, this half's columns.
     {
       Split8 A[2];
 #pragma unroll
@@ -490,7 +474,7 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
           const int m = 32 * s + 8 * g + j;
-          x[j] = sf[edTb + ip * kLDF + m] + sf[edTb + m * kLDF + ip];
+          x[j] = sf[edTb + ip * kLF + m] + sf[edTb + m * kLF + ip];
         }
         A[s] = split8(x);
       }
@@ -501,27 +485,33 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
           dK[t] = mma2(dK[t], A[s], lds_tr8(sb + eKb + 32 * s * kLK + 16 * (4 * hw + t), kLK, lt));
       }
     }
-    // E6: dG per position, then dg = reverse cumsum and dbeta.
+    // E5 (one wave): dG per position, dg = its reverse cumulative sum (a suffix scan over the wave), and dbeta.
     if (tid < kC) {
       const int t = tid;
-      float v = gam[t] * (tpos[0][t] + tpos[1][t]) + gpos[0][t] + gpos[1][t] - hpos[0][t] - hpos[1][t] + x1r[t] -
-                x1c[t] + x2r[0][t] + x2r[1][t] - (x2c[0][t] + x2c[1][t] + x2c[2][t] + x2c[3][t]);
-      if (t == kC - 1) {
-        float hsum = 0.f;
-        for (int i = 0; i < kC; ++i) hsum += hpos[0][i] + hpos[1][i];
-        v += hsum + gam[kC - 1] * SdS_total;
+      const float hs = hpos[0][t] + hpos[1][t];
+      float hsum = sum16(hs);
+      hsum += __shfl_xor(hsum, 16);
+      hsum += __shfl_xor(hsum, 32);
+      float sds_all = 0.f;
+#pragma unroll
+      for (int u = 0; u < kThreads / 64; ++u) sds_all += red[u];
+      const float dbA = dbAp[0][t] + dbAp[1][t];
+      float v = gam[t] * (tpos[0][t] + tpos[1][t]) + gpos[0][t] + gpos[1][t] - hs + bet[t] * dbA -
+                (x1cp[0][t] + x1cp[1][t] + x1cp[2][t] + x1cp[3][t]) + x2r[0][t] + x2r[1][t] -
+                (x2c[0][t] + x2c[1][t] + x2c[2][t] + x2c[3][t]);
+      if (t == kC - 1) v += hsum + gam[kC - 1] * sds_all;
+#pragma unroll
+      for (int off = 1; off < kC; off <<= 1) {
+        const float u = __shfl_down(v, off);
+        if (t + off < kC) v += u;
       }
-      dGt[t] = v;
-    }
-    __syncthreads();
-    if (tid < L) {
-      const int t = tid;
-      float da = 0.f;
-      for (int i = kC - 1; i >= t; --i) da += dGt[i];
-      const int64_t g0 = tok * a.Hv + hv;
-      const uint32_t gi = uint32_t(t * a.Hv);
-      a.dg[g0 + gi] = a.g_is_log ? da : da / a.g[g0 + gi];
-      IO<OutT>::st(static_cast<OutT*>(a.dbeta) + g0, gi, dbT[t] + dbA[t]);
+      if (t < L) {
+        const int64_t g0 = tok * a.Hv + hv;
+        const uint32_t gi = uint32_t(t * a.Hv);
+        a.dg[g0 + gi] = a.g_is_log ? v : v / a.g[g0 + gi];
+        const float dbT = dbTp[0][t] + dbTp[1][t] + dbTp[2][t] + dbTp[3][t];
+        IO<OutT>::st(static_cast<OutT*>(a.dbeta) + g0, gi, dbT + dbA);
+      }
     }
   }
 
