@@ -18,7 +18,7 @@ namespace qbgdn {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kLDK = 128 + kPadB;
+constexpr int kLDK = 144;  // rows 0..3 of a transposing read on distinct banks
 constexpr int kLDC = kC + kPadB;
 
 template <typename OutT>
@@ -196,12 +196,10 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_state_kernel(ChunkArgs a) 
     for (int nt = 0; nt < 2; ++nt) {
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj) dS[nt][jj] *= glast;
-      const int col = 32 * w + 16 * nt + li;
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
-        bf16x8 bq, bk;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) bq[j] = Qb[32 * s + 8 * g + j][col], bk[j] = Kb[32 * s + 8 * g + j][col];
+        const bf16x8 bq = lds_tr8(&Qb[32 * s][32 * w + 16 * nt], kLDK, tid);  // rows 32s.., this lane's state column
+        const bf16x8 bk = lds_tr8(&Kb[32 * s][32 * w + 16 * nt], kLDK, tid);
         dS[nt] = mma2(dS[nt], Split8{lds8(&GdYth[li][32 * s + 8 * g]), lds8(&GdYtl[li][32 * s + 8 * g])}, bq);
         dS[nt] = mma2(dS[nt], Split8{lds8(&GdRth[li][32 * s + 8 * g]), lds8(&GdRtl[li][32 * s + 8 * g])}, bk);
       }

@@ -16,7 +16,7 @@ namespace qbgdn {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kLDK = 128 + kPadB;  // bf16 row stride for Dk = 128
+constexpr int kLDK = 144;  // bf16 row stride for Dk = 128 (rows 0..3 of a transposing read on distinct banks)
 constexpr int kLDC = kC + kPadB;   // bf16 row stride for 64 positions
 
 template <typename OutT>
@@ -168,14 +168,10 @@ __global__ __launch_bounds__(kThreads) void chunk_fwd_kernel(ChunkArgs a) {
     for (int nt = 0; nt < 2; ++nt) {
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj) S[nt][jj] *= glast;
-      const int col = 32 * w + 16 * nt + li;
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
         const Split8 A{lds8(&DDth[li][32 * s + 8 * g]), lds8(&DDtl[li][32 * s + 8 * g])};
-        bf16x8 B;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) B[j] = Kb[32 * s + 8 * g + j][col];
-        S[nt] = mma2(S[nt], A, B);
+        S[nt] = mma2(S[nt], A, lds_tr8(&Kb[32 * s][32 * w + 16 * nt], kLDK, tid));  // K rows 32s.., this lane's state column
       }
     }
 
