@@ -41,10 +41,11 @@ constexpr int oDDh = oDl + 32 * kLP, oDDl = oDDh + 32 * kLP;      // D Delta
 constexpr int odDh = oDDl + 32 * kLP, odDl = odDh + 32 * kLP;     // dDelta
 constexpr int oGdRh = odDl + 32 * kLP, oGdRl = oGdRh + 32 * kLP;  // -diag(exp G) dR
 constexpr int kLoopBytes = (oGdRl + 32 * kLP) * 2;
-// End-phase region (aliases the block-loop region): bf16 K and Q rows, then f32 64 x 64 matrices.
+// End-phase region (aliases the block-loop region): bf16 Q rows, then f32 64 x 64 matrices. (K rows stay in their
+// own array for the whole block.)
 constexpr int kLK = 144;
-constexpr int eKb = 0, eQb = kC * kLK;   // bf16 offsets
-constexpr int eF = (2 * kC * kLK) / 2;  // first f32 offset
+constexpr int eQb = 0;             // bf16 offset
+constexpr int eF = (kC * kLK) / 2;  // first f32 offset
 constexpr int kLF = kC + 4;             // f32 [.][64] rows
 constexpr int edP = eF, edTb = edP + kC * kLF, eT = edTb + kC * kLF, eZt = eT + kC * kLF;
 constexpr int kEndBytes = (eZt + kC * kLF) * 4;
@@ -62,6 +63,7 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
   constexpr int Dk = 128;
   constexpr bool kExactDy = std::is_same<OutT, bf16_t>::value;
   __shared__ __align__(16) unsigned char smem[kSmemBytes];
+  __shared__ __align__(16) __bf16 Kres[kC * kLK];  // the chunk's K rows, for the whole block
   __shared__ float gam[kC], dec[kC], bet[kC], Gf[kC];
   __shared__ float gpos[2][kC], hpos[2][kC], tpos[2][kC];
   __shared__ float x2r[2][kC], x2c[4][kC], dbTp[4][kC], dbAp[2][kC], x1cp[4][kC], red[kThreads / 64];
@@ -77,7 +79,6 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
   const int64_t tok = sp.tok;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 4, li = lane & 15;
   const int pw = w & 3, hw = w >> 2;  // position tile, half
-  const int ip = 16 * pw + li;        // the lane's position as an A-operand row
   const OutT* dy = static_cast<const OutT*>(a.dy);
   const int sk = a.Hk * Dk, sv = a.Hv * a.Dv;  // token strides of k/q/dq/dk and v/dy
   const bf16_t* kbase = a.k + tok * sk + hk * Dk;
@@ -85,10 +86,11 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
   // Rows past the chunk's last row read as zeros.
   const auto krs = buffer_rsrc(kbase, uint32_t(L * sk) * 2u), qrs = buffer_rsrc(qbase, uint32_t(L * sk) * 2u);
 
-  // K rows of the wave's positions (A operands of K S0^T, K dS^T, K K^T).
-  bf16x8 Kf[4];
-#pragma unroll
-  for (int s = 0; s < 4; ++s) Kf[s] = __builtin_bit_cast(bf16x8, buf_ld16(krs, uint32_t(ip * sk + 32 * s + 8 * g) * 2));
+  // The chunk's K rows (A operands of K S0^T, K dS^T, K K^T; B of the K products of the end phase).
+  for (int e = tid; e < kC * 16; e += kThreads) {
+    const int t = e >> 4, c8 = (e & 15) * 8;
+    *reinterpret_cast<uint4*>(Kres + t * kLK + c8) = buf_ld16(krs, uint32_t(t * sk + c8) * 2);
+  }
   f32x4 dQ[4], dK[4];  // columns 16 (4 hw + t) + li, rows 16 pw + 4 g + jj
 #pragma unroll
   for (int t = 0; t < 4; ++t) dQ[t] = zero4(), dK[t] = zero4();
@@ -107,41 +109,54 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
     float gpart[4] = {0.f, 0.f, 0.f, 0.f}, hD[4] = {0.f, 0.f, 0.f, 0.f}, sds = 0.f;
     __syncthreads();
 
+    // One block's global reads (S0 and dS rows, dY, v), kept in registers from issue to staging. dy and v go through
+    // buffer resources that end at the chunk's last row, so rows past it read as zeros without a branch.
+    struct BlockIn {
+      float4 xs[2], ys[2];  // S0, dS: thread -> row tid / 16, columns 8 (tid % 16) .. + 7
+      uint4 yraw;           // dY: thread -> position tid / 8, rows 4 (tid % 8) .. + 3
+      uint16_t vraw[4];     // v at the wave's accumulator positions (16 pw + 4g + jj, column 16 hw + li)
+    };
+    auto load_block = [&](BlockIn& b, int r0, int lt) {
+      const int g = (lt >> 4) & 3, li = lt & 15, pw = (lt >> 6) & 3, hw = lt >> 8;
+      const int64_t rows0 = (sh * a.Dv + r0) * Dk;
+      const float* s0b = a.ckpt + rows0;
+      const float* dsb = a.dsend + rows0;
+      const auto yr = buffer_rsrc(dy + (tok * a.Hv + hv) * a.Dv + r0, uint32_t(L * sv) * uint32_t(sizeof(OutT)));
+      const auto vr = buffer_rsrc(a.v + (tok * a.Hv + hv) * a.Dv + r0, uint32_t(L * sv) * 2u);
+      const int sr = lt >> 4, sc = (lt & 15) * 8;
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        b.xs[q] = *reinterpret_cast<const float4*>(s0b + sr * Dk + sc + 4 * q);
+        b.ys[q] = *reinterpret_cast<const float4*>(dsb + sr * Dk + sc + 4 * q);
+      }
+      const int iy = lt >> 3, r4 = (lt & 7) * 4;
+      if constexpr (kExactDy) {
+        const auto t2 = __builtin_amdgcn_raw_buffer_load_b64(yr, int(uint32_t(iy * sv + r4) * 2), 0, 0);
+        b.yraw = uint4{t2[0], t2[1], 0u, 0u};
+      } else {
+        b.yraw = buf_ld16(yr, uint32_t(iy * sv + r4) * 4);
+      }
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj)
+        b.vraw[jj] = buf_ld2(vr, uint32_t((16 * pw + 4 * g + jj) * sv + 16 * hw + li) * 2);
+    };
+    BlockIn nb;
+    {
+      int lt0 = tid;
+      asm volatile("" : "+v"(lt0));
+      load_block(nb, 0, lt0);
+    }
+
     for (int r0 = 0; r0 < a.Dv; r0 += 32) {
       // Lane indices re-derived from an opaque copy, so their many address expressions are recomputed here instead
       // of being hoisted out of both loops and held (spilled) for the whole kernel.
       int lt = tid;
       asm volatile("" : "+v"(lt));
       const int g = (lt >> 4) & 3, li = lt & 15, pw = (lt >> 6) & 3, hw = lt >> 8, ip = 16 * pw + li;
-      __syncthreads();
-      // All of this block's global reads are issued together before any is used. dy and v go through buffer
-      // resources that end at the chunk's last row, so rows past it read as zeros without a branch.
-      const int64_t rows0 = (sh * a.Dv + r0) * Dk;
-      const float* s0b = a.ckpt + rows0;
-      const float* dsb = a.dsend + rows0;
-      const auto yr = buffer_rsrc(dy + (tok * a.Hv + hv) * a.Dv + r0, uint32_t(L * sv) * uint32_t(sizeof(OutT)));
-      const auto vr = buffer_rsrc(a.v + (tok * a.Hv + hv) * a.Dv + r0, uint32_t(L * sv) * 2u);
-      // S0 and dS: thread -> row tid / 16, columns 8 (tid % 16) .. + 7.
-      const int sr = lt >> 4, sc = (lt & 15) * 8;
-      float4 xs[2], ys[2];
-#pragma unroll
-      for (int q = 0; q < 2; ++q) {
-        xs[q] = *reinterpret_cast<const float4*>(s0b + sr * Dk + sc + 4 * q);
-        ys[q] = *reinterpret_cast<const float4*>(dsb + sr * Dk + sc + 4 * q);
-      }
-      // dY: thread -> position tid / 8, rows 4 (tid % 8) .. + 3.
-      const int iy = lt >> 3, r4 = (lt & 7) * 4;
-      uint4 yraw;
-      if constexpr (kExactDy) {
-        const auto t2 = __builtin_amdgcn_raw_buffer_load_b64(yr, int(uint32_t(iy * sv + r4) * 2), 0, 0);
-        yraw = uint4{t2[0], t2[1], 0u, 0u};
-      } else {
-        yraw = buf_ld16(yr, uint32_t(iy * sv + r4) * 4);
-      }
-      // v at the wave's accumulator positions (rows i = 16 pw + 4g + jj, column r = 16 hw + li).
-      uint16_t vraw[4];
-#pragma unroll
-      for (int jj = 0; jj < 4; ++jj) vraw[jj] = buf_ld2(vr, uint32_t((16 * pw + 4 * g + jj) * sv + 16 * hw + li) * 2);
+      const int sr = lt >> 4, sc = (lt & 15) * 8, iy = lt >> 3, r4 = (lt & 7) * 4;
+      const float4* xs = nb.xs;
+      const float4* ys = nb.ys;
+      const uint4 yraw = nb.yraw;
       // A operands from the tile for this block (reloaded per block from L2 to keep them out of the loop-carried
       // registers): Tb rows ip (k = j), Tb^T rows ip (k = j) and P^T rows ip (k = i).
       Split8 TbA[2], TbtA[2], PA[2];
@@ -178,8 +193,10 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
       }
       float vv[4];
 #pragma unroll
-      for (int jj = 0; jj < 4; ++jj) vv[jj] = bf16_to_f32(vraw[jj]);
+      for (int jj = 0; jj < 4; ++jj) vv[jj] = bf16_to_f32(nb.vraw[jj]);
       __syncthreads();
+      // The next block's global reads, in flight while this block computes.
+      if (r0 + 32 < a.Dv) load_block(nb, r0 + 32, lt);
 
       // The wave's own dY rows (i = ip, k = r = 8g..): A of dY S0, B of Delta dY^T.
       Split8 dYo;
@@ -192,8 +209,9 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
         const int at = r * kLS + 32 * s + 8 * g;
-        ks = mma(mma(ks, Kf[s], lds8(sb + oS0h + at)), Kf[s], lds8(sb + oS0l + at));
-        kds = mma(mma(kds, Kf[s], lds8(sb + odSh + at)), Kf[s], lds8(sb + odSl + at));
+        const bf16x8 ka = lds8(Kres + ip * kLK + 32 * s + 8 * g);
+        ks = mma(mma(ks, ka, lds8(sb + oS0h + at)), ka, lds8(sb + oS0l + at));
+        kds = mma(mma(kds, ka, lds8(sb + odSh + at)), ka, lds8(sb + odSl + at));
       }
       float gks[4], rv[4];
 #pragma unroll
@@ -313,7 +331,6 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
     // column sums of dP * P (the P factor's part of dG) and the column sums of dTb * T (dbeta's T part).
     for (int e = tid; e < kC * 16; e += kThreads) {
       const int t = e >> 4, c8 = (e & 15) * 8;
-      *reinterpret_cast<uint4*>(sb + eKb + t * kLK + c8) = buf_ld16(krs, uint32_t(t * sk + c8) * 2);
       *reinterpret_cast<uint4*>(sb + eQb + t * kLK + c8) = buf_ld16(qrs, uint32_t(t * sk + c8) * 2);
     }
     for (int q = tid; q < kC * kC; q += kThreads) sf[eT + (q >> 6) * kLF + (q & 63)] = tl->t[q];
@@ -375,7 +392,7 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
         if (m <= pw) {
 #pragma unroll
           for (int s = 0; s < 4; ++s)
-            kk[mi] = mma(kk[mi], Kf[s], lds8(sb + eKb + (16 * m + li) * kLK + 32 * s + 8 * g));
+            kk[mi] = mma(kk[mi], lds8(Kres + ip * kLK + 32 * s + 8 * g), lds8(Kres + (16 * m + li) * kLK + 32 * s + 8 * g));
         }
       }
       Split8 AdPM[2], AdPMt[2], AdT[2];
@@ -398,7 +415,7 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
       for (int t = 0; t < 4; ++t) {
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
-          dQ[t] = mma2(dQ[t], AdPM[s], lds_tr8(sb + eKb + 32 * s * kLK + 16 * (4 * hw + t), kLK, lt));
+          dQ[t] = mma2(dQ[t], AdPM[s], lds_tr8(Kres + 32 * s * kLK + 16 * (4 * hw + t), kLK, lt));
           dK[t] = mma2(dK[t], AdPMt[s], lds_tr8(sb + eQb + 32 * s * kLK + 16 * (4 * hw + t), kLK, lt));
         }
       }
@@ -482,7 +499,7 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
       for (int t = 0; t < 4; ++t) {
 #pragma unroll
         for (int s = 0; s < 2; ++s)
-          dK[t] = mma2(dK[t], A[s], lds_tr8(sb + eKb + 32 * s * kLK + 16 * (4 * hw + t), kLK, lt));
+          dK[t] = mma2(dK[t], A[s], lds_tr8(Kres + 32 * s * kLK + 16 * (4 * hw + t), kLK, lt));
       }
     }
     // E5 (one wave): dG per position, dg = its reverse cumulative sum (a suffix scan over the wave), and dbeta.
