@@ -14,7 +14,7 @@ namespace qbgdn {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kLDK = 128 + kPadB;
+constexpr int kLDK = 144;  // rows 0..3 of a transposing read on distinct banks
 constexpr int kLDF = kC + 1;  // float rows, padded
 
 __global__ __launch_bounds__(kThreads) void chunk_prep_kernel(ChunkArgs a) {
@@ -33,30 +33,54 @@ __global__ __launch_bounds__(kThreads) void chunk_prep_kernel(ChunkArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 4, li = lane & 15;
   Tile* tile = a.tiles + (slot * a.Hv + hv);
 
-  stage_rows_bf16<128>(&Kb[0][0], kLDK, a.k, sp.tok, a.Hk, hk, sp.L, kThreads);
-  stage_rows_bf16<128>(&Qb[0][0], kLDK, a.q, sp.tok, a.Hk, hk, sp.L, kThreads);
+  // K and Q rows through buffer resources that end at the chunk's last row (rows past it read as zeros), all
+  // issued before any is used.
+  {
+    const int sk = a.Hk * 128;
+    const uint32_t bytes = uint32_t(sp.L) * uint32_t(sk) * 2u;
+    const auto kr = buffer_rsrc(a.k + sp.tok * sk + hk * 128, bytes), qr = buffer_rsrc(a.q + sp.tok * sk + hk * 128, bytes);
+    uint4 kv[4], qv[4];
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4) {
+      const int e = tid + kThreads * q4, t = e >> 4, c8 = (e & 15) * 8;
+      kv[q4] = buf_ld16(kr, uint32_t(t * sk + c8) * 2);
+      qv[q4] = buf_ld16(qr, uint32_t(t * sk + c8) * 2);
+    }
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4) {
+      const int e = tid + kThreads * q4, t = e >> 4, c8 = (e & 15) * 8;
+      *reinterpret_cast<uint4*>(&Kb[t][c8]) = kv[q4];
+      *reinterpret_cast<uint4*>(&Qb[t][c8]) = qv[q4];
+    }
+  }
+  // One wave: beta, and G = the inclusive prefix sum of the log-decays (fp64, by a shuffle scan).
   if (tid < kC) {
     const int t = tid;
-    Gd[t] = t < sp.L ? log_decay(a.g, (sp.tok + t) * a.Hv + hv, a.g_is_log) : 0.0;
-    Bs[t] = t < sp.L ? bf16_to_f32(a.beta[(sp.tok + t) * a.Hv + hv]) : 0.f;
-  }
-  // Inclusive prefix sum of the log-decays (Hillis-Steele, fp64).
-  for (int off = 1; off < kC; off <<= 1) {
-    __syncthreads();
-    const double add = (tid < kC && tid >= off) ? Gd[tid - off] : 0.0;
-    __syncthreads();
-    if (tid < kC) Gd[tid] += add;
+    const uint32_t L = uint32_t(sp.L);
+    const int64_t s0 = sp.tok * a.Hv + hv;
+    const auto gr = buffer_rsrc(a.g + s0, L == 0 ? 0u : ((L - 1) * uint32_t(a.Hv) + 1) * 4u);
+    const auto br = buffer_rsrc(a.beta + s0, L == 0 ? 0u : ((L - 1) * uint32_t(a.Hv) + 1) * 2u);
+    const float gx = buf_ld4(gr, uint32_t(t * a.Hv) * 4);
+    const float bx = bf16_to_f32(buf_ld2(br, uint32_t(t * a.Hv) * 2));
+    double G = uint32_t(t) < L ? (a.g_is_log ? double(gx) : log(double(gx))) : 0.0;
+#pragma unroll
+    for (int off = 1; off < kC; off <<= 1) {
+      const double u = __shfl_up(G, off);
+      if (t >= off) G += u;
+    }
+    const double Glast = __shfl(G, kC - 1);
+    Gd[t] = G;
+    Bs[t] = uint32_t(t) < L ? bx : 0.f;
+    tile->beta[t] = Bs[t];
+    tile->gam[t] = expf(float(G));
+    tile->dec[t] = expf(float(Glast - G));
+    tile->G[t] = float(G);
   }
   __syncthreads();
-  if (tid < kC) {
-    const double G = Gd[tid];
-    tile->beta[tid] = Bs[tid];
-    tile->gam[tid] = expf(float(G));
-    tile->dec[tid] = expf(float(Gd[kC - 1] - G));
-    tile->G[tid] = float(G);
-  }
 
-  // Row strip w: A (into LDS) and P (straight out), lane -> column j = 16 nj + li, rows i = 16 w + 4 g + jj.
+  // Row strip w: A (into LDS) and P, lane -> column j = 16 nj + li, rows i = 16 w + 4g + jj. P's hi and lo halves go
+  // into this strip's own rows of Qb (columns 0..63 and 64..127), which no other wave reads.
+  f32x4 pq[4];
   for (int nj = 0; nj < 4; ++nj) {
     f32x4 kk = zero4(), qk = zero4();
     if (nj <= w) {
@@ -72,14 +96,41 @@ __global__ __launch_bounds__(kThreads) void chunk_prep_kernel(ChunkArgs a) {
       const int i = 16 * w + 4 * g + jj, j = 16 * nj + li;
       const float e = j <= i ? expf(float(Gd[i] - Gd[j])) : 0.f;
       Am[i][j] = j < i ? Bs[i] * e * kk[jj] : 0.f;
-      const float p = e * qk[jj];
-      const bf16_t h = __builtin_bit_cast(bf16_t, (__bf16)p);
-      const bf16_t l = __builtin_bit_cast(bf16_t, (__bf16)(p - bf16_to_f32(h)));
-      tile->p_hi[i * kC + j] = h, tile->p_lo[i * kC + j] = l;
-      tile->pt_hi[j * kC + i] = h, tile->pt_lo[j * kC + i] = l;
+      pq[nj][jj] = e * qk[jj];
     }
   }
+  // Every lane of the strip has read its Q rows (the MFMAs above): wave-level order suffices.
+  __builtin_amdgcn_wave_barrier();
+#pragma unroll
+  for (int nj = 0; nj < 4; ++nj)
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      const int i = 16 * w + 4 * g + jj, j = 16 * nj + li;
+      const float x = pq[nj][jj];
+      const __bf16 h = (__bf16)x;
+      Qb[i][j] = h;
+      Qb[i][64 + j] = (__bf16)(x - (float)h);
+    }
   __syncthreads();
+  // P rows (thread -> row tid / 4, 16 columns) and P^T rows (transposing reads of P's columns), as 16-byte stores.
+  {
+    const int i = tid >> 2, j0 = (tid & 3) * 16;
+#pragma unroll
+    for (int hl = 0; hl < 2; ++hl) {
+      bf16_t* dst = hl ? tile->p_lo : tile->p_hi;
+      *reinterpret_cast<uint4*>(dst + i * kC + j0) = *reinterpret_cast<const uint4*>(&Qb[i][64 * hl + j0]);
+      *reinterpret_cast<uint4*>(dst + i * kC + j0 + 8) = *reinterpret_cast<const uint4*>(&Qb[i][64 * hl + j0 + 8]);
+    }
+    // Wave w: P^T rows 16 w + n (n = lane % 16), columns 32 h + 8 (lane / 16) .. + 7, for h = 0, 1 and hi, lo.
+#pragma unroll
+    for (int hl = 0; hl < 2; ++hl)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const bf16x8 v = lds_tr8(&Qb[32 * h][64 * hl + 16 * w], kLDK, tid);
+        bf16_t* dst = hl ? tile->pt_lo : tile->pt_hi;
+        *reinterpret_cast<bf16x8*>(dst + (16 * w + li) * kC + 32 * h + 8 * g) = v;
+      }
+  }
 
   // Diagonal blocks: thread -> column j of block bd; the column lives in registers through the substitution.
   if (tid < kC) {
