@@ -15,13 +15,19 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kLDK = 144;  // rows 0..3 of a transposing read on distinct banks
-constexpr int kLDF = kC + 1;  // float rows, padded
+constexpr int kLDF = kC + 4;  // float rows, padded (16-byte aligned)
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+// v_mfma_f32_16x16x16_bf16: lane l holds A[l % 16][4 (l / 16) + j], B[4 (l / 16) + j][l % 16], j = 0..3.
+__device__ __forceinline__ f32x4 mma16(f32x4 c, s16x4 a, s16x4 b) {
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+}
 
 __global__ __launch_bounds__(kThreads) void chunk_prep_kernel(ChunkArgs a) {
   __shared__ __bf16 Kb[kC][kLDK], Qb[kC][kLDK];
   __shared__ float Am[kC][kLDF];
   __shared__ float Tm[kC][kLDF];
-  __shared__ float Ws[3][16][17];
   __shared__ double Gd[kC];
   __shared__ float Bs[kC];
 
@@ -151,22 +157,41 @@ __global__ __launch_bounds__(kThreads) void chunk_prep_kernel(ChunkArgs a) {
     if ((j >> 4) > (i >> 4)) Tm[i][j] = 0.f;
   }
   __syncthreads();
-  // Off-diagonal blocks at distance d = I - J: W = sum_{J <= K < I} A_IK T_KJ, then T_IJ = -T_II W.
+  // Off-diagonal blocks at distance d = I - J, one wave per block (wave w: I = d + w, J = w), on MFMA with split
+  // float32 operands:
+  //   W = sum_{J <= K < I} A_IK T_KJ    16 x 16 x 16d, k zero-padded to a multiple of 32
+  //   T_IJ = -T_II W                    16 x 16 x 16, with W's result tile as the B operand (k = W's rows)
   for (int d = 1; d < 4; ++d) {
-    const int nblk = 4 - d;
-    for (int e = tid; e < nblk * 256; e += kThreads) {
-      const int b = e >> 8, I = d + b, J = I - d, il = (e & 255) >> 4, jl = e & 15;
-      const int i = 16 * I + il, j = 16 * J + jl;
-      float acc = 0.f;
-      for (int k = 16 * J; k < 16 * I; ++k) acc += Am[i][k] * Tm[k][j];
-      Ws[b][il][jl] = acc;
-    }
-    __syncthreads();
-    for (int e = tid; e < nblk * 256; e += kThreads) {
-      const int b = e >> 8, I = d + b, J = I - d, il = (e & 255) >> 4, jl = e & 15;
-      float acc = 0.f;
-      for (int m = 0; m <= il; ++m) acc += Tm[16 * I + il][16 * I + m] * Ws[b][m][jl];
-      Tm[16 * I + il][16 * J + jl] = -acc;
+    if (w < 4 - d) {
+      const int I = d + w, J = w;
+      f32x4 W = zero4();
+      for (int s = 0; s < (d + 1) / 2; ++s) {
+        const int k0 = 16 * J + 32 * s + 8 * g;
+        const bool in = k0 < 16 * I;  // whole groups of 8 columns are in or out
+        float x[8], y[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          x[j] = in ? Am[16 * I + li][k0 + j] : 0.f;  // A rows 16 I + li, columns k
+          y[j] = in ? Tm[k0 + j][16 * J + li] : 0.f;  // T rows k, column 16 J + li
+        }
+        W = mma3(W, split8(x), split8(y));
+      }
+      s16x4 th, tl, wh, wl;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float t = Tm[16 * I + li][16 * I + 4 * g + j];  // T_II rows li, k = 4g + j
+        const __bf16 a = (__bf16)t, b = (__bf16)W[j];
+        th[j] = __builtin_bit_cast(short, a);
+        tl[j] = __builtin_bit_cast(short, (__bf16)(t - (float)a));
+        wh[j] = __builtin_bit_cast(short, b);
+        wl[j] = __builtin_bit_cast(short, (__bf16)(W[j] - (float)b));
+      }
+      f32x4 R = zero4();
+      R = mma16(R, th, wh);
+      R = mma16(R, th, wl);
+      R = mma16(R, tl, wh);
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) Tm[16 * I + 4 * g + jj][16 * J + li] = -R[jj];
     }
     __syncthreads();
   }
