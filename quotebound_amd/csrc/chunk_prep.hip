@@ -146,7 +146,7 @@ __global__ __launch_bounds__(kThreads) void chunk_prep_kernel(ChunkArgs a) {
     for (int il = 0; il < 16; ++il) {
       float v = il == jl ? 1.f : 0.f;
 #pragma unroll
-      for (int kl = 0; kl < il; ++kl) v -= kl >= jl ? Am[b0 + il][b0 + kl] * x[kl] : 0.f;
+      for (int kl = 0; kl < il; ++kl) v -= Am[b0 + il][b0 + kl] * x[kl];  // x[kl] = 0 for kl < jl
       x[il] = il >= jl ? v : 0.f;
     }
 #pragma unroll
