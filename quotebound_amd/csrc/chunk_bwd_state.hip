@@ -178,7 +178,8 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_state_kernel(ChunkArgs a) 
     dr = zero4();
 #pragma unroll
     for (int s = 0; s < 2; ++s)
-      dr = mma3(dr, Split8{f.t[2 * s], f.t[2 * s + 1]},
+      if (32 * s + 31 >= 16 * w)  // Tb^T is zero below the diagonal
+        dr = mma3(dr, Split8{f.t[2 * s], f.t[2 * s + 1]},
                 Split8{lds8(&dDth[li][32 * s + 8 * g]), lds8(&dDtl[li][32 * s + 8 * g])});
 #pragma unroll
     for (int jj = 0; jj < 4; ++jj) {

@@ -81,7 +81,8 @@ __global__ __launch_bounds__(kThreads) void chunk_fwd_kernel(ChunkArgs a) {
     const bf16_t* hi = side ? tl->p_hi : tl->tb_hi;
     const bf16_t* lo = side ? tl->p_lo : tl->tb_lo;
     const int ar = (16 * wp + li) * kC + 8 * g;
-    f.f[0] = gld8(hi + ar), f.f[1] = gld8(lo + ar), f.f[2] = gld8(hi + ar + 32), f.f[3] = gld8(lo + ar + 32);
+    f.f[0] = gld8(hi + ar), f.f[1] = gld8(lo + ar);
+    if (wp >= 2) f.f[2] = gld8(hi + ar + 32), f.f[3] = gld8(lo + ar + 32);  // columns 32.. are zero for rows < 32
   };
 
   // y of a chunk (waves 4-7) is stored during the next chunk, after that chunk's inputs are staged, so no wait for
@@ -151,9 +152,11 @@ __global__ __launch_bounds__(kThreads) void chunk_fwd_kernel(ChunkArgs a) {
     if (!side) {  // Delta = Tb R for positions i0 + jj
       f32x4 dl = zero4();
 #pragma unroll
-      for (int s = 0; s < 2; ++s)
-        dl = mma3(dl, Split8{f.f[2 * s], f.f[2 * s + 1]},
-                  Split8{lds8(&Rth[li][32 * s + 8 * g]), lds8(&Rtl[li][32 * s + 8 * g])});
+      for (int s = 0; s < 2; ++s) {
+        if (32 * s <= 16 * wp + 15)  // Tb is zero above the diagonal
+          dl = mma3(dl, Split8{f.f[2 * s], f.f[2 * s + 1]},
+                    Split8{lds8(&Rth[li][32 * s + 8 * g]), lds8(&Rtl[li][32 * s + 8 * g])});
+      }
       f32x4 dd;
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj) dd[jj] = dec[i0 + jj] * dl[jj];
