@@ -8,6 +8,11 @@ divided by its mean duration. cpu_baseline times the oracle (the CPU restatement
 the same inputs.
 
 python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--design auto|1|2] [--workload qwen35_4b] [--no-cpu]
+                [--copy-probe-mib N]
+
+roofline.traffic is the dominant kernel's HBM bytes per launch as rocprofv3 counted them (FETCH_SIZE + WRITE_SIZE,
+each scaled by what the counter reads for a plain device copy of known size), read from profiles/traffic.json
+when that file holds a measurement for this workload; --copy-probe-mib runs such a copy first, for those runs.
 """
 from __future__ import annotations
 
@@ -174,7 +179,32 @@ def run_design(torch, hip, lib, w, dev, design, steps, warmup):
             "nc": lib.num_chunks(desc_f)}, None
 
 
-def cpu_baseline(w, inp, budget_s=12.0, max_reps=5):
+def traffic_of(w, kernel):
+    """HBM bytes per launch of kernel from profiles/traffic.json (rocprofv3 FETCH_SIZE and WRITE_SIZE in KiB per
+    dispatch, scaled by the copy calibration recorded with them), or None."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            t = json.load(f)
+    except (OSError, ValueError):
+        return None
+    k = t.get("workloads", {}).get(w.name, {}).get(kernel)
+    cal = t.get("calibration")
+    if not k or not cal:
+        return None
+    return k["fetch_kib"] * 1024 * cal["fetch_factor"] + k["write_kib"] * 1024 * cal["write_factor"]
+
+
+def copy_probe(torch, mib):
+    """A plain device-to-device copy of mib MiB, three times: the calibration kernel of the traffic counters."""
+    src = torch.empty(mib << 20, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+
+
+def cpu_baseline(w, inp, budget_s=12.0, max_reps=60):
     """The oracle's float32 forward + backward on the host cores, repeated until about budget_s."""
     from oracle import gdn_ref
 
@@ -202,6 +232,7 @@ def main():
     ap.add_argument("--design", default="auto")
     ap.add_argument("--workload", default="qwen35_4b")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-probe-mib", type=int, default=0)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported (the recurrence shards "
@@ -218,6 +249,8 @@ def main():
     inp = make_inputs(w)
     dev = to_device(inp, "cuda")
     torch.cuda.synchronize()
+    if args.copy_probe_mib > 0:
+        copy_probe(torch, args.copy_probe_mib)
     hip = Hip()
     designs = [lib.RECURRENT, lib.CHUNKED] if args.design == "auto" else [int(args.design)]
     results = {}
@@ -239,7 +272,7 @@ def main():
     kind, amount = algorithmic_work(w, dom, r["nc"], best)
     roof = roofline_of(kind, amount, r["kernels_ms"][dom])
     roof.update({"kernel": dom, "mean_ms": r["kernels_ms"][dom], "algorithmic_" + kind + "_per_launch": amount,
-                 "traffic": None})
+                 "traffic": traffic_of(w, dom)})
     t_roof, nbytes, nflops = step_roof_us(w, r["nc"])
     out = {
         "metric": METRIC,
