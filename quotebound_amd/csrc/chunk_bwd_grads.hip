@@ -402,9 +402,11 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
           const int jj = 32 * s + 8 * g + j;
-          // M_ij = exp(G_i - G_j) only where j <= i (elsewhere the exponent is positive and may overflow)
-          x[j] = jj <= ip ? sf[edP + ip * kLF + jj] * __expf(Gf[ip] - Gf[jj]) : 0.f;
-          y[j] = jj >= ip ? sf[edP + jj * kLF + ip] * __expf(Gf[jj] - Gf[ip]) : 0.f;
+          // M_ij = exp(G_i - G_j) where j <= i. dP is stored zero elsewhere; there the exponent is positive, so it
+          // is clamped at 0 to keep exp finite. No branch: every load is in bounds.
+          const float gi = Gf[ip], gj = Gf[jj];
+          x[j] = sf[edP + ip * kLF + jj] * __expf(fminf(gi - gj, 0.f));
+          y[j] = sf[edP + jj * kLF + ip] * __expf(fminf(gj - gi, 0.f));
           z[j] = sf[edTb + ip * kLF + jj] * bet[jj];
         }
         AdPM[s] = split8(x);
@@ -464,7 +466,8 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) {
           const int pr = i0 + jj;
-          const float dae = mcol < pr ? -da[jj] * __expf(Gf[pr] - Gf[mcol]) : 0.f;  // dA_pm E_pm
+          const float e = __expf(fminf(Gf[pr] - Gf[mcol], 0.f));  // finite everywhere; used where mcol < pr
+          const float dae = mcol < pr ? -da[jj] * e : 0.f;           // dA_pm E_pm
           const float prod = dae * kk[mi][jj];
           rowp[jj] += prod;
           colp += bet[pr] * prod;
