@@ -33,6 +33,7 @@ constexpr int kThreads = 512;
 constexpr int kLS = 144;  // S0, dS [32][128]
 constexpr int kLY = 48;   // dY [64][32]
 constexpr int kLP = 72;   // [32][64]
+constexpr int kLT = 72;   // Tb, P [64][64]
 constexpr int oS0h = 0, oS0l = oS0h + 32 * kLS, odSh = oS0l + 32 * kLS, odSl = odSh + 32 * kLS;
 constexpr int odYh = odSl + 32 * kLS, odYl = odYh + kC * kLY;
 constexpr int oRh = odYl + kC * kLY, oRl = oRh + 32 * kLP;        // R = V - diag(exp G) K S0^T
@@ -64,6 +65,9 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
   constexpr bool kExactDy = std::is_same<OutT, bf16_t>::value;
   __shared__ __align__(16) unsigned char smem[kSmemBytes];
   __shared__ __align__(16) __bf16 Kres[kC * kLK];  // the chunk's K rows, for the whole block
+  // The value head's Tb and P (bf16 hi and lo, rows i, columns j), staged once per head: A operands of Tb rows
+  // directly, of Tb^T and P^T rows through the transposing read.
+  __shared__ __align__(16) __bf16 TbL[2][kC * kLT], PL[2][kC * kLT];
   __shared__ float gam[kC], dec[kC], bet[kC], Gf[kC];
   __shared__ float gpos[2][kC], hpos[2][kC], tpos[2][kC];
   __shared__ float x2r[2][kC], x2c[4][kC], dbTp[4][kC], dbAp[2][kC], x1cp[4][kC], red[kThreads / 64];
@@ -101,6 +105,17 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
     const Tile* tl = a.tiles + sh;
     __syncthreads();
     if (tid < kC) gam[tid] = tl->gam[tid], dec[tid] = tl->dec[tid], bet[tid] = tl->beta[tid], Gf[tid] = tl->G[tid];
+    {  // Tb and P, hi and lo: thread -> row tid / 8, columns 8 (tid % 8) ..
+      const int i = tid >> 3, c8 = (tid & 7) * 8, at = i * kC + c8, lt8 = i * kLT + c8;
+      const uint4 v0 = *reinterpret_cast<const uint4*>(tl->tb_hi + at);
+      const uint4 v1 = *reinterpret_cast<const uint4*>(tl->tb_lo + at);
+      const uint4 v2 = *reinterpret_cast<const uint4*>(tl->p_hi + at);
+      const uint4 v3 = *reinterpret_cast<const uint4*>(tl->p_lo + at);
+      *reinterpret_cast<uint4*>(TbL[0] + lt8) = v0;
+      *reinterpret_cast<uint4*>(TbL[1] + lt8) = v1;
+      *reinterpret_cast<uint4*>(PL[0] + lt8) = v2;
+      *reinterpret_cast<uint4*>(PL[1] + lt8) = v3;
+    }
     f32x4 dPt[2], dTbt[2], dQi[4];  // dPt, dTbt: key tiles m = 2 hw + mi; lane -> column i = ip, rows j
 #pragma unroll
     for (int t = 0; t < 2; ++t) dPt[t] = zero4(), dTbt[t] = zero4();
@@ -157,20 +172,6 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
       const float4* xs = nb.xs;
       const float4* ys = nb.ys;
       const uint4 yraw = nb.yraw;
-      // A operands from the tile for this block (reloaded per block from L2 to keep them out of the loop-carried
-      // registers): Tb rows ip (k = j), Tb^T rows ip (k = j) and P^T rows ip (k = i).
-      Split8 TbA[2], TbtA[2], PA[2];
-      {
-        const Tile* tb = tl;
-        asm volatile("" : "+s"(tb));  // the loads stay inside the loop
-        const int ar = ip * kC + 8 * g;
-#pragma unroll
-        for (int s = 0; s < 2; ++s) {
-          TbA[s] = Split8{gld8(tb->tb_hi + ar + 32 * s), gld8(tb->tb_lo + ar + 32 * s)};
-          TbtA[s] = Split8{gld8(tb->tbt_hi + ar + 32 * s), gld8(tb->tbt_lo + ar + 32 * s)};
-          PA[s] = Split8{gld8(tb->pt_hi + ar + 32 * s), gld8(tb->pt_lo + ar + 32 * s)};
-        }
-      }
       __syncthreads();  // the previous block's readers of LDS are done
 
       {  // Stage S0, dS rows and dY rows as hi / lo.
@@ -227,7 +228,8 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
         const int at = r * kLP + 32 * s + 8 * g;
-        dl = mma3(dl, TbA[s], Split8{lds8(sb + oRh + at), lds8(sb + oRl + at)});
+        const Split8 TbA{lds8(TbL[0] + ip * kLT + 32 * s + 8 * g), lds8(TbL[1] + ip * kLT + 32 * s + 8 * g)};
+        dl = mma3(dl, TbA, Split8{lds8(sb + oRh + at), lds8(sb + oRl + at)});
       }
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj) dd[jj] = dec[i0 + jj] * kds[jj];
@@ -235,10 +237,12 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
       for (int s = 0; s < 2; ++s) {
         if (32 * s + 31 >= 16 * pw) {  // P^T is zero below the diagonal
           const int at = 32 * s * kLY + 16 * hw;
+          // P^T rows ip (k = i): P's rows 32s.., column ip.
+          const Split8 PA{lds_tr8(PL[0] + 32 * s * kLT + 16 * pw, kLT, lt), lds_tr8(PL[1] + 32 * s * kLT + 16 * pw, kLT, lt)};
           if constexpr (kExactDy)
-            dd = mma2(dd, PA[s], lds_tr8(sb + odYh + at, kLY, lt));
+            dd = mma2(dd, PA, lds_tr8(sb + odYh + at, kLY, lt));
           else
-            dd = mma3(dd, PA[s], Split8{lds_tr8(sb + odYh + at, kLY, lt), lds_tr8(sb + odYl + at, kLY, lt)});
+            dd = mma3(dd, PA, Split8{lds_tr8(sb + odYh + at, kLY, lt), lds_tr8(sb + odYl + at, kLY, lt)});
         }
       }
       {
@@ -259,8 +263,13 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
         f32x4 dr = zero4();
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
-          const int at = r * kLP + 32 * s + 8 * g;
-          dr = mma3(dr, TbtA[s], Split8{lds8(sb + odDh + at), lds8(sb + odDl + at)});
+          if (32 * s + 31 >= 16 * pw) {  // Tb^T is zero below the diagonal
+            const int at = r * kLP + 32 * s + 8 * g;
+            // Tb^T rows ip (k = j): Tb's rows 32s.., column ip.
+            const Split8 TbtA{lds_tr8(TbL[0] + 32 * s * kLT + 16 * pw, kLT, lt),
+                              lds_tr8(TbL[1] + 32 * s * kLT + 16 * pw, kLT, lt)};
+            dr = mma3(dr, TbtA, Split8{lds8(sb + odDh + at), lds8(sb + odDl + at)});
+          }
         }
         float gdr[4];
 #pragma unroll
@@ -341,8 +350,8 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
 #pragma unroll
       for (int mi = 0; mi < 2; ++mi) {
         const int j0 = 16 * (2 * hw + mi) + 4 * g;
-        const uint2 ph = *reinterpret_cast<const uint2*>(tl->p_hi + ip * kC + j0);
-        const uint2 pl = *reinterpret_cast<const uint2*>(tl->p_lo + ip * kC + j0);
+        const uint2 ph = *reinterpret_cast<const uint2*>(PL[0] + ip * kLT + j0);
+        const uint2 pl = *reinterpret_cast<const uint2*>(PL[1] + ip * kLT + j0);
         const float4 t4 = *reinterpret_cast<const float4*>(tl->t + ip * kC + j0);
         const uint32_t hw4[2] = {ph.x, ph.y}, lw4[2] = {pl.x, pl.y};
         const float tv4[4] = {t4.x, t4.y, t4.z, t4.w};
