@@ -32,8 +32,8 @@ constexpr int kThreads = 512;
 // each 16-byte read touches, on distinct banks.
 constexpr int kLS = 144;  // S0, dS [32][128]
 constexpr int kLY = 48;   // dY [64][32]
-constexpr int kLP = 72;   // [32][64]
-constexpr int kLT = 72;   // Tb, P [64][64]
+constexpr int kLP = 80;   // [32][64]
+constexpr int kLT = 80;   // Tb, P [64][64]
 constexpr int oS0h = 0, oS0l = oS0h + 32 * kLS, odSh = oS0l + 32 * kLS, odSl = odSh + 32 * kLS;
 constexpr int odYh = odSl + 32 * kLS, odYl = odYh + kC * kLY;
 constexpr int oRh = odYl + kC * kLY, oRl = oRh + 32 * kLP;        // R = V - diag(exp G) K S0^T
@@ -49,7 +49,10 @@ constexpr int eQb = 0;             // bf16 offset
 constexpr int eF = (kC * kLK) / 2;  // first f32 offset
 constexpr int kLF = kC + 4;             // f32 [.][64] rows
 constexpr int edP = eF, edTb = edP + kC * kLF, eT = edTb + kC * kLF, eZt = eT + kC * kLF;
-constexpr int kEndBytes = (eZt + kC * kLF) * 4;
+// Per-position partial sums that the end phase produces and its last step reads.
+constexpr int eX2r = eZt + kC * kLF, eX2c = eX2r + 2 * kC, edbT = eX2c + 4 * kC, edbA = edbT + 4 * kC;
+constexpr int ex1c = edbA + 2 * kC, etq = ex1c + 4 * kC;
+constexpr int kEndBytes = (etq + 2 * kC) * 4;
 constexpr int kSmemBytes = kLoopBytes > kEndBytes ? kLoopBytes : kEndBytes;
 
 // Four consecutive values at element offset at (a multiple of 4) of the hi and lo matrices.
@@ -69,10 +72,16 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
   // directly, of Tb^T and P^T rows through the transposing read.
   __shared__ __align__(16) __bf16 TbL[2][kC * kLT], PL[2][kC * kLT];
   __shared__ float gam[kC], dec[kC], bet[kC], Gf[kC];
-  __shared__ float gpos[2][kC], hpos[2][kC], tpos[2][kC];
-  __shared__ float x2r[2][kC], x2c[4][kC], dbTp[4][kC], dbAp[2][kC], x1cp[4][kC], red[kThreads / 64];
+  __shared__ float gpos[2][kC], hpos[2][kC], red[kThreads / 64];
   __bf16* sb = reinterpret_cast<__bf16*>(smem);
   float* sf = reinterpret_cast<float*>(smem);
+  typedef float Row[kC];
+  Row* x2r = reinterpret_cast<Row*>(sf + eX2r);
+  Row* x2c = reinterpret_cast<Row*>(sf + eX2c);
+  Row* dbTp = reinterpret_cast<Row*>(sf + edbT);
+  Row* dbAp = reinterpret_cast<Row*>(sf + edbA);
+  Row* x1cp = reinterpret_cast<Row*>(sf + ex1c);
+  Row* tpos = reinterpret_cast<Row*>(sf + etq);
 
   const int total = int(a.lay.NC) * a.Hk;
   const int wid = xcd_remap(blockIdx.x, total);
@@ -93,7 +102,7 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
   // The chunk's K rows (A operands of K S0^T, K dS^T, K K^T; B of the K products of the end phase).
   for (int e = tid; e < kC * 16; e += kThreads) {
     const int t = e >> 4, c8 = (e & 15) * 8;
-    *reinterpret_cast<uint4*>(Kres + t * kLK + c8) = buf_ld16(krs, uint32_t(t * sk + c8) * 2);
+    *reinterpret_cast<uint4*>(Kres + swz(t, c8, kLK)) = buf_ld16(krs, uint32_t(t * sk + c8) * 2);
   }
   f32x4 dQ[4], dK[4];  // columns 16 (4 hw + t) + li, rows 16 pw + 4 g + jj
 #pragma unroll
@@ -106,7 +115,7 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
     __syncthreads();
     if (tid < kC) gam[tid] = tl->gam[tid], dec[tid] = tl->dec[tid], bet[tid] = tl->beta[tid], Gf[tid] = tl->G[tid];
     {  // Tb and P, hi and lo: thread -> row tid / 8, columns 8 (tid % 8) ..
-      const int i = tid >> 3, c8 = (tid & 7) * 8, at = i * kC + c8, lt8 = i * kLT + c8;
+      const int i = tid >> 3, c8 = (tid & 7) * 8, at = i * kC + c8, lt8 = swz(i, c8, kLT);
       const uint4 v0 = *reinterpret_cast<const uint4*>(tl->tb_hi + at);
       const uint4 v1 = *reinterpret_cast<const uint4*>(tl->tb_lo + at);
       const uint4 v2 = *reinterpret_cast<const uint4*>(tl->p_hi + at);
@@ -180,15 +189,15 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
 #pragma unroll
         for (int u = 0; u < 8; ++u) sds += x[u] * y[u];
         const Split8 xsp = split8(x), ysp = split8(y);
-        const int at = sr * kLS + sc;
+        const int at = swz(sr, sc, kLS);
         *reinterpret_cast<bf16x8*>(sb + oS0h + at) = xsp.hi;
         *reinterpret_cast<bf16x8*>(sb + oS0l + at) = xsp.lo;
         *reinterpret_cast<bf16x8*>(sb + odSh + at) = ysp.hi;
         *reinterpret_cast<bf16x8*>(sb + odSl + at) = ysp.lo;
         if constexpr (kExactDy) {
-          *reinterpret_cast<uint2*>(sb + odYh + iy * kLY + r4) = uint2{yraw.x, yraw.y};
+          *reinterpret_cast<uint2*>(sb + odYh + swz(iy, r4, kLY)) = uint2{yraw.x, yraw.y};
         } else {
-          put4(sb + odYh, sb + odYl, iy * kLY + r4, __uint_as_float(yraw.x), __uint_as_float(yraw.y),
+          put4(sb + odYh, sb + odYl, swz(iy, r4, kLY), __uint_as_float(yraw.x), __uint_as_float(yraw.y),
                __uint_as_float(yraw.z), __uint_as_float(yraw.w));
         }
       }
@@ -201,16 +210,16 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
 
       // The wave's own dY rows (i = ip, k = r = 8g..): A of dY S0, B of Delta dY^T.
       Split8 dYo;
-      dYo.hi = lds8(sb + odYh + ip * kLY + 8 * g);
-      if constexpr (!kExactDy) dYo.lo = lds8(sb + odYl + ip * kLY + 8 * g);
+      dYo.hi = lds8(sb + odYh + swz(ip, 8 * g, kLY));
+      if constexpr (!kExactDy) dYo.lo = lds8(sb + odYl + swz(ip, 8 * g, kLY));
 
       // Phase 1: KS and KdS for positions i = 16 pw + 4g + jj, state rows r = 16 hw + li.
       const int r = 16 * hw + li, i0 = 16 * pw + 4 * g;
       f32x4 ks = zero4(), kds = zero4();
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        const int at = r * kLS + 32 * s + 8 * g;
-        const bf16x8 ka = lds8(Kres + ip * kLK + 32 * s + 8 * g);
+        const int at = swz(r, 32 * s + 8 * g, kLS);
+        const bf16x8 ka = lds8(Kres + swz(ip, 32 * s + 8 * g, kLK));
         ks = mma(mma(ks, ka, lds8(sb + oS0h + at)), ka, lds8(sb + oS0l + at));
         kds = mma(mma(kds, ka, lds8(sb + odSh + at)), ka, lds8(sb + odSl + at));
       }
@@ -220,15 +229,15 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
         gks[jj] = gam[i0 + jj] * ks[jj];
         rv[jj] = vv[jj] - gks[jj];
       }
-      put4(sb + oRh, sb + oRl, r * kLP + i0, rv[0], rv[1], rv[2], rv[3]);
+      put4(sb + oRh, sb + oRl, swz(r, i0, kLP), rv[0], rv[1], rv[2], rv[3]);
       __syncthreads();
 
       // Phase 2: Delta = Tb R and dDelta = P^T dY + D KdS (rows: the wave's positions; lane: row r).
       f32x4 dl = zero4(), dd;
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
-        const int at = r * kLP + 32 * s + 8 * g;
-        const Split8 TbA{lds8(TbL[0] + ip * kLT + 32 * s + 8 * g), lds8(TbL[1] + ip * kLT + 32 * s + 8 * g)};
+        const int at = swz(r, 32 * s + 8 * g, kLP), atb = swz(ip, 32 * s + 8 * g, kLT);
+        const Split8 TbA{lds8(TbL[0] + atb), lds8(TbL[1] + atb)};
         dl = mma3(dl, TbA, Split8{lds8(sb + oRh + at), lds8(sb + oRl + at)});
       }
 #pragma unroll
@@ -238,11 +247,11 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
         if (32 * s + 31 >= 16 * pw) {  // P^T is zero below the diagonal
           const int at = 32 * s * kLY + 16 * hw;
           // P^T rows ip (k = i): P's rows 32s.., column ip.
-          const Split8 PA{lds_tr8(PL[0] + 32 * s * kLT + 16 * pw, kLT, lt), lds_tr8(PL[1] + 32 * s * kLT + 16 * pw, kLT, lt)};
+          const Split8 PA{lds_tr8s(PL[0] + 32 * s * kLT + 16 * pw, kLT, lt), lds_tr8s(PL[1] + 32 * s * kLT + 16 * pw, kLT, lt)};
           if constexpr (kExactDy)
-            dd = mma2(dd, PA, lds_tr8(sb + odYh + at, kLY, lt));
+            dd = mma2(dd, PA, lds_tr8s(sb + odYh + at, kLY, lt));
           else
-            dd = mma3(dd, PA, Split8{lds_tr8(sb + odYh + at, kLY, lt), lds_tr8(sb + odYl + at, kLY, lt)});
+            dd = mma3(dd, PA, Split8{lds_tr8s(sb + odYh + at, kLY, lt), lds_tr8s(sb + odYl + at, kLY, lt)});
         }
       }
       {
@@ -252,9 +261,9 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
           hD[jj] += dec[i0 + jj] * dl[jj] * kds[jj];
           ddl[jj] = dec[i0 + jj] * dl[jj];
         }
-        put4(sb + oDh, sb + oDl, r * kLP + i0, dl[0], dl[1], dl[2], dl[3]);
-        put4(sb + oDDh, sb + oDDl, r * kLP + i0, ddl[0], ddl[1], ddl[2], ddl[3]);
-        put4(sb + odDh, sb + odDl, r * kLP + i0, dd[0], dd[1], dd[2], dd[3]);
+        put4(sb + oDh, sb + oDl, swz(r, i0, kLP), dl[0], dl[1], dl[2], dl[3]);
+        put4(sb + oDDh, sb + oDDl, swz(r, i0, kLP), ddl[0], ddl[1], ddl[2], ddl[3]);
+        put4(sb + odDh, sb + odDl, swz(r, i0, kLP), dd[0], dd[1], dd[2], dd[3]);
       }
       __syncthreads();
 
@@ -264,10 +273,10 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
           if (32 * s + 31 >= 16 * pw) {  // Tb^T is zero below the diagonal
-            const int at = r * kLP + 32 * s + 8 * g;
+            const int at = swz(r, 32 * s + 8 * g, kLP);
             // Tb^T rows ip (k = j): Tb's rows 32s.., column ip.
-            const Split8 TbtA{lds_tr8(TbL[0] + 32 * s * kLT + 16 * pw, kLT, lt),
-                              lds_tr8(TbL[1] + 32 * s * kLT + 16 * pw, kLT, lt)};
+            const Split8 TbtA{lds_tr8s(TbL[0] + 32 * s * kLT + 16 * pw, kLT, lt),
+                              lds_tr8s(TbL[1] + 32 * s * kLT + 16 * pw, kLT, lt)};
             dr = mma3(dr, TbtA, Split8{lds8(sb + odDh + at), lds8(sb + odDl + at)});
           }
         }
@@ -277,22 +286,22 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
           gpart[jj] -= dr[jj] * gks[jj];
           gdr[jj] = -gam[i0 + jj] * dr[jj];
         }
-        put4(sb + oGdRh, sb + oGdRl, r * kLP + i0, gdr[0], gdr[1], gdr[2], gdr[3]);
+        put4(sb + oGdRh, sb + oGdRl, swz(r, i0, kLP), gdr[0], gdr[1], gdr[2], gdr[3]);
       }
       {
         // dDelta[i][r] of the wave's positions as B (k = r, n = i).
-        const Split8 BdD{lds_tr8(sb + odDh + 16 * pw, kLP, lt), lds_tr8(sb + odDl + 16 * pw, kLP, lt)};
+        const Split8 BdD{lds_tr8s(sb + odDh + 16 * pw, kLP, lt), lds_tr8s(sb + odDl + 16 * pw, kLP, lt)};
 #pragma unroll
         for (int mi = 0; mi < 2; ++mi) {
           const int m = 2 * hw + mi;
           if (m <= pw) {
             // Delta and R rows j of key tile m as A (m = j, k = r).
-            const Split8 AD{lds_tr8(sb + oDh + 16 * m, kLP, lt), lds_tr8(sb + oDl + 16 * m, kLP, lt)};
+            const Split8 AD{lds_tr8s(sb + oDh + 16 * m, kLP, lt), lds_tr8s(sb + oDl + 16 * m, kLP, lt)};
             if constexpr (kExactDy)
               dPt[mi] = mma2(dPt[mi], AD, dYo.hi);
             else
               dPt[mi] = mma3(dPt[mi], AD, dYo);
-            const Split8 AR{lds_tr8(sb + oRh + 16 * m, kLP, lt), lds_tr8(sb + oRl + 16 * m, kLP, lt)};
+            const Split8 AR{lds_tr8s(sb + oRh + 16 * m, kLP, lt), lds_tr8s(sb + oRl + 16 * m, kLP, lt)};
             dTbt[mi] = mma3(dTbt[mi], AR, BdD);
           }
         }
@@ -301,13 +310,13 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
 
       // Phase 4: dQ_inter += dY S0; dK += -diag(exp G) dR S0 + D Delta dS (columns of this half).
       {
-        const Split8 AGdR{lds_tr8(sb + oGdRh + 16 * pw, kLP, lt), lds_tr8(sb + oGdRl + 16 * pw, kLP, lt)};
-        const Split8 ADD{lds_tr8(sb + oDDh + 16 * pw, kLP, lt), lds_tr8(sb + oDDl + 16 * pw, kLP, lt)};
+        const Split8 AGdR{lds_tr8s(sb + oGdRh + 16 * pw, kLP, lt), lds_tr8s(sb + oGdRl + 16 * pw, kLP, lt)};
+        const Split8 ADD{lds_tr8s(sb + oDDh + 16 * pw, kLP, lt), lds_tr8s(sb + oDDl + 16 * pw, kLP, lt)};
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
           const int c0 = 16 * (4 * hw + t);
-          const Split8 B0{lds_tr8(sb + oS0h + c0, kLS, lt), lds_tr8(sb + oS0l + c0, kLS, lt)};
-          const Split8 B1{lds_tr8(sb + odSh + c0, kLS, lt), lds_tr8(sb + odSl + c0, kLS, lt)};
+          const Split8 B0{lds_tr8s(sb + oS0h + c0, kLS, lt), lds_tr8s(sb + oS0l + c0, kLS, lt)};
+          const Split8 B1{lds_tr8s(sb + odSh + c0, kLS, lt), lds_tr8s(sb + odSl + c0, kLS, lt)};
           if constexpr (kExactDy)
             dQi[t] = mma2(dQi[t], dYo.hi, B0);
           else
@@ -340,7 +349,7 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
     // column sums of dP * P (the P factor's part of dG) and the column sums of dTb * T (dbeta's T part).
     for (int e = tid; e < kC * 16; e += kThreads) {
       const int t = e >> 4, c8 = (e & 15) * 8;
-      *reinterpret_cast<uint4*>(sb + eQb + t * kLK + c8) = buf_ld16(qrs, uint32_t(t * sk + c8) * 2);
+      *reinterpret_cast<uint4*>(sb + eQb + swz(t, c8, kLK)) = buf_ld16(qrs, uint32_t(t * sk + c8) * 2);
     }
     for (int q = tid; q < kC * kC; q += kThreads) sf[eT + (q >> 6) * kLF + (q & 63)] = tl->t[q];
     {
@@ -350,8 +359,8 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
 #pragma unroll
       for (int mi = 0; mi < 2; ++mi) {
         const int j0 = 16 * (2 * hw + mi) + 4 * g;
-        const uint2 ph = *reinterpret_cast<const uint2*>(PL[0] + ip * kLT + j0);
-        const uint2 pl = *reinterpret_cast<const uint2*>(PL[1] + ip * kLT + j0);
+        const uint2 ph = *reinterpret_cast<const uint2*>(PL[0] + swz(ip, j0, kLT));
+        const uint2 pl = *reinterpret_cast<const uint2*>(PL[1] + swz(ip, j0, kLT));
         const float4 t4 = *reinterpret_cast<const float4*>(tl->t + ip * kC + j0);
         const uint32_t hw4[2] = {ph.x, ph.y}, lw4[2] = {pl.x, pl.y};
         const float tv4[4] = {t4.x, t4.y, t4.z, t4.w};
@@ -386,7 +395,7 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) {
           const int i = i0 + jj, c = 16 * (4 * hw + t) + li;
-          tq[jj] += (float)sb[eQb + i * kLK + c] * dQi[t][jj];
+          tq[jj] += (float)sb[eQb + swz(i, c, kLK)] * dQi[t][jj];
           dQ[t][jj] += gam[i] * dQi[t][jj];
         }
 #pragma unroll
@@ -401,7 +410,7 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
         if (m <= pw) {
 #pragma unroll
           for (int s = 0; s < 4; ++s)
-            kk[mi] = mma(kk[mi], lds8(Kres + ip * kLK + 32 * s + 8 * g), lds8(Kres + (16 * m + li) * kLK + 32 * s + 8 * g));
+            kk[mi] = mma(kk[mi], lds8(Kres + swz(ip, 32 * s + 8 * g, kLK)), lds8(Kres + swz(16 * m + li, 32 * s + 8 * g, kLK)));
         }
       }
       Split8 AdPM[2], AdPMt[2], AdT[2];
@@ -426,8 +435,8 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
       for (int t = 0; t < 4; ++t) {
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
-          dQ[t] = mma2(dQ[t], AdPM[s], lds_tr8(Kres + 32 * s * kLK + 16 * (4 * hw + t), kLK, lt));
-          dK[t] = mma2(dK[t], AdPMt[s], lds_tr8(sb + eQb + 32 * s * kLK + 16 * (4 * hw + t), kLK, lt));
+          dQ[t] = mma2(dQ[t], AdPM[s], lds_tr8s(Kres + 32 * s * kLK + 16 * (4 * hw + t), kLK, lt));
+          dK[t] = mma2(dK[t], AdPMt[s], lds_tr8s(sb + eQb + 32 * s * kLK + 16 * (4 * hw + t), kLK, lt));
         }
       }
 #pragma unroll
@@ -511,7 +520,7 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
       for (int t = 0; t < 4; ++t) {
 #pragma unroll
         for (int s = 0; s < 2; ++s)
-          dK[t] = mma2(dK[t], A[s], lds_tr8(Kres + 32 * s * kLK + 16 * (4 * hw + t), kLK, lt));
+          dK[t] = mma2(dK[t], A[s], lds_tr8s(Kres + 32 * s * kLK + 16 * (4 * hw + t), kLK, lt));
       }
     }
     // E5 (one wave): dG per position, dg = its reverse cumulative sum (a suffix scan over the wave), and dbeta.
