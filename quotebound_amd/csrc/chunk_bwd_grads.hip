@@ -42,15 +42,16 @@ constexpr int oDDh = oDl + 32 * kLP, oDDl = oDDh + 32 * kLP;      // D Delta
 constexpr int odDh = oDDl + 32 * kLP, odDl = odDh + 32 * kLP;     // dDelta
 constexpr int oGdRh = odDl + 32 * kLP, oGdRl = oGdRh + 32 * kLP;  // -diag(exp G) dR
 constexpr int kLoopBytes = (oGdRl + 32 * kLP) * 2;
-// End-phase region (aliases the block-loop region): bf16 Q rows, then f32 64 x 64 matrices. (K rows stay in their
-// own array for the whole block.)
+// End-phase region (aliases the block-loop region), bf16 element offsets: Q rows, then the value head's T, Z^T
+// (Z = dTb diag(beta) T^T) and dKK^T, each as hi and lo 64 x 64 matrices; then float32 per-position partial sums.
+// (K rows stay in their own array for the whole block; P * M and dTb diag(beta) reuse the Tb and P arrays.)
 constexpr int kLK = 144;
-constexpr int eQb = 0;             // bf16 offset
-constexpr int eF = (kC * kLK) / 2;  // first f32 offset
-constexpr int kLF = kC + 4;             // f32 [.][64] rows
-constexpr int edP = eF, edTb = edP + kC * kLF, eT = edTb + kC * kLF, eZt = eT + kC * kLF;
-// Per-position partial sums that the end phase produces and its last step reads.
-constexpr int eX2r = eZt + kC * kLF, eX2c = eX2r + 2 * kC, edbT = eX2c + 4 * kC, edbA = edbT + 4 * kC;
+constexpr int eQb = 0;
+constexpr int eTh = eQb + kC * kLK, eTl = eTh + kC * kLT;
+constexpr int eZh = eTl + kC * kLT, eZl = eZh + kC * kLT;
+constexpr int eKh = eZl + kC * kLT, eKl = eKh + kC * kLT;
+constexpr int eF = (eKl + kC * kLT) / 2;  // first float32 offset
+constexpr int eX2r = eF, eX2c = eX2r + 2 * kC, edbT = eX2c + 4 * kC, edbA = edbT + 4 * kC;
 constexpr int ex1c = edbA + 2 * kC, etq = ex1c + 4 * kC;
 constexpr int kEndBytes = (etq + 2 * kC) * 4;
 constexpr int kSmemBytes = kLoopBytes > kEndBytes ? kLoopBytes : kEndBytes;
@@ -133,26 +134,24 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
     float gpart[4] = {0.f, 0.f, 0.f, 0.f}, hD[4] = {0.f, 0.f, 0.f, 0.f}, sds = 0.f;
     __syncthreads();
 
-    // One block's global reads (S0 and dS rows, dY, v), kept in registers from issue to staging. dy and v go through
-    // buffer resources that end at the chunk's last row, so rows past it read as zeros without a branch.
+    // One block's global reads (S0 and dS rows, dY, v), kept in registers from issue to staging. They are issued in
+    // three groups at three points of the previous block's work, so no wave stalls long on a full load queue. dy
+    // and v go through buffer resources that end at the chunk's last row, so rows past it read as zeros without a
+    // branch.
     struct BlockIn {
       float4 xs[2], ys[2];  // S0, dS: thread -> row tid / 16, columns 8 (tid % 16) .. + 7
       uint4 yraw;           // dY: thread -> position tid / 8, rows 4 (tid % 8) .. + 3
       uint16_t vraw[4];     // v at the wave's accumulator positions (16 pw + 4g + jj, column 16 hw + li)
     };
-    auto load_block = [&](BlockIn& b, int r0, int lt) {
+    auto load_rows = [&](float4 (&x)[2], const float* base, int r0, int lt) {
+      const float* p = base + (sh * a.Dv + r0) * Dk + (lt >> 4) * Dk + (lt & 15) * 8;
+      x[0] = *reinterpret_cast<const float4*>(p);
+      x[1] = *reinterpret_cast<const float4*>(p + 4);
+    };
+    auto load_dy_v = [&](BlockIn& b, int r0, int lt) {
       const int g = (lt >> 4) & 3, li = lt & 15, pw = (lt >> 6) & 3, hw = lt >> 8;
-      const int64_t rows0 = (sh * a.Dv + r0) * Dk;
-      const float* s0b = a.ckpt + rows0;
-      const float* dsb = a.dsend + rows0;
       const auto yr = buffer_rsrc(dy + (tok * a.Hv + hv) * a.Dv + r0, uint32_t(L * sv) * uint32_t(sizeof(OutT)));
       const auto vr = buffer_rsrc(a.v + (tok * a.Hv + hv) * a.Dv + r0, uint32_t(L * sv) * 2u);
-      const int sr = lt >> 4, sc = (lt & 15) * 8;
-#pragma unroll
-      for (int q = 0; q < 2; ++q) {
-        b.xs[q] = *reinterpret_cast<const float4*>(s0b + sr * Dk + sc + 4 * q);
-        b.ys[q] = *reinterpret_cast<const float4*>(dsb + sr * Dk + sc + 4 * q);
-      }
       const int iy = lt >> 3, r4 = (lt & 7) * 4;
       if constexpr (kExactDy) {
         const auto t2 = __builtin_amdgcn_raw_buffer_load_b64(yr, int(uint32_t(iy * sv + r4) * 2), 0, 0);
@@ -164,11 +163,26 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
       for (int jj = 0; jj < 4; ++jj)
         b.vraw[jj] = buf_ld2(vr, uint32_t((16 * pw + 4 * g + jj) * sv + 16 * hw + li) * 2);
     };
+    // The end phase's inputs (T rows as float32, Q rows as bf16 bits), loaded during the value head's last block
+    // into the registers the next block's reads would use: thread -> T row tid / 8, columns 8 (tid % 8) .. + 7, and
+    // Q row e / 16, columns 8 (e % 16) .. + 7 for e = tid, tid + 512.
+    auto load_end = [&](BlockIn& b, int lt) {
+      const float* tp = tl->t + (lt >> 3) * kC + (lt & 7) * 8;
+      b.xs[0] = *reinterpret_cast<const float4*>(tp);
+      b.xs[1] = *reinterpret_cast<const float4*>(tp + 4);
+#pragma unroll
+      for (int q2 = 0; q2 < 2; ++q2) {
+        const int e = lt + kThreads * q2, t = e >> 4, c8 = (e & 15) * 8;
+        b.ys[q2] = __builtin_bit_cast(float4, buf_ld16(qrs, uint32_t(t * sk + c8) * 2));
+      }
+    };
     BlockIn nb;
     {
       int lt0 = tid;
       asm volatile("" : "+v"(lt0));
-      load_block(nb, 0, lt0);
+      load_rows(nb.xs, a.ckpt, 0, lt0);
+      load_rows(nb.ys, a.dsend, 0, lt0);
+      load_dy_v(nb, 0, lt0);
     }
 
     for (int r0 = 0; r0 < a.Dv; r0 += 32) {
@@ -205,8 +219,11 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj) vv[jj] = bf16_to_f32(nb.vraw[jj]);
       __syncthreads();
-      // The next block's global reads, in flight while this block computes.
-      if (r0 + 32 < a.Dv) load_block(nb, r0 + 32, lt);
+      const bool more = r0 + 32 < a.Dv;
+      if (more)
+        load_rows(nb.xs, a.ckpt, r0 + 32, lt);  // the next block's reads, first group
+      else
+        load_end(nb, lt);
 
       // The wave's own dY rows (i = ip, k = r = 8g..): A of dY S0, B of Delta dY^T.
       Split8 dYo;
@@ -231,6 +248,7 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
       }
       put4(sb + oRh, sb + oRl, swz(r, i0, kLP), rv[0], rv[1], rv[2], rv[3]);
       __syncthreads();
+      if (more) load_rows(nb.ys, a.dsend, r0 + 32, lt);
 
       // Phase 2: Delta = Tb R and dDelta = P^T dY + D KdS (rows: the wave's positions; lane: row r).
       f32x4 dl = zero4(), dd;
@@ -266,6 +284,7 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
         put4(sb + odDh, sb + odDl, swz(r, i0, kLP), dd[0], dd[1], dd[2], dd[3]);
       }
       __syncthreads();
+      if (more) load_dy_v(nb, r0 + 32, lt);
 
       // Phase 3: dR = Tb^T dDelta; dP^T += Delta dY^T and dTb^T += R dDelta^T over this half's key tiles.
       {
@@ -345,39 +364,50 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
     }
     __syncthreads();
 
-    // E1: K, Q rows, T, and dP, dTb (masked to j <= i) into the end-phase region. From the accumulators: the row and
-    // column sums of dP * P (the P factor's part of dG) and the column sums of dTb * T (dbeta's T part).
-    for (int e = tid; e < kC * 16; e += kThreads) {
-      const int t = e >> 4, c8 = (e & 15) * 8;
-      *reinterpret_cast<uint4*>(sb + eQb + swz(t, c8, kLK)) = buf_ld16(qrs, uint32_t(t * sk + c8) * 2);
-    }
-    for (int q = tid; q < kC * kC; q += kThreads) sf[eT + (q >> 6) * kLF + (q & 63)] = tl->t[q];
+    // E1: Q rows and T (hi, lo) into the end-phase region. Per lane, at i = ip and j = 16 (2 hw + mi) + 4g + jj (dP
+    // and dTb masked to j <= i): the row and column sums of dP * P (the P factor's part of dG), P * M with
+    // M_ij = exp(G_i - G_j) over P's entries, and dTb diag(beta), both as hi and lo in place of Tb and P (each lane
+    // rewrites only the P entries it has just read).
     {
-      // Lane: i = ip, j = 16 (2 hw + mi) + 4g + jj. Row sums (over j) add up over g here and over hw in dG; column
-      // sums (over i) over li here and over pw in dG.
+      {
+        const float x[8] = {nb.xs[0].x, nb.xs[0].y, nb.xs[0].z, nb.xs[0].w, nb.xs[1].x, nb.xs[1].y, nb.xs[1].z, nb.xs[1].w};
+        const Split8 ts = split8(x);
+        const int at = swz(lt >> 3, (lt & 7) * 8, kLT);
+        *reinterpret_cast<bf16x8*>(sb + eTh + at) = ts.hi;
+        *reinterpret_cast<bf16x8*>(sb + eTl + at) = ts.lo;
+#pragma unroll
+        for (int q2 = 0; q2 < 2; ++q2) {
+          const int e = lt + kThreads * q2;
+          *reinterpret_cast<uint4*>(sb + eQb + swz(e >> 4, (e & 15) * 8, kLK)) = __builtin_bit_cast(uint4, nb.ys[q2]);
+        }
+      }
+      // Row sums (over j) add up over g here and over hw in dG; column sums (over i) over li here and over pw in dG.
       float prow = 0.f;
+      const float gi = Gf[ip];
 #pragma unroll
       for (int mi = 0; mi < 2; ++mi) {
-        const int j0 = 16 * (2 * hw + mi) + 4 * g;
-        const uint2 ph = *reinterpret_cast<const uint2*>(PL[0] + swz(ip, j0, kLT));
-        const uint2 pl = *reinterpret_cast<const uint2*>(PL[1] + swz(ip, j0, kLT));
-        const float4 t4 = *reinterpret_cast<const float4*>(tl->t + ip * kC + j0);
+        const int j0 = 16 * (2 * hw + mi) + 4 * g, at = swz(ip, j0, kLT);
+        const uint2 ph = *reinterpret_cast<const uint2*>(PL[0] + at);
+        const uint2 pl = *reinterpret_cast<const uint2*>(PL[1] + at);
         const uint32_t hw4[2] = {ph.x, ph.y}, lw4[2] = {pl.x, pl.y};
-        const float tv4[4] = {t4.x, t4.y, t4.z, t4.w};
+        float pm[4], db[4];
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) {
           const int j = j0 + jj;
-          const float dp = j <= ip ? dPt[mi][jj] : 0.f, db = j <= ip ? dTbt[mi][jj] : 0.f;
-          sf[edP + ip * kLF + j] = dp;
-          sf[edTb + ip * kLF + j] = db;
+          const float dp = j <= ip ? dPt[mi][jj] : 0.f;
           const uint32_t hb = hw4[jj >> 1], lb = lw4[jj >> 1];
           const float pv = jj & 1 ? __uint_as_float(hb & 0xffff0000u) + __uint_as_float(lb & 0xffff0000u)
                                   : __uint_as_float(hb << 16) + __uint_as_float(lb << 16);
           const float x = dp * pv;
           prow += x;
-          const float col = sum16(x), colb = sum16(db * tv4[jj]);
-          if (li == 0) x2c[pw][j] = col, dbTp[pw][j] = colb;
+          const float col = sum16(x);
+          if (li == 0) x2c[pw][j] = col;
+          // Where j > i, dp is zero and the exponent positive: clamped at 0 to keep the product finite.
+          pm[jj] = dp * __expf(fminf(gi - Gf[j], 0.f));
+          db[jj] = (j <= ip ? dTbt[mi][jj] : 0.f) * bet[j];
         }
+        put4(TbL[0], TbL[1], at, pm[0], pm[1], pm[2], pm[3]);
+        put4(PL[0], PL[1], at, db[0], db[1], db[2], db[3]);
       }
       prow += __shfl_xor(prow, 16);
       prow += __shfl_xor(prow, 32);
@@ -385,10 +415,26 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
     }
     __syncthreads();
 
-    // E2: dQ += diag(exp G) dQ_inter and its dG term; K K^T (kept in registers); dQ += (dP * M) K;
-    // dK += (dP * M)^T Q; Z = dT T^T.
+    // E2: the column sums of dTb * T (dbeta's T part); dQ += diag(exp G) dQ_inter and its dG term; K K^T (kept in
+    // registers); dQ += (P * M) K; dK += (P * M)^T Q; Z = dTb diag(beta) T^T, stored as Z^T.
     f32x4 kk[2];  // (K K^T)[p][m], rows p = 16 pw + 4g + jj, columns m = 16 (2 hw + mi) + li; zero above tile pw
     {
+#pragma unroll
+      for (int mi = 0; mi < 2; ++mi) {
+        const int j0 = 16 * (2 * hw + mi) + 4 * g, at = swz(ip, j0, kLT);
+        const uint2 th = *reinterpret_cast<const uint2*>(sb + eTh + at);
+        const uint2 tlo = *reinterpret_cast<const uint2*>(sb + eTl + at);
+        const uint32_t hw4[2] = {th.x, th.y}, lw4[2] = {tlo.x, tlo.y};
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          const int j = j0 + jj;
+          const uint32_t hb = hw4[jj >> 1], lb = lw4[jj >> 1];
+          const float tv = jj & 1 ? __uint_as_float(hb & 0xffff0000u) + __uint_as_float(lb & 0xffff0000u)
+                                  : __uint_as_float(hb << 16) + __uint_as_float(lb << 16);
+          const float colb = sum16((j <= ip ? dTbt[mi][jj] : 0.f) * tv);
+          if (li == 0) dbTp[pw][j] = colb;
+        }
+      }
       float tq[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int t = 0; t < 4; ++t)
@@ -413,61 +459,40 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
             kk[mi] = mma(kk[mi], lds8(Kres + swz(ip, 32 * s + 8 * g, kLK)), lds8(Kres + swz(16 * m + li, 32 * s + 8 * g, kLK)));
         }
       }
-      Split8 AdPM[2], AdPMt[2], AdT[2];
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
-        float x[8], y[8], z[8];
+        const int at = swz(ip, 32 * s + 8 * g, kLT);
+        const Split8 Apm{lds8(TbL[0] + at), lds8(TbL[1] + at)};  // (P * M) rows i = ip, k = j
+        const Split8 Apmt{lds_tr8s(TbL[0] + 32 * s * kLT + 16 * pw, kLT, lt),
+                          lds_tr8s(TbL[1] + 32 * s * kLT + 16 * pw, kLT, lt)};  // (P * M)^T rows j = ip, k = i
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const int jj = 32 * s + 8 * g + j;
-          // M_ij = exp(G_i - G_j) where j <= i. dP is stored zero elsewhere; there the exponent is positive, so it
-          // is clamped at 0 to keep exp finite. No branch: every load is in bounds.
-          const float gi = Gf[ip], gj = Gf[jj];
-          x[j] = sf[edP + ip * kLF + jj] * __expf(fminf(gi - gj, 0.f));
-          y[j] = sf[edP + jj * kLF + ip] * __expf(fminf(gj - gi, 0.f));
-          z[j] = sf[edTb + ip * kLF + jj] * bet[jj];
-        }
-        AdPM[s] = split8(x);
-        AdPMt[s] = split8(y);
-        AdT[s] = split8(z);
-      }
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-#pragma unroll
-        for (int s = 0; s < 2; ++s) {
-          dQ[t] = mma2(dQ[t], AdPM[s], lds_tr8s(Kres + 32 * s * kLK + 16 * (4 * hw + t), kLK, lt));
-          dK[t] = mma2(dK[t], AdPMt[s], lds_tr8s(sb + eQb + 32 * s * kLK + 16 * (4 * hw + t), kLK, lt));
+        for (int t = 0; t < 4; ++t) {
+          dQ[t] = mma2(dQ[t], Apm, lds_tr8s(Kres + 32 * s * kLK + 16 * (4 * hw + t), kLK, lt));
+          dK[t] = mma2(dK[t], Apmt, lds_tr8s(sb + eQb + 32 * s * kLK + 16 * (4 * hw + t), kLK, lt));
         }
       }
 #pragma unroll
       for (int mi = 0; mi < 2; ++mi) {
-        const int m = 2 * hw + mi;
+        const int mr = 16 * (2 * hw + mi) + li;  // this lane's column m of Z
         f32x4 z = zero4();
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
-          float tv[8];
-#pragma unroll
-          for (int j = 0; j < 8; ++j) tv[j] = sf[eT + (16 * m + li) * kLF + 32 * s + 8 * g + j];
-          z = mma3(z, AdT[s], split8(tv));
+          const int aa = swz(ip, 32 * s + 8 * g, kLT), ab = swz(mr, 32 * s + 8 * g, kLT);
+          z = mma3(z, Split8{lds8(PL[0] + aa), lds8(PL[1] + aa)}, Split8{lds8(sb + eTh + ab), lds8(sb + eTl + ab)});
         }
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj) sf[eZt + (16 * m + li) * kLF + i0 + jj] = z[jj];
+        put4(sb + eZh, sb + eZl, swz(mr, i0, kLT), z[0], z[1], z[2], z[3]);
       }
     }
     __syncthreads();
 
     // E3: dA = -T^T Z below the diagonal (rows p = i0 + jj, columns m = 16 (2 hw + mi) + li, as kk), and at once
     // its products with E = exp(G_p - G_m) and K K^T: the A part of dbeta (row sums), of dG (row and column sums),
-    // and dKK = diag(beta) (dA * E), written over dTb.
+    // and dKK = diag(beta) (dA * E), stored as dKK^T.
     {
-      Split8 AT[2];
+      Split8 AT[2];  // T^T rows p = ip, k = i
 #pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        float x[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) x[j] = sf[eT + (32 * s + 8 * g + j) * kLF + ip];
-        AT[s] = split8(x);
-      }
+      for (int s = 0; s < 2; ++s)
+        AT[s] = Split8{lds_tr8s(sb + eTh + 32 * s * kLT + 16 * pw, kLT, lt), lds_tr8s(sb + eTl + 32 * s * kLT + 16 * pw, kLT, lt)};
       float rowp[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int mi = 0; mi < 2; ++mi) {
@@ -475,12 +500,10 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
         f32x4 da = zero4();
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
-          float zv[8];
-#pragma unroll
-          for (int j = 0; j < 8; ++j) zv[j] = sf[eZt + (16 * mt + li) * kLF + 32 * s + 8 * g + j];
-          da = mma3(da, AT[s], split8(zv));
+          const int ab = swz(mcol, 32 * s + 8 * g, kLT);
+          da = mma3(da, AT[s], Split8{lds8(sb + eZh + ab), lds8(sb + eZl + ab)});
         }
-        float colp = 0.f;
+        float colp = 0.f, kkt[4];
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) {
           const int pr = i0 + jj;
@@ -489,8 +512,9 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
           const float prod = dae * kk[mi][jj];
           rowp[jj] += prod;
           colp += bet[pr] * prod;
-          sf[edTb + pr * kLF + mcol] = bet[pr] * dae;
+          kkt[jj] = bet[pr] * dae;
         }
+        put4(sb + eKh, sb + eKl, swz(mcol, i0, kLT), kkt[0], kkt[1], kkt[2], kkt[3]);
         colp += __shfl_xor(colp, 16);
         colp += __shfl_xor(colp, 32);
         if (g == 0) x1cp[pw][mcol] = colp;
@@ -503,24 +527,17 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
     }
     __syncthreads();
 
-    // E4: dK += (dKK + dKK^T) K for rows j = ip, this half's columns.
-    {
-      Split8 A[2];
+    // E4: dK += (dKK + dKK^T) K for rows j = ip, this half's columns: dKK rows j through the transposing read of
+    // dKK^T, dKK^T rows j directly.
 #pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        float x[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const int m = 32 * s + 8 * g + j;
-          x[j] = sf[edTb + ip * kLF + m] + sf[edTb + m * kLF + ip];
-        }
-        A[s] = split8(x);
-      }
+    for (int s = 0; s < 2; ++s) {
+      const int at = swz(ip, 32 * s + 8 * g, kLT);
+      const Split8 A1{lds_tr8s(sb + eKh + 32 * s * kLT + 16 * pw, kLT, lt), lds_tr8s(sb + eKl + 32 * s * kLT + 16 * pw, kLT, lt)};
+      const Split8 A2{lds8(sb + eKh + at), lds8(sb + eKl + at)};
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
-#pragma unroll
-        for (int s = 0; s < 2; ++s)
-          dK[t] = mma2(dK[t], A[s], lds_tr8s(Kres + 32 * s * kLK + 16 * (4 * hw + t), kLK, lt));
+        const bf16x8 B = lds_tr8s(Kres + 32 * s * kLK + 16 * (4 * hw + t), kLK, lt);
+        dK[t] = mma2(mma2(dK[t], A1, B), A2, B);
       }
     }
     // E5 (one wave): dG per position, dg = its reverse cumulative sum (a suffix scan over the wave), and dbeta.
