@@ -115,16 +115,15 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
     const Tile* tl = a.tiles + sh;
     __syncthreads();
     if (tid < kC) gam[tid] = tl->gam[tid], dec[tid] = tl->dec[tid], bet[tid] = tl->beta[tid], Gf[tid] = tl->G[tid];
-    {  // Tb and P, hi and lo: thread -> row tid / 8, columns 8 (tid % 8) ..
-      const int i = tid >> 3, c8 = (tid & 7) * 8, at = i * kC + c8, lt8 = swz(i, c8, kLT);
-      const uint4 v0 = *reinterpret_cast<const uint4*>(tl->tb_hi + at);
-      const uint4 v1 = *reinterpret_cast<const uint4*>(tl->tb_lo + at);
-      const uint4 v2 = *reinterpret_cast<const uint4*>(tl->p_hi + at);
-      const uint4 v3 = *reinterpret_cast<const uint4*>(tl->p_lo + at);
-      *reinterpret_cast<uint4*>(TbL[0] + lt8) = v0;
-      *reinterpret_cast<uint4*>(TbL[1] + lt8) = v1;
-      *reinterpret_cast<uint4*>(PL[0] + lt8) = v2;
-      *reinterpret_cast<uint4*>(PL[1] + lt8) = v3;
+    {  // Tb and P, hi and lo: thread -> row tid / 8, columns 8 (tid % 8) ..; zeros above the diagonal blocks
+      const int i = tid >> 3, c8 = (tid & 7) * 8, lt8 = swz(i, c8, kLT);
+      const auto tr = buffer_rsrc(tl->tb[0], 4 * kTri * 2);  // tb[0], tb[1], p[0], p[1] are contiguous
+      const bf16x8 v0 = tri_ld8(tr, 0, i, c8), v1 = tri_ld8(tr, kTri, i, c8);
+      const bf16x8 v2 = tri_ld8(tr, 2 * kTri, i, c8), v3 = tri_ld8(tr, 3 * kTri, i, c8);
+      *reinterpret_cast<bf16x8*>(TbL[0] + lt8) = v0;
+      *reinterpret_cast<bf16x8*>(TbL[1] + lt8) = v1;
+      *reinterpret_cast<bf16x8*>(PL[0] + lt8) = v2;
+      *reinterpret_cast<bf16x8*>(PL[1] + lt8) = v3;
     }
     f32x4 dPt[2], dTbt[2], dQi[4];  // dPt, dTbt: key tiles m = 2 hw + mi; lane -> column i = ip, rows j
 #pragma unroll
@@ -163,13 +162,13 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
       for (int jj = 0; jj < 4; ++jj)
         b.vraw[jj] = buf_ld2(vr, uint32_t((16 * pw + 4 * g + jj) * sv + 16 * hw + li) * 2);
     };
-    // The end phase's inputs (T rows as float32, Q rows as bf16 bits), loaded during the value head's last block
-    // into the registers the next block's reads would use: thread -> T row tid / 8, columns 8 (tid % 8) .. + 7, and
-    // Q row e / 16, columns 8 (e % 16) .. + 7 for e = tid, tid + 512.
+    // The end phase's inputs (T rows hi and lo, Q rows, as bf16 bits), loaded during the value head's last block
+    // into the registers the next block's reads would use: thread -> T row tid / 8, columns 8 (tid % 8) .. + 7
+    // (zeros above the diagonal blocks), and Q row e / 16, columns 8 (e % 16) .. + 7 for e = tid, tid + 512.
     auto load_end = [&](BlockIn& b, int lt) {
-      const float* tp = tl->t + (lt >> 3) * kC + (lt & 7) * 8;
-      b.xs[0] = *reinterpret_cast<const float4*>(tp);
-      b.xs[1] = *reinterpret_cast<const float4*>(tp + 4);
+      const auto trr = buffer_rsrc(tl->t[0], 2 * kTri * 2);
+      b.xs[0] = __builtin_bit_cast(float4, tri_ld8(trr, 0, lt >> 3, (lt & 7) * 8));
+      b.xs[1] = __builtin_bit_cast(float4, tri_ld8(trr, kTri, lt >> 3, (lt & 7) * 8));
 #pragma unroll
       for (int q2 = 0; q2 < 2; ++q2) {
         const int e = lt + kThreads * q2, t = e >> 4, c8 = (e & 15) * 8;
@@ -370,11 +369,9 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
     // rewrites only the P entries it has just read).
     {
       {
-        const float x[8] = {nb.xs[0].x, nb.xs[0].y, nb.xs[0].z, nb.xs[0].w, nb.xs[1].x, nb.xs[1].y, nb.xs[1].z, nb.xs[1].w};
-        const Split8 ts = split8(x);
         const int at = swz(lt >> 3, (lt & 7) * 8, kLT);
-        *reinterpret_cast<bf16x8*>(sb + eTh + at) = ts.hi;
-        *reinterpret_cast<bf16x8*>(sb + eTl + at) = ts.lo;
+        *reinterpret_cast<float4*>(sb + eTh + at) = nb.xs[0];
+        *reinterpret_cast<float4*>(sb + eTl + at) = nb.xs[1];
 #pragma unroll
         for (int q2 = 0; q2 < 2; ++q2) {
           const int e = lt + kThreads * q2;

@@ -20,6 +20,7 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kLDK = 144;  // rows 0..3 of a transposing read on distinct banks
 constexpr int kLDC = kC + kPadB;
+constexpr int kLT = 80;  // Tb, P rows (swz placement)
 
 template <typename OutT>
 __global__ __launch_bounds__(kThreads) void chunk_bwd_state_kernel(ChunkArgs a) {
@@ -32,6 +33,9 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_state_kernel(ChunkArgs a) 
   __shared__ __bf16 dDth[16][kLDC], dDtl[16][kLDC];   // dDelta^T [r][j]
   __shared__ __bf16 GdRth[16][kLDC], GdRtl[16][kLDC]; // -(diag(exp G) dR)^T
   __shared__ float gam[kC], dec[kC];
+  // Tb (hi, lo) and P (hi, lo) of the chunk, 64 x 64 each (swz placement; the blocks above the diagonal stay zero):
+  // the A operands Tb^T and P^T come from their columns through the transposing read.
+  __shared__ __align__(16) __bf16 TPL[4][kC * kLT];
 
   const int total = a.nblk * a.Hv * a.N;
   const int wid = xcd_remap(blockIdx.x, total);
@@ -55,12 +59,12 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_state_kernel(ChunkArgs a) 
 
   // One chunk's inputs, loaded into registers a chunk ahead (in the reverse sweep): k and q rows (thread e of
   // [0, 1024) in steps of 256 covers row e / 16, columns 8 (e % 16)), dy (row e / 16, state row e % 16) with its
-  // exp G, the chunk's exp G and D, and the wave's A operands Tb^T rows 16w + li and P^T rows 16w + li (k = 8g..,
-  // two k steps, hi and lo). k, q, dy are read through buffer resources that end at the sequence's last row, so rows
-  // past it read as zeros without a branch.
+  // exp G, the chunk's exp G and D, and the packed blocks of Tb and P (staged into LDS, where the transposing read
+  // gives the A operands Tb^T and P^T). k, q, dy are read through buffer resources that end at the sequence's last
+  // row, so rows past it read as zeros without a branch.
   struct Pre {
     uint4 k[4], q[4];
-    bf16x8 t[4], p[4];
+    uint4 tp[5];     // the packed Tb and P blocks: thread -> 16-byte units tid + 256 u of tb[0..1], p[0..1]
     uint32_t dy[4];  // raw bits (bf16 in the low half, or float32)
     float gt[4];
     float gam, dec;
@@ -85,11 +89,9 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_state_kernel(ChunkArgs a) 
         f.dy[q4] = __float_as_uint(buf_ld4(yr, yo * 4));
       f.gt[q4] = tl->gam[t];
     }
-    const int ar = (16 * w + li) * kC + 8 * g;
-    f.t[0] = gld8(tl->tbt_hi + ar), f.t[1] = gld8(tl->tbt_lo + ar), f.t[2] = gld8(tl->tbt_hi + ar + 32),
-    f.t[3] = gld8(tl->tbt_lo + ar + 32);
-    f.p[0] = gld8(tl->pt_hi + ar), f.p[1] = gld8(tl->pt_lo + ar), f.p[2] = gld8(tl->pt_hi + ar + 32),
-    f.p[3] = gld8(tl->pt_lo + ar + 32);
+    const auto tr = buffer_rsrc(tl->tb[0], 4 * kTri * 2);  // tb[0], tb[1], p[0], p[1] are contiguous
+#pragma unroll
+    for (int u = 0; u < 5; ++u) f.tp[u] = buf_ld16(tr, uint32_t(tid + kThreads * u) * 16);
   };
 
   // dv of a chunk is stored during the chunk processed after it (after that chunk's inputs are staged), so no wait
@@ -122,9 +124,14 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_state_kernel(ChunkArgs a) 
       GdYtl[r][t] = (__bf16)(gx - (float)gh);
     }
     if (tid < kC) gam[tid] = f.gam, dec[tid] = f.dec;
-    // The A operands are consumed later in the step: take them here, so their waits are here too.
+    // The packed blocks to their places: unit e of a matrix half is row (e % 32) / 2, columns 8 (e % 2) .. of
+    // block e / 32 = (I, J) in the order of tri_off.
 #pragma unroll
-    for (int u = 0; u < 4; ++u) asm volatile("" : "+v"(f.t[u]), "+v"(f.p[u]));
+    for (int u = 0; u < 5; ++u) {
+      const int x = tid + kThreads * u, m = x / 320, e = x - 320 * m, b = e >> 5;
+      const int I = (b >= 1) + (b >= 3) + (b >= 6), J = b - I * (I + 1) / 2;
+      *reinterpret_cast<uint4*>(&TPL[m][swz(16 * I + ((e & 31) >> 1), 16 * J + 8 * (e & 1), kLT)]) = f.tp[u];
+    }
     if (c + 1 < nch) store_dv(c + 1, dr);
     {
       const auto out = buffer_rsrc(a.dsend + ((slot * a.Hv + hv) * a.Dv + row0) * Dk, 16 * Dk * 4);
@@ -157,7 +164,8 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_state_kernel(ChunkArgs a) 
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
       if (32 * s + 31 >= 16 * w) {
-        const Split8 A{f.p[2 * s], f.p[2 * s + 1]};
+        // P^T rows j = 16w + li, k = i: column j of P, rows 32s..
+        const Split8 A{lds_tr8s(&TPL[2][32 * s * kLT + 16 * w], kLT, tid), lds_tr8s(&TPL[3][32 * s * kLT + 16 * w], kLT, tid)};
         if constexpr (kExactDy) {
           dd = mma2(dd, A, lds8(&dYth[li][32 * s + 8 * g]));
         } else {
@@ -179,8 +187,10 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_state_kernel(ChunkArgs a) 
 #pragma unroll
     for (int s = 0; s < 2; ++s)
       if (32 * s + 31 >= 16 * w)  // Tb^T is zero below the diagonal
-        dr = mma3(dr, Split8{f.t[2 * s], f.t[2 * s + 1]},
-                Split8{lds8(&dDth[li][32 * s + 8 * g]), lds8(&dDtl[li][32 * s + 8 * g])});
+        dr = mma3(dr,
+                  Split8{lds_tr8s(&TPL[0][32 * s * kLT + 16 * w], kLT, tid),
+                         lds_tr8s(&TPL[1][32 * s * kLT + 16 * w], kLT, tid)},  // Tb^T rows i, k = j
+                  Split8{lds8(&dDth[li][32 * s + 8 * g]), lds8(&dDtl[li][32 * s + 8 * g])});
 #pragma unroll
     for (int jj = 0; jj < 4; ++jj) {
       const int i = 16 * w + 4 * g + jj;
@@ -207,6 +217,11 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_state_kernel(ChunkArgs a) 
     }
   };
 
+  // The blocks above the diagonal of Tb and P are zero and never written by the staging.
+  for (int x = tid; x < 4 * kC * kC / 8; x += kThreads) {
+    const int m = x >> 9, r = (x >> 3) & 63, c = (x & 7) * 8;
+    if ((c >> 4) > (r >> 4)) *reinterpret_cast<uint4*>(&TPL[m][swz(r, c, kLT)]) = uint4{0u, 0u, 0u, 0u};
+  }
   // Two register sets in turn: chunk c computes from one while chunk c - 1 loads into the other.
   Pre pa, pb;
   f32x4 dr = zero4();

@@ -15,21 +15,38 @@ constexpr int kC = kChunk;  // 64 positions per chunk
 constexpr int kPadB = 8;    // bf16 row padding in LDS (keeps 16-byte alignment, staggers banks)
 
 // Everything about a (chunk, value head) that does not depend on the state, as MFMA-ready bf16 hi/lo pairs:
-//   Tb = T diag(beta), T = (I + A)^-1, A = strict_lower(diag(beta) (E * K K^T)), E_ij = exp(G_i - G_j)
-//   P  = lower_incl(E * Q K^T)
+//   T = (I + A)^-1, A = strict_lower(diag(beta) (E * K K^T)), E_ij = exp(G_i - G_j),  Tb = T diag(beta)
+//   P = lower_incl(E * Q K^T)
 // and the per-position vectors. Positions past the chunk's end are padded (beta 0, log-decay 0, k = q = 0).
+// The three 64 x 64 matrices are lower triangular; each is stored as its ten 16 x 16 blocks on or below the
+// diagonal (tri_off), so the record holds no zero blocks.
+constexpr int kTri = 10 * 256;
+
+// Element offset of (i, j), j / 16 <= i / 16, in a lower-triangular 64 x 64 matrix stored as the blocks (I, J),
+// J <= I, in the order (0,0) (1,0) (1,1) (2,0) .. (3,3), each row-major: a row of a block is 16 contiguous
+// elements (32 bytes), and the blocks (I, 0..I) of a row strip are contiguous.
+__host__ __device__ constexpr int tri_off(int i, int j) {
+  return (((i >> 4) * ((i >> 4) + 1) / 2 + (j >> 4)) << 8) + ((i & 15) << 4) + (j & 15);
+}
+
 struct Tile {
-  bf16_t tb_hi[kC * kC], tb_lo[kC * kC];    // Tb, row i, column j
-  bf16_t tbt_hi[kC * kC], tbt_lo[kC * kC];  // Tb^T, row j, column i
-  bf16_t p_hi[kC * kC], p_lo[kC * kC];      // P, row i (query), column j (key)
-  bf16_t pt_hi[kC * kC], pt_lo[kC * kC];    // P^T, row j (key), column i (query)
-  float t[kC * kC];                         // T, row i, column j
+  bf16_t tb[2][kTri];  // Tb, hi and lo (row i, column j)
+  bf16_t p[2][kTri];   // P, hi and lo (row i: query, column j: key)
+  bf16_t t[2][kTri];   // T, hi and lo
   float beta[kC];
   float gam[kC];  // exp(G_i)
   float dec[kC];  // exp(G_63 - G_i)
   float G[kC];    // G_i = sum_{j <= i} a_j within the chunk
 };
 static_assert(sizeof(Tile) % 16 == 0, "Tile records stay 16-byte aligned");
+
+// Eight bf16 of row i, columns c .. c + 7 (c a multiple of 8), of the packed triangular matrix whose hi half starts
+// at element h0 of the buffer resource r (lo at h0 + kTri); groups in a block above the diagonal read zeros (their
+// offset lies past the resource).
+__device__ __forceinline__ bf16x8 tri_ld8(__amdgpu_buffer_rsrc_t r, int h0, int i, int c) {
+  const uint32_t off = (c >> 4) <= (i >> 4) ? uint32_t(h0 + tri_off(i, c)) * 2u : 0x80000000u;
+  return __builtin_bit_cast(bf16x8, buf_ld16(r, off));
+}
 
 struct ChunkLayout {
   int64_t NC;

@@ -78,11 +78,10 @@ __global__ __launch_bounds__(kThreads) void chunk_fwd_kernel(ChunkArgs a) {
       f.q[q2] = buf_ld16(qr, uint32_t(t * sk + c8) * 2);
       f.v[q2] = buf_ld2(vr, uint32_t(t * sv + (e & 15)) * 2);
     }
-    const bf16_t* hi = side ? tl->p_hi : tl->tb_hi;
-    const bf16_t* lo = side ? tl->p_lo : tl->tb_lo;
-    const int ar = (16 * wp + li) * kC + 8 * g;
-    f.f[0] = gld8(hi + ar), f.f[1] = gld8(lo + ar);
-    if (wp >= 2) f.f[2] = gld8(hi + ar + 32), f.f[3] = gld8(lo + ar + 32);  // columns 32.. are zero for rows < 32
+    const auto mr = buffer_rsrc(side ? tl->p[0] : tl->tb[0], 2 * kTri * 2);  // hi, then lo
+    const int ar = 16 * wp + li;
+    f.f[0] = tri_ld8(mr, 0, ar, 8 * g), f.f[1] = tri_ld8(mr, kTri, ar, 8 * g);
+    if (wp >= 2) f.f[2] = tri_ld8(mr, 0, ar, 32 + 8 * g), f.f[3] = tri_ld8(mr, kTri, ar, 32 + 8 * g);  // else zero
   };
 
   // y of a chunk (waves 4-7) is stored during the next chunk, after that chunk's inputs are staged, so no wait for

@@ -1,5 +1,6 @@
 // Chunked design, kernel 1 (prep), one block per (chunk slot, value head): everything about the chunk that does not
-// depend on the state, written once as MFMA-ready operands (the Tile record, chunk_common.h).
+// depend on the state, written once as MFMA-ready operands (the Tile record, chunk_common.h: T, Tb and P as bf16
+// hi/lo pairs of their lower-triangular blocks).
 //   G = cumsum of the log-decays (fp64, so G_i - G_j keeps its bits when |G| is large)
 //   A = strict_lower(diag(beta) (E * K K^T)),  T = (I + A)^-1,  Tb = T diag(beta)
 //   P = lower_incl(E * Q K^T),  E_ij = exp(G_i - G_j)
@@ -118,24 +119,18 @@ __global__ __launch_bounds__(kThreads) void chunk_prep_kernel(ChunkArgs a) {
       Qb[i][64 + j] = (__bf16)(x - (float)h);
     }
   __syncthreads();
-  // P rows (thread -> row tid / 4, 16 columns) and P^T rows (transposing reads of P's columns), as 16-byte stores.
+  // P's blocks on or below the diagonal: thread -> row tid / 4 of block (row tid / 64, column tid % 4), as two
+  // 16-byte stores per half.
   {
     const int i = tid >> 2, j0 = (tid & 3) * 16;
+    if ((j0 >> 4) <= (i >> 4)) {
 #pragma unroll
-    for (int hl = 0; hl < 2; ++hl) {
-      bf16_t* dst = hl ? tile->p_lo : tile->p_hi;
-      *reinterpret_cast<uint4*>(dst + i * kC + j0) = *reinterpret_cast<const uint4*>(&Qb[i][64 * hl + j0]);
-      *reinterpret_cast<uint4*>(dst + i * kC + j0 + 8) = *reinterpret_cast<const uint4*>(&Qb[i][64 * hl + j0 + 8]);
-    }
-    // Wave w: P^T rows 16 w + n (n = lane % 16), columns 32 h + 8 (lane / 16) .. + 7, for h = 0, 1 and hi, lo.
-#pragma unroll
-    for (int hl = 0; hl < 2; ++hl)
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const bf16x8 v = lds_tr8(&Qb[32 * h][64 * hl + 16 * w], kLDK, tid);
-        bf16_t* dst = hl ? tile->pt_lo : tile->pt_hi;
-        *reinterpret_cast<bf16x8*>(dst + (16 * w + li) * kC + 32 * h + 8 * g) = v;
+      for (int hl = 0; hl < 2; ++hl) {
+        bf16_t* dst = tile->p[hl] + tri_off(i, j0);
+        *reinterpret_cast<uint4*>(dst) = *reinterpret_cast<const uint4*>(&Qb[i][64 * hl + j0]);
+        *reinterpret_cast<uint4*>(dst + 8) = *reinterpret_cast<const uint4*>(&Qb[i][64 * hl + j0 + 8]);
       }
+    }
   }
 
   // Diagonal blocks: thread -> column j of block bd; the column lives in registers through the substitution.
@@ -196,29 +191,30 @@ __global__ __launch_bounds__(kThreads) void chunk_prep_kernel(ChunkArgs a) {
     __syncthreads();
   }
 
-  // T, Tb = T diag(beta) and Tb^T: thread -> row tid / 4, columns 16 (tid % 4) .. (of T for T and Tb; of Tb^T,
-  // i.e. column tid / 4 of Tb, for Tb^T).
+  // T and Tb = T diag(beta), hi and lo, on and below the diagonal blocks: thread -> row tid / 4, columns
+  // 16 (tid % 4) .. + 15.
   {
     const int i = tid >> 2, j0 = (tid & 3) * 16;
-    bf16x8 h[2], l[2], th[2], tl[2];
+    if ((j0 >> 4) <= (i >> 4)) {
+      bf16x8 th[2], tl[2], bh[2], bl[2];
 #pragma unroll
-    for (int u = 0; u < 16; ++u) {
-      const float t = Tm[i][j0 + u], x = t * Bs[j0 + u], xt = Tm[j0 + u][i] * Bs[i];
-      tile->t[i * kC + j0 + u] = t;
-      const __bf16 hh = (__bf16)x, ht = (__bf16)xt;
-      h[u >> 3][u & 7] = hh;
-      l[u >> 3][u & 7] = (__bf16)(x - (float)hh);
-      th[u >> 3][u & 7] = ht;
-      tl[u >> 3][u & 7] = (__bf16)(xt - (float)ht);
+      for (int u = 0; u < 16; ++u) {
+        const float t = Tm[i][j0 + u], x = t * Bs[j0 + u];
+        const __bf16 ht = (__bf16)t, hx = (__bf16)x;
+        th[u >> 3][u & 7] = ht;
+        tl[u >> 3][u & 7] = (__bf16)(t - (float)ht);
+        bh[u >> 3][u & 7] = hx;
+        bl[u >> 3][u & 7] = (__bf16)(x - (float)hx);
+      }
+      const int at = tri_off(i, j0);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        *reinterpret_cast<bf16x8*>(tile->t[0] + at + 8 * h) = th[h];
+        *reinterpret_cast<bf16x8*>(tile->t[1] + at + 8 * h) = tl[h];
+        *reinterpret_cast<bf16x8*>(tile->tb[0] + at + 8 * h) = bh[h];
+        *reinterpret_cast<bf16x8*>(tile->tb[1] + at + 8 * h) = bl[h];
+      }
     }
-    *reinterpret_cast<bf16x8*>(&tile->tb_hi[i * kC + j0]) = h[0];
-    *reinterpret_cast<bf16x8*>(&tile->tb_hi[i * kC + j0 + 8]) = h[1];
-    *reinterpret_cast<bf16x8*>(&tile->tb_lo[i * kC + j0]) = l[0];
-    *reinterpret_cast<bf16x8*>(&tile->tb_lo[i * kC + j0 + 8]) = l[1];
-    *reinterpret_cast<bf16x8*>(&tile->tbt_hi[i * kC + j0]) = th[0];
-    *reinterpret_cast<bf16x8*>(&tile->tbt_hi[i * kC + j0 + 8]) = th[1];
-    *reinterpret_cast<bf16x8*>(&tile->tbt_lo[i * kC + j0]) = tl[0];
-    *reinterpret_cast<bf16x8*>(&tile->tbt_lo[i * kC + j0 + 8]) = tl[1];
   }
 }
 
