@@ -66,32 +66,43 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_state_kernel(ChunkArgs a) 
     uint4 k[4], q[4];
     uint4 tp[5];     // the packed Tb and P blocks: thread -> 16-byte units tid + 256 u of tb[0..1], p[0..1]
     uint32_t dy[4];  // raw bits (bf16 in the low half, or float32)
-    float gt[4];
     float gam, dec;
   };
-  auto prefetch = [&](Pre& f, int c) {
-    const int64_t slot = sq.slot0 + c, tok = sq.tok0 + int64_t(c) * kC;
+  // The loads come in three groups, issued at three points of the chunk before, so no wave stalls long on a full
+  // load queue.
+  auto load_kq = [&](Pre& f, int c) {
+    const int64_t tok = sq.tok0 + int64_t(c) * kC;
     const uint32_t L = uint32_t(min(kC, sq.len - c * kC));
     const auto kr = buffer_rsrc(a.k + tok * sk + hk * Dk, L * sk * 2);
     const auto qr = buffer_rsrc(a.q + tok * sk + hk * Dk, L * sk * 2);
-    const auto yr = buffer_rsrc(dy + tok * sv + hv * a.Dv + row0, L * sv * uint32_t(sizeof(OutT)));
-    const Tile* tl = a.tiles + (slot * a.Hv + hv);
-    f.gam = tl->gam[tid & (kC - 1)], f.dec = tl->dec[tid & (kC - 1)];
 #pragma unroll
     for (int q4 = 0; q4 < 4; ++q4) {
       const int e = tid + kThreads * q4, t = e >> 4, c8 = (e & 15) * 8;
       f.k[q4] = buf_ld16(kr, uint32_t(t * sk + c8) * 2);
       f.q[q4] = buf_ld16(qr, uint32_t(t * sk + c8) * 2);
+    }
+  };
+  auto load_tp = [&](Pre& f, int c) {
+    const Tile* tl = a.tiles + ((sq.slot0 + c) * a.Hv + hv);
+    const auto tr = buffer_rsrc(tl->tb[0], 4 * kTri * 2);  // tb[0], tb[1], p[0], p[1] are contiguous
+#pragma unroll
+    for (int u = 0; u < 5; ++u) f.tp[u] = buf_ld16(tr, uint32_t(tid + kThreads * u) * 16);
+  };
+  auto load_dy = [&](Pre& f, int c) {
+    const int64_t tok = sq.tok0 + int64_t(c) * kC;
+    const uint32_t L = uint32_t(min(kC, sq.len - c * kC));
+    const auto yr = buffer_rsrc(dy + tok * sv + hv * a.Dv + row0, L * sv * uint32_t(sizeof(OutT)));
+    const Tile* tl = a.tiles + ((sq.slot0 + c) * a.Hv + hv);
+    f.gam = tl->gam[tid & (kC - 1)], f.dec = tl->dec[tid & (kC - 1)];
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4) {
+      const int e = tid + kThreads * q4, t = e >> 4;
       const uint32_t yo = uint32_t(t * sv + (e & 15));
       if constexpr (kExactDy)
         f.dy[q4] = buf_ld2(yr, yo * 2);
       else
         f.dy[q4] = __float_as_uint(buf_ld4(yr, yo * 4));
-      f.gt[q4] = tl->gam[t];
     }
-    const auto tr = buffer_rsrc(tl->tb[0], 4 * kTri * 2);  // tb[0], tb[1], p[0], p[1] are contiguous
-#pragma unroll
-    for (int u = 0; u < 5; ++u) f.tp[u] = buf_ld16(tr, uint32_t(tid + kThreads * u) * 16);
   };
 
   // dv of a chunk is stored during the chunk processed after it (after that chunk's inputs are staged), so no wait
@@ -118,10 +129,6 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_state_kernel(ChunkArgs a) 
       const __bf16 h = (__bf16)x;
       dYth[r][t] = h;
       dYtl[r][t] = (__bf16)(x - (float)h);
-      const float gx = f.gt[q4] * x;
-      const __bf16 gh = (__bf16)gx;
-      GdYth[r][t] = gh;
-      GdYtl[r][t] = (__bf16)(gx - (float)gh);
     }
     if (tid < kC) gam[tid] = f.gam, dec[tid] = f.dec;
     // The packed blocks to their places: unit e of a matrix half is row (e % 32) / 2, columns 8 (e % 2) .. of
@@ -148,7 +155,17 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_state_kernel(ChunkArgs a) 
         }
     }
     __syncthreads();
-    if (c > 0) prefetch(nxt, c - 1);
+    if (c > 0) load_kq(nxt, c - 1);
+    // (diag(exp G) dY)^T, split (exp G is in LDS now); read in the state update.
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4) {
+      const int e = tid + kThreads * q4, t = e >> 4, r = e & 15;
+      const float x = kExactDy ? __uint_as_float(f.dy[q4] << 16) : __uint_as_float(f.dy[q4]);
+      const float gx = gam[t] * x;
+      const __bf16 gh = (__bf16)gx;
+      GdYth[r][t] = gh;
+      GdYtl[r][t] = (__bf16)(gx - (float)gh);
+    }
 
     // K dS^T for positions j = 16w..: lane -> column r = li, rows j = 16w + 4g + jj.
     f32x4 kds = zero4();
@@ -181,6 +198,7 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_state_kernel(ChunkArgs a) 
       dDtl[li][j] = (__bf16)(dd[jj] - (float)h);
     }
     __syncthreads();
+    if (c > 0) load_tp(nxt, c - 1);
 
     // dR = Tb^T dDelta for positions i = 16w.. (A = Tb^T rows i, k = j); dv = dR.
     dr = zero4();
@@ -200,6 +218,7 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_state_kernel(ChunkArgs a) 
       GdRtl[li][i] = (__bf16)(x - (float)h);
     }
     __syncthreads();
+    if (c > 0) load_dy(nxt, c - 1);
 
     // dS <- exp(G_63) dS + (diag(exp G) dY)^T Q - (diag(exp G) dR)^T K.
     const float glast = gam[kC - 1];
@@ -225,7 +244,7 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_state_kernel(ChunkArgs a) 
   // Two register sets in turn: chunk c computes from one while chunk c - 1 loads into the other.
   Pre pa, pb;
   f32x4 dr = zero4();
-  if (nch > 0) prefetch(pa, nch - 1);
+  if (nch > 0) load_kq(pa, nch - 1), load_tp(pa, nch - 1), load_dy(pa, nch - 1);
   for (int c = nch - 1; c >= 0; c -= 2) {
     step(c, pa, pb, dr);
     if (c > 0) step(c - 1, pb, pa, dr);

@@ -55,13 +55,15 @@ __global__ __launch_bounds__(kThreads) void chunk_fwd_kernel(ChunkArgs a) {
   for (int jj = 0; jj < 4; ++jj)
     S[jj] = a.s0 ? a.s0[((int64_t(n) * a.Hv + hv) * a.Dv + row0 + 4 * g + jj) * Dk + 16 * w + li] : 0.f;
 
-  // One chunk's inputs, loaded into registers a chunk ahead. k, q, v go through buffer resources that end at the
-  // sequence's last row, so rows past it read as zeros without a branch.
+  // One chunk's inputs, loaded into registers a chunk ahead: k and q rows by waves 0-3, right after they have
+  // written the state (they then wait for waves 4-7 anyway); v, exp G, D by waves 4-7 after the barrier; each wave's
+  // own A operand rows. k, q, v go through buffer resources that end at the sequence's last row, so rows past it
+  // read as zeros without a branch.
   struct Pre {
-    uint4 k[2], q[2];  // thread e = tid + 512 q2: row e / 16, columns 8 (e % 16) ..
-    uint16_t v[2];     // thread e: v row e / 16, state row e % 16
+    uint4 k[4], q[4];  // waves 0-3, thread e = tid + 256 q4: row e / 16, columns 8 (e % 16) ..
+    uint16_t v[4];     // waves 4-7, e = tid - 256 + 256 q4: v row e / 16, state row e % 16
     bf16x8 f[4];       // waves 0-3: Tb rows 16 wp + li; waves 4-7: P rows (k = 8g.., two k steps, hi and lo)
-    float gd;          // threads 0..63: exp G; the others: D = exp(G_63 - G)
+    float gd;          // waves 4-5: exp G (tid - 256 < 64), then D = exp(G_63 - G)
   };
   auto prefetch = [&](Pre& f, int c) {
     const int64_t slot = sq.slot0 + c, tok = sq.tok0 + int64_t(c) * kC;
@@ -70,13 +72,21 @@ __global__ __launch_bounds__(kThreads) void chunk_fwd_kernel(ChunkArgs a) {
     const auto qr = buffer_rsrc(a.q + tok * sk + hk * Dk, L * sk * 2);
     const auto vr = buffer_rsrc(a.v + tok * sv + hv * a.Dv + row0, L * sv * 2);
     const Tile* tl = a.tiles + (slot * a.Hv + hv);
-    f.gd = (tid < kC ? tl->gam : tl->dec)[tid & (kC - 1)];
+    if (!side) {
 #pragma unroll
-    for (int q2 = 0; q2 < 2; ++q2) {
-      const int e = tid + kThreads * q2, t = e >> 4, c8 = (e & 15) * 8;
-      f.k[q2] = buf_ld16(kr, uint32_t(t * sk + c8) * 2);
-      f.q[q2] = buf_ld16(qr, uint32_t(t * sk + c8) * 2);
-      f.v[q2] = buf_ld2(vr, uint32_t(t * sv + (e & 15)) * 2);
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const int e = tid + 256 * q4, t = e >> 4, c8 = (e & 15) * 8;
+        f.k[q4] = buf_ld16(kr, uint32_t(t * sk + c8) * 2);
+        f.q[q4] = buf_ld16(qr, uint32_t(t * sk + c8) * 2);
+      }
+    } else {
+      const int u = tid - 256;
+      f.gd = (u < kC ? tl->gam : tl->dec)[u & (kC - 1)];
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const int e = u + 256 * q4, t = e >> 4;
+        f.v[q4] = buf_ld2(vr, uint32_t(t * sv + (e & 15)) * 2);
+      }
     }
     const auto mr = buffer_rsrc(side ? tl->p[0] : tl->tb[0], 2 * kTri * 2);  // hi, then lo
     const int ar = 16 * wp + li;
@@ -99,17 +109,25 @@ __global__ __launch_bounds__(kThreads) void chunk_fwd_kernel(ChunkArgs a) {
     const int64_t slot = sq.slot0 + c;
     __syncthreads();  // the previous chunk's readers of LDS are done
     // Stage the chunk first: the waits for its loads then come before this chunk's own stores.
+    if (!side) {
 #pragma unroll
-    for (int q2 = 0; q2 < 2; ++q2) {
-      const int e = tid + kThreads * q2, t = e >> 4, c8 = (e & 15) * 8;
-      *reinterpret_cast<uint4*>(&Kb[t][c8]) = f.k[q2];
-      *reinterpret_cast<uint4*>(&Qb[t][c8]) = f.q[q2];
-      Vs[t][e & 15] = bf16_to_f32(f.v[q2]);
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const int e = tid + 256 * q4, t = e >> 4, c8 = (e & 15) * 8;
+        *reinterpret_cast<uint4*>(&Kb[t][c8]) = f.k[q4];
+        *reinterpret_cast<uint4*>(&Qb[t][c8]) = f.q[q4];
+      }
+    } else {
+      const int u = tid - 256;
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const int e = u + 256 * q4;
+        Vs[e >> 4][e & 15] = bf16_to_f32(f.v[q4]);
+      }
+      if (u < kC)
+        gam[u] = f.gd;
+      else if (u < 2 * kC)
+        dec[u - kC] = f.gd;
     }
-    if (tid < kC)
-      gam[tid] = f.gd;
-    else if (tid < 2 * kC)
-      dec[tid - kC] = f.gd;
     // The A operands are consumed later in the step: take them here, so their waits are here too.
 #pragma unroll
     for (int u = 0; u < 4; ++u) asm volatile("" : "+v"(f.f[u]));
@@ -127,8 +145,9 @@ __global__ __launch_bounds__(kThreads) void chunk_fwd_kernel(ChunkArgs a) {
         Sl[r][col] = (__bf16)(x - (float)h);
       }
     }
+    if (!side && c + 1 < nch) prefetch(nxt, c + 1);
     __syncthreads();
-    if (c + 1 < nch) prefetch(nxt, c + 1);
+    if (side && c + 1 < nch) prefetch(nxt, c + 1);
 
     // K S^T (waves 0-3) or Q S^T (waves 4-7) for positions i0 + jj, state row li.
     f32x4 xs = zero4();
