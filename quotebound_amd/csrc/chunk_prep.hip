@@ -15,7 +15,7 @@ namespace qbgdn {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kLDK = 144;  // rows 0..3 of a transposing read on distinct banks
+constexpr int kLDK = 144;  // bf16 row stride for Dk = 128: 16-byte aligned rows on staggered banks
 constexpr int kLDF = kC + 4;  // float rows, padded (16-byte aligned)
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
