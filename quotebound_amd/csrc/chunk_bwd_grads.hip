@@ -56,13 +56,6 @@ constexpr int ex1c = edbA + 2 * kC, etq = ex1c + 4 * kC;
 constexpr int kEndBytes = (etq + 2 * kC) * 4;
 constexpr int kSmemBytes = kLoopBytes > kEndBytes ? kLoopBytes : kEndBytes;
 
-// Four consecutive values at element offset at (a multiple of 4) of the hi and lo matrices.
-__device__ __forceinline__ void put4(__bf16* hi, __bf16* lo, int at, float x0, float x1, float x2, float x3) {
-  const Split4 v = split4(x0, x1, x2, x3);
-  *reinterpret_cast<uint2*>(hi + at) = v.hi;
-  *reinterpret_cast<uint2*>(lo + at) = v.lo;
-}
-
 template <typename OutT>
 __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) {
   constexpr int Dk = 128;

@@ -18,20 +18,23 @@ namespace qbgdn {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kLDK = 144;  // rows 0..3 of a transposing read on distinct banks
-constexpr int kLDC = kC + kPadB;
-constexpr int kLT = 80;  // Tb, P rows (swz placement)
+// Row pitches (elements) of the swz-placed LDS matrices: 16 x an odd number.
+constexpr int kLDK = 144;  // k, q rows [64][128]
+constexpr int kLT = 80;    // [.][64]: Tb, P, dDelta^T, (diag(exp G) dR)^T
+constexpr int kLR = 48;    // [.][16]: dS^T, dY, diag(exp G) dY (state rows as columns)
 
 template <typename OutT>
 __global__ __launch_bounds__(kThreads) void chunk_bwd_state_kernel(ChunkArgs a) {
   constexpr int Dk = 128;
   constexpr bool kExactDy = std::is_same<OutT, bf16_t>::value;  // bf16 cotangents enter MFMA exactly
-  __shared__ __bf16 Kb[kC][kLDK], Qb[kC][kLDK];
-  __shared__ __bf16 dSh[16][kLDK], dSl[16][kLDK];
-  __shared__ __bf16 dYth[16][kLDC], dYtl[16][kLDC];   // dY^T [r][i]
-  __shared__ __bf16 GdYth[16][kLDC], GdYtl[16][kLDC]; // (diag(exp G) dY)^T
-  __shared__ __bf16 dDth[16][kLDC], dDtl[16][kLDC];   // dDelta^T [r][j]
-  __shared__ __bf16 GdRth[16][kLDC], GdRtl[16][kLDC]; // -(diag(exp G) dR)^T
+  // Every matrix is placed by swz and stored once, hi and lo: row reads and transposing reads both come free of
+  // bank conflicts.
+  __shared__ __align__(16) __bf16 Kb[kC * kLDK], Qb[kC * kLDK];
+  __shared__ __align__(16) __bf16 dSt[2][Dk * kLR];  // dS^T [c][r]
+  __shared__ __align__(16) __bf16 dYm[2][kC * kLR];  // dY [i][r]
+  __shared__ __align__(16) __bf16 GdYm[2][kC * kLR]; // diag(exp G) dY [i][r]
+  __shared__ __align__(16) __bf16 dDt[2][16 * kLT];  // dDelta^T [r][j]
+  __shared__ __align__(16) __bf16 GdRt[2][16 * kLT]; // -(diag(exp G) dR)^T [r][i]
   __shared__ float gam[kC], dec[kC];
   // Tb (hi, lo) and P (hi, lo) of the chunk, 64 x 64 each (swz placement; the blocks above the diagonal stay zero):
   // the A operands Tb^T and P^T come from their columns through the transposing read.
@@ -65,7 +68,7 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_state_kernel(ChunkArgs a) 
   struct Pre {
     uint4 k[4], q[4];
     uint4 tp[5];     // the packed Tb and P blocks: thread -> 16-byte units tid + 256 u of tb[0..1], p[0..1]
-    uint32_t dy[4];  // raw bits (bf16 in the low half, or float32)
+    uint4 dy;        // dy row tid / 4, state rows 4 (tid % 4) .. + 3: raw bits (4 bf16 in .x, .y, or 4 float32)
     float gam, dec;
   };
   // The loads come in three groups, issued at three points of the chunk before, so no wave stalls long on a full
@@ -94,14 +97,12 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_state_kernel(ChunkArgs a) 
     const auto yr = buffer_rsrc(dy + tok * sv + hv * a.Dv + row0, L * sv * uint32_t(sizeof(OutT)));
     const Tile* tl = a.tiles + ((sq.slot0 + c) * a.Hv + hv);
     f.gam = tl->gam[tid & (kC - 1)], f.dec = tl->dec[tid & (kC - 1)];
-#pragma unroll
-    for (int q4 = 0; q4 < 4; ++q4) {
-      const int e = tid + kThreads * q4, t = e >> 4;
-      const uint32_t yo = uint32_t(t * sv + (e & 15));
-      if constexpr (kExactDy)
-        f.dy[q4] = buf_ld2(yr, yo * 2);
-      else
-        f.dy[q4] = __float_as_uint(buf_ld4(yr, yo * 4));
+    const uint32_t yo = uint32_t((tid >> 2) * sv + 4 * (tid & 3));
+    if constexpr (kExactDy) {
+      const auto t2 = __builtin_amdgcn_raw_buffer_load_b64(yr, int(yo * 2), 0, 0);
+      f.dy = uint4{t2[0], t2[1], 0u, 0u};
+    } else {
+      f.dy = buf_ld16(yr, yo * 4);
     }
   };
 
@@ -120,16 +121,21 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_state_kernel(ChunkArgs a) 
     const int64_t slot = sq.slot0 + c;
     __syncthreads();
     // Stage the chunk first: the waits for its loads then come before this chunk's own stores.
+    // dy's four values of row tid / 4 as floats.
+    const int yt = tid >> 2, yr4 = 4 * (tid & 3);
+    float yv[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const uint32_t b = kExactDy ? (u & 1 ? (&f.dy.x)[u >> 1] & 0xffff0000u : (&f.dy.x)[u >> 1] << 16) : (&f.dy.x)[u];
+      yv[u] = __uint_as_float(b);
+    }
 #pragma unroll
     for (int q4 = 0; q4 < 4; ++q4) {
-      const int e = tid + kThreads * q4, t = e >> 4, r = e & 15, c8 = (e & 15) * 8;
-      *reinterpret_cast<uint4*>(&Kb[t][c8]) = f.k[q4];
-      *reinterpret_cast<uint4*>(&Qb[t][c8]) = f.q[q4];
-      const float x = kExactDy ? __uint_as_float(f.dy[q4] << 16) : __uint_as_float(f.dy[q4]);
-      const __bf16 h = (__bf16)x;
-      dYth[r][t] = h;
-      dYtl[r][t] = (__bf16)(x - (float)h);
+      const int e = tid + kThreads * q4, t = e >> 4, c8 = (e & 15) * 8;
+      *reinterpret_cast<uint4*>(&Kb[swz(t, c8, kLDK)]) = f.k[q4];
+      *reinterpret_cast<uint4*>(&Qb[swz(t, c8, kLDK)]) = f.q[q4];
     }
+    put4(dYm[0], dYm[1], swz(yt, yr4, kLR), yv[0], yv[1], yv[2], yv[3]);
     if (tid < kC) gam[tid] = f.gam, dec[tid] = f.dec;
     // The packed blocks to their places: unit e of a matrix half is row (e % 32) / 2, columns 8 (e % 2) .. of
     // block e / 32 = (I, J) in the order of tri_off.
@@ -140,98 +146,88 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_state_kernel(ChunkArgs a) 
       *reinterpret_cast<uint4*>(&TPL[m][swz(16 * I + ((e & 31) >> 1), 16 * J + 8 * (e & 1), kLT)]) = f.tp[u];
     }
     if (c + 1 < nch) store_dv(c + 1, dr);
-    {
+    {  // dS to the workspace and, as dS^T (four consecutive state rows per lane), to LDS.
       const auto out = buffer_rsrc(a.dsend + ((slot * a.Hv + hv) * a.Dv + row0) * Dk, 16 * Dk * 4);
 #pragma unroll
-      for (int nt = 0; nt < 2; ++nt)
+      for (int nt = 0; nt < 2; ++nt) {
+        const int col = 32 * w + 16 * nt + li;
 #pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-          const int r = 4 * g + jj, col = 32 * w + 16 * nt + li;
-          const float x = dS[nt][jj];
-          BufIO<float>::st(out, uint32_t(r * Dk + col), x);
-          const __bf16 h = (__bf16)x;
-          dSh[r][col] = h;
-          dSl[r][col] = (__bf16)(x - (float)h);
-        }
+        for (int jj = 0; jj < 4; ++jj) BufIO<float>::st(out, uint32_t((4 * g + jj) * Dk + col), dS[nt][jj]);
+        put4(dSt[0], dSt[1], swz(col, 4 * g, kLR), dS[nt]);
+      }
     }
     __syncthreads();
     if (c > 0) load_kq(nxt, c - 1);
-    // (diag(exp G) dY)^T, split (exp G is in LDS now); read in the state update.
-#pragma unroll
-    for (int q4 = 0; q4 < 4; ++q4) {
-      const int e = tid + kThreads * q4, t = e >> 4, r = e & 15;
-      const float x = kExactDy ? __uint_as_float(f.dy[q4] << 16) : __uint_as_float(f.dy[q4]);
-      const float gx = gam[t] * x;
-      const __bf16 gh = (__bf16)gx;
-      GdYth[r][t] = gh;
-      GdYtl[r][t] = (__bf16)(gx - (float)gh);
+    // diag(exp G) dY, split (exp G is in LDS now); read in the state update.
+    {
+      const float gy = gam[yt];
+      put4(GdYm[0], GdYm[1], swz(yt, yr4, kLR), gy * yv[0], gy * yv[1], gy * yv[2], gy * yv[3]);
     }
 
-    // K dS^T for positions j = 16w..: lane -> column r = li, rows j = 16w + 4g + jj.
+    // K dS^T for positions j = 16w..: lane -> column r = li, rows j = 16w + 4g + jj. B = dS rows r, k = c, through
+    // the transposing read of dS^T.
     f32x4 kds = zero4();
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      const bf16x8 ak = lds8(&Kb[16 * w + li][32 * s + 8 * g]);
-      kds = mma(mma(kds, ak, lds8(&dSh[li][32 * s + 8 * g])), ak, lds8(&dSl[li][32 * s + 8 * g]));
+      const bf16x8 ak = lds8(&Kb[swz(16 * w + li, 32 * s + 8 * g, kLDK)]);
+      kds = mma(mma(kds, ak, lds_tr8s(dSt[0] + 32 * s * kLR, kLR, tid)), ak, lds_tr8s(dSt[1] + 32 * s * kLR, kLR, tid));
     }
-    // dDelta rows j = 16w.. = D KdS + P^T dY (A = P^T rows j, k = i).
+    // dDelta rows j = 16w.. = D KdS + P^T dY (A = P^T rows j, k = i; B = dY rows i through the transposing read).
     f32x4 dd;
 #pragma unroll
     for (int jj = 0; jj < 4; ++jj) dd[jj] = dec[16 * w + 4 * g + jj] * kds[jj];
+    // (Both k steps for every wave: the ones above the diagonal add zeros, and the waves that need both set the
+    // pace, so skipping them would only add branches.)
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
-      if (32 * s + 31 >= 16 * w) {
-        // P^T rows j = 16w + li, k = i: column j of P, rows 32s..
-        const Split8 A{lds_tr8s(&TPL[2][32 * s * kLT + 16 * w], kLT, tid), lds_tr8s(&TPL[3][32 * s * kLT + 16 * w], kLT, tid)};
-        if constexpr (kExactDy) {
-          dd = mma2(dd, A, lds8(&dYth[li][32 * s + 8 * g]));
-        } else {
-          dd = mma3(dd, A, Split8{lds8(&dYth[li][32 * s + 8 * g]), lds8(&dYtl[li][32 * s + 8 * g])});
-        }
+      // P^T rows j = 16w + li, k = i: column j of P, rows 32s..
+      const Split8 A{lds_tr8s(&TPL[2][32 * s * kLT + 16 * w], kLT, tid), lds_tr8s(&TPL[3][32 * s * kLT + 16 * w], kLT, tid)};
+      if constexpr (kExactDy) {
+        dd = mma2(dd, A, lds_tr8s(dYm[0] + 32 * s * kLR, kLR, tid));
+      } else {
+        dd = mma3(dd, A, Split8{lds_tr8s(dYm[0] + 32 * s * kLR, kLR, tid), lds_tr8s(dYm[1] + 32 * s * kLR, kLR, tid)});
       }
     }
-#pragma unroll
-    for (int jj = 0; jj < 4; ++jj) {
-      const int j = 16 * w + 4 * g + jj;
-      const __bf16 h = (__bf16)dd[jj];
-      dDth[li][j] = h;
-      dDtl[li][j] = (__bf16)(dd[jj] - (float)h);
-    }
+    put4(dDt[0], dDt[1], swz(li, 16 * w + 4 * g, kLT), dd);
     __syncthreads();
     if (c > 0) load_tp(nxt, c - 1);
 
     // dR = Tb^T dDelta for positions i = 16w.. (A = Tb^T rows i, k = j); dv = dR.
     dr = zero4();
 #pragma unroll
-    for (int s = 0; s < 2; ++s)
-      if (32 * s + 31 >= 16 * w)  // Tb^T is zero below the diagonal
-        dr = mma3(dr,
-                  Split8{lds_tr8s(&TPL[0][32 * s * kLT + 16 * w], kLT, tid),
-                         lds_tr8s(&TPL[1][32 * s * kLT + 16 * w], kLT, tid)},  // Tb^T rows i, k = j
-                  Split8{lds8(&dDth[li][32 * s + 8 * g]), lds8(&dDtl[li][32 * s + 8 * g])});
-#pragma unroll
-    for (int jj = 0; jj < 4; ++jj) {
-      const int i = 16 * w + 4 * g + jj;
-      const float x = -gam[i] * dr[jj];
-      const __bf16 h = (__bf16)x;
-      GdRth[li][i] = h;
-      GdRtl[li][i] = (__bf16)(x - (float)h);
+    for (int s = 0; s < 2; ++s) {  // (both k steps for every wave, as above)
+      const int at = swz(li, 32 * s + 8 * g, kLT);
+      dr = mma3(dr,
+                Split8{lds_tr8s(&TPL[0][32 * s * kLT + 16 * w], kLT, tid),
+                       lds_tr8s(&TPL[1][32 * s * kLT + 16 * w], kLT, tid)},  // Tb^T rows i, k = j
+                Split8{lds8(dDt[0] + at), lds8(dDt[1] + at)});
+    }
+    {
+      const int i0 = 16 * w + 4 * g;
+      put4(GdRt[0], GdRt[1], swz(li, i0, kLT), -gam[i0] * dr[0], -gam[i0 + 1] * dr[1], -gam[i0 + 2] * dr[2],
+           -gam[i0 + 3] * dr[3]);
     }
     __syncthreads();
     if (c > 0) load_dy(nxt, c - 1);
 
-    // dS <- exp(G_63) dS + (diag(exp G) dY)^T Q - (diag(exp G) dR)^T K.
+    // dS <- exp(G_63) dS + (diag(exp G) dY)^T Q - (diag(exp G) dR)^T K: A operands rows r = li, k = i.
     const float glast = gam[kC - 1];
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
+    for (int s = 0; s < 2; ++s) {
+      const int at = swz(li, 32 * s + 8 * g, kLT);
+      const Split8 Ay{lds_tr8s(GdYm[0] + 32 * s * kLR, kLR, tid), lds_tr8s(GdYm[1] + 32 * s * kLR, kLR, tid)};
+      const Split8 Ar{lds8(GdRt[0] + at), lds8(GdRt[1] + at)};
 #pragma unroll
-      for (int jj = 0; jj < 4; ++jj) dS[nt][jj] *= glast;
+      for (int nt = 0; nt < 2; ++nt) {
+        if (s == 0) {
 #pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        const bf16x8 bq = lds_tr8(&Qb[32 * s][32 * w + 16 * nt], kLDK, tid);  // rows 32s.., this lane's state column
-        const bf16x8 bk = lds_tr8(&Kb[32 * s][32 * w + 16 * nt], kLDK, tid);
-        dS[nt] = mma2(dS[nt], Split8{lds8(&GdYth[li][32 * s + 8 * g]), lds8(&GdYtl[li][32 * s + 8 * g])}, bq);
-        dS[nt] = mma2(dS[nt], Split8{lds8(&GdRth[li][32 * s + 8 * g]), lds8(&GdRtl[li][32 * s + 8 * g])}, bk);
+          for (int jj = 0; jj < 4; ++jj) dS[nt][jj] *= glast;
+        }
+        // q and k rows 32s.., this lane's state column
+        const bf16x8 bq = lds_tr8s(&Qb[32 * s * kLDK + 32 * w + 16 * nt], kLDK, tid);
+        const bf16x8 bk = lds_tr8s(&Kb[32 * s * kLDK + 32 * w + 16 * nt], kLDK, tid);
+        dS[nt] = mma2(dS[nt], Ay, bq);
+        dS[nt] = mma2(dS[nt], Ar, bk);
       }
     }
   };

@@ -82,6 +82,16 @@ __device__ __forceinline__ SlotPos slot_pos(const SeqTable& tab, int64_t slot) {
   return SlotPos{n, c, sq.tok0 + t0, min(kC, sq.len - t0)};
 }
 
+// Four consecutive values at element offset at (a multiple of 4) of the hi and lo matrices, as bf16 hi/lo halves.
+__device__ __forceinline__ void put4(__bf16* hi, __bf16* lo, int at, float x0, float x1, float x2, float x3) {
+  const Split4 v = split4(x0, x1, x2, x3);
+  *reinterpret_cast<uint2*>(hi + at) = v.hi;
+  *reinterpret_cast<uint2*>(lo + at) = v.lo;
+}
+__device__ __forceinline__ void put4(__bf16* hi, __bf16* lo, int at, const f32x4& x) {
+  put4(hi, lo, at, x[0], x[1], x[2], x[3]);
+}
+
 // Copies rows [0, L) of a [tokens, H, D] bf16 tensor's head h into LDS rows of length D (stride ld), zero rows past
 // L. 8 elements per access.
 template <int D>

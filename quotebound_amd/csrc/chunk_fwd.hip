@@ -19,13 +19,6 @@ constexpr int kThreads = 512;
 constexpr int kLDK = 144;         // bf16 row stride for Dk = 128 (rows 0..3 of a transposing read on distinct banks)
 constexpr int kLDC = kC + kPadB;  // bf16 row stride for 64 positions
 
-// Four consecutive values as bf16 hi / lo at hi + at, lo + at (at a multiple of 4).
-__device__ __forceinline__ void put4(__bf16* hi, __bf16* lo, int at, const f32x4& x) {
-  const Split4 v = split4(x[0], x[1], x[2], x[3]);
-  *reinterpret_cast<uint2*>(hi + at) = v.hi;
-  *reinterpret_cast<uint2*>(lo + at) = v.lo;
-}
-
 template <typename OutT>
 __global__ __launch_bounds__(kThreads) void chunk_fwd_kernel(ChunkArgs a) {
   constexpr int Dk = 128;
