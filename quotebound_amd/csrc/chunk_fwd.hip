@@ -16,16 +16,20 @@ namespace qbgdn {
 namespace {
 
 constexpr int kThreads = 512;
-constexpr int kLDK = 144;         // bf16 row stride for Dk = 128 (rows 0..3 of a transposing read on distinct banks)
-constexpr int kLDC = kC + kPadB;  // bf16 row stride for 64 positions
+// Row pitches (elements) of the swz-placed LDS matrices: 16 x an odd number.
+constexpr int kLDK = 144;  // k, q rows [64][128]
+constexpr int kLDC = 80;   // [16][64]: R^T, Delta^T, (D Delta)^T
+constexpr int kLR = 48;    // [128][16]: S^T (state rows as columns)
 
 template <typename OutT>
 __global__ __launch_bounds__(kThreads) void chunk_fwd_kernel(ChunkArgs a) {
   constexpr int Dk = 128;
-  __shared__ __align__(16) __bf16 Kb[kC][kLDK], Qb[kC][kLDK];
-  __shared__ __align__(16) __bf16 Sh[16][kLDK], Sl[16][kLDK];
-  __shared__ __align__(16) __bf16 Rth[16][kLDC], Rtl[16][kLDC], Dth[16][kLDC], Dtl[16][kLDC];
-  __shared__ __align__(16) __bf16 DDth[16][kLDC], DDtl[16][kLDC];
+  // Every matrix is placed by swz and stored once, hi and lo: row reads and transposing reads both come free of
+  // bank conflicts.
+  __shared__ __align__(16) __bf16 Kb[kC * kLDK], Qb[kC * kLDK];
+  __shared__ __align__(16) __bf16 St[2][128 * kLR];                       // S^T [c][r]
+  __shared__ __align__(16) __bf16 Rt[2][16 * kLDC], Dt[2][16 * kLDC];  // [r][i]
+  __shared__ __align__(16) __bf16 DDt[2][16 * kLDC];
   __shared__ float Vs[kC][16];
   __shared__ float gam[kC], dec[kC];
 
@@ -84,7 +88,7 @@ __global__ __launch_bounds__(kThreads) void chunk_fwd_kernel(ChunkArgs a) {
     const auto mr = buffer_rsrc(side ? tl->p[0] : tl->tb[0], 2 * kTri * 2);  // hi, then lo
     const int ar = 16 * wp + li;
     f.f[0] = tri_ld8(mr, 0, ar, 8 * g), f.f[1] = tri_ld8(mr, kTri, ar, 8 * g);
-    if (wp >= 2) f.f[2] = tri_ld8(mr, 0, ar, 32 + 8 * g), f.f[3] = tri_ld8(mr, kTri, ar, 32 + 8 * g);  // else zero
+    f.f[2] = tri_ld8(mr, 0, ar, 32 + 8 * g), f.f[3] = tri_ld8(mr, kTri, ar, 32 + 8 * g);  // zeros for rows < 32
   };
 
   // y of a chunk (waves 4-7) is stored during the next chunk, after that chunk's inputs are staged, so no wait for
@@ -106,8 +110,8 @@ __global__ __launch_bounds__(kThreads) void chunk_fwd_kernel(ChunkArgs a) {
 #pragma unroll
       for (int q4 = 0; q4 < 4; ++q4) {
         const int e = tid + 256 * q4, t = e >> 4, c8 = (e & 15) * 8;
-        *reinterpret_cast<uint4*>(&Kb[t][c8]) = f.k[q4];
-        *reinterpret_cast<uint4*>(&Qb[t][c8]) = f.q[q4];
+        *reinterpret_cast<uint4*>(&Kb[swz(t, c8, kLDK)]) = f.k[q4];
+        *reinterpret_cast<uint4*>(&Qb[swz(t, c8, kLDK)]) = f.q[q4];
       }
     } else {
       const int u = tid - 256;
@@ -133,10 +137,8 @@ __global__ __launch_bounds__(kThreads) void chunk_fwd_kernel(ChunkArgs a) {
         const int r = 4 * g + jj, col = 16 * w + li;
         const float x = S[jj];
         BufIO<float>::st(ck, uint32_t(r * Dk + col), x);
-        const __bf16 h = (__bf16)x;
-        Sh[r][col] = h;
-        Sl[r][col] = (__bf16)(x - (float)h);
       }
+      put4(St[0], St[1], swz(16 * w + li, 4 * g, kLR), S);  // S^T: this lane's column, its four rows
     }
     if (!side && c + 1 < nch) prefetch(nxt, c + 1);
     __syncthreads();
@@ -145,34 +147,36 @@ __global__ __launch_bounds__(kThreads) void chunk_fwd_kernel(ChunkArgs a) {
     // K S^T (waves 0-3) or Q S^T (waves 4-7) for positions i0 + jj, state row li.
     f32x4 xs = zero4();
     {
-      const __bf16* M = side ? &Qb[0][0] : &Kb[0][0];
+      const __bf16* M = side ? Qb : Kb;
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        const bf16x8 am = lds8(M + (16 * wp + li) * kLDK + 32 * s + 8 * g);
-        xs = mma(mma(xs, am, lds8(&Sh[li][32 * s + 8 * g])), am, lds8(&Sl[li][32 * s + 8 * g]));
+        const bf16x8 am = lds8(M + swz(16 * wp + li, 32 * s + 8 * g, kLDK));
+        // B = S rows r (n), k = c: the transposing read of S^T
+        xs = mma(mma(xs, am, lds_tr8s(St[0] + 32 * s * kLR, kLR, tid)), am, lds_tr8s(St[1] + 32 * s * kLR, kLR, tid));
       }
     }
     if (!side) {
       f32x4 r;
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj) r[jj] = Vs[i0 + jj][li] - gam[i0 + jj] * xs[jj];
-      put4(&Rth[0][0], &Rtl[0][0], li * kLDC + i0, r);
+      put4(Rt[0], Rt[1], swz(li, i0, kLDC), r);
     }
     __syncthreads();
 
     if (!side) {  // Delta = Tb R for positions i0 + jj
       f32x4 dl = zero4();
+      // Both k steps for every wave: Tb's entries above the diagonal are zeros, and the waves that need both set
+      // the pace, so skipping would only add branches.
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
-        if (32 * s <= 16 * wp + 15)  // Tb is zero above the diagonal
-          dl = mma3(dl, Split8{f.f[2 * s], f.f[2 * s + 1]},
-                    Split8{lds8(&Rth[li][32 * s + 8 * g]), lds8(&Rtl[li][32 * s + 8 * g])});
+        const int at = swz(li, 32 * s + 8 * g, kLDC);
+        dl = mma3(dl, Split8{f.f[2 * s], f.f[2 * s + 1]}, Split8{lds8(Rt[0] + at), lds8(Rt[1] + at)});
       }
       f32x4 dd;
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj) dd[jj] = dec[i0 + jj] * dl[jj];
-      put4(&Dth[0][0], &Dtl[0][0], li * kLDC + i0, dl);
-      put4(&DDth[0][0], &DDtl[0][0], li * kLDC + i0, dd);
+      put4(Dt[0], Dt[1], swz(li, i0, kLDC), dl);
+      put4(DDt[0], DDt[1], swz(li, i0, kLDC), dd);
     }
     __syncthreads();
 
@@ -183,8 +187,9 @@ __global__ __launch_bounds__(kThreads) void chunk_fwd_kernel(ChunkArgs a) {
       for (int jj = 0; jj < 4; ++jj) S[jj] *= glast;
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
-        const Split8 A{lds8(&DDth[li][32 * s + 8 * g]), lds8(&DDtl[li][32 * s + 8 * g])};
-        S = mma2(S, A, lds_tr8(&Kb[32 * s][16 * w], kLDK, tid));  // K rows 32s.., this lane's state column
+        const int at = swz(li, 32 * s + 8 * g, kLDC);
+        const Split8 A{lds8(DDt[0] + at), lds8(DDt[1] + at)};
+        S = mma2(S, A, lds_tr8s(Kb + 32 * s * kLDK + 16 * w, kLDK, tid));  // K rows 32s.., this lane's state column
       }
     }
     if (side) {  // Y = diag(exp G) QS + P Delta for positions i0 + jj (P is zero above the diagonal)
@@ -192,9 +197,8 @@ __global__ __launch_bounds__(kThreads) void chunk_fwd_kernel(ChunkArgs a) {
       for (int jj = 0; jj < 4; ++jj) yacc[jj] = gam[i0 + jj] * xs[jj];
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
-        if (32 * s <= 16 * wp + 15)
-          yacc = mma3(yacc, Split8{f.f[2 * s], f.f[2 * s + 1]},
-                      Split8{lds8(&Dth[li][32 * s + 8 * g]), lds8(&Dtl[li][32 * s + 8 * g])});
+        const int at = swz(li, 32 * s + 8 * g, kLDC);
+        yacc = mma3(yacc, Split8{f.f[2 * s], f.f[2 * s + 1]}, Split8{lds8(Dt[0] + at), lds8(Dt[1] + at)});
       }
     }
   };
