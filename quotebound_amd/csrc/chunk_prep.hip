@@ -16,7 +16,6 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kLDK = 144;  // bf16 row stride for Dk = 128: 16-byte aligned rows on staggered banks
-constexpr int kLDF = kC + 4;  // float rows, padded (16-byte aligned)
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 
@@ -25,12 +24,21 @@ __device__ __forceinline__ f32x4 mma16(f32x4 c, s16x4 a, s16x4 b) {
   return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
 }
 
+// LDS: k and q rows while K K^T and Q K^T run; then, in the same bytes, A and T in float32 and P as bf16 hi/lo,
+// each as its ten lower-triangular blocks (tri_off). About 37 KB, so four blocks share a CU.
+constexpr int kKQBytes = 2 * kC * kLDK * 2;
+constexpr int kAoff = 0, kToff = kTri * 4, kPoff = 2 * kTri * 4;  // byte offsets of A, T, P (hi then lo)
+static_assert(kPoff + 2 * kTri * 2 <= kKQBytes, "A, T and P fit in the k/q staging bytes");
+
 __global__ __launch_bounds__(kThreads) void chunk_prep_kernel(ChunkArgs a) {
-  __shared__ __bf16 Kb[kC][kLDK], Qb[kC][kLDK];
-  __shared__ float Am[kC][kLDF];
-  __shared__ float Tm[kC][kLDF];
+  __shared__ __align__(16) unsigned char smem[kKQBytes];
   __shared__ double Gd[kC];
   __shared__ float Bs[kC];
+  __bf16* Kb = reinterpret_cast<__bf16*>(smem);  // [kC][kLDK]
+  __bf16* Qb = Kb + kC * kLDK;
+  float* Am = reinterpret_cast<float*>(smem + kAoff);
+  float* Tm = reinterpret_cast<float*>(smem + kToff);
+  __bf16* Pp = reinterpret_cast<__bf16*>(smem + kPoff);  // hi; lo at + kTri
 
   const int total = int(a.lay.NC) * a.Hv;
   const int wid = xcd_remap(blockIdx.x, total);
@@ -40,11 +48,20 @@ __global__ __launch_bounds__(kThreads) void chunk_prep_kernel(ChunkArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 4, li = lane & 15;
   Tile* tile = a.tiles + (slot * a.Hv + hv);
 
-  // K and Q rows through buffer resources that end at the chunk's last row (rows past it read as zeros), all
-  // issued before any is used.
+  // g and beta first (one wave), then the K and Q rows, through buffer resources that end at the chunk's last row
+  // (rows past it read as zeros); all issued before any is used.
+  const uint32_t L = uint32_t(sp.L);
+  float gx = 0.f, bx = 0.f;
+  if (tid < kC) {
+    const int64_t s0 = sp.tok * a.Hv + hv;
+    const auto gr = buffer_rsrc(a.g + s0, L == 0 ? 0u : ((L - 1) * uint32_t(a.Hv) + 1) * 4u);
+    const auto br = buffer_rsrc(a.beta + s0, L == 0 ? 0u : ((L - 1) * uint32_t(a.Hv) + 1) * 2u);
+    gx = buf_ld4(gr, uint32_t(tid * a.Hv) * 4);
+    bx = bf16_to_f32(buf_ld2(br, uint32_t(tid * a.Hv) * 2));
+  }
   {
     const int sk = a.Hk * 128;
-    const uint32_t bytes = uint32_t(sp.L) * uint32_t(sk) * 2u;
+    const uint32_t bytes = L * uint32_t(sk) * 2u;
     const auto kr = buffer_rsrc(a.k + sp.tok * sk + hk * 128, bytes), qr = buffer_rsrc(a.q + sp.tok * sk + hk * 128, bytes);
     uint4 kv[4], qv[4];
 #pragma unroll
@@ -56,20 +73,15 @@ __global__ __launch_bounds__(kThreads) void chunk_prep_kernel(ChunkArgs a) {
 #pragma unroll
     for (int q4 = 0; q4 < 4; ++q4) {
       const int e = tid + kThreads * q4, t = e >> 4, c8 = (e & 15) * 8;
-      *reinterpret_cast<uint4*>(&Kb[t][c8]) = kv[q4];
-      *reinterpret_cast<uint4*>(&Qb[t][c8]) = qv[q4];
+      *reinterpret_cast<uint4*>(Kb + t * kLDK + c8) = kv[q4];
+      *reinterpret_cast<uint4*>(Qb + t * kLDK + c8) = qv[q4];
     }
   }
-  // One wave: beta, and G = the inclusive prefix sum of the log-decays (fp64, by a shuffle scan).
+  // One wave: G = the inclusive prefix sum of the log-decays, accumulated in fp64 by a shuffle scan (so G_i - G_j
+  // keeps its bits when |G| is large).
   if (tid < kC) {
     const int t = tid;
-    const uint32_t L = uint32_t(sp.L);
-    const int64_t s0 = sp.tok * a.Hv + hv;
-    const auto gr = buffer_rsrc(a.g + s0, L == 0 ? 0u : ((L - 1) * uint32_t(a.Hv) + 1) * 4u);
-    const auto br = buffer_rsrc(a.beta + s0, L == 0 ? 0u : ((L - 1) * uint32_t(a.Hv) + 1) * 2u);
-    const float gx = buf_ld4(gr, uint32_t(t * a.Hv) * 4);
-    const float bx = bf16_to_f32(buf_ld2(br, uint32_t(t * a.Hv) * 2));
-    double G = uint32_t(t) < L ? (a.g_is_log ? double(gx) : log(double(gx))) : 0.0;
+    double G = uint32_t(t) < L ? (a.g_is_log ? double(gx) : double(logf(gx))) : 0.0;
 #pragma unroll
     for (int off = 1; off < kC; off <<= 1) {
       const double u = __shfl_up(G, off);
@@ -85,53 +97,46 @@ __global__ __launch_bounds__(kThreads) void chunk_prep_kernel(ChunkArgs a) {
   }
   __syncthreads();
 
-  // Row strip w: A (into LDS) and P, lane -> column j = 16 nj + li, rows i = 16 w + 4g + jj. P's hi and lo halves go
-  // into this strip's own rows of Qb (columns 0..63 and 64..127), which no other wave reads.
-  f32x4 pq[4];
-  for (int nj = 0; nj < 4; ++nj) {
-    f32x4 kk = zero4(), qk = zero4();
-    if (nj <= w) {
+  // The ten lower-triangular 16 x 16 blocks (I, J) of A and P, block b = tri_off order, round-robin over the waves
+  // (three, three, two, two): K K^T and Q K^T on MFMA, lane -> column j = 16 J + li, rows i = 16 I + 4g + jj. The
+  // results wait in registers until every wave is done with the k and q rows, whose bytes A and P then take.
+  f32x4 kk[3], qk[3];
+#pragma unroll
+  for (int u = 0; u < 3; ++u) {
+    const int b = w + 4 * u;
+    const int I = (b >= 1) + (b >= 3) + (b >= 6), J = b - I * (I + 1) / 2;
+    kk[u] = zero4(), qk[u] = zero4();
+    if (b < 10) {
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        const bf16x8 b = lds8(&Kb[16 * nj + li][32 * s + 8 * g]);
-        kk = mma(kk, lds8(&Kb[16 * w + li][32 * s + 8 * g]), b);
-        qk = mma(qk, lds8(&Qb[16 * w + li][32 * s + 8 * g]), b);
+        const bf16x8 bk = lds8(Kb + (16 * J + li) * kLDK + 32 * s + 8 * g);
+        kk[u] = mma(kk[u], lds8(Kb + (16 * I + li) * kLDK + 32 * s + 8 * g), bk);
+        qk[u] = mma(qk[u], lds8(Qb + (16 * I + li) * kLDK + 32 * s + 8 * g), bk);
       }
     }
-#pragma unroll
-    for (int jj = 0; jj < 4; ++jj) {
-      const int i = 16 * w + 4 * g + jj, j = 16 * nj + li;
-      const float e = j <= i ? expf(float(Gd[i] - Gd[j])) : 0.f;
-      Am[i][j] = j < i ? Bs[i] * e * kk[jj] : 0.f;
-      pq[nj][jj] = e * qk[jj];
-    }
   }
-  // Every lane of the strip has read its Q rows (the MFMAs above): wave-level order suffices.
-  __builtin_amdgcn_wave_barrier();
-#pragma unroll
-  for (int nj = 0; nj < 4; ++nj)
-#pragma unroll
-    for (int jj = 0; jj < 4; ++jj) {
-      const int i = 16 * w + 4 * g + jj, j = 16 * nj + li;
-      const float x = pq[nj][jj];
-      const __bf16 h = (__bf16)x;
-      Qb[i][j] = h;
-      Qb[i][64 + j] = (__bf16)(x - (float)h);
-    }
   __syncthreads();
-  // P's blocks on or below the diagonal: thread -> row tid / 4 of block (row tid / 64, column tid % 4), as two
-  // 16-byte stores per half.
-  {
-    const int i = tid >> 2, j0 = (tid & 3) * 16;
-    if ((j0 >> 4) <= (i >> 4)) {
 #pragma unroll
-      for (int hl = 0; hl < 2; ++hl) {
-        bf16_t* dst = tile->p[hl] + tri_off(i, j0);
-        *reinterpret_cast<uint4*>(dst) = *reinterpret_cast<const uint4*>(&Qb[i][64 * hl + j0]);
-        *reinterpret_cast<uint4*>(dst + 8) = *reinterpret_cast<const uint4*>(&Qb[i][64 * hl + j0 + 8]);
+  for (int u = 0; u < 3; ++u) {
+    const int b = w + 4 * u;
+    if (b < 10) {
+      const int I = (b >= 1) + (b >= 3) + (b >= 6), J = b - I * (I + 1) / 2;
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        const int i = 16 * I + 4 * g + jj, j = 16 * J + li, at = tri_off(i, j);
+        const float e = j <= i ? expf(float(Gd[i] - Gd[j])) : 0.f;
+        Am[at] = j < i ? Bs[i] * e * kk[u][jj] : 0.f;
+        const float x = e * qk[u][jj];
+        const __bf16 h = (__bf16)x;
+        Pp[at] = h;
+        Pp[kTri + at] = (__bf16)(x - (float)h);
       }
     }
   }
+  __syncthreads();
+  // P, hi and lo, to the tile: the packed bytes as they are, 16 bytes per thread and step.
+  for (int u = tid; u < 2 * kTri / 8; u += kThreads)
+    *reinterpret_cast<uint4*>(tile->p[0] + 8 * u) = *reinterpret_cast<const uint4*>(Pp + 8 * u);
 
   // Diagonal blocks: thread -> column j of block bd; the column lives in registers through the substitution.
   if (tid < kC) {
@@ -141,15 +146,11 @@ __global__ __launch_bounds__(kThreads) void chunk_prep_kernel(ChunkArgs a) {
     for (int il = 0; il < 16; ++il) {
       float v = il == jl ? 1.f : 0.f;
 #pragma unroll
-      for (int kl = 0; kl < il; ++kl) v -= Am[b0 + il][b0 + kl] * x[kl];  // x[kl] = 0 for kl < jl
+      for (int kl = 0; kl < il; ++kl) v -= Am[tri_off(b0 + il, b0 + kl)] * x[kl];  // x[kl] = 0 for kl < jl
       x[il] = il >= jl ? v : 0.f;
     }
 #pragma unroll
-    for (int il = 0; il < 16; ++il) Tm[b0 + il][b0 + jl] = x[il];
-  }
-  for (int e = tid; e < kC * kC; e += kThreads) {  // blocks above the diagonal are zero
-    const int i = e / kC, j = e % kC;
-    if ((j >> 4) > (i >> 4)) Tm[i][j] = 0.f;
+    for (int il = 0; il < 16; ++il) Tm[tri_off(b0 + il, b0 + jl)] = x[il];
   }
   __syncthreads();
   // Off-diagonal blocks at distance d = I - J, one wave per block (wave w: I = d + w, J = w), on MFMA with split
@@ -166,15 +167,15 @@ __global__ __launch_bounds__(kThreads) void chunk_prep_kernel(ChunkArgs a) {
         float x[8], y[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-          x[j] = in ? Am[16 * I + li][k0 + j] : 0.f;  // A rows 16 I + li, columns k
-          y[j] = in ? Tm[k0 + j][16 * J + li] : 0.f;  // T rows k, column 16 J + li
+          x[j] = in ? Am[tri_off(16 * I + li, k0 + j)] : 0.f;  // A rows 16 I + li, columns k
+          y[j] = in ? Tm[tri_off(k0 + j, 16 * J + li)] : 0.f;  // T rows k, column 16 J + li
         }
         W = mma3(W, split8(x), split8(y));
       }
       s16x4 th, tl, wh, wl;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const float t = Tm[16 * I + li][16 * I + 4 * g + j];  // T_II rows li, k = 4g + j
+        const float t = Tm[tri_off(16 * I + li, 16 * I + 4 * g + j)];  // T_II rows li, k = 4g + j
         const __bf16 a = (__bf16)t, b = (__bf16)W[j];
         th[j] = __builtin_bit_cast(short, a);
         tl[j] = __builtin_bit_cast(short, (__bf16)(t - (float)a));
@@ -186,7 +187,7 @@ __global__ __launch_bounds__(kThreads) void chunk_prep_kernel(ChunkArgs a) {
       R = mma16(R, th, wl);
       R = mma16(R, tl, wh);
 #pragma unroll
-      for (int jj = 0; jj < 4; ++jj) Tm[16 * I + 4 * g + jj][16 * J + li] = -R[jj];
+      for (int jj = 0; jj < 4; ++jj) Tm[tri_off(16 * I + 4 * g + jj, 16 * J + li)] = -R[jj];
     }
     __syncthreads();
   }
@@ -199,7 +200,7 @@ __global__ __launch_bounds__(kThreads) void chunk_prep_kernel(ChunkArgs a) {
       bf16x8 th[2], tl[2], bh[2], bl[2];
 #pragma unroll
       for (int u = 0; u < 16; ++u) {
-        const float t = Tm[i][j0 + u], x = t * Bs[j0 + u];
+        const float t = Tm[tri_off(i, j0 + u)], x = t * Bs[j0 + u];
         const __bf16 ht = (__bf16)t, hx = (__bf16)x;
         th[u >> 3][u & 7] = ht;
         tl[u >> 3][u & 7] = (__bf16)(t - (float)ht);
