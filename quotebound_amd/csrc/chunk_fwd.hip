@@ -1,14 +1,20 @@
 // Chunked design, kernel 2: the forward state pass. One block (8 waves) per (sequence, value head, 16 state rows),
 // sequential over the sequence's chunks; rows of the state evolve independently (reference src/delta_grad.cpp:13),
-// so a 16-row block needs no other block. Per chunk, with S the block's rows of the state at the chunk start:
-//   write S to the chunk's checkpoint slot (the reference's ckpt, src/delta_grad.cpp:172-181)
-//   KS = K S^T, R = V - diag(exp G) KS, Delta = Tb R             waves 0-3, positions 16w..16w+15: the chain
-//   QS = Q S^T, Y = diag(exp G) QS + P Delta                      waves 4-7, positions 16(w-4)..: off the chain
-//   S <- exp(G_63) S + (diag(exp(G_63 - G)) Delta)^T K            every wave: state columns 16w..16w+15
-// Two waves share each SIMD, one on the chain and one beside it. Tb and P come ready from the prep kernel (each
-// wave loads its rows as MFMA A operands). All products run on v_mfma_f32_16x16x32_bf16; float32 operands (S, R,
-// Delta, Tb, P) are split into bf16 hi + lo pairs so the state keeps float32 accuracy, while k, q, v enter exactly.
-// The next chunk's inputs are loaded into registers while the current chunk computes.
+// so a 16-row block needs no other block. Per chunk, with S the block's rows of the state at the chunk start, every
+// product is formed transposed, so that a lane holds one position i and four consecutive state rows r (or one
+// state row and four consecutive columns):
+//   write S to LDS and to the chunk's checkpoint slot (the reference's ckpt, src/delta_grad.cpp:172-181)
+//   R^T = V^T - (S K^T) diag(exp G),  Delta^T = R^T Tb^T          waves 0-3, positions 16w..16w+15
+//   S^T <- exp(G_63) S^T + K^T (D Delta),  D = diag(exp(G_63 - G)) waves 0-3, state columns 32w..32w+31
+//   Y^T = (S Q^T) diag(exp G) + Delta^T P^T                        waves 4-7, positions 16(w-4)..: off the chain
+// Three barriers per chunk. Waves 0-3 carry the recurrence and touch no global memory but the checkpoint stores:
+// waves 4-7 load every input of the next chunk, in two groups issued in the two windows where they would otherwise
+// wait for the chain, keep their own q and P rows in registers, and stage the chain's k rows, packed Tb, v and
+// exp G in LDS (two buffers, by chunk parity); K^T for the state update comes from the staged k rows through the
+// transposing read. The two groups run loops of their own, so that each loop holds only its own group's memory
+// operations: the compiler's waits stay exact and none covers a load issued for a later chunk. All products run
+// on v_mfma_f32_16x16x32_bf16; float32 operands (S, R, Delta, Tb, P) are split into bf16 hi + lo pairs so the state
+// keeps float32 accuracy, while k, q, v enter exactly.
 #include "chunk_common.h"
 #include "chunk_kernels.h"
 
@@ -17,205 +23,238 @@ namespace {
 
 constexpr int kThreads = 512;
 // Row pitches (elements) of the swz-placed LDS matrices: 16 x an odd number.
-constexpr int kLDK = 144;  // k, q rows [64][128]
-constexpr int kLDC = 80;   // [16][64]: R^T, Delta^T, (D Delta)^T
-constexpr int kLR = 48;    // [128][16]: S^T (state rows as columns)
+constexpr int kLS = 144;  // S [16][128]
+constexpr int kLK = 144;  // K [64][128]
+constexpr int kLP = 48;   // [64][16]: R, Delta, D Delta (positions as rows)
+constexpr int kTbUnits = 3 * 256;  // 16-byte units of a staged packed Tb (hi, lo: 640 used, the rest padding)
+
+__device__ __forceinline__ float bf16_lo(uint32_t x) { return __uint_as_float(x << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t x) { return __uint_as_float(x & 0xffff0000u); }
 
 template <typename OutT>
 __global__ __launch_bounds__(kThreads) void chunk_fwd_kernel(ChunkArgs a) {
   constexpr int Dk = 128;
   // Every matrix is placed by swz and stored once, hi and lo: row reads and transposing reads both come free of
-  // bank conflicts.
-  __shared__ __align__(16) __bf16 Kb[kC * kLDK], Qb[kC * kLDK];
-  __shared__ __align__(16) __bf16 St[2][128 * kLR];                       // S^T [c][r]
-  __shared__ __align__(16) __bf16 Rt[2][16 * kLDC], Dt[2][16 * kLDC];  // [r][i]
-  __shared__ __align__(16) __bf16 DDt[2][16 * kLDC];
-  __shared__ float Vs[kC][16];
-  __shared__ float gam[kC], dec[kC];
+  // bank conflicts. The staged inputs have two buffers, by chunk parity.
+  __shared__ __align__(16) __bf16 Sm[2][16 * kLS];
+  __shared__ __align__(16) __bf16 Rm[2][kC * kLP], Dm[2][kC * kLP], DDm[2][kC * kLP];
+  __shared__ __align__(16) __bf16 Kb[2][kC * kLK];
+  __shared__ __align__(16) __bf16 Tbp[2][kTbUnits * 8];  // packed Tb (tri_off), hi then lo
+  __shared__ __align__(16) bf16_t Vs[2][256 * 8];        // v [64][16] (units 128.. padding)
+  __shared__ __align__(16) float Gs[2][256];             // exp G [64], D [64] (the rest padding)
 
   const int total = a.nblk * a.Hv * a.N;
   const int wid = xcd_remap(blockIdx.x, total);
   const int blk = wid % a.nblk, hv = (wid / a.nblk) % a.Hv, n = wid / (a.nblk * a.Hv);
   const int hk = hv / (a.Hv / a.Hk), row0 = 16 * blk;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 4, li = lane & 15;
-  const int wp = w & 3;            // position tile
-  const bool side = w >= 4;        // off the chain: Q S^T and Y
-  const int i0 = 16 * wp + 4 * g;  // first of the lane's accumulator positions
+  const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, li = lane & 15;
+  // The wave index, made visibly uniform so that its branches are scalar and buffer resources stay in scalar
+  // registers.
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const bool side = w >= 4;
+  const int wp = w & 3, ip = 16 * wp + li;  // position tile; the lane's position in products over positions
+  const int u = tid & 255;                   // waves 4-7: thread index within the loading group
   const Seq sq = seq_of(a.tab, n);
   const int nch = (sq.len + kC - 1) / kC;
   OutT* y = static_cast<OutT*>(a.y);
   const int sk = a.Hk * Dk, sv = a.Hv * a.Dv;  // token strides of k/q and v/y
+  const int64_t srow = (int64_t(n) * a.Hv + hv) * a.Dv + row0 + li;  // the lane's state row
 
-  // State: wave w holds rows 4g + jj, columns 16w + li.
-  f32x4 S;
-#pragma unroll
-  for (int jj = 0; jj < 4; ++jj)
-    S[jj] = a.s0 ? a.s0[((int64_t(n) * a.Hv + hv) * a.Dv + row0 + 4 * g + jj) * Dk + 16 * w + li] : 0.f;
-
-  // One chunk's inputs, loaded into registers a chunk ahead: k and q rows by waves 0-3, right after they have
-  // written the state (they then wait for waves 4-7 anyway); v, exp G, D by waves 4-7 after the barrier; each wave's
-  // own A operand rows. k, q, v go through buffer resources that end at the sequence's last row, so rows past it
-  // read as zeros without a branch.
-  struct Pre {
-    uint4 k[4], q[4];  // waves 0-3, thread e = tid + 256 q4: row e / 16, columns 8 (e % 16) ..
-    uint16_t v[4];     // waves 4-7, e = tid - 256 + 256 q4: v row e / 16, state row e % 16
-    bf16x8 f[4];       // waves 0-3: Tb rows 16 wp + li; waves 4-7: P rows (k = 8g.., two k steps, hi and lo)
-    float gd;          // waves 4-5: exp G (tid - 256 < 64), then D = exp(G_63 - G)
+  // Waves 4-7: one chunk's inputs. q and P rows stay in registers as MFMA operands of the wave's positions (two
+  // register sets in turn); the rest goes to LDS in the same chunk. k, q, v go through buffer resources that end
+  // at the sequence's last row, so rows past it read as zeros without a branch; units past the packed Tb, v or the
+  // two per-position vectors read as zeros and land in padding.
+  struct Own {
+    uint4 q[4];   // q at position ip, columns 32 s + 8 g ..
+    bf16x8 p[4];  // P row ip, columns 8 g.. and 32 + 8 g.., hi and lo
   };
-  auto prefetch = [&](Pre& f, int c) {
+  struct Stage {
+    uint4 k[4];   // k units u + 256 q4: row e / 16, columns 8 (e % 16) ..
+    uint4 tb[3];  // packed Tb units u + 256 t
+    uint4 v;      // v unit u: row u / 2, state rows 8 (u % 2) ..
+    float gd;     // exp G_u (u < 64), D_(u - 64) (u < 128)
+  };
+  // Two load groups per chunk, each issued where these waves would otherwise wait for the chain: (a) k, packed Tb
+  // and the per-position vectors, staged later in the same chunk; (b) q and P rows for the wave's own products, and
+  // v.
+  auto load_a = [&](Stage& st, int c) {
     const int64_t slot = sq.slot0 + c, tok = sq.tok0 + int64_t(c) * kC;
     const uint32_t L = uint32_t(min(kC, sq.len - c * kC));
-    const auto kr = buffer_rsrc(a.k + tok * sk + hk * Dk, L * sk * 2);
-    const auto qr = buffer_rsrc(a.q + tok * sk + hk * Dk, L * sk * 2);
-    const auto vr = buffer_rsrc(a.v + tok * sv + hv * a.Dv + row0, L * sv * 2);
     const Tile* tl = a.tiles + (slot * a.Hv + hv);
-    if (!side) {
+    const auto kr = buffer_rsrc(a.k + tok * sk + hk * Dk, L * sk * 2);
 #pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4) {
-        const int e = tid + 256 * q4, t = e >> 4, c8 = (e & 15) * 8;
-        f.k[q4] = buf_ld16(kr, uint32_t(t * sk + c8) * 2);
-        f.q[q4] = buf_ld16(qr, uint32_t(t * sk + c8) * 2);
-      }
-    } else {
-      const int u = tid - 256;
-      f.gd = (u < kC ? tl->gam : tl->dec)[u & (kC - 1)];
-#pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4) {
-        const int e = u + 256 * q4, t = e >> 4;
-        f.v[q4] = buf_ld2(vr, uint32_t(t * sv + (e & 15)) * 2);
-      }
+    for (int q4 = 0; q4 < 4; ++q4) {
+      const int e = u + 256 * q4;
+      st.k[q4] = buf_ld16(kr, uint32_t((e >> 4) * sk + (e & 15) * 8) * 2);
     }
-    const auto mr = buffer_rsrc(side ? tl->p[0] : tl->tb[0], 2 * kTri * 2);  // hi, then lo
-    const int ar = 16 * wp + li;
-    f.f[0] = tri_ld8(mr, 0, ar, 8 * g), f.f[1] = tri_ld8(mr, kTri, ar, 8 * g);
-    f.f[2] = tri_ld8(mr, 0, ar, 32 + 8 * g), f.f[3] = tri_ld8(mr, kTri, ar, 32 + 8 * g);  // zeros for rows < 32
+    const auto tr = buffer_rsrc(tl->tb[0], 2 * kTri * 2);
+#pragma unroll
+    for (int t = 0; t < 3; ++t) st.tb[t] = buf_ld16(tr, uint32_t(u + 256 * t) * 16);
+    const auto gr = buffer_rsrc(tl->gam, 2 * kC * 4);  // gam, then dec
+    st.gd = buf_ld4(gr, uint32_t(u) * 4);
   };
-
-  // y of a chunk (waves 4-7) is stored during the next chunk, after that chunk's inputs are staged, so no wait for
-  // the staged loads ever covers these stores.
-  auto store_y = [&](int c, const f32x4& yacc) {
-    const int64_t tok = sq.tok0 + int64_t(c) * kC;
+  auto load_b = [&](Own& o, Stage& st, int c) {
+    const int64_t slot = sq.slot0 + c, tok = sq.tok0 + int64_t(c) * kC;
     const uint32_t L = uint32_t(min(kC, sq.len - c * kC));
-    // Rows i >= L fall past the resource and are dropped.
-    const auto yr = buffer_rsrc(y + tok * sv + hv * a.Dv + row0, L * sv * uint32_t(sizeof(OutT)));
+    const Tile* tl = a.tiles + (slot * a.Hv + hv);
+    const auto qr = buffer_rsrc(a.q + tok * sk + hk * Dk, L * sk * 2);
 #pragma unroll
-    for (int jj = 0; jj < 4; ++jj) BufIO<OutT>::st(yr, uint32_t((i0 + jj) * sv + li), yacc[jj]);
+    for (int s = 0; s < 4; ++s) o.q[s] = buf_ld16(qr, uint32_t(ip * sk + 32 * s + 8 * g) * 2);
+    const auto vr = buffer_rsrc(a.v + tok * sv + hv * a.Dv + row0, L * sv * 2);
+    st.v = buf_ld16(vr, u < 128 ? uint32_t((u >> 1) * sv + 8 * (u & 1)) * 2 : 0x80000000u);
+    const auto pr = buffer_rsrc(tl->p[0], 2 * kTri * 2);  // hi, then lo
+    o.p[0] = tri_ld8(pr, 0, ip, 8 * g), o.p[1] = tri_ld8(pr, kTri, ip, 8 * g);
+    o.p[2] = tri_ld8(pr, 0, ip, 32 + 8 * g), o.p[3] = tri_ld8(pr, kTri, ip, 32 + 8 * g);  // zeros for rows < 32
   };
-
-  auto step = [&](int c, Pre& f, Pre& nxt, f32x4& yacc) {
-    const int64_t slot = sq.slot0 + c;
-    __syncthreads();  // the previous chunk's readers of LDS are done
-    // Stage the chunk first: the waits for its loads then come before this chunk's own stores.
-    if (!side) {
+  auto stage_a = [&](const Stage& st, int b) {
 #pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4) {
-        const int e = tid + 256 * q4, t = e >> 4, c8 = (e & 15) * 8;
-        *reinterpret_cast<uint4*>(&Kb[swz(t, c8, kLDK)]) = f.k[q4];
-        *reinterpret_cast<uint4*>(&Qb[swz(t, c8, kLDK)]) = f.q[q4];
-      }
-    } else {
-      const int u = tid - 256;
-#pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4) {
-        const int e = u + 256 * q4;
-        Vs[e >> 4][e & 15] = bf16_to_f32(f.v[q4]);
-      }
-      if (u < kC)
-        gam[u] = f.gd;
-      else if (u < 2 * kC)
-        dec[u - kC] = f.gd;
+    for (int q4 = 0; q4 < 4; ++q4) {
+      const int e = u + 256 * q4;
+      *reinterpret_cast<uint4*>(Kb[b] + swz(e >> 4, (e & 15) * 8, kLK)) = st.k[q4];
     }
-    // The A operands are consumed later in the step: take them here, so their waits are here too.
 #pragma unroll
-    for (int u = 0; u < 4; ++u) asm volatile("" : "+v"(f.f[u]));
-    if (side && c > 0) store_y(c - 1, yacc);
-    {  // S to the checkpoint and, split, to LDS.
-      const auto ck = a.ckpt ? buffer_rsrc(a.ckpt + ((slot * a.Hv + hv) * a.Dv + row0) * Dk, 16 * Dk * 4)
-                             : buffer_rsrc(a.s0, 0);
-#pragma unroll
-      for (int jj = 0; jj < 4; ++jj) {
-        const int r = 4 * g + jj, col = 16 * w + li;
-        const float x = S[jj];
-        BufIO<float>::st(ck, uint32_t(r * Dk + col), x);
-      }
-      put4(St[0], St[1], swz(16 * w + li, 4 * g, kLR), S);  // S^T: this lane's column, its four rows
-    }
-    if (!side && c + 1 < nch) prefetch(nxt, c + 1);
-    __syncthreads();
-    if (side && c + 1 < nch) prefetch(nxt, c + 1);
+    for (int t = 0; t < 3; ++t) *reinterpret_cast<uint4*>(Tbp[b] + 8 * (u + 256 * t)) = st.tb[t];
+    Gs[b][u] = st.gd;
+  };
+  auto stage_b = [&](const Stage& st, int b) { *reinterpret_cast<uint4*>(Vs[b] + 8 * u) = st.v; };
 
-    // K S^T (waves 0-3) or Q S^T (waves 4-7) for positions i0 + jj, state row li.
-    f32x4 xs = zero4();
-    {
-      const __bf16* M = side ? Qb : Kb;
+  // The two wave groups run loops of their own, with the same three barriers per chunk (a barrier counts waves,
+  // not program points): each loop then holds only its own group's memory operations, and the compiler's waits in
+  // it are exact.
+  if (side) {
+    auto step = [&](int c, Own& f, Own& nxt, Stage& st) {
+      const int b = c & 1, cn = min(c + 1, nch - 1);  // the last chunk loads itself again rather than branch
+      __syncthreads();
+      load_a(st, cn);
+      f32x4 xh = zero4(), xl = zero4();  // the hi and lo halves of S in two independent chains
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        const bf16x8 am = lds8(M + swz(16 * wp + li, 32 * s + 8 * g, kLDK));
-        // B = S rows r (n), k = c: the transposing read of S^T
-        xs = mma(mma(xs, am, lds_tr8s(St[0] + 32 * s * kLR, kLR, tid)), am, lds_tr8s(St[1] + 32 * s * kLR, kLR, tid));
+        const int at = swz(li, 32 * s + 8 * g, kLS);
+        const bf16x8 bq = __builtin_bit_cast(bf16x8, f.q[s]);
+        xh = mma(xh, lds8(Sm[0] + at), bq);
+        xl = mma(xl, lds8(Sm[1] + at), bq);
       }
-    }
-    if (!side) {
-      f32x4 r;
-#pragma unroll
-      for (int jj = 0; jj < 4; ++jj) r[jj] = Vs[i0 + jj][li] - gam[i0 + jj] * xs[jj];
-      put4(Rt[0], Rt[1], swz(li, i0, kLDC), r);
-    }
-    __syncthreads();
-
-    if (!side) {  // Delta = Tb R for positions i0 + jj
-      f32x4 dl = zero4();
-      // Both k steps for every wave: Tb's entries above the diagonal are zeros, and the waves that need both set
-      // the pace, so skipping would only add branches.
+      const f32x4 xs = xh + xl;
+      const float gam = Gs[b][ip];
+      __syncthreads();
+      // While the chain computes Delta: the second load group, and the first one to the other LDS buffers (their
+      // last readers were the previous chunk's).
+      load_b(nxt, st, cn);
+      stage_a(st, b ^ 1);
+      __syncthreads();
+      // Y^T = (S Q^T) diag(exp G) + Delta^T P^T at state rows 4g + jj, position ip.
+      f32x4 yv = gam * xs;
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
-        const int at = swz(li, 32 * s + 8 * g, kLDC);
-        dl = mma3(dl, Split8{f.f[2 * s], f.f[2 * s + 1]}, Split8{lds8(Rt[0] + at), lds8(Rt[1] + at)});
+        const Split8 A{lds_tr8s(Dm[0] + 32 * s * kLP, kLP, lane), lds_tr8s(Dm[1] + 32 * s * kLP, kLP, lane)};
+        yv = mma3(yv, A, Split8{f.p[2 * s], f.p[2 * s + 1]});
       }
-      f32x4 dd;
-#pragma unroll
-      for (int jj = 0; jj < 4; ++jj) dd[jj] = dec[i0 + jj] * dl[jj];
-      put4(Dt[0], Dt[1], swz(li, i0, kLDC), dl);
-      put4(DDt[0], DDt[1], swz(li, i0, kLDC), dd);
+      const int64_t tok = sq.tok0 + int64_t(c) * kC;
+      const uint32_t L = uint32_t(min(kC, sq.len - c * kC));
+      // Positions past the chunk's end fall past the resource and are dropped.
+      const auto yr = buffer_rsrc(y + tok * sv + hv * a.Dv + row0, L * sv * uint32_t(sizeof(OutT)));
+      BufIO<OutT>::st4(yr, uint32_t(ip * sv + 4 * g), yv);
+      stage_b(st, b ^ 1);
+    };
+    // Chunk 0's inputs, then the chunks in pairs: chunk c computes from one register set while chunk c + 1 loads
+    // into the other.
+    Own oa, ob;
+    Stage st;
+    if (nch > 0) {
+      load_a(st, 0);
+      load_b(oa, st, 0);
+      stage_a(st, 0);
+      stage_b(st, 0);
     }
-    __syncthreads();
-
-    // S <- exp(G_63) S + (D Delta)^T K: this wave's columns 16w + li, rows 4g + jj.
-    {
-      const float glast = gam[kC - 1];
-#pragma unroll
-      for (int jj = 0; jj < 4; ++jj) S[jj] *= glast;
-#pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        const int at = swz(li, 32 * s + 8 * g, kLDC);
-        const Split8 A{lds8(DDt[0] + at), lds8(DDt[1] + at)};
-        S = mma2(S, A, lds_tr8s(Kb + 32 * s * kLDK + 16 * w, kLDK, tid));  // K rows 32s.., this lane's state column
-      }
+    int c = 0;
+    for (; c + 1 < nch; c += 2) {
+      step(c, oa, ob, st);
+      step(c + 1, ob, oa, st);
     }
-    if (side) {  // Y = diag(exp G) QS + P Delta for positions i0 + jj (P is zero above the diagonal)
-#pragma unroll
-      for (int jj = 0; jj < 4; ++jj) yacc[jj] = gam[i0 + jj] * xs[jj];
-#pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        const int at = swz(li, 32 * s + 8 * g, kLDC);
-        yacc = mma3(yacc, Split8{f.f[2 * s], f.f[2 * s + 1]}, Split8{lds8(Dt[0] + at), lds8(Dt[1] + at)});
-      }
-    }
-  };
-
-  // Two register sets in turn: chunk c computes from one while chunk c + 1 loads into the other.
-  Pre pa, pb;
-  f32x4 yacc = zero4();
-  if (nch > 0) prefetch(pa, 0);
-  for (int c = 0; c < nch; c += 2) {
-    step(c, pa, pb, yacc);
-    if (c + 1 < nch) step(c + 1, pb, pa, yacc);
+    if (c < nch) step(c, oa, ob, st);
+    return;
   }
-  if (side && nch > 0) store_y(nch - 1, yacc);
+
+  // Waves 0-3. State: tile t holds S[li][32 wp + 16 t + 4 g + jj]. (s0 and s_out need only 4-byte alignment: one
+  // element at a time.)
+  f32x4 S[2] = {zero4(), zero4()};
+  if (a.s0) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) S[t][jj] = a.s0[srow * Dk + 32 * wp + 16 * t + 4 * g + jj];
+  }
+  const uint32_t ck_bytes = a.ckpt ? 16u * Dk * 4 : 0u;  // a forward without checkpoints drops the stores
+  for (int c = 0; c < nch; ++c) {
+    const int64_t slot = sq.slot0 + c;
+    const int b = c & 1;
+    {  // S to LDS, split, and to the checkpoint (the last readers of Sm are two barriers back)
+      const float* ckb = a.ckpt ? a.ckpt + ((slot * a.Hv + hv) * a.Dv + row0) * Dk : a.s0;
+      const auto ck = buffer_rsrc(ckb, ck_bytes);
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const int col = 32 * wp + 16 * t + 4 * g;
+        put4(Sm[0], Sm[1], swz(li, col, kLS), S[t]);
+        BufIO<float>::st4(ck, uint32_t(li * Dk + col), S[t]);
+      }
+    }
+    __syncthreads();
+
+    // S K^T (k rows from LDS): state rows 4g + jj, position ip; then R[ip][4g + jj].
+    const float gam = Gs[b][ip];
+    const uint2 v = *reinterpret_cast<const uint2*>(Vs[b] + 16 * ip + 4 * g);
+    f32x4 xh = zero4(), xl = zero4();  // the hi and lo halves of S in two independent chains
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const int at = swz(li, 32 * s + 8 * g, kLS);
+      const bf16x8 bk = lds8(Kb[b] + swz(ip, 32 * s + 8 * g, kLK));
+      xh = mma(xh, lds8(Sm[0] + at), bk);
+      xl = mma(xl, lds8(Sm[1] + at), bk);
+    }
+    {
+      const f32x4 xs = xh + xl;
+      const f32x4 r = {bf16_lo(v.x) - gam * xs[0], bf16_hi(v.x) - gam * xs[1], bf16_lo(v.y) - gam * xs[2],
+                       bf16_hi(v.y) - gam * xs[3]};
+      put4(Rm[0], Rm[1], swz(ip, 4 * g, kLP), r);
+    }
+    __syncthreads();
+
+    {  // Delta^T = R^T Tb^T: A = R^T through the transposing read, B = Tb rows ip from the packed copy
+      f32x4 d2[2];  // the two k steps in independent chains
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        const int c8 = 32 * s + 8 * g;
+        const bool in = (c8 >> 4) <= wp;  // blocks above the diagonal are zeros
+        const int at = in ? tri_off(ip, c8) : 0;
+        const bf16x8 z = {};
+        const bf16x8 th = lds8(Tbp[b] + at), tl = lds8(Tbp[b] + kTri + at);
+        const Split8 A{lds_tr8s(Rm[0] + 32 * s * kLP, kLP, lane), lds_tr8s(Rm[1] + 32 * s * kLP, kLP, lane)};
+        d2[s] = mma3(zero4(), A, Split8{in ? th : z, in ? tl : z});
+      }
+      const f32x4 dl = d2[0] + d2[1];
+      put4(Dm[0], Dm[1], swz(ip, 4 * g, kLP), dl);
+      put4(DDm[0], DDm[1], swz(ip, 4 * g, kLP), Gs[b][kC + ip] * dl);
+    }
+    __syncthreads();
+
+    // S^T <- exp(G_63) S^T + K^T (D Delta): A = K^T rows 32 wp + 16 t + li and B = D Delta, both through the
+    // transposing read.
+    const float glast = Gs[b][kC - 1];
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const Split8 B{lds_tr8s(DDm[0] + 32 * s * kLP, kLP, lane), lds_tr8s(DDm[1] + 32 * s * kLP, kLP, lane)};
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        if (s == 0) S[t] = glast * S[t];
+        S[t] = mma2(S[t], lds_tr8s(Kb[b] + swz(32 * s, 32 * wp + 16 * t, kLK), kLK, lane), B);
+      }
+    }
+  }
   if (a.s_out) {
 #pragma unroll
-    for (int jj = 0; jj < 4; ++jj)
-      a.s_out[((int64_t(n) * a.Hv + hv) * a.Dv + row0 + 4 * g + jj) * Dk + 16 * w + li] = S[jj];
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) a.s_out[srow * Dk + 32 * wp + 16 * t + 4 * g + jj] = S[t][jj];
   }
 }
 

@@ -62,6 +62,10 @@ __device__ __forceinline__ uint4 buf_ld16(__amdgpu_buffer_rsrc_t r, uint32_t byt
   const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, int(byte_off), 0, 0);
   return uint4{v[0], v[1], v[2], v[3]};
 }
+__device__ __forceinline__ uint2 buf_ld8(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, int(byte_off), 0, 0);
+  return uint2{v[0], v[1]};
+}
 __device__ __forceinline__ uint16_t buf_ld2(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
   return __builtin_amdgcn_raw_buffer_load_b16(r, int(byte_off), 0, 0);
 }
@@ -76,11 +80,26 @@ struct BufIO<float> {
   static __device__ __forceinline__ void st(__amdgpu_buffer_rsrc_t r, uint32_t i, float x) {
     __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x), r, int(i * 4), 0, 0);
   }
+  // Elements i .. i + 3 (i a multiple of 4) in one 16-byte store.
+  template <typename V4>
+  static __device__ __forceinline__ void st4(__amdgpu_buffer_rsrc_t r, uint32_t i, const V4& x) {
+    typedef __attribute__((__vector_size__(4 * sizeof(uint32_t)))) uint32_t u32x4;
+    const u32x4 v = {__float_as_uint(x[0]), __float_as_uint(x[1]), __float_as_uint(x[2]), __float_as_uint(x[3])};
+    __builtin_amdgcn_raw_buffer_store_b128(v, r, int(i * 4), 0, 0);
+  }
 };
 template <>
 struct BufIO<bf16_t> {
   static __device__ __forceinline__ void st(__amdgpu_buffer_rsrc_t r, uint32_t i, float x) {
     __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16(x), r, int(i * 2), 0, 0);
+  }
+  // Elements i .. i + 3 (i a multiple of 4) in one 8-byte store.
+  template <typename V4>
+  static __device__ __forceinline__ void st4(__amdgpu_buffer_rsrc_t r, uint32_t i, const V4& x) {
+    typedef __attribute__((__vector_size__(2 * sizeof(uint32_t)))) uint32_t u32x2;
+    const u32x2 v = {uint32_t(f32_to_bf16(x[0])) | (uint32_t(f32_to_bf16(x[1])) << 16),
+                     uint32_t(f32_to_bf16(x[2])) | (uint32_t(f32_to_bf16(x[3])) << 16)};
+    __builtin_amdgcn_raw_buffer_store_b64(v, r, int(i * 2), 0, 0);
   }
 };
 
