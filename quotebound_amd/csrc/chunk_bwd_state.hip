@@ -1,15 +1,20 @@
 // Chunked design, kernel 3: the backward state pass. One block (8 waves) per (sequence, value head, 16 state rows),
 // over the chunks in reverse. With dS the cotangent of the block's rows of the chunk's end state (ds_out for the
-// last chunk), per chunk:
+// last chunk), per chunk, every product formed transposed so that a lane holds one position and four consecutive
+// state rows (or one state row and four consecutive columns):
 //   store dS (the gradient kernel needs it)
-//   dDelta = P^T dY + D K dS^T,  D = diag(exp(G_63 - G))        waves 0-3, positions 16w..16w+15: the chain
-//   dR = Tb^T dDelta;   dv = dR                                   waves 0-3
-//   X = (diag(exp G) dY)^T Q                                      waves 4-7, beside the chain (no dS in it)
-//   dS <- exp(G_63) dS + X - (diag(exp G) dR)^T K                 every wave: state columns 16w..16w+15
+//   dDelta^T = (dS K^T) D + dY^T P,  D = diag(exp(G_63 - G))      waves 0-3, positions 16w..16w+15: the chain
+//   dR^T = dDelta^T Tb;   dv = dR                                  waves 0-3
+//   X^T = Q^T (diag(exp G) dY)                                     waves 4-7, beside the chain (no dS in it)
+//   dS^T <- exp(G_63) dS^T + X^T - K^T (diag(exp G) dR)            waves 0-3, state columns 32w..32w+31
 // This is the adjoint of the forward state pass; together with the gradient kernel it reproduces the reference's
 // backward (src/delta_grad.cpp:14-18). dS0 is what remains after the first chunk. Tb and P come ready from the prep
-// kernel; MFMA with split float32 operands as in the forward. Waves 4-7 also load and stage every chunk input, so
-// the chain waves issue no loads.
+// kernel, packed; the products that contract over their rows read them through the transposing LDS read (tri_tr8).
+// MFMA with split float32 operands as in the forward. Three barriers per chunk. Waves 4-7 load every input of the
+// next chunk (in the reverse sweep) in two groups, in windows where they would otherwise wait for the chain, and
+// stage them in LDS; waves 0-3 touch global memory only to store dS and dv. The two wave groups run loops of their
+// own, with the same barriers, so that each loop holds only its own group's memory operations and the compiler's
+// waits stay exact.
 #include <type_traits>
 
 #include "chunk_common.h"
@@ -20,238 +25,252 @@ namespace {
 
 constexpr int kThreads = 512;
 // Row pitches (elements) of the swz-placed LDS matrices: 16 x an odd number.
-constexpr int kLDK = 144;  // k, q rows [64][128]
-constexpr int kLT = 80;    // [.][64]: Tb, P, dDelta^T, (diag(exp G) dR)^T
-constexpr int kLR = 48;    // [.][16]: dS^T, dY, diag(exp G) dY (state rows as columns)
-constexpr int kLX = 128 + 4;  // float32 X rows
+constexpr int kLS = 144;  // dS [16][128]
+constexpr int kLK = 144;  // k, q rows [64][128]
+constexpr int kLP = 48;   // [64][16]: dY, diag(exp G) dY, dDelta, -diag(exp G) dR (positions as rows)
+constexpr int kLX = 128 + 4;       // float32 X^T rows [16][..] (state row, then column)
+constexpr int kTriUnits = 3 * 256;  // 16-byte units of a staged packed matrix (hi, lo: 640 used, the rest padding)
 
 template <typename OutT>
 __global__ __launch_bounds__(kThreads) void chunk_bwd_state_kernel(ChunkArgs a) {
   constexpr int Dk = 128;
   constexpr bool kExactDy = std::is_same<OutT, bf16_t>::value;  // bf16 cotangents enter MFMA exactly
-  // Every matrix is placed by swz and stored once, hi and lo: row reads and transposing reads both come free of
-  // bank conflicts.
-  __shared__ __align__(16) __bf16 Kb[kC * kLDK], Qb[kC * kLDK];
-  __shared__ __align__(16) __bf16 dSt[2][Dk * kLR];  // dS^T [c][r]
-  __shared__ __align__(16) __bf16 dYm[2][kC * kLR];  // dY [i][r]
-  __shared__ __align__(16) __bf16 GdYm[2][kC * kLR]; // diag(exp G) dY [i][r]
-  __shared__ __align__(16) __bf16 dDt[2][16 * kLT];  // dDelta^T [r][j]
-  __shared__ __align__(16) __bf16 GdRt[2][16 * kLT]; // -(diag(exp G) dR)^T [r][i]
-  __shared__ __align__(16) float Xs[16 * kLX];       // X [r][c]
-  __shared__ float gam[kC], dec[kC];
-  // Tb (hi, lo) and P (hi, lo) of the chunk, 64 x 64 each (swz placement; the blocks above the diagonal stay zero):
-  // the A operands Tb^T and P^T come from their columns through the transposing read.
-  __shared__ __align__(16) __bf16 TPL[4][kC * kLT];
+  __shared__ __align__(16) __bf16 dSm[2][16 * kLS];               // dS rows, hi and lo
+  __shared__ __align__(16) __bf16 Kb[2][kC * kLK];                // k rows, by chunk parity
+  __shared__ __align__(16) __bf16 Qb[kC * kLK];                   // q rows
+  __shared__ __align__(16) __bf16 dYm[2][kC * kLP], GdYm[2][kC * kLP];
+  __shared__ __align__(16) __bf16 dDm[2][kC * kLP], GdRm[2][kC * kLP];
+  __shared__ __align__(16) __bf16 Tbp[kTriUnits * 8], Pp[kTriUnits * 8];  // packed Tb, P (hi then lo)
+  __shared__ __align__(16) float Xs[16 * kLX];
+  __shared__ float Gs[2][2 * kC];  // exp G, then D, by chunk parity
 
   const int total = a.nblk * a.Hv * a.N;
   const int wid = xcd_remap(blockIdx.x, total);
   const int blk = wid % a.nblk, hv = (wid / a.nblk) % a.Hv, n = wid / (a.nblk * a.Hv);
   const int hk = hv / (a.Hv / a.Hk), row0 = 16 * blk;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 4, li = lane & 15;
+  const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, li = lane & 15;
+  // The wave index, made visibly uniform so that its branches are scalar and buffer resources stay in scalar
+  // registers.
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const bool side = w >= 4;
-  const int wp = w & 3, u = tid & 255;  // position tile (waves 0-3); thread index within the wave group
+  const int wp = w & 3, ip = 16 * wp + li;  // position tile; the lane's position in products over positions
+  const int u = tid & 255;                   // waves 4-7: thread index within the loading group
   const Seq sq = seq_of(a.tab, n);
   const int nch = (sq.len + kC - 1) / kC;
   const OutT* dy = static_cast<const OutT*>(a.dy);
   OutT* dv = static_cast<OutT*>(a.dv);
   const int sk = a.Hk * Dk, sv = a.Hv * a.Dv;
+  const int64_t srow = (int64_t(n) * a.Hv + hv) * a.Dv + row0 + li;  // the lane's state row
 
-  f32x4 dS;  // wave w: rows 4g + jj, columns 16w + li
+  if (side) {
+    // Waves 4-7. One chunk's inputs, loaded a chunk ahead: (a) k and q rows, staged while the chain computes dR;
+    // (b) dy, the packed Tb and P, and exp G, D, staged after the chain's last use of the previous ones. k, q, dy go
+    // through buffer resources that end at the sequence's last row, so rows past it read as zeros without a branch;
+    // units past the packed matrices read as zeros and land in padding.
+    struct GroupA {
+      uint4 k[4], q[4];  // units u + 256 q4: row e / 16, columns 8 (e % 16) ..
+    };
+    struct GroupB {
+      uint4 dy;           // row u / 4, state rows 4 (u % 4) .. + 3: raw bits (4 bf16 in .x, .y, or 4 float32)
+      uint4 tb[3], p[3];  // packed units u + 256 t
+      float gam, dec;     // of position lane (every wave loads all 64)
+    };
+    auto load_a = [&](GroupA& f, int c) {
+      const int64_t tok = sq.tok0 + int64_t(c) * kC;
+      const uint32_t L = uint32_t(min(kC, sq.len - c * kC));
+      const auto kr = buffer_rsrc(a.k + tok * sk + hk * Dk, L * sk * 2);
+      const auto qr = buffer_rsrc(a.q + tok * sk + hk * Dk, L * sk * 2);
 #pragma unroll
-  for (int jj = 0; jj < 4; ++jj)
-    dS[jj] = a.ds_out ? a.ds_out[((int64_t(n) * a.Hv + hv) * a.Dv + row0 + 4 * g + jj) * Dk + 16 * w + li] : 0.f;
-
-  // One chunk's inputs, loaded by waves 4-7 into registers a chunk ahead (in the reverse sweep), in two groups at
-  // two barriers: k and q rows (e = u + 256 q4 covers row e / 16, columns 8 (e % 16)); then the packed blocks of Tb
-  // and P (16-byte units u + 256 t of tb[0..1], p[0..1]), dy row u / 4 at state rows 4 (u % 4) .. + 3, and exp G, D
-  // of position u % 64. k, q, dy are read through buffer resources that end at the sequence's last row, so rows
-  // past it read as zeros without a branch.
-  struct Pre {
-    uint4 k[4], q[4];
-    uint4 tp[5];
-    uint4 dy;  // raw bits (4 bf16 in .x, .y, or 4 float32)
-    float gam, dec;
-  };
-  auto load_kq = [&](Pre& f, int c) {
-    const int64_t tok = sq.tok0 + int64_t(c) * kC;
-    const uint32_t L = uint32_t(min(kC, sq.len - c * kC));
-    const auto kr = buffer_rsrc(a.k + tok * sk + hk * Dk, L * sk * 2);
-    const auto qr = buffer_rsrc(a.q + tok * sk + hk * Dk, L * sk * 2);
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const int e = u + 256 * q4;
+        f.k[q4] = buf_ld16(kr, uint32_t((e >> 4) * sk + (e & 15) * 8) * 2);
+      }
 #pragma unroll
-    for (int q4 = 0; q4 < 4; ++q4) {
-      const int e = u + 256 * q4, t = e >> 4, c8 = (e & 15) * 8;
-      f.k[q4] = buf_ld16(kr, uint32_t(t * sk + c8) * 2);
-      f.q[q4] = buf_ld16(qr, uint32_t(t * sk + c8) * 2);
-    }
-  };
-  auto load_rest = [&](Pre& f, int c) {
-    const int64_t tok = sq.tok0 + int64_t(c) * kC;
-    const uint32_t L = uint32_t(min(kC, sq.len - c * kC));
-    const Tile* tl = a.tiles + ((sq.slot0 + c) * a.Hv + hv);
-    const auto tr = buffer_rsrc(tl->tb[0], 4 * kTri * 2);  // tb[0], tb[1], p[0], p[1] are contiguous
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const int e = u + 256 * q4;
+        f.q[q4] = buf_ld16(qr, uint32_t((e >> 4) * sk + (e & 15) * 8) * 2);
+      }
+    };
+    auto load_b = [&](GroupB& f, int c) {
+      const int64_t tok = sq.tok0 + int64_t(c) * kC;
+      const uint32_t L = uint32_t(min(kC, sq.len - c * kC));
+      const Tile* tl = a.tiles + ((sq.slot0 + c) * a.Hv + hv);
+      const auto yr = buffer_rsrc(dy + tok * sv + hv * a.Dv + row0, L * sv * uint32_t(sizeof(OutT)));
+      const uint32_t yo = uint32_t((u >> 2) * sv + 4 * (u & 3));
+      if constexpr (kExactDy) {
+        const uint2 t2 = buf_ld8(yr, yo * 2);
+        f.dy = uint4{t2.x, t2.y, 0u, 0u};
+      } else {
+        f.dy = buf_ld16(yr, yo * 4);
+      }
+      const auto tr = buffer_rsrc(tl->tb[0], 2 * kTri * 2), pr = buffer_rsrc(tl->p[0], 2 * kTri * 2);
 #pragma unroll
-    for (int t5 = 0; t5 < 5; ++t5) f.tp[t5] = buf_ld16(tr, uint32_t(u + 256 * t5) * 16);
-    const auto yr = buffer_rsrc(dy + tok * sv + hv * a.Dv + row0, L * sv * uint32_t(sizeof(OutT)));
-    const uint32_t yo = uint32_t((u >> 2) * sv + 4 * (u & 3));
-    if constexpr (kExactDy) {
-      const auto t2 = __builtin_amdgcn_raw_buffer_load_b64(yr, int(yo * 2), 0, 0);
-      f.dy = uint4{t2[0], t2[1], 0u, 0u};
-    } else {
-      f.dy = buf_ld16(yr, yo * 4);
-    }
-    f.gam = tl->gam[u & (kC - 1)], f.dec = tl->dec[u & (kC - 1)];
-  };
-
-  // dv of a chunk (waves 0-3) is stored during the chunk processed after it.
-  auto store_dv = [&](int c, const f32x4& dr) {
-    const int64_t tok = sq.tok0 + int64_t(c) * kC;
-    const uint32_t L = uint32_t(min(kC, sq.len - c * kC));
-    // Rows i >= L fall past the resource and are dropped.
-    const auto vr = buffer_rsrc(dv + tok * sv + hv * a.Dv + row0, L * sv * uint32_t(sizeof(OutT)));
+      for (int t = 0; t < 3; ++t) f.tb[t] = buf_ld16(tr, uint32_t(u + 256 * t) * 16);
 #pragma unroll
-    for (int jj = 0; jj < 4; ++jj) BufIO<OutT>::st(vr, uint32_t((16 * wp + 4 * g + jj) * sv + li), dr[jj]);
-  };
-
-  auto step = [&](int c, Pre& f, Pre& nxt, f32x4& dr) {
-    const int64_t slot = sq.slot0 + c;
-    __syncthreads();
-    if (side) {
-      // Stage the chunk. dy's four values of row u / 4 as floats, and the same times exp G of that row (lane u / 4
-      // of this wave holds it: every wave of the group loads exp G of position lane).
+      for (int t = 0; t < 3; ++t) f.p[t] = buf_ld16(pr, uint32_t(u + 256 * t) * 16);
+      const auto gr = buffer_rsrc(tl->gam, 2 * kC * 4);  // gam, then dec
+      f.gam = buf_ld4(gr, uint32_t(lane) * 4), f.dec = buf_ld4(gr, uint32_t(kC + lane) * 4);
+    };
+    auto stage_a = [&](const GroupA& f, int b) {
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const int e = u + 256 * q4, at = swz(e >> 4, (e & 15) * 8, kLK);
+        *reinterpret_cast<uint4*>(Kb[b] + at) = f.k[q4];
+        *reinterpret_cast<uint4*>(Qb + at) = f.q[q4];
+      }
+    };
+    auto stage_b = [&](const GroupB& f, int b) {
+      // dy's four values of row u / 4, as floats, and the same times exp G of that row (lane u / 4 of this wave
+      // holds it).
       const int yt = u >> 2, yr4 = 4 * (u & 3);
       float yv[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const uint32_t b = kExactDy ? (j & 1 ? (&f.dy.x)[j >> 1] & 0xffff0000u : (&f.dy.x)[j >> 1] << 16) : (&f.dy.x)[j];
-        yv[j] = __uint_as_float(b);
+        const uint32_t x = kExactDy ? (j & 1 ? (&f.dy.x)[j >> 1] & 0xffff0000u : (&f.dy.x)[j >> 1] << 16) : (&f.dy.x)[j];
+        yv[j] = __uint_as_float(x);
       }
       const float gy = __shfl(f.gam, yt);
+      put4(dYm[0], dYm[1], swz(yt, yr4, kLP), yv[0], yv[1], yv[2], yv[3]);
+      put4(GdYm[0], GdYm[1], swz(yt, yr4, kLP), gy * yv[0], gy * yv[1], gy * yv[2], gy * yv[3]);
 #pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4) {
-        const int e = u + 256 * q4, t = e >> 4, c8 = (e & 15) * 8;
-        *reinterpret_cast<uint4*>(&Kb[swz(t, c8, kLDK)]) = f.k[q4];
-        *reinterpret_cast<uint4*>(&Qb[swz(t, c8, kLDK)]) = f.q[q4];
+      for (int t = 0; t < 3; ++t) {
+        *reinterpret_cast<uint4*>(Tbp + 8 * (u + 256 * t)) = f.tb[t];
+        *reinterpret_cast<uint4*>(Pp + 8 * (u + 256 * t)) = f.p[t];
       }
-      put4(dYm[0], dYm[1], swz(yt, yr4, kLR), yv[0], yv[1], yv[2], yv[3]);
-      put4(GdYm[0], GdYm[1], swz(yt, yr4, kLR), gy * yv[0], gy * yv[1], gy * yv[2], gy * yv[3]);
-      if (u < kC) gam[u] = f.gam, dec[u] = f.dec;
-      // The packed blocks to their places: unit e of a matrix half is row (e % 32) / 2, columns 8 (e % 2) .. of
-      // block e / 32 = (I, J) in the order of tri_off.
+      if (u < kC) Gs[b][u] = f.gam, Gs[b][kC + u] = f.dec;
+    };
+    // Per chunk c: X^T for it (its q and diag(exp G) dY were staged during chunk c + 1); the inputs of chunk c - 1,
+    // loaded during chunk c + 1, to LDS; the loads of chunk c - 2 (clamped at 0: the last chunks load chunk 0 again
+    // rather than branch). Two register sets in turn.
+    struct Group {
+      GroupA a;
+      GroupB b;
+    };
+    auto step = [&](int c, Group& cur, Group& nxt) {
+      const int cs = max(c - 1, 0), cn = max(c - 2, 0);
+      __syncthreads();
+      load_a(nxt.a, cn);
+      // X^T = Q^T (diag(exp G) dY) for state columns 32 wp + 16 t + 4g + jj, state row li: A = Q^T through the
+      // transposing read of the q rows, B = diag(exp G) dY through the transposing read.
 #pragma unroll
-      for (int t5 = 0; t5 < 5; ++t5) {
-        const int x = u + 256 * t5, m = x / 320, e = x - 320 * m, b = e >> 5;
-        const int I = (b >= 1) + (b >= 3) + (b >= 6), J = b - I * (I + 1) / 2;
-        *reinterpret_cast<uint4*>(&TPL[m][swz(16 * I + ((e & 31) >> 1), 16 * J + 8 * (e & 1), kLT)]) = f.tp[t5];
-      }
-    } else if (c + 1 < nch) {
-      store_dv(c + 1, dr);
-    }
-    {  // dS to the workspace and, as dS^T (four consecutive state rows per lane), to LDS.
-      const auto out = buffer_rsrc(a.dsend + ((slot * a.Hv + hv) * a.Dv + row0) * Dk, 16 * Dk * 4);
-      const int col = 16 * w + li;
-#pragma unroll
-      for (int jj = 0; jj < 4; ++jj) BufIO<float>::st(out, uint32_t((4 * g + jj) * Dk + col), dS[jj]);
-      put4(dSt[0], dSt[1], swz(col, 4 * g, kLR), dS);
-    }
-    __syncthreads();
-
-    if (!side) {
-      // K dS^T for positions j = 16wp..: lane -> column r = li, rows j = 16wp + 4g + jj. B = dS rows r, k = c,
-      // through the transposing read of dS^T.
-      f32x4 kds = zero4();
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const bf16x8 ak = lds8(&Kb[swz(16 * wp + li, 32 * s + 8 * g, kLDK)]);
-        kds = mma(mma(kds, ak, lds_tr8s(dSt[0] + 32 * s * kLR, kLR, tid)), ak, lds_tr8s(dSt[1] + 32 * s * kLR, kLR, tid));
-      }
-      // dDelta rows j = 16wp.. = D KdS + P^T dY (A = P^T rows j, k = i; B = dY rows i through the transposing
-      // read). Both k steps for every wave: the ones above the diagonal add zeros, and the waves that need both
-      // set the pace, so skipping them would only add branches.
-      f32x4 dd;
-#pragma unroll
-      for (int jj = 0; jj < 4; ++jj) dd[jj] = dec[16 * wp + 4 * g + jj] * kds[jj];
-#pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        // P^T rows j = 16wp + li, k = i: column j of P, rows 32s..
-        const Split8 A{lds_tr8s(&TPL[2][32 * s * kLT + 16 * wp], kLT, tid), lds_tr8s(&TPL[3][32 * s * kLT + 16 * wp], kLT, tid)};
-        if constexpr (kExactDy) {
-          dd = mma2(dd, A, lds_tr8s(dYm[0] + 32 * s * kLR, kLR, tid));
-        } else {
-          dd = mma3(dd, A, Split8{lds_tr8s(dYm[0] + 32 * s * kLR, kLR, tid), lds_tr8s(dYm[1] + 32 * s * kLR, kLR, tid)});
-        }
-      }
-      put4(dDt[0], dDt[1], swz(li, 16 * wp + 4 * g, kLT), dd);
-    } else {
-      if (c > 0) load_kq(nxt, c - 1);
-      // X = (diag(exp G) dY)^T Q for state columns 32 wp + 16 nt + li: A rows r = li, k = i (transposing read of
-      // diag(exp G) dY), B = q rows i.
-#pragma unroll
-      for (int nt = 0; nt < 2; ++nt) {
-        const int c0 = 32 * wp + 16 * nt;
-        f32x4 x = zero4();
+      for (int t = 0; t < 2; ++t) {
+        f32x4 x2[2];
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
-          const Split8 Ay{lds_tr8s(GdYm[0] + 32 * s * kLR, kLR, tid), lds_tr8s(GdYm[1] + 32 * s * kLR, kLR, tid)};
-          x = mma2(x, Ay, lds_tr8s(&Qb[32 * s * kLDK + c0], kLDK, tid));
+          const bf16x8 aq = lds_tr8s(Qb + swz(32 * s, 32 * wp + 16 * t, kLK), kLK, lane);
+          x2[s] = mma2(zero4(), aq, Split8{lds_tr8s(GdYm[0] + 32 * s * kLP, kLP, lane),
+                                           lds_tr8s(GdYm[1] + 32 * s * kLP, kLP, lane)});
         }
+        *reinterpret_cast<f32x4*>(Xs + li * kLX + 32 * wp + 16 * t + 4 * g) = x2[0] + x2[1];
+      }
+      __syncthreads();
+      load_b(nxt.b, cn);
+      stage_a(cur.a, cs & 1);  // q's last readers (the X^T above) and k's (chunk c + 1) are a barrier back
+      __syncthreads();
+      stage_b(cur.b, cs & 1);  // the chain's last readers of dY, Tb, P were before this barrier
+    };
+    Group ga, gb;
+    if (nch > 0) {
+      load_a(ga.a, nch - 1);
+      load_b(ga.b, nch - 1);
+      stage_a(ga.a, (nch - 1) & 1);
+      stage_b(ga.b, (nch - 1) & 1);
+      load_a(ga.a, max(nch - 2, 0));
+      load_b(ga.b, max(nch - 2, 0));
+    }
+    int c = nch - 1;
+    for (; c >= 1; c -= 2) {
+      step(c, ga, gb);
+      step(c - 1, gb, ga);
+    }
+    if (c == 0) step(0, ga, gb);
+    return;
+  }
+
+  // Waves 0-3: the recurrence. dS tile t holds dS[li][32 wp + 16 t + 4 g + jj]. (ds_out and ds0 need only 4-byte
+  // alignment: one element at a time.)
+  f32x4 dS[2] = {zero4(), zero4()};
+  if (a.ds_out) {
 #pragma unroll
-        for (int jj = 0; jj < 4; ++jj) Xs[(4 * g + jj) * kLX + c0 + li] = x[jj];
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) dS[t][jj] = a.ds_out[srow * Dk + 32 * wp + 16 * t + 4 * g + jj];
+  }
+  for (int c = nch - 1; c >= 0; --c) {
+    const int64_t slot = sq.slot0 + c, tok = sq.tok0 + int64_t(c) * kC;
+    const uint32_t L = uint32_t(min(kC, sq.len - c * kC));
+    const int b = c & 1;
+    {  // dS to the workspace and, split, to LDS (its last readers are two barriers back)
+      const auto out = buffer_rsrc(a.dsend + ((slot * a.Hv + hv) * a.Dv + row0) * Dk, 16 * Dk * 4);
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const int col = 32 * wp + 16 * t + 4 * g;
+        put4(dSm[0], dSm[1], swz(li, col, kLS), dS[t]);
+        BufIO<float>::st4(out, uint32_t(li * Dk + col), dS[t]);
       }
     }
     __syncthreads();
 
-    if (!side) {
-      // dR = Tb^T dDelta for positions i = 16wp.. (A = Tb^T rows i, k = j); dv = dR.
-      dr = zero4();
+    {  // dDelta^T at state rows 4g + jj, position ip = (dS K^T) D + dY^T P
+      f32x4 xh = zero4(), xl = zero4(), z = zero4();  // three independent chains
 #pragma unroll
-      for (int s = 0; s < 2; ++s) {  // (both k steps for every wave, as above)
-        const int at = swz(li, 32 * s + 8 * g, kLT);
-        dr = mma3(dr,
-                  Split8{lds_tr8s(&TPL[0][32 * s * kLT + 16 * wp], kLT, tid),
-                         lds_tr8s(&TPL[1][32 * s * kLT + 16 * wp], kLT, tid)},  // Tb^T rows i, k = j
-                  Split8{lds8(dDt[0] + at), lds8(dDt[1] + at)});
+      for (int s = 0; s < 4; ++s) {
+        const int at = swz(li, 32 * s + 8 * g, kLS);
+        const bf16x8 bk = lds8(Kb[b] + swz(ip, 32 * s + 8 * g, kLK));
+        xh = mma(xh, lds8(dSm[0] + at), bk);
+        xl = mma(xl, lds8(dSm[1] + at), bk);
       }
-      const int i0 = 16 * wp + 4 * g;
-      put4(GdRt[0], GdRt[1], swz(li, i0, kLT), -gam[i0] * dr[0], -gam[i0 + 1] * dr[1], -gam[i0 + 2] * dr[2],
-           -gam[i0 + 3] * dr[3]);
-    } else if (c > 0) {
-      load_rest(nxt, c - 1);
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {  // dY^T P: A = dY^T through the transposing read, B = P's column ip
+        const Split8 B{tri_tr8(Pp, 32 * s, wp, lane), tri_tr8(Pp + kTri, 32 * s, wp, lane)};
+        if constexpr (kExactDy) {
+          z = mma2(z, lds_tr8s(dYm[0] + 32 * s * kLP, kLP, lane), B);
+        } else {
+          z = mma3(z, Split8{lds_tr8s(dYm[0] + 32 * s * kLP, kLP, lane), lds_tr8s(dYm[1] + 32 * s * kLP, kLP, lane)},
+                   B);
+        }
+      }
+      const f32x4 dd = Gs[b][kC + ip] * (xh + xl) + z;
+      put4(dDm[0], dDm[1], swz(ip, 4 * g, kLP), dd);
     }
     __syncthreads();
 
-    // dS <- exp(G_63) dS + X - (diag(exp G) dR)^T K for this wave's columns: A rows r = li, k = i.
-    {
-      const float glast = gam[kC - 1];
-      const int col = 16 * w + li;
-#pragma unroll
-      for (int jj = 0; jj < 4; ++jj) dS[jj] = glast * dS[jj] + Xs[(4 * g + jj) * kLX + col];
+    {  // dR^T = dDelta^T Tb: A = dDelta^T through the transposing read, B = Tb's column ip; dv = dR
+      f32x4 d2[2];
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
-        const int at = swz(li, 32 * s + 8 * g, kLT);
-        const bf16x8 bk = lds_tr8s(&Kb[32 * s * kLDK + 16 * w], kLDK, tid);  // k rows 32s.., this lane's column
-        dS = mma2(dS, Split8{lds8(GdRt[0] + at), lds8(GdRt[1] + at)}, bk);
+        const Split8 A{lds_tr8s(dDm[0] + 32 * s * kLP, kLP, lane), lds_tr8s(dDm[1] + 32 * s * kLP, kLP, lane)};
+        d2[s] = mma3(zero4(), A, Split8{tri_tr8(Tbp, 32 * s, wp, lane), tri_tr8(Tbp + kTri, 32 * s, wp, lane)});
       }
+      const f32x4 dr = d2[0] + d2[1];
+      // Positions past the chunk's end fall past the resource and are dropped.
+      const auto vr = buffer_rsrc(dv + tok * sv + hv * a.Dv + row0, L * sv * uint32_t(sizeof(OutT)));
+      BufIO<OutT>::st4(vr, uint32_t(ip * sv + 4 * g), dr);
+      put4(GdRm[0], GdRm[1], swz(ip, 4 * g, kLP), -Gs[b][ip] * dr);
     }
-  };
+    __syncthreads();
 
-  // The blocks above the diagonal of Tb and P are zero and never written by the staging.
-  for (int x = tid; x < 4 * kC * kC / 8; x += kThreads) {
-    const int m = x >> 9, r = (x >> 3) & 63, c = (x & 7) * 8;
-    if ((c >> 4) > (r >> 4)) *reinterpret_cast<uint4*>(&TPL[m][swz(r, c, kLT)]) = uint4{0u, 0u, 0u, 0u};
+    // dS^T <- exp(G_63) dS^T + X^T + K^T (-diag(exp G) dR): A = K^T rows 32 wp + 16 t + li through the transposing
+    // read, B = -diag(exp G) dR through the transposing read.
+    const float glast = Gs[b][kC - 1];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const f32x4 x = *reinterpret_cast<const f32x4*>(Xs + li * kLX + 32 * wp + 16 * t + 4 * g);
+      dS[t] = glast * dS[t] + x;
+    }
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const Split8 B{lds_tr8s(GdRm[0] + 32 * s * kLP, kLP, lane), lds_tr8s(GdRm[1] + 32 * s * kLP, kLP, lane)};
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+        dS[t] = mma2(dS[t], lds_tr8s(Kb[b] + swz(32 * s, 32 * wp + 16 * t, kLK), kLK, lane), B);
+    }
   }
-  // Two register sets in turn: chunk c computes from one while chunk c - 1 loads into the other.
-  Pre pa, pb;
-  f32x4 dr = zero4();
-  if (side && nch > 0) load_kq(pa, nch - 1), load_rest(pa, nch - 1);
-  for (int c = nch - 1; c >= 0; c -= 2) {
-    step(c, pa, pb, dr);
-    if (c > 0) step(c - 1, pb, pa, dr);
-  }
-  if (!side && nch > 0) store_dv(0, dr);
   if (a.ds0) {
 #pragma unroll
-    for (int jj = 0; jj < 4; ++jj)
-      a.ds0[((int64_t(n) * a.Hv + hv) * a.Dv + row0 + 4 * g + jj) * Dk + 16 * w + li] = dS[jj];
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) a.ds0[srow * Dk + 32 * wp + 16 * t + 4 * g + jj] = dS[t][jj];
   }
 }
 

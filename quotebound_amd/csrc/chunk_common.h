@@ -48,6 +48,25 @@ __device__ __forceinline__ bf16x8 tri_ld8(__amdgpu_buffer_rsrc_t r, int h0, int 
   return __builtin_bit_cast(bf16x8, buf_ld16(r, off));
 }
 
+// The MFMA operand whose k index runs down the rows of a packed lower-triangular matrix M held in LDS (tri_off
+// layout, M at element 0): lane (g = lane / 16, n = lane % 16) gets M[r0 + 8g + jj][16 J + n], jj = 0..7, for a
+// multiple r0 of 32. Each lane supplies its own addresses to gfx950's transposing LDS read (four consecutive
+// columns of one row are contiguous in a block); the rows 8g .. 8g + 7 lie in one block, and a block above the
+// diagonal reads zeros.
+__device__ __forceinline__ bf16x8 tri_tr8(const __bf16* M, int r0, int J, int lane) {
+  typedef short s16x4 __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+  typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4;
+  const int s = lane & 15, g = (lane >> 4) & 3, ra = r0 + 8 * g + (s >> 2), c = 16 * J + 4 * (s & 3);
+  const bool in = (ra >> 4) >= J;
+  const s16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(M + (in ? tri_off(ra, c) : 0)));
+  const s16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(M + (in ? tri_off(ra + 4, c) : 0)));
+  const bf16x4 x = __builtin_bit_cast(bf16x4, a), y = __builtin_bit_cast(bf16x4, b);
+  const bf16x8 v = __builtin_shufflevector(x, y, 0, 1, 2, 3, 4, 5, 6, 7);
+  const bf16x8 z = {};
+  return in ? v : z;
+}
+
 struct ChunkLayout {
   int64_t NC;
   int Hv, Dv, Dk;
