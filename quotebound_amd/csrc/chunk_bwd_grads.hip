@@ -177,7 +177,11 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
       load_dy_v(nb, 0, lt0);
     }
 
-    for (int r0 = 0; r0 < a.Dv; r0 += 32) {
+    // One 32-row block of the state. The last block of the value head (more = false) loads the end phase's inputs
+    // instead of the next block's: it is a separate copy of the code, so that every copy issues the same loads in
+    // the same order whatever the path, and the compiler's count of outstanding loads stays exact.
+    auto block = [&](const int r0, auto more_tag) {
+      constexpr bool more = decltype(more_tag)::value;
       // Lane indices re-derived from an opaque copy, so their many address expressions are recomputed here instead
       // of being hoisted out of both loops and held (spilled) for the whole kernel.
       int lt = tid;
@@ -211,8 +215,7 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj) vv[jj] = bf16_to_f32(nb.vraw[jj]);
       __syncthreads();
-      const bool more = r0 + 32 < a.Dv;
-      if (more)
+      if constexpr (more)
         load_rows(nb.xs, a.ckpt, r0 + 32, lt);  // the next block's reads, first group
       else
         load_end(nb, lt);
@@ -240,7 +243,7 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
       }
       put4(sb + oRh, sb + oRl, swz(r, i0, kLP), rv[0], rv[1], rv[2], rv[3]);
       __syncthreads();
-      if (more) load_rows(nb.ys, a.dsend, r0 + 32, lt);
+      if constexpr (more) load_rows(nb.ys, a.dsend, r0 + 32, lt);
 
       // Phase 2: Delta = Tb R and dDelta = P^T dY + D KdS (rows: the wave's positions; lane: row r).
       f32x4 dl = zero4(), dd;
@@ -276,7 +279,7 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
         put4(sb + odDh, sb + odDl, swz(r, i0, kLP), dd[0], dd[1], dd[2], dd[3]);
       }
       __syncthreads();
-      if (more) load_dy_v(nb, r0 + 32, lt);
+      if constexpr (more) load_dy_v(nb, r0 + 32, lt);
 
       // Phase 3: dR = Tb^T dDelta; dP^T += Delta dY^T and dTb^T += R dDelta^T over this half's key tiles.
       {
@@ -336,7 +339,10 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
           dK[t] = mma3(dK[t], ADD, B1);
         }
       }
-    }
+    };
+    int r0 = 0;
+    for (; r0 + 32 < a.Dv; r0 += 32) block(r0, std::true_type{});
+    block(r0, std::false_type{});
 
     // End of the state rows for this value head: per-position partials, then the 64 x 64 part.
     int lt = tid;
