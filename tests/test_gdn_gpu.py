@@ -195,6 +195,38 @@ def test_layer_shapes_bf16(torch_dev, oracle, design, wname):
 
 
 @pytest.mark.parametrize("design", DESIGNS, ids=DESIGN_IDS.get)
+def test_decode_steps_carry_the_state(torch_dev, oracle, design):
+    """The inference path: a prefill of 66 tokens, then one-token calls that carry the state (the reference's decode
+    and exact-draft rows, src/deltanet.cpp:101-120), give the y and final state of one call over the whole sequence,
+    and both match the oracle."""
+    torch = torch_dev
+    from quotebound_amd import gdn
+    from quotebound_amd.synthetic import Workload, make_inputs, to_device
+
+    w = Workload("decode", 1, 72, 4, 8, 128, 128, seed=23, s0_std=0.02)
+    inp = make_inputs(w)
+    y_ref, s_ref, _ = oracle.fwd(inp.f32["q"], inp.f32["k"], inp.f32["v"], inp.f32["g"], inp.f32["beta"],
+                                 inp.f32["s0"], dtype=np.float32)
+    d = to_device(inp)
+    fwd = lambda sl, state: gdn.forward(d["q"][:, sl], d["k"][:, sl], d["v"][:, sl], d["g"][:, sl], d["beta"][:, sl],
+                                        state, log_decay=True, design=design, save_ckpt=False, out_f32=True)[:2]
+    y_one, s_one = fwd(slice(0, w.T), d["s0"])
+    ys, state = [], d["s0"]
+    y_pre, state = fwd(slice(0, 66), state)
+    ys.append(y_pre)
+    for t in range(66, w.T):
+        y_t, state = fwd(slice(t, t + 1), state)
+        ys.append(y_t)
+    torch.cuda.synchronize()
+    y_steps = torch.cat(ys, dim=1)
+    got_one = {"y": y_one.cpu().numpy(), "s_out": s_one.cpu().numpy()}
+    got_steps = {"y": y_steps.cpu().numpy(), "s_out": state.cpu().numpy()}
+    assert_close(got_steps, got_one, F32_TOL, names=("y", "s_out"), label=f"decode vs one call, design {design}")
+    assert_close(got_steps, {"y": y_ref, "s_out": s_ref}, BF16_TOL, names=("y", "s_out"),
+                 label=f"decode vs oracle, design {design}")
+
+
+@pytest.mark.parametrize("design", DESIGNS, ids=DESIGN_IDS.get)
 def test_deterministic(torch_dev, design):
     """Same inputs, same bits: every sum runs in a fixed order (the reference's resume bit-identity relies on it,
     reference src/delta_grad.cpp:19-22)."""
