@@ -179,6 +179,39 @@ def run_design(torch, hip, lib, w, dev, design, steps, warmup):
             "nc": lib.num_chunks(desc_f)}, None
 
 
+def run_decode(torch, lib, w, design, calls=200, warmup=20):
+    """The inference step: one-token forward calls at the workload's head shape, each carrying the state to the
+    next (the reference's decode, src/deltanet.cpp:101-120), timed back to back on the host clock (launch included).
+    Returns microseconds per call, or None when the design rejects the shape."""
+    from quotebound_amd.synthetic import Workload, make_inputs, to_device
+
+    dw = Workload("decode", w.B, 1, w.Hk, w.Hv, w.Dk, w.Dv, seed=5, s0_std=0.02)
+    dev = to_device(make_inputs(dw), "cuda")
+    dt = lib.BF16 if w.dtype == "bf16" else lib.F32
+    desc, keep = lib.make_desc(w.B, 1, w.Hk, w.Hv, w.Dk, w.Dv, dtype=dt, design=design)
+    if lib.validate(desc):
+        return None
+    y = torch.empty_like(dev["v"])
+    states = [dev["s0"].clone(), torch.empty_like(dev["s0"])]
+    ws = torch.empty(max(lib.workspace_bytes(desc), 1), dtype=torch.uint8, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+    p = lambda t: None if t is None else t.data_ptr()  # noqa: E731
+
+    def call(i):
+        lib.fwd(desc, p(dev["q"]), p(dev["k"]), p(dev["v"]), p(dev["g"]), p(dev["beta"]), p(states[i & 1]), p(y),
+                p(states[(i + 1) & 1]), None, p(ws), stream)
+
+    for i in range(warmup):
+        call(i)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(calls):
+        call(i)
+    torch.cuda.synchronize()
+    del keep
+    return (time.perf_counter() - t0) * 1e6 / calls
+
+
 def traffic_of(w, kernel):
     """HBM bytes per launch of kernel from profiles/traffic.json (rocprofv3 FETCH_SIZE and WRITE_SIZE in KiB per
     dispatch, scaled by the copy calibration recorded with them), or None."""
@@ -297,6 +330,11 @@ def main():
         "designs": {k: ({kk: vv for kk, vv in v.items() if kk != "nc"} if "ms_per_step" in v else v)
                     for k, v in results.items()},
     }
+    out["decode"] = {"unit": "us per one-token call (state carried, host clock, launch included)",
+                     "config": f"B={w.B} Hk={w.Hk} Hv={w.Hv} Dk={w.Dk} Dv={w.Dv}, {w.dtype} I/O, fp32 state"}
+    for d in designs:
+        name = {lib.RECURRENT: "recurrent", lib.CHUNKED: "chunked"}[d]
+        out["decode"][name] = run_decode(torch, lib, w, d)
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(w, inp)
     print(json.dumps(out))
