@@ -101,6 +101,9 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
   f32x4 dQ[4], dK[4];  // columns 16 (4 hw + t) + li, rows 16 pw + 4 g + jj
 #pragma unroll
   for (int t = 0; t < 4; ++t) dQ[t] = zero4(), dK[t] = zero4();
+  // (K K^T)[p][m], rows p = 16 pw + 4g + jj, columns m = 16 (2 hw + mi) + li; zero above tile pw. The same for every
+  // value head of the group: formed in the first one's end phase.
+  f32x4 kk[2];
 
   for (int e = 0; e < grp; ++e) {
     const int hv = hk * grp + e;
@@ -411,9 +414,8 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
     }
     __syncthreads();
 
-    // E2: the column sums of dTb * T (dbeta's T part); dQ += diag(exp G) dQ_inter and its dG term; K K^T (kept in
-    // registers); dQ += (P * M) K; dK += (P * M)^T Q; Z = dTb diag(beta) T^T, stored as Z^T.
-    f32x4 kk[2];  // (K K^T)[p][m], rows p = 16 pw + 4g + jj, columns m = 16 (2 hw + mi) + li; zero above tile pw
+    // E2: the column sums of dTb * T (dbeta's T part); dQ += diag(exp G) dQ_inter and its dG term; K K^T (the first
+    // value head only, kept in registers); dQ += (P * M) K; dK += (P * M)^T Q; Z = dTb diag(beta) T^T, stored as Z^T.
     {
 #pragma unroll
       for (int mi = 0; mi < 2; ++mi) {
@@ -445,14 +447,16 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
         const float v = sum16(tq[jj]);
         if (li == 0) tpos[hw][i0 + jj] = v;
       }
+      if (e == 0) {
 #pragma unroll
-      for (int mi = 0; mi < 2; ++mi) {
-        const int m = 2 * hw + mi;
-        kk[mi] = zero4();
-        if (m <= pw) {
+        for (int mi = 0; mi < 2; ++mi) {
+          const int m = 2 * hw + mi;
+          kk[mi] = zero4();
+          if (m <= pw) {
 #pragma unroll
-          for (int s = 0; s < 4; ++s)
-            kk[mi] = mma(kk[mi], lds8(Kres + swz(ip, 32 * s + 8 * g, kLK)), lds8(Kres + swz(16 * m + li, 32 * s + 8 * g, kLK)));
+            for (int s = 0; s < 4; ++s)
+              kk[mi] = mma(kk[mi], lds8(Kres + swz(ip, 32 * s + 8 * g, kLK)), lds8(Kres + swz(16 * m + li, 32 * s + 8 * g, kLK)));
+          }
         }
       }
 #pragma unroll
