@@ -103,6 +103,43 @@ int qb_gdn_bwd(const qb_gdn_desc* desc, const void* q, const void* k, const void
                const void* beta, const float* ckpt, const void* dy, const float* ds_out, void* dq, void* dk, void* dv,
                float* dg, void* dbeta, float* ds0, void* workspace, void* stream, char* err, int errlen);
 
+/* The layer's pointwise neighbours of the recurrence, each one pass over its rows (reference src/deltanet.cpp). They
+ * read B, T, Hk, Hv, Dk, Dv and dtype from desc (the other fields are not used; Dk and Dv must be 64, 128 or 256)
+ * and take the activations in dtype and the parameters in float32. With bf16 activations each op's output is
+ * rounded to bf16 where the reference's op rounds it; arithmetic inside an op is float32. The backward entry points
+ * are float32 inside with one rounding of each output, and sum the parameter gradients over tokens in a fixed order
+ * (deterministic). */
+
+/* Scratch the neighbours' backward entry points need (the per-block partial sums); 0 on an invalid desc. */
+size_t qb_gdn_neighbours_workspace_bytes(const qb_gdn_desc* desc);
+
+/* Prologue, before qb_gdn_fwd (src/deltanet.cpp:22-33, 94-100): q = s_q rms_norm(q_raw) and k = s_k rms_norm(k_raw)
+ * (no weight, eps 1e-6; s_q = 1/Dk and s_k = Dk^-1/2 in dtype), beta = sigmoid(b), and the log-decay
+ * -exp(a_log) softplus(a + dt_bias), the g of qb_gdn_fwd with g_is_log = 1 (the reference's compute_g takes its
+ * exp). q_raw, k_raw, q, k [B, T, Hk, Dk]; a, b, beta [B, T, Hv] in dtype; a_log, dt_bias [Hv]; log_decay
+ * [B, T, Hv] float32. */
+int qb_gdn_prologue_fwd(const qb_gdn_desc* desc, const void* q_raw, const void* k_raw, const void* a, const void* b,
+                        const float* a_log, const float* dt_bias, void* q, void* k, void* beta, float* log_decay,
+                        void* stream, char* err, int errlen);
+
+/* Its backward: from the cotangents of q, k, beta (dtype) and of the log-decay (float32), those of q_raw, k_raw, a,
+ * b (dtype) and of a_log, dt_bias ([Hv] float32, summed over every token). */
+int qb_gdn_prologue_bwd(const qb_gdn_desc* desc, const void* q_raw, const void* k_raw, const void* a, const void* b,
+                        const float* a_log, const float* dt_bias, const void* dq, const void* dk, const void* dbeta,
+                        const float* dlog_decay, void* dq_raw, void* dk_raw, void* da, void* db, float* da_log,
+                        float* ddt_bias, void* workspace, void* stream, char* err, int errlen);
+
+/* Epilogue, after qb_gdn_fwd (src/deltanet.cpp:35-45, 122, the gated RMSNorm): o = silu(z) rms_norm(y, norm_w, eps).
+ * y, z, o [B, T, Hv, Dv] in dtype; norm_w [Dv] float32. */
+int qb_gdn_epilogue_fwd(const qb_gdn_desc* desc, const void* y, const void* z, const float* norm_w, float eps, void* o,
+                        void* stream, char* err, int errlen);
+
+/* Its backward: from the cotangent of o, those of y and z (dtype) and of norm_w ([Dv] float32, summed over every
+ * row). */
+int qb_gdn_epilogue_bwd(const qb_gdn_desc* desc, const void* y, const void* z, const float* norm_w, float eps,
+                        const void* dout, void* dy, void* dz, float* dnorm_w, void* workspace, void* stream, char* err,
+                        int errlen);
+
 #ifdef __cplusplus
 }
 #endif

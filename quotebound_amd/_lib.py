@@ -65,6 +65,17 @@ def load():
     L.qb_gdn_fwd.restype = ctypes.c_int
     L.qb_gdn_bwd.argtypes = [D] + [P] * 16 + [ctypes.c_char_p, ctypes.c_int]
     L.qb_gdn_bwd.restype = ctypes.c_int
+    L.qb_gdn_neighbours_workspace_bytes.argtypes = [D]
+    L.qb_gdn_neighbours_workspace_bytes.restype = ctypes.c_size_t
+    L.qb_gdn_prologue_fwd.argtypes = [D] + [P] * 11 + [ctypes.c_char_p, ctypes.c_int]
+    L.qb_gdn_prologue_fwd.restype = ctypes.c_int
+    L.qb_gdn_prologue_bwd.argtypes = [D] + [P] * 18 + [ctypes.c_char_p, ctypes.c_int]
+    L.qb_gdn_prologue_bwd.restype = ctypes.c_int
+    F = ctypes.c_float
+    L.qb_gdn_epilogue_fwd.argtypes = [D, P, P, P, F, P, P, ctypes.c_char_p, ctypes.c_int]
+    L.qb_gdn_epilogue_fwd.restype = ctypes.c_int
+    L.qb_gdn_epilogue_bwd.argtypes = [D, P, P, P, F, P, P, P, P, P, P, ctypes.c_char_p, ctypes.c_int]
+    L.qb_gdn_epilogue_bwd.restype = ctypes.c_int
     _lib = L
     return L
 
@@ -135,3 +146,31 @@ def bwd(desc, q, k, v, g, beta, ckpt, dy, ds_out, dq, dk, dv, dg, dbeta, ds0, wo
                            workspace, stream, err, len(err))
     if rc != 0:
         raise RuntimeError(err.value.decode())
+
+
+def neighbours_workspace_bytes(desc) -> int:
+    return int(load().qb_gdn_neighbours_workspace_bytes(ctypes.byref(desc)))
+
+
+def _call(fn, desc, *args) -> None:
+    err = ctypes.create_string_buffer(512)
+    if fn(ctypes.byref(desc), *args, err, len(err)) != 0:
+        raise RuntimeError(err.value.decode())
+
+
+def prologue_fwd(desc, q_raw, k_raw, a, b, a_log, dt_bias, q, k, beta, log_decay, stream) -> None:
+    _call(load().qb_gdn_prologue_fwd, desc, q_raw, k_raw, a, b, a_log, dt_bias, q, k, beta, log_decay, stream)
+
+
+def prologue_bwd(desc, q_raw, k_raw, a, b, a_log, dt_bias, dq, dk, dbeta, dlog_decay, dq_raw, dk_raw, da, db, da_log,
+                 ddt_bias, workspace, stream) -> None:
+    _call(load().qb_gdn_prologue_bwd, desc, q_raw, k_raw, a, b, a_log, dt_bias, dq, dk, dbeta, dlog_decay, dq_raw,
+          dk_raw, da, db, da_log, ddt_bias, workspace, stream)
+
+
+def epilogue_fwd(desc, y, z, norm_w, eps, o, stream) -> None:
+    _call(load().qb_gdn_epilogue_fwd, desc, y, z, norm_w, eps, o, stream)
+
+
+def epilogue_bwd(desc, y, z, norm_w, eps, dout, dy, dz, dnorm_w, workspace, stream) -> None:
+    _call(load().qb_gdn_epilogue_bwd, desc, y, z, norm_w, eps, dout, dy, dz, dnorm_w, workspace, stream)

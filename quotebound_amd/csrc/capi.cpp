@@ -5,6 +5,8 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+#include <cmath>
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
@@ -12,6 +14,7 @@
 #include <string>
 
 #include "gdn_kernels.h"
+#include "neighbours.h"
 
 namespace {
 
@@ -263,6 +266,185 @@ int qb_gdn_bwd(const qb_gdn_desc* desc, const void* q, const void* k, const void
                                                           : qbgdn::chunk_bwd(p, a, workspace, s, tr);
     if (e != hipSuccess) {
       set_err(err, errlen, hip_fail("backward launch", e));
+      return -1;
+    }
+    return 0;
+  });
+}
+
+}  // extern "C"
+
+// ---- the pointwise neighbours ----------------------------------------------------------------------------------
+
+namespace {
+
+float round_bf16_host(float x) {
+  uint32_t u;
+  std::memcpy(&u, &x, 4);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  u &= 0xffff0000u;
+  float r;
+  std::memcpy(&r, &u, 4);
+  return r;
+}
+
+std::string nb_resolve(const qb_gdn_desc* d, qbgdn::NbProblem& p) {
+  if (!d) return "gated delta neighbours: null descriptor";
+  const std::string sh = shape_of(*d);
+  if (d->B < 1 || d->T < 0 || d->Hk < 1 || d->Hv < 1 || d->Dk < 1 || d->Dv < 1)
+    return "gated delta neighbours: sizes must be positive " + sh;
+  if (d->Hv % d->Hk) return "gated delta neighbours: value heads must be a multiple of key heads " + sh;
+  if (d->dtype != QB_DTYPE_F32 && d->dtype != QB_DTYPE_BF16) return "gated delta neighbours: dtype must be f32 or bf16";
+  const int64_t BT = int64_t(d->B) * d->T;
+  if (BT * std::max(d->Hk * int64_t(d->Dk), d->Hv * int64_t(d->Dv)) > (int64_t(1) << 40))
+    return "gated delta neighbours: problem too large " + sh;
+  p = qbgdn::NbProblem{};
+  p.BT = BT, p.Hk = d->Hk, p.Hv = d->Hv, p.Dk = d->Dk, p.Dv = d->Dv;
+  p.bf16 = d->dtype == QB_DTYPE_BF16;
+  // The reference's scalars: float(Dk^-1/2 * Dk^-1/2) and float(Dk^-1/2), in the activation dtype
+  // (src/deltanet.cpp:95-97).
+  const double inv = 1.0 / std::sqrt(double(d->Dk));
+  p.scale_q = float(inv * inv), p.scale_k = float(inv);
+  if (p.bf16) p.scale_q = round_bf16_host(p.scale_q), p.scale_k = round_bf16_host(p.scale_k);
+  if (const char* why = qbgdn::nb_supports(p)) return std::string("gated delta neighbours: ") + why + " " + sh;
+  return {};
+}
+
+struct PtrCheck {
+  const char* name;
+  const void* ptr;
+  bool req;
+  size_t align;
+};
+
+template <size_t N>
+std::string check_all(const PtrCheck (&c)[N]) {
+  for (const auto& x : c) {
+    std::string why = check_ptr(x.name, x.ptr, x.req, x.align);
+    if (!why.empty()) return why;
+  }
+  return {};
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t qb_gdn_neighbours_workspace_bytes(const qb_gdn_desc* desc) {
+  try {
+    qbgdn::NbProblem p;
+    if (!nb_resolve(desc, p).empty()) return 0;
+    return qbgdn::nb_workspace_bytes(p);
+  } catch (...) {
+    return 0;
+  }
+}
+
+int qb_gdn_prologue_fwd(const qb_gdn_desc* desc, const void* q_raw, const void* k_raw, const void* a, const void* b,
+                        const float* a_log, const float* dt_bias, void* q, void* k, void* beta, float* log_decay,
+                        void* stream, char* err, int errlen) {
+  return guarded(err, errlen, [&] {
+    qbgdn::NbProblem p;
+    std::string why = nb_resolve(desc, p);
+    const bool any = why.empty() && p.BT > 0;
+    const size_t el = why.empty() && p.bf16 ? 2 : 4;
+    const PtrCheck c[] = {{"q_raw", q_raw, any, el}, {"k_raw", k_raw, any, el}, {"a", a, any, el},
+                          {"b", b, any, el},         {"a_log", a_log, true, 4},  {"dt_bias", dt_bias, true, 4},
+                          {"q", q, any, el},         {"k", k, any, el},          {"beta", beta, any, el},
+                          {"log_decay", log_decay, any, 4}};
+    if (why.empty()) why = check_all(c);
+    if (!why.empty()) {
+      set_err(err, errlen, why);
+      return -1;
+    }
+    const qbgdn::NbPrologue x{q_raw, k_raw, a, b, a_log, dt_bias, q, k, beta, log_decay};
+    const hipError_t e = qbgdn::nb_prologue_fwd(p, x, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) {
+      set_err(err, errlen, hip_fail("prologue launch", e));
+      return -1;
+    }
+    return 0;
+  });
+}
+
+int qb_gdn_prologue_bwd(const qb_gdn_desc* desc, const void* q_raw, const void* k_raw, const void* a, const void* b,
+                        const float* a_log, const float* dt_bias, const void* dq, const void* dk, const void* dbeta,
+                        const float* dlog_decay, void* dq_raw, void* dk_raw, void* da, void* db, float* da_log,
+                        float* ddt_bias, void* workspace, void* stream, char* err, int errlen) {
+  return guarded(err, errlen, [&] {
+    qbgdn::NbProblem p;
+    std::string why = nb_resolve(desc, p);
+    const bool any = why.empty() && p.BT > 0;
+    const size_t el = why.empty() && p.bf16 ? 2 : 4;
+    const PtrCheck c[] = {{"q_raw", q_raw, any, el},   {"k_raw", k_raw, any, el},     {"a", a, any, el},
+                          {"b", b, any, el},           {"a_log", a_log, true, 4},      {"dt_bias", dt_bias, true, 4},
+                          {"dq", dq, any, el},         {"dk", dk, any, el},            {"dbeta", dbeta, any, el},
+                          {"dlog_decay", dlog_decay, any, 4}, {"dq_raw", dq_raw, any, el}, {"dk_raw", dk_raw, any, el},
+                          {"da", da, any, el},         {"db", db, any, el},            {"da_log", da_log, true, 4},
+                          {"ddt_bias", ddt_bias, true, 4},
+                          {"workspace", workspace, why.empty() && qbgdn::nb_workspace_bytes(p) > 0, 4}};
+    if (why.empty()) why = check_all(c);
+    if (!why.empty()) {
+      set_err(err, errlen, why);
+      return -1;
+    }
+    const qbgdn::NbPrologueGrad x{q_raw, k_raw, a,  b,      a_log,  dt_bias, dq, dk,
+                                  dbeta, dlog_decay, dq_raw, dk_raw, da, db, da_log, ddt_bias};
+    const hipError_t e = qbgdn::nb_prologue_bwd(p, x, workspace, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) {
+      set_err(err, errlen, hip_fail("prologue backward launch", e));
+      return -1;
+    }
+    return 0;
+  });
+}
+
+int qb_gdn_epilogue_fwd(const qb_gdn_desc* desc, const void* y, const void* z, const float* norm_w, float eps, void* o,
+                        void* stream, char* err, int errlen) {
+  return guarded(err, errlen, [&] {
+    qbgdn::NbProblem p;
+    std::string why = nb_resolve(desc, p);
+    if (why.empty() && !(eps > 0.f)) why = "gated delta neighbours: eps must be positive";
+    const bool any = why.empty() && p.BT > 0;
+    const size_t el = why.empty() && p.bf16 ? 2 : 4;
+    const PtrCheck c[] = {{"y", y, any, el}, {"z", z, any, el}, {"norm_w", norm_w, true, 4}, {"o", o, any, el}};
+    if (why.empty()) why = check_all(c);
+    if (!why.empty()) {
+      set_err(err, errlen, why);
+      return -1;
+    }
+    const qbgdn::NbEpilogue x{y, z, norm_w, eps, o};
+    const hipError_t e = qbgdn::nb_epilogue_fwd(p, x, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) {
+      set_err(err, errlen, hip_fail("epilogue launch", e));
+      return -1;
+    }
+    return 0;
+  });
+}
+
+int qb_gdn_epilogue_bwd(const qb_gdn_desc* desc, const void* y, const void* z, const float* norm_w, float eps,
+                        const void* dout, void* dy, void* dz, float* dnorm_w, void* workspace, void* stream, char* err,
+                        int errlen) {
+  return guarded(err, errlen, [&] {
+    qbgdn::NbProblem p;
+    std::string why = nb_resolve(desc, p);
+    if (why.empty() && !(eps > 0.f)) why = "gated delta neighbours: eps must be positive";
+    const bool any = why.empty() && p.BT > 0;
+    const size_t el = why.empty() && p.bf16 ? 2 : 4;
+    const PtrCheck c[] = {{"y", y, any, el},       {"z", z, any, el},   {"norm_w", norm_w, true, 4},
+                          {"dout", dout, any, el}, {"dy", dy, any, el}, {"dz", dz, any, el},
+                          {"dnorm_w", dnorm_w, true, 4},
+                          {"workspace", workspace, why.empty() && qbgdn::nb_workspace_bytes(p) > 0, 4}};
+    if (why.empty()) why = check_all(c);
+    if (!why.empty()) {
+      set_err(err, errlen, why);
+      return -1;
+    }
+    const qbgdn::NbEpilogueGrad x{y, z, norm_w, eps, dout, dy, dz, dnorm_w};
+    const hipError_t e = qbgdn::nb_epilogue_bwd(p, x, workspace, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) {
+      set_err(err, errlen, hip_fail("epilogue backward launch", e));
       return -1;
     }
     return 0;

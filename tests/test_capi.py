@@ -118,3 +118,20 @@ def test_launch_errors_before_any_gpu_work(lib):
         _lib.bwd(d, 16, 16, 16, 16, 16, None, 16, None, 16, 16, 16, 16, 16, None, 16, None)
     with pytest.raises(RuntimeError, match="workspace is null"):
         _lib.bwd(d, 16, 16, 16, 16, 16, 16, 16, None, 16, 16, 16, 16, 16, None, None, None)
+
+
+def test_neighbours_errors_before_any_gpu_work(lib):
+    d, _ = desc(Dk=32, Dv=32)
+    with pytest.raises(RuntimeError, match="Dk of 64, 128 or 256"):
+        _lib.prologue_fwd(d, 16, 16, 16, 16, 16, 16, 16, 16, 16, 16, None)
+    assert _lib.neighbours_workspace_bytes(d) == 0
+    d, _ = desc()
+    assert _lib.neighbours_workspace_bytes(d) > 0
+    with pytest.raises(RuntimeError, match="a_log is null"):
+        _lib.prologue_fwd(d, 16, 16, 16, 16, None, 16, 16, 16, 16, 16, None)
+    with pytest.raises(RuntimeError, match="workspace is null"):
+        _lib.prologue_bwd(d, *([16] * 16), None, None)
+    with pytest.raises(RuntimeError, match="eps must be positive"):
+        _lib.epilogue_fwd(d, 16, 16, 16, 0.0, 16, None)
+    with pytest.raises(RuntimeError, match="y must be 2-byte aligned"):
+        _lib.epilogue_bwd(d, 17, 16, 16, 1e-6, 16, 16, 16, 16, 16, None)
