@@ -212,6 +212,57 @@ def run_decode(torch, lib, w, design, calls=200, warmup=20):
     return (time.perf_counter() - t0) * 1e6 / calls
 
 
+def run_neighbours(torch, lib, w, calls=50, warmup=5):
+    """The layer's pointwise neighbours at the workload's shape (bf16 activations): each C-ABI entry point called
+    back to back on one stream into preallocated outputs (so the host keeps ahead of the GPU), timed with events
+    around the calls. Returns, per entry point, microseconds per call, the algorithmic HBM bytes (each activation
+    read or written once) and their rate against the HBM peak."""
+    if w.dtype != "bf16":
+        return None
+    g = torch.Generator(device="cuda").manual_seed(11)
+    bt = w.B * w.T
+    r = lambda *shape: torch.randn(*shape, device="cuda", generator=g).to(torch.bfloat16)  # noqa: E731
+    qr, kr, dq, dk, q, k, dqr, dkr = (r(w.B, w.T, w.Hk, w.Dk) for _ in range(8))
+    a, b, dbeta, beta, da, db = (r(w.B, w.T, w.Hv) for _ in range(6))
+    dld, ld = (torch.randn(w.B, w.T, w.Hv, device="cuda", generator=g) for _ in range(2))
+    a_log = torch.rand(w.Hv, device="cuda", generator=g) * 2.7
+    dt_bias = torch.randn(w.Hv, device="cuda", generator=g) * 0.5
+    da_log, ddt = torch.empty_like(a_log), torch.empty_like(dt_bias)
+    y, z, dout, o, dy, dz = (r(w.B, w.T, w.Hv, w.Dv) for _ in range(6))
+    nw, dnw = torch.ones(w.Dv, device="cuda"), torch.empty(w.Dv, device="cuda")
+    desc, keep = lib.make_desc(w.B, w.T, w.Hk, w.Hv, w.Dk, w.Dv, dtype=lib.BF16)
+    ws = torch.empty(max(lib.neighbours_workspace_bytes(desc), 1), dtype=torch.uint8, device="cuda")
+    st = torch.cuda.current_stream().cuda_stream
+    P = lambda *ts: [t.data_ptr() for t in ts]  # noqa: E731
+    qk, gv, yz = bt * w.Hk * w.Dk * 2, bt * w.Hv, bt * w.Hv * w.Dv * 2
+    cases = {
+        "prologue_fwd": (lambda: lib.prologue_fwd(desc, *P(qr, kr, a, b, a_log, dt_bias, q, k, beta, ld), st),
+                         4 * qk + 10 * gv),
+        "prologue_bwd": (lambda: lib.prologue_bwd(desc, *P(qr, kr, a, b, a_log, dt_bias, dq, dk, dbeta, dld, dqr, dkr,
+                                                         da, db, da_log, ddt, ws), st), 6 * qk + 14 * gv),
+        "epilogue_fwd": (lambda: lib.epilogue_fwd(desc, y.data_ptr(), z.data_ptr(), nw.data_ptr(), 1e-6,
+                                                  o.data_ptr(), st), 3 * yz),
+        "epilogue_bwd": (lambda: lib.epilogue_bwd(desc, y.data_ptr(), z.data_ptr(), nw.data_ptr(), 1e-6,
+                                                  *P(dout, dy, dz, dnw, ws), st), 5 * yz),
+    }
+    out = {"unit": "us per call (events around back-to-back calls on the launch stream)",
+           "config": f"B={w.B} T={w.T} Hk={w.Hk} Hv={w.Hv} Dk={w.Dk} Dv={w.Dv}, bf16 activations"}
+    for name, (fn, nbytes) in cases.items():
+        for _ in range(warmup):
+            fn()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(calls):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / calls
+        gbs = nbytes / (us * 1e-6) / 1e9
+        out[name] = {"us": us, "bytes_alg": nbytes, "GB/s": gbs, "frac_hbm": gbs / HBM_PEAK_GBS}
+    del keep
+    return out
+
+
 def traffic_of(w, kernel):
     """HBM bytes per launch of kernel from profiles/traffic.json (rocprofv3 FETCH_SIZE and WRITE_SIZE in KiB per
     dispatch, scaled by the copy calibration recorded with them), or None."""
@@ -335,6 +386,7 @@ def main():
     for d in designs:
         name = {lib.RECURRENT: "recurrent", lib.CHUNKED: "chunked"}[d]
         out["decode"][name] = run_decode(torch, lib, w, d)
+    out["neighbours"] = run_neighbours(torch, lib, w)
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(w, inp)
     print(json.dumps(out))

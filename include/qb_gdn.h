@@ -108,7 +108,8 @@ int qb_gdn_bwd(const qb_gdn_desc* desc, const void* q, const void* k, const void
  * and take the activations in dtype and the parameters in float32. With bf16 activations each op's output is
  * rounded to bf16 where the reference's op rounds it; arithmetic inside an op is float32. The backward entry points
  * are float32 inside with one rounding of each output, and sum the parameter gradients over tokens in a fixed order
- * (deterministic). */
+ * (deterministic). Pointers to the row tensors (q_raw, k_raw, q, k, y, z, o, dout and their cotangents) and to
+ * norm_w must be 16-byte aligned, the others aligned to their element size. */
 
 /* Scratch the neighbours' backward entry points need (the per-block partial sums); 0 on an invalid desc. */
 size_t qb_gdn_neighbours_workspace_bytes(const qb_gdn_desc* desc);

@@ -348,9 +348,9 @@ int qb_gdn_prologue_fwd(const qb_gdn_desc* desc, const void* q_raw, const void* 
     std::string why = nb_resolve(desc, p);
     const bool any = why.empty() && p.BT > 0;
     const size_t el = why.empty() && p.bf16 ? 2 : 4;
-    const PtrCheck c[] = {{"q_raw", q_raw, any, el}, {"k_raw", k_raw, any, el}, {"a", a, any, el},
+    const PtrCheck c[] = {{"q_raw", q_raw, any, 16}, {"k_raw", k_raw, any, 16}, {"a", a, any, el},
                           {"b", b, any, el},         {"a_log", a_log, true, 4},  {"dt_bias", dt_bias, true, 4},
-                          {"q", q, any, el},         {"k", k, any, el},          {"beta", beta, any, el},
+                          {"q", q, any, 16},         {"k", k, any, 16},          {"beta", beta, any, el},
                           {"log_decay", log_decay, any, 4}};
     if (why.empty()) why = check_all(c);
     if (!why.empty()) {
@@ -376,10 +376,10 @@ int qb_gdn_prologue_bwd(const qb_gdn_desc* desc, const void* q_raw, const void* 
     std::string why = nb_resolve(desc, p);
     const bool any = why.empty() && p.BT > 0;
     const size_t el = why.empty() && p.bf16 ? 2 : 4;
-    const PtrCheck c[] = {{"q_raw", q_raw, any, el},   {"k_raw", k_raw, any, el},     {"a", a, any, el},
+    const PtrCheck c[] = {{"q_raw", q_raw, any, 16},   {"k_raw", k_raw, any, 16},     {"a", a, any, el},
                           {"b", b, any, el},           {"a_log", a_log, true, 4},      {"dt_bias", dt_bias, true, 4},
-                          {"dq", dq, any, el},         {"dk", dk, any, el},            {"dbeta", dbeta, any, el},
-                          {"dlog_decay", dlog_decay, any, 4}, {"dq_raw", dq_raw, any, el}, {"dk_raw", dk_raw, any, el},
+                          {"dq", dq, any, 16},         {"dk", dk, any, 16},            {"dbeta", dbeta, any, el},
+                          {"dlog_decay", dlog_decay, any, 4}, {"dq_raw", dq_raw, any, 16}, {"dk_raw", dk_raw, any, 16},
                           {"da", da, any, el},         {"db", db, any, el},            {"da_log", da_log, true, 4},
                           {"ddt_bias", ddt_bias, true, 4},
                           {"workspace", workspace, why.empty() && qbgdn::nb_workspace_bytes(p) > 0, 4}};
@@ -406,8 +406,7 @@ int qb_gdn_epilogue_fwd(const qb_gdn_desc* desc, const void* y, const void* z, c
     std::string why = nb_resolve(desc, p);
     if (why.empty() && !(eps > 0.f)) why = "gated delta neighbours: eps must be positive";
     const bool any = why.empty() && p.BT > 0;
-    const size_t el = why.empty() && p.bf16 ? 2 : 4;
-    const PtrCheck c[] = {{"y", y, any, el}, {"z", z, any, el}, {"norm_w", norm_w, true, 4}, {"o", o, any, el}};
+    const PtrCheck c[] = {{"y", y, any, 16}, {"z", z, any, 16}, {"norm_w", norm_w, true, 16}, {"o", o, any, 16}};
     if (why.empty()) why = check_all(c);
     if (!why.empty()) {
       set_err(err, errlen, why);
@@ -431,9 +430,8 @@ int qb_gdn_epilogue_bwd(const qb_gdn_desc* desc, const void* y, const void* z, c
     std::string why = nb_resolve(desc, p);
     if (why.empty() && !(eps > 0.f)) why = "gated delta neighbours: eps must be positive";
     const bool any = why.empty() && p.BT > 0;
-    const size_t el = why.empty() && p.bf16 ? 2 : 4;
-    const PtrCheck c[] = {{"y", y, any, el},       {"z", z, any, el},   {"norm_w", norm_w, true, 4},
-                          {"dout", dout, any, el}, {"dy", dy, any, el}, {"dz", dz, any, el},
+    const PtrCheck c[] = {{"y", y, any, 16},       {"z", z, any, 16},   {"norm_w", norm_w, true, 16},
+                          {"dout", dout, any, 16}, {"dy", dy, any, 16}, {"dz", dz, any, 16},
                           {"dnorm_w", dnorm_w, true, 4},
                           {"workspace", workspace, why.empty() && qbgdn::nb_workspace_bytes(p) > 0, 4}};
     if (why.empty()) why = check_all(c);

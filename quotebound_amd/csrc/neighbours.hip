@@ -5,13 +5,17 @@
 //             recurrence takes itself when fed the log-decay)
 //   epilogue  o = silu(z) * rms_norm(y, w, eps)                       (:35-45, :122: the gated RMSNorm)
 // and their backward. With bf16 activations the forward rounds where the reference's ops do, each op's output
-// taking the activation dtype: rms_norm's output, then its product with the scale; a + dt_bias, then its softplus;
-// the rms_norm's normalised row, then its product with the weight, then that with silu(z). Arithmetic inside an op is float32. The backward is float32
-// throughout, with one rounding of each output; the parameter gradients (A_log, dt_bias per value head, w per
-// column) are summed over tokens in a fixed order: per-block partials, then one pass over the blocks in order.
+// taking the activation dtype: rms_norm's normalised row, then its product with the scale; a + dt_bias, then its
+// softplus; the rms_norm's normalised row, then its product with the weight, then that with silu(z). Arithmetic
+// inside an op is float32. The backward is float32 throughout, with one rounding of each output; the parameter
+// gradients (A_log, dt_bias per value head, w per column) are summed over tokens in a fixed order: per-block
+// partials, then one pass over the blocks in order.
 //
-// One wave per row of D = 64 E elements (E = 1, 2, 4): lane l holds elements E l .. E l + E - 1, so a row is one
-// contiguous read; the sum of squares is a fixed-order reduction over the wave.
+// Rows of D = 64, 128 or 256 elements: a lane holds 8 consecutive elements (one 16-byte load in bf16), a row takes
+// D / 8 consecutive lanes and a group of 64 / (D / 8) rows fills a wave; a wave of the one-pass kernels takes two
+// such groups, issuing both groups' loads before it computes. The sum of squares is a fixed-order reduction over the
+// row's lanes. Lanes past the last row compute on a copy of the last row and store nothing, so every lane takes part in
+// the reductions.
 #include <hip/hip_runtime.h>
 
 #include <type_traits>
@@ -23,216 +27,324 @@ namespace qbgdn {
 namespace {
 
 constexpr float kNormEps = 1e-6f;  // the q/k rms_norm's eps (src/deltanet.cpp:96-97)
+constexpr int kVec = 8;            // elements per lane
+constexpr int kNormBwdBlocks = 256;  // gated-norm backward: at most one block of 16 waves per CU
+constexpr int kGateSteps = 4;      // gates backward: steps per thread, so a tile is 4 (256 / Hv) tokens
+constexpr int kSlots = 2;          // row groups per wave in the one-pass kernels, their loads issued together
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// Round to nearest even bf16 in hardware (v_cvt_pk_bf16_f32), two values per instruction.
+__device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, bf16x2_t));
+}
 
 template <typename T>
 __device__ __forceinline__ float rnd(float x) {  // the activation dtype's rounding
-  if constexpr (sizeof(T) == 2) return bf16_to_f32(f32_to_bf16(x));
+  if constexpr (sizeof(T) == 2) return float(static_cast<__bf16>(x));
   return x;
 }
 
-__device__ __forceinline__ float wave_sum(float x) {
-  x = sum16(x);
-  x += __shfl_xor(x, 16);
-  x += __shfl_xor(x, 32);
+// Sum over aligned groups of L consecutive lanes (L = 8, 16, 32, 64); every lane of a group gets the same bits.
+template <int L>
+__device__ __forceinline__ float group_sum(float x) {
+  x += dpp_mov<0xb1>(x);   // quad_perm [1,0,3,2]
+  x += dpp_mov<0x4e>(x);   // quad_perm [2,3,0,1]
+  x += dpp_mov<0x141>(x);  // row_half_mirror: the two quads of each 8 lanes
+  if constexpr (L >= 16) x += dpp_mov<0x140>(x);  // row_mirror: the two halves of each 16 lanes
+  if constexpr (L >= 32) x += __shfl_xor(x, 16);
+  if constexpr (L >= 64) x += __shfl_xor(x, 32);
   return x;
 }
 
-__device__ __forceinline__ float sigmoidf(float x) { return 1.f / (1.f + expf(-x)); }
+// The hardware exp2 and reciprocal (a few float32 ulps).
+__device__ __forceinline__ float sigmoidf(float x) { return __builtin_amdgcn_rcpf(1.f + __expf(-x)); }
+__device__ __forceinline__ float rsqrt_mean(float ss, int n, float eps) { return __builtin_amdgcn_rsqf(ss / n + eps); }
 __device__ __forceinline__ float softplusf(float x) { return fmaxf(x, 0.f) + log1pf(expf(-fabsf(x))); }
 
-template <typename T, int E>
-__device__ __forceinline__ void load_row(const T* p, float (&x)[E]) {
-#pragma unroll
-  for (int e = 0; e < E; ++e) x[e] = IO<T>::ld(p, e);
-}
-
-// Rows of q_raw then k_raw (2 R rows of D): out = rnd(scale * rnd(x * rho)), rho = (mean(x^2) + eps)^-1/2.
-template <typename T, int E>
-__global__ __launch_bounds__(256) void qk_norm_fwd(const T* __restrict__ qr, const T* __restrict__ kr,
-                                                   T* __restrict__ q, T* __restrict__ k, int64_t R, float sq,
-                                                   float sk) {
-  constexpr int D = 64 * E;
-  const int lane = threadIdx.x & 63;
-  const int64_t row = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
-  if (row >= 2 * R) return;
-  const bool isk = row >= R;
-  const int64_t r = isk ? row - R : row;
-  const T* src = (isk ? kr : qr) + r * D + E * lane;
-  T* dst = (isk ? k : q) + r * D + E * lane;
-  const float s = isk ? sk : sq;
-  float x[E];
-  load_row<T, E>(src, x);
-  float ss = 0.f;
-#pragma unroll
-  for (int e = 0; e < E; ++e) ss += x[e] * x[e];
-  const float rho = 1.f / sqrtf(wave_sum(ss) / D + kNormEps);
-#pragma unroll
-  for (int e = 0; e < E; ++e) IO<T>::st(dst, e, rnd<T>(s * rnd<T>(x[e] * rho)));
-}
-
-// beta and the log-decay per (token, value head).
 template <typename T>
-__global__ __launch_bounds__(256) void gates_fwd(const T* __restrict__ a, const T* __restrict__ b,
-                                                 const float* __restrict__ a_log, const float* __restrict__ dt_bias,
-                                                 T* __restrict__ beta, float* __restrict__ log_decay, int64_t n,
-                                                 int Hv) {
-  const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
-  if (i >= n) return;
-  const int h = int(i % Hv);
-  IO<T>::st(beta, i, sigmoidf(IO<T>::ld(b, i)));
-  const float x = rnd<T>(IO<T>::ld(a, i) + dt_bias[h]);
-  log_decay[i] = -expf(a_log[h]) * rnd<T>(softplusf(x));
+__device__ __forceinline__ void ld8(const T* p, float (&x)[kVec]) {
+  IO<T>::ld8(p, x);
 }
 
-// The backward of qk_norm_fwd: g = scale * dout, dx = rho g - rho^3 x (sum g x) / D.
-template <typename T, int E>
-__global__ __launch_bounds__(256) void qk_norm_bwd(const T* __restrict__ qr, const T* __restrict__ kr,
-                                                   const T* __restrict__ dq, const T* __restrict__ dk,
-                                                   T* __restrict__ dqr, T* __restrict__ dkr, int64_t R, float sq,
-                                                   float sk) {
-  constexpr int D = 64 * E;
-  const int lane = threadIdx.x & 63;
-  const int64_t row = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
-  if (row >= 2 * R) return;
-  const bool isk = row >= R;
-  const int64_t r = isk ? row - R : row;
-  const int64_t off = r * D + E * lane;
-  const float s = isk ? sk : sq;
-  float x[E], gd[E];
-  load_row<T, E>((isk ? kr : qr) + off, x);
-  load_row<T, E>((isk ? dk : dq) + off, gd);
-  float ss = 0.f, gx = 0.f;
-#pragma unroll
-  for (int e = 0; e < E; ++e) {
-    gd[e] *= s;
-    ss += x[e] * x[e];
-    gx += gd[e] * x[e];
+template <typename T>
+__device__ __forceinline__ void st8(T* p, const float (&x)[kVec]) {
+  if constexpr (sizeof(T) == 2) {
+    *reinterpret_cast<uint4*>(p) =
+        make_uint4(pack_bf16(x[0], x[1]), pack_bf16(x[2], x[3]), pack_bf16(x[4], x[5]), pack_bf16(x[6], x[7]));
+  } else {
+    reinterpret_cast<float4*>(p)[0] = make_float4(x[0], x[1], x[2], x[3]);
+    reinterpret_cast<float4*>(p)[1] = make_float4(x[4], x[5], x[6], x[7]);
   }
-  const float rho = 1.f / sqrtf(wave_sum(ss) / D + kNormEps);
-  const float c = rho * rho * rho * wave_sum(gx) / D;
-  T* out = (isk ? dkr : dqr) + off;
-#pragma unroll
-  for (int e = 0; e < E; ++e) IO<T>::st(out, e, rho * gd[e] - c * x[e]);
 }
 
-// The backward of gates_fwd for 64 consecutive tokens of one value head (one wave): db, da, and the tile's partial
-// sums of dA_log = sum dlog_decay * log_decay and ddt_bias = sum da.
-template <typename T>
-__global__ __launch_bounds__(64) void gates_bwd(const T* __restrict__ a, const T* __restrict__ b,
-                                                const float* __restrict__ a_log, const float* __restrict__ dt_bias,
-                                                const T* __restrict__ dbeta, const float* __restrict__ dld,
-                                                T* __restrict__ da, T* __restrict__ db, float* __restrict__ part,
-                                                int64_t BT, int Hv) {
-  const int h = blockIdx.y;
-  const int64_t t = int64_t(blockIdx.x) * 64 + threadIdx.x;
-  float pa = 0.f, pd = 0.f;
-  if (t < BT) {
-    const int64_t i = t * Hv + h;
-    const float sb = sigmoidf(IO<T>::ld(b, i));
-    IO<T>::st(db, i, IO<T>::ld(dbeta, i) * sb * (1.f - sb));
-    const float ea = expf(a_log[h]);
+__device__ __forceinline__ void ld8f(const float* p, float (&x)[kVec]) { IO<float>::ld8(p, x); }
+
+// The lane's row of D (clamped to the last one), whether it is a real row, and its first column, for the waves of
+// a block taking consecutive rows from first_row, each wave `slots` groups of RPW rows (this lane's in group j).
+template <int D>
+struct RowLane {
+  static constexpr int L = D / kVec, RPW = 64 / L;
+  int64_t row;
+  bool live;
+  int col;
+  __device__ RowLane(int64_t first_row, int64_t rows, int slots = 1, int j = 0) {
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int64_t r = first_row + (int64_t(wv) * slots + j) * RPW + lane / L;
+    live = r < rows;
+    row = live ? r : rows - 1;
+    col = (lane % L) * kVec;
+  }
+};
+
+// ---- prologue ----------------------------------------------------------------------------------------------------
+
+// Blocks [0, nrow_blocks): rows of q_raw then k_raw (2 R rows of D), out = rnd(scale * rnd(x * rho)),
+// rho = (mean(x^2) + eps)^-1/2. The blocks after them: beta and the log-decay, one (token, value head) per thread.
+template <typename T, int D>
+__global__ __launch_bounds__(256) void prologue_fwd_kernel(const T* __restrict__ qr, const T* __restrict__ kr,
+                                                           T* __restrict__ q, T* __restrict__ k, int64_t R,
+                                                           float sq, float sk, int64_t nrow_blocks,
+                                                           const T* __restrict__ a, const T* __restrict__ b,
+                                                           const float* __restrict__ a_log,
+                                                           const float* __restrict__ dt_bias, T* __restrict__ beta,
+                                                           float* __restrict__ log_decay, int64_t n, int Hv) {
+  if (int64_t(blockIdx.x) >= nrow_blocks) {
+    const int64_t i = (int64_t(blockIdx.x) - nrow_blocks) * 256 + threadIdx.x;
+    if (i >= n) return;
+    const int h = int(i % Hv);
+    IO<T>::st(beta, i, sigmoidf(IO<T>::ld(b, i)));
     const float x = rnd<T>(IO<T>::ld(a, i) + dt_bias[h]);
-    const float g = dld[i];
-    const float dx = -g * ea * sigmoidf(x);
-    IO<T>::st(da, i, dx);
-    pa = g * (-ea * rnd<T>(softplusf(x)));  // d log_decay / d A_log = log_decay
-    pd = dx;
+    log_decay[i] = -expf(a_log[h]) * rnd<T>(softplusf(x));
+    return;
   }
-  pa = wave_sum(pa), pd = wave_sum(pd);
-  if (threadIdx.x == 0) {
-    part[(int64_t(blockIdx.x) * Hv + h) * 2] = pa;
-    part[(int64_t(blockIdx.x) * Hv + h) * 2 + 1] = pd;
+  using RL = RowLane<D>;
+  float x[kSlots][kVec];
+  int64_t off[kSlots];
+  bool isk[kSlots], live[kSlots];
+#pragma unroll
+  for (int j = 0; j < kSlots; ++j) {
+    const RL rl(int64_t(blockIdx.x) * 4 * kSlots * RL::RPW, 2 * R, kSlots, j);
+    isk[j] = rl.row >= R, live[j] = rl.live;
+    off[j] = (isk[j] ? rl.row - R : rl.row) * D + rl.col;
+    ld8((isk[j] ? kr : qr) + off[j], x[j]);
+  }
+#pragma unroll
+  for (int j = 0; j < kSlots; ++j) {
+    const float s = isk[j] ? sk : sq;
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < kVec; ++e) ss += x[j][e] * x[j][e];
+    const float rho = rsqrt_mean(group_sum<RL::L>(ss), D, kNormEps);
+#pragma unroll
+    for (int e = 0; e < kVec; ++e) x[j][e] = rnd<T>(s * rnd<T>(x[j][e] * rho));
+    if (live[j]) st8((isk[j] ? k : q) + off[j], x[j]);
   }
 }
 
-// out[c] = sum over parts p of part[p * stride + c * step + comp], for c < width, in a fixed order: 64 columns per
-// block, wave v summing the parts p = v mod 4 in increasing order, then the four waves' sums in order.
-__global__ __launch_bounds__(256) void sum_parts(const float* __restrict__ part, int64_t nparts, int stride,
-                                                 int step, int comp, int width, float* __restrict__ out) {
-  __shared__ float red[4][64];
+// The backward. Row blocks: g = scale * dout, dx = rho g - rho^3 x (sum g x) / D. The blocks after them each take a
+// tile of kGateSteps k tokens (k = 256 / Hv): thread t < k Hv handles value head t % Hv of tokens t / Hv,
+// t / Hv + k, ..., so each step reads k Hv contiguous (token, head) elements. It writes db and da, and the tile's partial sums
+// of dA_log = sum dlog_decay * log_decay and ddt_bias = sum da per head (the k threads of a head in order) at
+// part[(tile * Hv + h) * 2 + {0, 1}].
+template <typename T, int D>
+__global__ __launch_bounds__(256) void prologue_bwd_kernel(
+    const T* __restrict__ qr, const T* __restrict__ kr, const T* __restrict__ dq, const T* __restrict__ dk,
+    T* __restrict__ dqr, T* __restrict__ dkr, int64_t R, float sq, float sk, int64_t nrow_blocks,
+    const T* __restrict__ a, const T* __restrict__ b, const float* __restrict__ a_log,
+    const float* __restrict__ dt_bias, const T* __restrict__ dbeta, const float* __restrict__ dld,
+    T* __restrict__ da, T* __restrict__ db, float* __restrict__ part, int64_t BT, int Hv) {
+  if (int64_t(blockIdx.x) >= nrow_blocks) {
+    __shared__ float red[2][256];
+    const int64_t tile = int64_t(blockIdx.x) - nrow_blocks;
+    const int k = 256 / Hv, t = threadIdx.x, h = t % Hv;
+    float pa = 0.f, pd = 0.f;
+    if (t < k * Hv) {
+      const float ea = expf(a_log[h]), bias = dt_bias[h];
+      const int64_t tt = int64_t(kGateSteps) * k, end = (tile + 1) * tt < BT ? (tile + 1) * tt : BT;
+      for (int64_t tok = tile * tt + t / Hv; tok < end; tok += k) {
+        const int64_t i = tok * Hv + h;
+        const float sb = sigmoidf(IO<T>::ld(b, i));
+        IO<T>::st(db, i, IO<T>::ld(dbeta, i) * sb * (1.f - sb));
+        const float x = rnd<T>(IO<T>::ld(a, i) + bias);
+        const float g = dld[i];
+        const float dx = -g * ea * sigmoidf(x);
+        IO<T>::st(da, i, dx);
+        pa += g * (-ea * rnd<T>(softplusf(x)));  // d log_decay / d A_log = log_decay
+        pd += dx;
+      }
+    }
+    red[0][t] = pa, red[1][t] = pd;
+    __syncthreads();
+    if (t < Hv) {
+      float sa = 0.f, sd = 0.f;
+      for (int j = 0; j < k; ++j) sa += red[0][j * Hv + t], sd += red[1][j * Hv + t];
+      part[(tile * Hv + t) * 2] = sa;
+      part[(tile * Hv + t) * 2 + 1] = sd;
+    }
+    return;
+  }
+  using RL = RowLane<D>;
+  float x[kSlots][kVec], g[kSlots][kVec];
+  int64_t off[kSlots];
+  bool isk[kSlots], live[kSlots];
+#pragma unroll
+  for (int j = 0; j < kSlots; ++j) {
+    const RL rl(int64_t(blockIdx.x) * 4 * kSlots * RL::RPW, 2 * R, kSlots, j);
+    isk[j] = rl.row >= R, live[j] = rl.live;
+    off[j] = (isk[j] ? rl.row - R : rl.row) * D + rl.col;
+    ld8((isk[j] ? kr : qr) + off[j], x[j]);
+    ld8((isk[j] ? dk : dq) + off[j], g[j]);
+  }
+#pragma unroll
+  for (int j = 0; j < kSlots; ++j) {
+    const float s = isk[j] ? sk : sq;
+    float ss = 0.f, gx = 0.f;
+#pragma unroll
+    for (int e = 0; e < kVec; ++e) {
+      g[j][e] *= s;
+      ss += x[j][e] * x[j][e];
+      gx += g[j][e] * x[j][e];
+    }
+    const float rho = rsqrt_mean(group_sum<RL::L>(ss), D, kNormEps);
+    const float c = rho * rho * rho * group_sum<RL::L>(gx) / D;
+#pragma unroll
+    for (int e = 0; e < kVec; ++e) x[j][e] = rho * g[j][e] - c * x[j][e];
+    if (live[j]) st8((isk[j] ? dkr : dqr) + off[j], x[j]);
+  }
+}
+
+// ---- epilogue ----------------------------------------------------------------------------------------------------
+
+// The gated RMSNorm: o = rnd(silu(z) * rnd(w * rnd(y * rho))) (rms_norm normalises, takes the output dtype, then
+// multiplies by its weight).
+template <typename T, int D>
+__global__ __launch_bounds__(256) void epilogue_fwd_kernel(const T* __restrict__ y, const T* __restrict__ z,
+                                                           const float* __restrict__ w, float eps,
+                                                           T* __restrict__ o, int64_t R) {
+  using RL = RowLane<D>;
+  float x[kSlots][kVec], zz[kSlots][kVec], wl[kVec];
+  int64_t off[kSlots];
+  bool live[kSlots];
+#pragma unroll
+  for (int j = 0; j < kSlots; ++j) {
+    const RL rl(int64_t(blockIdx.x) * 4 * kSlots * RL::RPW, R, kSlots, j);
+    live[j] = rl.live, off[j] = rl.row * D + rl.col;
+    ld8(y + off[j], x[j]);
+    ld8(z + off[j], zz[j]);
+  }
+  ld8f(w + ((threadIdx.x & 63) % RL::L) * kVec, wl);
+#pragma unroll
+  for (int j = 0; j < kSlots; ++j) {
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < kVec; ++e) ss += x[j][e] * x[j][e];
+    const float rho = rsqrt_mean(group_sum<RL::L>(ss), D, eps);
+#pragma unroll
+    for (int e = 0; e < kVec; ++e) {
+      const float n = rnd<T>(wl[e] * rnd<T>(x[j][e] * rho));
+      x[j][e] = zz[j][e] * sigmoidf(zz[j][e]) * n;
+    }
+    if (live[j]) st8(o + off[j], x[j]);
+  }
+}
+
+// Its backward, blocks of 16 waves striding over the rows: dz = dout n silu'(z), dy through the norm, and the
+// block's partial dw per column, summed in a fixed order: each lane over its rows, the wave's row slots by a
+// butterfly over lanes, then the 16 waves in order.
+template <typename T, int D>
+__global__ __launch_bounds__(1024) void epilogue_bwd_kernel(const T* __restrict__ y, const T* __restrict__ z,
+                                                            const float* __restrict__ w, float eps,
+                                                            const T* __restrict__ dout, T* __restrict__ dy,
+                                                            T* __restrict__ dz, float* __restrict__ part,
+                                                            int64_t R) {
+  using RL = RowLane<D>;
+  constexpr int kRowsPerStep = 16 * RL::RPW;
+  __shared__ float acc[16][D];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  float pw[kVec], wl[kVec];
+  ld8f(w + (lane % RL::L) * kVec, wl);
+#pragma unroll
+  for (int e = 0; e < kVec; ++e) pw[e] = 0.f;
+  for (int64_t first = int64_t(blockIdx.x) * kRowsPerStep; first < R; first += int64_t(gridDim.x) * kRowsPerStep) {
+    const RL rl(first, R);
+    const int64_t off = rl.row * D + rl.col;
+    float x[kVec], zz[kVec], go[kVec];
+    ld8(y + off, x);
+    ld8(z + off, zz);
+    ld8(dout + off, go);
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < kVec; ++e) ss += x[e] * x[e];
+    const float rho = rsqrt_mean(group_sum<RL::L>(ss), D, eps);
+    const float keep = rl.live ? 1.f : 0.f;
+    float gx = 0.f, g[kVec];
+#pragma unroll
+    for (int e = 0; e < kVec; ++e) {
+      const float sg = sigmoidf(zz[e]), silu = zz[e] * sg, nh = x[e] * rho;
+      zz[e] = go[e] * nh * wl[e] * sg * (1.f + zz[e] * (1.f - sg));  // dz
+      const float dn = go[e] * silu;
+      pw[e] += keep * (dn * nh);
+      g[e] = dn * wl[e];
+      gx += g[e] * x[e];
+    }
+    const float c = rho * rho * rho * group_sum<RL::L>(gx) / D;
+#pragma unroll
+    for (int e = 0; e < kVec; ++e) x[e] = rho * g[e] - c * x[e];
+    if (rl.live) {
+      st8(dz + off, zz);
+      st8(dy + off, x);
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < kVec; ++e)
+    for (int s = RL::L; s < 64; s <<= 1) pw[e] += __shfl_xor(pw[e], s);
+  if (lane < RL::L) {
+#pragma unroll
+    for (int e = 0; e < kVec; ++e) acc[wv][lane * kVec + e] = pw[e];
+  }
+  __syncthreads();
+  if (threadIdx.x < D) {
+    float s = 0.f;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) s += acc[v][threadIdx.x];
+    part[int64_t(blockIdx.x) * D + threadIdx.x] = s;
+  }
+}
+
+// Sums of partials: column c < width of out is the sum over parts p of part[p * width + c], in a fixed order (64
+// columns per block, wave v summing the parts p = v mod 16 in increasing order, then the 16 waves in order). With
+// `pairs`, columns alternate between two outputs: column 2 h + j goes to out_j[h].
+template <bool pairs>
+__global__ __launch_bounds__(1024) void sum_parts(const float* __restrict__ part, int64_t nparts, int width,
+                                                  float* __restrict__ out0, float* __restrict__ out1) {
+  __shared__ float red[16][64];
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int c = blockIdx.x * 64 + lane;
   float s = 0.f;
   if (c < width)
-    for (int64_t p = wv; p < nparts; p += 4) s += part[p * stride + int64_t(c) * step + comp];
+    for (int64_t p0 = wv; p0 < nparts; p0 += 16 * 16) {  // 16 loads in flight, then summed in order
+      float v[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int64_t p = p0 + 16 * i;
+        v[i] = p < nparts ? part[p * width + c] : 0.f;
+      }
+#pragma unroll
+      for (int i = 0; i < 16; ++i) s += v[i];
+    }
   red[wv][lane] = s;
   __syncthreads();
-  if (wv == 0 && c < width) out[c] = ((red[0][lane] + red[1][lane]) + red[2][lane]) + red[3][lane];
-}
-
-// The gated RMSNorm: o = rnd(silu(z) * rnd(w * rnd(y * rho))), one row of Dv per wave (rms_norm normalises, takes
-// the output dtype, then multiplies by its weight).
-template <typename T, int E>
-__global__ __launch_bounds__(256) void gated_norm_fwd(const T* __restrict__ y, const T* __restrict__ z,
-                                                      const float* __restrict__ w, float eps, T* __restrict__ o,
-                                                      int64_t R) {
-  constexpr int D = 64 * E;
-  const int lane = threadIdx.x & 63;
-  const int64_t row = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
-  if (row >= R) return;
-  const int64_t off = row * D + E * lane;
-  float x[E], zz[E];
-  load_row<T, E>(y + off, x);
-  load_row<T, E>(z + off, zz);
-  float ss = 0.f;
+  if (wv == 0 && c < width) {
+    float t = 0.f;
 #pragma unroll
-  for (int e = 0; e < E; ++e) ss += x[e] * x[e];
-  const float rho = 1.f / sqrtf(wave_sum(ss) / D + eps);
-#pragma unroll
-  for (int e = 0; e < E; ++e) {
-    const float n = rnd<T>(w[E * lane + e] * rnd<T>(x[e] * rho));
-    IO<T>::st(o + off, e, rnd<T>(zz[e] * sigmoidf(zz[e]) * n));
+    for (int v = 0; v < 16; ++v) t += red[v][lane];
+    if constexpr (pairs)
+      ((c & 1) ? out1 : out0)[c >> 1] = t;
+    else
+      out0[c] = t;
   }
-}
-
-// Its backward over groups of 64 rows (16 per wave), block b taking groups b, b + gridDim.x, ...: dz = do n silu'(z),
-// dy through the norm, and the block's partial dw per column (summed over its rows in a fixed order: each wave over
-// its rows, then the four waves in order).
-template <typename T, int E>
-__global__ __launch_bounds__(256) void gated_norm_bwd(const T* __restrict__ y, const T* __restrict__ z,
-                                                      const float* __restrict__ w, float eps,
-                                                      const T* __restrict__ dout, T* __restrict__ dy,
-                                                      T* __restrict__ dz, float* __restrict__ part, int64_t R) {
-  constexpr int D = 64 * E;
-  __shared__ float acc[4][D];
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  float pw[E];
-  float wl[E];
-#pragma unroll
-  for (int e = 0; e < E; ++e) pw[e] = 0.f, wl[e] = w[E * lane + e];
-  for (int64_t grp = blockIdx.x; grp * 64 < R; grp += gridDim.x) {
-    for (int k = 0; k < 16; ++k) {
-      const int64_t row = grp * 64 + wv * 16 + k;
-      if (row >= R) break;
-      const int64_t off = row * D + E * lane;
-      float x[E], zz[E], go[E];
-      load_row<T, E>(y + off, x);
-      load_row<T, E>(z + off, zz);
-      load_row<T, E>(dout + off, go);
-      float ss = 0.f;
-#pragma unroll
-      for (int e = 0; e < E; ++e) ss += x[e] * x[e];
-      const float rho = 1.f / sqrtf(wave_sum(ss) / D + eps);
-      float g[E], gx = 0.f;
-#pragma unroll
-      for (int e = 0; e < E; ++e) {
-        const float sg = sigmoidf(zz[e]), silu = zz[e] * sg, nh = x[e] * rho;
-        IO<T>::st(dz + off, e, go[e] * nh * wl[e] * sg * (1.f + zz[e] * (1.f - sg)));
-        const float dn = go[e] * silu;
-        pw[e] += dn * nh;
-        g[e] = dn * wl[e];
-        gx += g[e] * x[e];
-      }
-      const float c = rho * rho * rho * wave_sum(gx) / D;
-#pragma unroll
-      for (int e = 0; e < E; ++e) IO<T>::st(dy + off, e, rho * g[e] - c * x[e]);
-    }
-  }
-#pragma unroll
-  for (int e = 0; e < E; ++e) acc[wv][E * lane + e] = pw[e];
-  __syncthreads();
-  for (int c = threadIdx.x; c < D; c += 256)
-    part[int64_t(blockIdx.x) * D + c] = ((acc[0][c] + acc[1][c]) + acc[2][c]) + acc[3][c];
 }
 
 }  // namespace
@@ -241,68 +353,94 @@ __global__ __launch_bounds__(256) void gated_norm_bwd(const T* __restrict__ y, c
 
 namespace {
 
-// Blocks of the gated-norm backward: one per 64 rows up to 1024 (four per CU), so the partial dw stays small.
+template <int D>
+constexpr int64_t rows_per_block() {
+  return 4 * kSlots * RowLane<D>::RPW;
+}
+
+int64_t gate_tiles(int64_t BT, int Hv) {
+  const int64_t tt = int64_t(kGateSteps) * (256 / Hv);
+  return (BT + tt - 1) / tt;
+}
+
+template <int D>
 int64_t norm_bwd_blocks(int64_t R) {
-  const int64_t groups = (R + 63) / 64;
-  return groups < 1024 ? groups : 1024;
+  const int64_t steps = (R + 16 * RowLane<D>::RPW - 1) / (16 * RowLane<D>::RPW);
+  return steps < kNormBwdBlocks ? steps : kNormBwdBlocks;
 }
 
-template <int E, typename T>
-hipError_t qk_fwd_e(const NbProblem& p, const NbPrologue& x, hipStream_t s) {
-  const int64_t R = p.BT * p.Hk;
-  const unsigned blocks = unsigned((2 * R + 3) / 4);
-  if (blocks)
-    hipLaunchKernelGGL((qk_norm_fwd<T, E>), dim3(blocks), dim3(256), 0, s, static_cast<const T*>(x.q_raw),
-                       static_cast<const T*>(x.k_raw), static_cast<T*>(x.q), static_cast<T*>(x.k), R, p.scale_q,
-                       p.scale_k);
-  return hipGetLastError();
-}
-
-template <int E, typename T>
-hipError_t qk_bwd_e(const NbProblem& p, const NbPrologueGrad& x, hipStream_t s) {
-  const int64_t R = p.BT * p.Hk;
-  const unsigned blocks = unsigned((2 * R + 3) / 4);
-  if (blocks)
-    hipLaunchKernelGGL((qk_norm_bwd<T, E>), dim3(blocks), dim3(256), 0, s, static_cast<const T*>(x.q_raw),
-                       static_cast<const T*>(x.k_raw), static_cast<const T*>(x.dq), static_cast<const T*>(x.dk),
-                       static_cast<T*>(x.dq_raw), static_cast<T*>(x.dk_raw), R, p.scale_q, p.scale_k);
-  return hipGetLastError();
-}
-
-template <int E, typename T>
-hipError_t gn_fwd_e(const NbProblem& p, const NbEpilogue& x, hipStream_t s) {
-  const int64_t R = p.BT * p.Hv;
-  const unsigned blocks = unsigned((R + 3) / 4);
-  if (blocks)
-    hipLaunchKernelGGL((gated_norm_fwd<T, E>), dim3(blocks), dim3(256), 0, s, static_cast<const T*>(x.y),
-                       static_cast<const T*>(x.z), x.w, x.eps, static_cast<T*>(x.o), R);
-  return hipGetLastError();
-}
-
-template <int E, typename T>
-hipError_t gn_bwd_e(const NbProblem& p, const NbEpilogueGrad& x, void* ws, hipStream_t s) {
-  const int64_t R = p.BT * p.Hv;
-  const int64_t blocks = norm_bwd_blocks(R);
-  float* part = static_cast<float*>(ws);
-  if (blocks) {
-    hipLaunchKernelGGL((gated_norm_bwd<T, E>), dim3(unsigned(blocks)), dim3(256), 0, s, static_cast<const T*>(x.y),
-                       static_cast<const T*>(x.z), x.w, x.eps, static_cast<const T*>(x.dout), static_cast<T*>(x.dy),
-                       static_cast<T*>(x.dz), part, R);
-    hipLaunchKernelGGL(sum_parts, dim3(unsigned((p.Dv + 63) / 64)), dim3(256), 0, s, part, blocks, p.Dv, 1, 0,
-                       p.Dv, x.dw);
-  } else {  // no rows: zeros (a sum over no parts)
-    hipLaunchKernelGGL(sum_parts, dim3(unsigned((p.Dv + 63) / 64)), dim3(256), 0, s, part, 0, p.Dv, 1, 0, p.Dv,
-                       x.dw);
+int64_t norm_bwd_blocks_of(int D, int64_t R) {
+  switch (D) {
+    case 64: return norm_bwd_blocks<64>(R);
+    case 128: return norm_bwd_blocks<128>(R);
+    default: return norm_bwd_blocks<256>(R);
   }
+}
+
+template <int D, typename T>
+hipError_t prologue_fwd_d(const NbProblem& p, const NbPrologue& x, hipStream_t s) {
+  const int64_t R = p.BT * p.Hk, n = p.BT * p.Hv;
+  const int64_t row_blocks = (2 * R + rows_per_block<D>() - 1) / rows_per_block<D>();
+  const int64_t blocks = row_blocks + (n + 255) / 256;
+  if (blocks)
+    hipLaunchKernelGGL((prologue_fwd_kernel<T, D>), dim3(unsigned(blocks)), dim3(256), 0, s,
+                       static_cast<const T*>(x.q_raw), static_cast<const T*>(x.k_raw), static_cast<T*>(x.q),
+                       static_cast<T*>(x.k), R, p.scale_q, p.scale_k, row_blocks, static_cast<const T*>(x.a),
+                       static_cast<const T*>(x.b), x.a_log, x.dt_bias, static_cast<T*>(x.beta), x.log_decay, n,
+                       p.Hv);
+  return hipGetLastError();
+}
+
+template <int D, typename T>
+hipError_t prologue_bwd_d(const NbProblem& p, const NbPrologueGrad& x, void* ws, hipStream_t s) {
+  const int64_t R = p.BT * p.Hk, tiles = gate_tiles(p.BT, p.Hv);
+  const int64_t row_blocks = (2 * R + rows_per_block<D>() - 1) / rows_per_block<D>();
+  const int64_t blocks = row_blocks + tiles;
+  float* part = static_cast<float*>(ws);
+  if (blocks)
+    hipLaunchKernelGGL((prologue_bwd_kernel<T, D>), dim3(unsigned(blocks)), dim3(256), 0, s,
+                       static_cast<const T*>(x.q_raw), static_cast<const T*>(x.k_raw), static_cast<const T*>(x.dq),
+                       static_cast<const T*>(x.dk), static_cast<T*>(x.dq_raw), static_cast<T*>(x.dk_raw), R,
+                       p.scale_q, p.scale_k, row_blocks, static_cast<const T*>(x.a), static_cast<const T*>(x.b),
+                       x.a_log, x.dt_bias, static_cast<const T*>(x.dbeta), x.dlog_decay, static_cast<T*>(x.da),
+                       static_cast<T*>(x.db), part, p.BT, p.Hv);
+  // (With no tokens, sums over no parts: zeros.)
+  hipLaunchKernelGGL(sum_parts<true>, dim3(unsigned((2 * p.Hv + 63) / 64)), dim3(1024), 0, s, part, tiles,
+                     2 * p.Hv, x.da_log, x.ddt_bias);
+  return hipGetLastError();
+}
+
+template <int D, typename T>
+hipError_t epilogue_fwd_d(const NbProblem& p, const NbEpilogue& x, hipStream_t s) {
+  const int64_t R = p.BT * p.Hv;
+  const int64_t blocks = (R + rows_per_block<D>() - 1) / rows_per_block<D>();
+  if (blocks)
+    hipLaunchKernelGGL((epilogue_fwd_kernel<T, D>), dim3(unsigned(blocks)), dim3(256), 0, s,
+                       static_cast<const T*>(x.y), static_cast<const T*>(x.z), x.w, x.eps, static_cast<T*>(x.o), R);
+  return hipGetLastError();
+}
+
+template <int D, typename T>
+hipError_t epilogue_bwd_d(const NbProblem& p, const NbEpilogueGrad& x, void* ws, hipStream_t s) {
+  const int64_t R = p.BT * p.Hv;
+  const int64_t blocks = norm_bwd_blocks<D>(R);
+  float* part = static_cast<float*>(ws);
+  if (blocks)
+    hipLaunchKernelGGL((epilogue_bwd_kernel<T, D>), dim3(unsigned(blocks)), dim3(1024), 0, s,
+                       static_cast<const T*>(x.y), static_cast<const T*>(x.z), x.w, x.eps,
+                       static_cast<const T*>(x.dout), static_cast<T*>(x.dy), static_cast<T*>(x.dz), part, R);
+  // (With no rows, a sum over no parts: zeros.)
+  hipLaunchKernelGGL(sum_parts<false>, dim3(unsigned((D + 63) / 64)), dim3(1024), 0, s, part, blocks, D, x.dw,
+                     nullptr);
   return hipGetLastError();
 }
 
 template <typename F>
 hipError_t by_width(int D, F&& f) {
   switch (D) {
-    case 64: return f(std::integral_constant<int, 1>{});
-    case 128: return f(std::integral_constant<int, 2>{});
-    case 256: return f(std::integral_constant<int, 4>{});
+    case 64: return f(std::integral_constant<int, 64>{});
+    case 128: return f(std::integral_constant<int, 128>{});
+    case 256: return f(std::integral_constant<int, 256>{});
     default: return hipErrorInvalidValue;
   }
 }
@@ -312,70 +450,41 @@ hipError_t by_width(int D, F&& f) {
 const char* nb_supports(const NbProblem& p) {
   if (p.Dk != 64 && p.Dk != 128 && p.Dk != 256) return "the neighbour kernels need Dk of 64, 128 or 256";
   if (p.Dv != 64 && p.Dv != 128 && p.Dv != 256) return "the neighbour kernels need Dv of 64, 128 or 256";
+  if (p.Hv > 256) return "the neighbour kernels need at most 256 value heads";
   return nullptr;
 }
 
 size_t nb_workspace_bytes(const NbProblem& p) {
-  const size_t gates = size_t((p.BT + 63) / 64) * p.Hv * 2 * 4;
-  const size_t norm = size_t(norm_bwd_blocks(p.BT * p.Hv)) * p.Dv * 4;
+  const size_t gates = size_t(gate_tiles(p.BT, p.Hv)) * p.Hv * 2 * 4;
+  const size_t norm = size_t(norm_bwd_blocks_of(p.Dv, p.BT * p.Hv)) * p.Dv * 4;
   return gates > norm ? gates : norm;
 }
 
 hipError_t nb_prologue_fwd(const NbProblem& p, const NbPrologue& x, hipStream_t s) {
-  hipError_t e = by_width(p.Dk, [&](auto ec) {
-    return p.bf16 ? qk_fwd_e<decltype(ec)::value, bf16_t>(p, x, s) : qk_fwd_e<decltype(ec)::value, float>(p, x, s);
+  return by_width(p.Dk, [&](auto dc) {
+    constexpr int D = decltype(dc)::value;
+    return p.bf16 ? prologue_fwd_d<D, bf16_t>(p, x, s) : prologue_fwd_d<D, float>(p, x, s);
   });
-  if (e != hipSuccess) return e;
-  const int64_t n = p.BT * p.Hv;
-  if (n) {
-    const dim3 grid(unsigned((n + 255) / 256));
-    if (p.bf16)
-      hipLaunchKernelGGL(gates_fwd<bf16_t>, grid, dim3(256), 0, s, static_cast<const bf16_t*>(x.a),
-                         static_cast<const bf16_t*>(x.b), x.a_log, x.dt_bias, static_cast<bf16_t*>(x.beta),
-                         x.log_decay, n, p.Hv);
-    else
-      hipLaunchKernelGGL(gates_fwd<float>, grid, dim3(256), 0, s, static_cast<const float*>(x.a),
-                         static_cast<const float*>(x.b), x.a_log, x.dt_bias, static_cast<float*>(x.beta),
-                         x.log_decay, n, p.Hv);
-  }
-  return hipGetLastError();
 }
 
 hipError_t nb_prologue_bwd(const NbProblem& p, const NbPrologueGrad& x, void* ws, hipStream_t s) {
-  hipError_t e = by_width(p.Dk, [&](auto ec) {
-    return p.bf16 ? qk_bwd_e<decltype(ec)::value, bf16_t>(p, x, s) : qk_bwd_e<decltype(ec)::value, float>(p, x, s);
+  return by_width(p.Dk, [&](auto dc) {
+    constexpr int D = decltype(dc)::value;
+    return p.bf16 ? prologue_bwd_d<D, bf16_t>(p, x, ws, s) : prologue_bwd_d<D, float>(p, x, ws, s);
   });
-  if (e != hipSuccess) return e;
-  const int64_t tiles = (p.BT + 63) / 64;
-  float* part = static_cast<float*>(ws);
-  const dim3 g2(unsigned((p.Hv + 63) / 64));
-  if (tiles) {
-    const dim3 grid(unsigned(tiles), unsigned(p.Hv));
-    if (p.bf16)
-      hipLaunchKernelGGL(gates_bwd<bf16_t>, grid, dim3(64), 0, s, static_cast<const bf16_t*>(x.a),
-                         static_cast<const bf16_t*>(x.b), x.a_log, x.dt_bias, static_cast<const bf16_t*>(x.dbeta),
-                         x.dlog_decay, static_cast<bf16_t*>(x.da), static_cast<bf16_t*>(x.db), part, p.BT, p.Hv);
-    else
-      hipLaunchKernelGGL(gates_bwd<float>, grid, dim3(64), 0, s, static_cast<const float*>(x.a),
-                         static_cast<const float*>(x.b), x.a_log, x.dt_bias, static_cast<const float*>(x.dbeta),
-                         x.dlog_decay, static_cast<float*>(x.da), static_cast<float*>(x.db), part, p.BT, p.Hv);
-  }
-  // (With no tokens, sums over no parts: zeros.)
-  hipLaunchKernelGGL(sum_parts, g2, dim3(256), 0, s, part, tiles, p.Hv * 2, 2, 0, p.Hv, x.da_log);
-  hipLaunchKernelGGL(sum_parts, g2, dim3(256), 0, s, part, tiles, p.Hv * 2, 2, 1, p.Hv, x.ddt_bias);
-  return hipGetLastError();
 }
 
 hipError_t nb_epilogue_fwd(const NbProblem& p, const NbEpilogue& x, hipStream_t s) {
-  return by_width(p.Dv, [&](auto ec) {
-    return p.bf16 ? gn_fwd_e<decltype(ec)::value, bf16_t>(p, x, s) : gn_fwd_e<decltype(ec)::value, float>(p, x, s);
+  return by_width(p.Dv, [&](auto dc) {
+    constexpr int D = decltype(dc)::value;
+    return p.bf16 ? epilogue_fwd_d<D, bf16_t>(p, x, s) : epilogue_fwd_d<D, float>(p, x, s);
   });
 }
 
 hipError_t nb_epilogue_bwd(const NbProblem& p, const NbEpilogueGrad& x, void* ws, hipStream_t s) {
-  return by_width(p.Dv, [&](auto ec) {
-    return p.bf16 ? gn_bwd_e<decltype(ec)::value, bf16_t>(p, x, ws, s)
-                  : gn_bwd_e<decltype(ec)::value, float>(p, x, ws, s);
+  return by_width(p.Dv, [&](auto dc) {
+    constexpr int D = decltype(dc)::value;
+    return p.bf16 ? epilogue_bwd_d<D, bf16_t>(p, x, ws, s) : epilogue_bwd_d<D, float>(p, x, ws, s);
   });
 }
 

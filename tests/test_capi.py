@@ -133,5 +133,5 @@ def test_neighbours_errors_before_any_gpu_work(lib):
         _lib.prologue_bwd(d, *([16] * 16), None, None)
     with pytest.raises(RuntimeError, match="eps must be positive"):
         _lib.epilogue_fwd(d, 16, 16, 16, 0.0, 16, None)
-    with pytest.raises(RuntimeError, match="y must be 2-byte aligned"):
+    with pytest.raises(RuntimeError, match="y must be 16-byte aligned"):
         _lib.epilogue_bwd(d, 17, 16, 16, 1e-6, 16, 16, 16, 16, 16, None)

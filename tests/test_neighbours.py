@@ -226,6 +226,7 @@ PROLOGUE_CASES = [  # (B, T, Hk, Hv, Dk, bf16)
     (1, 70, 2, 4, 64, False),
     (3, 37, 2, 6, 256, True),
     (1, 1, 16, 32, 128, True),
+    (1, 600, 16, 48, 128, True),  # several 256-token tiles of the gates' sums; 48 heads do not divide 256 threads
 ]
 
 
