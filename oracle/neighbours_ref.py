@@ -12,9 +12,10 @@ is rounded to bf16 where the reference's op rounds it, each op returning its inp
                                                            the activation dtype; the reference then takes exp)
   o = silu(z) * rms_norm(y, w, eps)                         :35-45, :122 (precise_swiglu: silu in float32 times the
                                                            normed y, rounded once to the activation dtype; the
-                                                           rms_norm is MLX 0.32.3's fast::rms_norm, which rounds
-                                                           the normalised row to the output dtype, then multiplies
-                                                           by the weight, taken here in the activation dtype)
+                                                           weight is float32, as the checkpoints store it (reference
+                                                           src/model.h:95; tests/tiny.h:53-55), so MLX 0.32.3's
+                                                           fast::rms_norm returns float32 and nothing rounds before
+                                                           the product)
 Backward: the exact adjoint in float64 of the same ops without the roundings (the GPU kernels compute it in
 float32 and round each output once).
 """
@@ -98,7 +99,7 @@ def prologue_bwd(q_raw, k_raw, a, b, a_log, dt_bias, dq, dk, dbeta, dlog_decay, 
 def epilogue_fwd(y, z, w, eps, *, bf16):
     """o = silu(z) * rms_norm(y, w, eps), as float64 holding the activation dtype's values."""
     y, z, w = (np.asarray(x, np.float64) for x in (y, z, w))
-    n = _rnd(w * _rnd(y * _rho(y, eps), bf16), bf16)
+    n = w * (y * _rho(y, eps))
     return _rnd(z * _sigmoid(z) * n, bf16)
 
 

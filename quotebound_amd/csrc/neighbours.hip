@@ -5,9 +5,9 @@
 //             recurrence takes itself when fed the log-decay)
 //   epilogue  o = silu(z) * rms_norm(y, w, eps)                       (:35-45, :122: the gated RMSNorm)
 // and their backward. With bf16 activations the forward rounds where the reference's ops do, each op's output
-// taking the activation dtype: rms_norm's normalised row, then its product with the scale; a + dt_bias, then its
-// softplus; the rms_norm's normalised row, then its product with the weight, then that with silu(z). Arithmetic
-// inside an op is float32. The backward is float32 throughout, with one rounding of each output; the parameter
+// taking its inputs' dtype: rms_norm's normalised row, then its product with the scale; a + dt_bias, then its
+// softplus; and o once (the gated rms_norm's weight is float32, so its output is float32 until the product with
+// silu(z) takes the activation dtype). Arithmetic inside an op is float32. The backward is float32 throughout, with one rounding of each output; the parameter
 // gradients (A_log, dt_bias per value head, w per column) are summed over tokens in a fixed order: per-block
 // partials, then one pass over the blocks in order.
 //
@@ -217,8 +217,8 @@ __global__ __launch_bounds__(256) void prologue_bwd_kernel(
 
 // ---- epilogue ----------------------------------------------------------------------------------------------------
 
-// The gated RMSNorm: o = rnd(silu(z) * rnd(w * rnd(y * rho))) (rms_norm normalises, takes the output dtype, then
-// multiplies by its weight).
+// The gated RMSNorm: o = rnd(silu(z) * (w * (y * rho))), float32 until the one rounding (the weight is float32, so
+// the rms_norm's output is; the product with silu(z) is taken in float32 and rounded once).
 template <typename T, int D>
 __global__ __launch_bounds__(256) void epilogue_fwd_kernel(const T* __restrict__ y, const T* __restrict__ z,
                                                            const float* __restrict__ w, float eps,
@@ -243,7 +243,7 @@ __global__ __launch_bounds__(256) void epilogue_fwd_kernel(const T* __restrict__
     const float rho = rsqrt_mean(group_sum<RL::L>(ss), D, eps);
 #pragma unroll
     for (int e = 0; e < kVec; ++e) {
-      const float n = rnd<T>(wl[e] * rnd<T>(x[j][e] * rho));
+      const float n = wl[e] * (x[j][e] * rho);
       x[j][e] = zz[j][e] * sigmoidf(zz[j][e]) * n;
     }
     if (live[j]) st8(o + off[j], x[j]);

@@ -1,0 +1,242 @@
+"""One LoRA training step on a Qwen3.5-architecture model (quotebound_amd/lora.py) against the CPU reference
+(oracle/lora_ref.py), and the reference pinned first.
+
+Pins of the CPU reference (on the CPU):
+  * its adapter gradient against central differences of its own loss in float64, along the gradient, three random
+    directions and the eight largest coordinates (the reference's own check, tests/test_train.cpp:99-181, there in
+    float32 at 1%);
+  * zero-b adapters leave the loss bit-identical (tests/test_train.cpp:82-99);
+  * its recurrence function (the oracle inside autograd) against torch.autograd.gradcheck in float64;
+  * rope: position 0 is the identity, and q.k depends only on the distance of the two positions; the model's and
+    the reference's restatements agree;
+  * the AdamW update against torch.optim.AdamW after torch.nn.utils.clip_grad_norm_, the same algorithm
+    (src/adamw.cpp:22-42 follows torch's).
+On the GPU, the step's loss and every adapter gradient against the reference run on the same weights and batch:
+  * a float32 model: the kernels' float32 path against the float32 reference, normwise (max|x - ref| / max|ref|)
+    1e-4 per gradient, 1e-5 relative on the loss;
+  * the LoRA workload (bf16 base, 8 layers, hidden 1024, batch 4 x 1024): bf16 activations against the float32
+    reference. The adapter gradients are sums over 4096 tokens of products of bf16-rounded cotangents and
+    activations, so bf16 rounding moves them far more than it moves the loss. The bar is that noise, measured: the
+    reference run in bf16 on the same inputs sets it. The GPU's whole-gradient relative error ||g - ref|| / ||ref||
+    must be at most 1.25 times the bf16 reference's, with a cosine of at least 0.98. The loss must agree to 1e-3
+    relative (the bf16 reference's loss is off by about 2e-3, the GPU's by about 3e-6: its low-rank path,
+    attention, convolution accumulations and recurrence state stay in float32).
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import normwise
+from oracle import lora_ref
+from quotebound_amd import lora
+
+TINY = lora.Config(hidden=64, layers=4, heads=2, kv_heads=1, head_dim=32, rope_dims=16, rope_theta=1e4,
+                   intermediate=128, vocab=97, lin_k_heads=2, lin_v_heads=4, lin_k_dim=32, lin_v_dim=32)
+
+
+def _tiny_case(dtype=torch.float64):
+    w = lora.init_weights(TINY, seed=3)
+    ads = lora.init_adapters(TINY, w, rank=4, alpha=8.0, seed=1, b_std=0.05)
+    tokens, positions, targets = lora.last_half_batch(2, 20, TINY.vocab, seed=5)
+    ads = lora.with_adapter_list(ads, [t.to(dtype) for t in lora.adapter_list(ads)])
+    return w, ads, tokens, positions, targets
+
+
+def test_reference_gradient_matches_finite_differences(oracle):
+    w, ads, tokens, positions, targets = _tiny_case()
+    loss, grads = lora_ref.loss_and_grads(w, ads, tokens, positions, targets, TINY, torch.float64)
+    p0 = lora.adapter_list(ads)
+
+    def loss_at(params):
+        return float(lora_ref.mean_loss(w, lora.with_adapter_list(ads, params), tokens, positions, targets, TINY,
+                                        torch.float64))
+
+    def along(d):
+        n = math.sqrt(sum(float((x * x).sum()) for x in d))
+        an = sum(float((g * x).sum()) for g, x in zip(grads, d)) / n
+        eps = 1e-6  # the error falls as eps^2 (curvature) down to float64 roundoff, about 1e-9 absolute here
+        plus = [p + x * (eps / n) for p, x in zip(p0, d)]
+        minus = [p - x * (eps / n) for p, x in zip(p0, d)]
+        return an, (loss_at(plus) - loss_at(minus)) / (2 * eps)
+
+    gen = torch.Generator().manual_seed(9)
+    dirs = [grads] + [[torch.randn(p.shape, generator=gen, dtype=torch.float64) for p in p0] for _ in range(3)]
+    flat = torch.cat([g.reshape(-1) for g in grads])
+    top = torch.argsort(flat.abs(), descending=True)[:8]
+    sizes = np.cumsum([0] + [g.numel() for g in grads])
+    for idx in top.tolist():
+        i = int(np.searchsorted(sizes, idx, side="right") - 1)
+        d = [torch.zeros_like(p) for p in p0]
+        d[i].view(-1)[idx - sizes[i]] = 1.0
+        dirs.append(d)
+    for d in dirs:
+        an, fd = along(d)
+        assert abs(fd - an) <= 1e-5 * abs(an) + 1e-8, (an, fd)
+    assert math.isfinite(float(loss)) and float(loss) > 0
+
+
+def test_zero_b_adapters_leave_the_loss(oracle):
+    w = lora.init_weights(TINY, seed=3)
+    tokens, positions, targets = lora.last_half_batch(2, 20, TINY.vocab, seed=5)
+    zero = lora.init_adapters(TINY, w, rank=4, alpha=8.0, seed=1)
+    none = {"scale": 1.0, "adapters": {}}
+    a = lora_ref.mean_loss(w, zero, tokens, positions, targets, TINY)
+    b = lora_ref.mean_loss(w, none, tokens, positions, targets, TINY)
+    assert torch.equal(a, b)
+
+
+def test_recurrence_function_gradcheck(oracle):
+    g = torch.Generator().manual_seed(2)
+    B, T, Hk, Hv, D = 1, 7, 1, 2, 4
+    q = torch.randn(B, T, Hk, D, generator=g, dtype=torch.float64) * 0.5
+    k = torch.nn.functional.normalize(torch.randn(B, T, Hk, D, generator=g, dtype=torch.float64), dim=-1)
+    v = torch.randn(B, T, Hv, D, generator=g, dtype=torch.float64)
+    ld = -torch.rand(B, T, Hv, generator=g, dtype=torch.float64)
+    beta = torch.rand(B, T, Hv, generator=g, dtype=torch.float64)
+    args = [t.requires_grad_(True) for t in (q, k, v, ld, beta)]
+    assert torch.autograd.gradcheck(lora_ref.Recurrence.apply, args, eps=1e-6, atol=1e-8, rtol=1e-6)
+
+
+def test_rope_closed_forms():
+    g = torch.Generator().manual_seed(4)
+    x = torch.randn(1, 2, 9, 16, generator=g, dtype=torch.float64)
+    y = torch.randn(1, 2, 9, 16, generator=g, dtype=torch.float64)
+    a, b = lora.rope(x, 8, 1e4), lora_ref._rope(x, 8, 1e4)
+    assert torch.allclose(a, b, rtol=0, atol=1e-12)
+    assert torch.equal(a[:, :, 0], x[:, :, 0])  # position 0 rotates by nothing
+    assert torch.equal(a[..., 8:], x[..., 8:])  # dims past rope_dims pass through
+    # The same pair of vectors placed at (t, s) and (t + 3, s + 3): equal dot products.
+    same = x[:, :, :1].expand(1, 2, 9, 16).contiguous()
+    other = y[:, :, :1].expand(1, 2, 9, 16).contiguous()
+    rq, rk = lora.rope(same, 8, 1e4), lora.rope(other, 8, 1e4)
+    d1 = (rq[:, :, 5] * rk[:, :, 2]).sum(-1)
+    d2 = (rq[:, :, 8] * rk[:, :, 5]).sum(-1)
+    assert torch.allclose(d1, d2, rtol=1e-12, atol=1e-12)
+
+
+def test_model_ops_match_library_ops_on_cpu():
+    """The model's hand-written conv, rms_norm and silu against torch's library ops, in float64 on the CPU."""
+    F = torch.nn.functional
+    g = torch.Generator().manual_seed(6)
+    x = torch.randn(2, 11, 24, generator=g, dtype=torch.float64)
+    w = torch.randn(24, 4, 1, generator=g, dtype=torch.float64)
+    ref = F.conv1d(F.pad(x.transpose(1, 2), (3, 0)), w.transpose(1, 2), groups=24).transpose(1, 2)
+    assert torch.allclose(lora.causal_conv(x, w), ref, rtol=1e-12, atol=1e-12)
+    nw = torch.randn(24, generator=g, dtype=torch.float64)
+    assert torch.allclose(lora.rms_norm(x, nw, 1e-6), F.rms_norm(x, (24,), weight=nw, eps=1e-6), rtol=1e-12, atol=0)
+    assert torch.allclose(lora.silu(x), F.silu(x), rtol=1e-15, atol=0)
+
+
+def test_adamw_matches_torch():
+    g = torch.Generator().manual_seed(8)
+    params = [torch.randn(5, 3, generator=g), torch.randn(7, generator=g)]
+    opt = lora.AdamW(lr=1e-2, weight_decay=0.1, clip=1.0)
+    state = opt.init(params)
+    tparams = [p.clone().requires_grad_(True) for p in params]
+    topt = torch.optim.AdamW(tparams, lr=1e-2, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.1)
+    ours = params
+    for step in range(3):
+        grads = [torch.randn(p.shape, generator=g) * (3.0 if step == 0 else 0.1) for p in params]
+        norm = torch.sqrt(sum((x * x).sum() for x in grads))
+        ours = opt.update(ours, grads, norm, state)
+        for tp, gr in zip(tparams, grads):
+            tp.grad = gr.clone()
+        torch.nn.utils.clip_grad_norm_(tparams, 1.0)
+        topt.step()
+        for a, b in zip(ours, tparams):
+            assert torch.allclose(a, b.detach(), rtol=1e-6, atol=1e-7)
+
+
+def test_adapter_layout():
+    cfg = lora.Config()
+    w = {n: torch.empty(t.shape) for n, t in lora.init_weights(lora.Config(layers=4, vocab=16), seed=1).items()}
+    ads = lora.init_adapters(lora.Config(layers=4, vocab=16), w)
+    names = list(ads["adapters"])
+    assert names[:2] == ["model.layers.0.linear_attn.in_proj_qkv", "model.layers.0.linear_attn.out_proj"]
+    assert "model.layers.3.self_attn.q_proj" in names and "model.layers.3.mlp.gate_proj" not in names
+    a, b = ads["adapters"]["model.layers.3.self_attn.q_proj"]
+    assert a.shape == (16, 1024) and b.shape == (2 * cfg.heads * cfg.head_dim, 16) and not b.any()
+    assert ads["scale"] == 2.0
+    assert [cfg.is_linear(i) for i in range(8)] == [True, True, True, False, True, True, True, False]
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# On the GPU
+
+SMALL = lora.Config(hidden=256, layers=4, heads=2, kv_heads=1, head_dim=128, rope_dims=32, intermediate=512,
+                    vocab=1000, lin_k_heads=2, lin_v_heads=4, lin_k_dim=128, lin_v_dim=128)
+
+
+@pytest.fixture(scope="module")
+def dev():
+    if not torch.cuda.is_available():
+        pytest.skip("needs a GPU")
+    from quotebound_amd import _lib
+
+    _lib.load()  # raises when the library is missing: there is no fallback
+    return torch
+
+
+def _rel(g, r):
+    gv = torch.cat([x.detach().cpu().reshape(-1).double() for x in g])
+    rv = torch.cat([x.reshape(-1).double() for x in r])
+    return float((gv - rv).norm() / rv.norm()), float(gv @ rv / (gv.norm() * rv.norm()))
+
+
+def _compare(cfg, dtype, batch, seq, seed, bf16_floor=False):
+    w = lora.init_weights(cfg, seed=seed)
+    ads = lora.init_adapters(cfg, w, seed=seed + 1, b_std=0.05)
+    tokens, positions, targets = lora.last_half_batch(batch, seq, cfg.vocab, seed=seed + 2)
+    wd = lora.to_device(w, "cuda", dtype)
+    loss, grads, norm = lora.loss_and_grads(wd, lora.adapters_to(ads, "cuda"), tokens.cuda(), positions.cuda(),
+                                            targets.cuda(), cfg)
+    torch.cuda.synchronize()
+    rloss, rgrads = lora_ref.loss_and_grads(w, ads, tokens, positions, targets, cfg, torch.float32)
+    names = [f"{n}.{ab}" for n in ads["adapters"] for ab in ("a", "b")]
+    errs = {n: normwise(g.cpu().numpy(), r.numpy()) for n, g, r in zip(names, grads, rgrads)}
+    rel, cos = _rel(grads, rgrads)
+    lrel = abs(float(loss) - float(rloss)) / abs(float(rloss))
+    worst = max(errs, key=errs.get)
+    print(f"loss {float(loss):.6f} vs {float(rloss):.6f} (rel {lrel:.2e}); worst gradient {worst} {errs[worst]:.2e}; "
+          f"whole gradient rel {rel:.3e}, cosine {cos:.6f}; norm {float(norm):.4e}")
+    floor = None
+    if bf16_floor:
+        bloss, bgrads = lora_ref.loss_and_grads(w, ads, tokens, positions, targets, cfg, torch.bfloat16)
+        floor = _rel([g.float() for g in bgrads], rgrads)
+        print(f"bf16 reference: loss {float(bloss):.6f}; whole gradient rel {floor[0]:.3e}, cosine {floor[1]:.6f}")
+    return lrel, errs, rel, cos, floor
+
+
+@pytest.mark.gpu
+def test_lora_step_float32_small(dev, oracle):
+    lrel, errs, rel, cos, _ = _compare(SMALL, torch.float32, 2, 128, seed=21)
+    assert lrel <= 1e-5
+    assert max(errs.values()) <= 1e-4, errs
+
+
+@pytest.mark.gpu
+def test_lora_step_workload_bf16(dev, oracle):
+    """The LoRA workload: the default Config, bf16 base, 4 sequences of 1024 tokens, loss on the last half."""
+    lrel, errs, rel, cos, floor = _compare(lora.Config(), torch.bfloat16, 4, 1024, seed=31, bf16_floor=True)
+    assert lrel <= 1e-3
+    assert rel <= 1.25 * floor[0], (rel, floor)
+    assert cos >= 0.98
+
+
+@pytest.mark.gpu
+def test_train_step_runs_and_moves_the_adapters(dev):
+    cfg = SMALL
+    w = lora.to_device(lora.init_weights(cfg, seed=41), "cuda", torch.bfloat16)
+    ads = lora.adapters_to(lora.init_adapters(cfg, lora.init_weights(cfg, seed=41), seed=42), "cuda")
+    tokens, positions, targets = (t.cuda() for t in lora.last_half_batch(2, 128, cfg.vocab, seed=43))
+    opt = lora.AdamW(lr=1e-3)
+    state = opt.init(lora.adapter_list(ads))
+    loss0, norm, ads1 = lora.train_step(w, ads, opt, state, tokens, positions, targets, cfg)
+    loss1, _, _ = lora.train_step(w, ads1, opt, state, tokens, positions, targets, cfg)
+    torch.cuda.synchronize()
+    assert math.isfinite(float(loss0)) and math.isfinite(float(loss1)) and float(norm) > 0
+    moved = [not torch.equal(a, b) for a, b in zip(lora.adapter_list(ads), lora.adapter_list(ads1))]
+    assert all(moved[1::2])  # every b moves off zero on the first step
+    assert float(loss1) < float(loss0)
