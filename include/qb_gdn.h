@@ -97,6 +97,15 @@ int qb_gdn_fwd(const qb_gdn_desc* desc, const void* q, const void* k, const void
                const float* s0, void* y, float* s_out, float* ckpt, void* workspace, void* stream, char* err,
                int errlen);
 
+/* Forward that also keeps the state after every token, for decoding that may roll back (exact drafts): replaces
+ * the reference's rows pass, one gated_delta call per token keeping each step's state (src/deltanet.cpp:101-117;
+ * RowStates, src/model.h:80-86; keep_rows, src/exact.cpp:152-162). row_states [tokens, Hv, Dv, Dk] float32, where
+ * tokens is B*T (or the packed total): entry t is the state after token t. Always runs the recurrent design, whatever
+ * desc->design says (the shape must suit it: Dk of 32, 64 or 128), so no ckpt or workspace is taken. */
+int qb_gdn_fwd_rows(const qb_gdn_desc* desc, const void* q, const void* k, const void* v, const float* g,
+                    const void* beta, const float* s0, void* y, float* row_states, void* stream, char* err,
+                    int errlen);
+
 /* Backward from the forward's ckpt: the cotangents of (q, k, v, g, beta, s0) given dy and ds_out (the cotangent of
  * the final state; NULL is zero). ds0 may be NULL. Deterministic: sums run in a fixed order, no atomics. */
 int qb_gdn_bwd(const qb_gdn_desc* desc, const void* q, const void* k, const void* v, const float* g,

@@ -63,6 +63,8 @@ def load():
     L.qb_gdn_launches.restype = ctypes.c_int
     L.qb_gdn_fwd.argtypes = [D] + [P] * 11 + [ctypes.c_char_p, ctypes.c_int]
     L.qb_gdn_fwd.restype = ctypes.c_int
+    L.qb_gdn_fwd_rows.argtypes = [D] + [P] * 9 + [ctypes.c_char_p, ctypes.c_int]
+    L.qb_gdn_fwd_rows.restype = ctypes.c_int
     L.qb_gdn_bwd.argtypes = [D] + [P] * 16 + [ctypes.c_char_p, ctypes.c_int]
     L.qb_gdn_bwd.restype = ctypes.c_int
     L.qb_gdn_neighbours_workspace_bytes.argtypes = [D]
@@ -129,6 +131,11 @@ def ckpt_bytes(desc) -> int:
 
 def workspace_bytes(desc) -> int:
     return int(load().qb_gdn_workspace_bytes(ctypes.byref(desc)))
+
+
+def fwd_rows(desc, q, k, v, g, beta, s0, y, row_states, stream) -> None:
+    """The forward keeping the state after every token (always the recurrent design)."""
+    _call(load().qb_gdn_fwd_rows, desc, q, k, v, g, beta, s0, y, row_states, stream)
 
 
 def fwd(desc, q, k, v, g, beta, s0, y, s_out, ckpt, workspace, stream) -> None:

@@ -112,6 +112,22 @@ std::string check_ptr(const char* name, const void* ptr, bool required, size_t a
   return {};
 }
 
+struct PtrCheck {
+  const char* name;
+  const void* ptr;
+  bool req;
+  size_t align;
+};
+
+template <size_t N>
+std::string check_all(const PtrCheck (&c)[N]) {
+  for (const auto& x : c) {
+    std::string why = check_ptr(x.name, x.ptr, x.req, x.align);
+    if (!why.empty()) return why;
+  }
+  return {};
+}
+
 size_t ckpt_bytes(const qb_gdn_desc* d, const Problem& p) {
   return d->design == QB_GDN_RECURRENT ? qbgdn::rec_ckpt_bytes(p) : qbgdn::chunk_ckpt_bytes(p);
 }
@@ -234,6 +250,41 @@ int qb_gdn_fwd(const qb_gdn_desc* desc, const void* q, const void* k, const void
   });
 }
 
+int qb_gdn_fwd_rows(const qb_gdn_desc* desc, const void* q, const void* k, const void* v, const float* g,
+                    const void* beta, const float* s0, void* y, float* row_states, void* stream, char* err,
+                    int errlen) {
+  return guarded(err, errlen, [&] {
+    if (!desc) {
+      set_err(err, errlen, "gated delta: null descriptor");
+      return -1;
+    }
+    qb_gdn_desc d = *desc;
+    d.design = QB_GDN_RECURRENT;
+    Problem p;
+    std::string why = resolve(&d, p);
+    const size_t el = p.in_bf16 ? 2 : 4, eo = p.out_bf16 ? 2 : 4;
+    const bool any = why.empty() && p.BT > 0;
+    const PtrCheck c[] = {{"q", q, any, 16},       {"k", k, any, 16},     {"v", v, any, el},
+                          {"g", g, any, 4},        {"beta", beta, any, el}, {"s0", s0, false, 4},
+                          {"y", y, any, eo},       {"row_states", row_states, any, 16}};
+    if (why.empty()) why = check_all(c);
+    if (!why.empty()) {
+      set_err(err, errlen, why);
+      return -1;
+    }
+    qbgdn::FwdPtrs a{q, k, v, g, beta, s0, y, nullptr, nullptr};
+    a.rows = row_states;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    qbgdn::Tracer tr = tracer_of(&d, s);
+    const hipError_t e = qbgdn::rec_fwd(p, a, nullptr, s, tr);
+    if (e != hipSuccess) {
+      set_err(err, errlen, hip_fail("forward launch", e));
+      return -1;
+    }
+    return 0;
+  });
+}
+
 int qb_gdn_bwd(const qb_gdn_desc* desc, const void* q, const void* k, const void* v, const float* g,
                const void* beta, const float* ckpt, const void* dy, const float* ds_out, void* dq, void* dk, void* dv,
                float* dg, void* dbeta, float* ds0, void* workspace, void* stream, char* err, int errlen) {
@@ -307,22 +358,6 @@ std::string nb_resolve(const qb_gdn_desc* d, qbgdn::NbProblem& p) {
   p.scale_q = float(inv * inv), p.scale_k = float(inv);
   if (p.bf16) p.scale_q = round_bf16_host(p.scale_q), p.scale_k = round_bf16_host(p.scale_k);
   if (const char* why = qbgdn::nb_supports(p)) return std::string("gated delta neighbours: ") + why + " " + sh;
-  return {};
-}
-
-struct PtrCheck {
-  const char* name;
-  const void* ptr;
-  bool req;
-  size_t align;
-};
-
-template <size_t N>
-std::string check_all(const PtrCheck (&c)[N]) {
-  for (const auto& x : c) {
-    std::string why = check_ptr(x.name, x.ptr, x.req, x.align);
-    if (!why.empty()) return why;
-  }
   return {};
 }
 

@@ -31,6 +31,7 @@ struct FwdPtrs {
   void* y;
   float* s_out;
   float* ckpt;
+  float* rows = nullptr;  // the state after every token [tokens, Hv, Dv, Dk] (recurrent design only); may be null
 };
 
 // Backward pointers (device). ds_out, ds0 may be null.

@@ -154,6 +154,11 @@ __global__ __launch_bounds__(kThreads) void rec_fwd_kernel(RecFwdArgs a) {
 #pragma unroll
       for (int i = 0; i < NPT; ++i) s[i] = gt * s[i] + d * kk[i];
       if (cl == 0) Ys[tt][rl] = yv;
+      if (a.p.rows && live) {  // the state after this token
+        float* dst = a.p.rows + ((tok + tt) * a.Hv + hv) * SS + int64_t(row) * Dk + cl * NPT;
+#pragma unroll
+        for (int i = 0; i < NPT; ++i) dst[i] = s[i];
+      }
     }
     __syncthreads();
     for (int e = tid; e < L * kRows; e += kThreads) {

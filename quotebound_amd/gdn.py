@@ -114,6 +114,25 @@ def backward(q, k, v, g, beta, ckpt, dy, ds_out=None, *, log_decay=False, design
     return dq, dk, dv, dg, dbeta, ds0
 
 
+def forward_rows(q, k, v, g, beta, state=None, *, log_decay=False, cu_seqlens=None):
+    """(y, row_states): the forward keeping the state after every token, row_states [B, T, Hv, Dv, Dk] float32 (or
+    [total, Hv, Dv, Dk] packed) — the reference's rows pass for exact drafts (src/deltanet.cpp:101-117), whose
+    decoder rolls back to any row's state (src/exact.cpp:152-162). Runs the recurrent design."""
+    dtype = _io_dtype(q, k, v, beta)
+    q, k, v, g, beta = _prep(q, k, v, g, beta, dtype)
+    desc, keep = _desc(q, v, dtype, log_decay, _lib.RECURRENT, cu_seqlens, False)
+    B, T, Hv, Dv = v.shape
+    y = torch.empty(v.shape, dtype=dtype, device=v.device)
+    rows = torch.empty((B, T, Hv, Dv, q.shape[-1]), dtype=torch.float32, device=v.device)
+    s0 = None if state is None else state.to(torch.float32).contiguous()
+    _lib.fwd_rows(desc, _dev_ptr(q), _dev_ptr(k), _dev_ptr(v), _dev_ptr(g), _dev_ptr(beta), _dev_ptr(s0),
+                  _dev_ptr(y), _dev_ptr(rows), _stream(q.device))
+    del keep
+    if cu_seqlens is not None:
+        rows = rows.view(B * T, Hv, Dv, q.shape[-1])
+    return y, rows
+
+
 class _GatedDelta(torch.autograd.Function):
     """custom_vjp of the recurrence: the forward keeps the chunk-start states, the backward is gated_delta_vjp
     (reference src/delta_grad.cpp:204-211, which saves only the primals and rebuilds the states instead)."""

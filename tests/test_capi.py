@@ -135,3 +135,13 @@ def test_neighbours_errors_before_any_gpu_work(lib):
         _lib.epilogue_fwd(d, 16, 16, 16, 0.0, 16, None)
     with pytest.raises(RuntimeError, match="y must be 16-byte aligned"):
         _lib.epilogue_bwd(d, 17, 16, 16, 1e-6, 16, 16, 16, 16, 16, None)
+
+
+def test_fwd_rows_errors_before_any_gpu_work(lib):
+    d, _ = desc(Dk=256, Dv=64, design=_lib.CHUNKED)
+    with pytest.raises(RuntimeError, match="Dk"):
+        _lib.fwd_rows(d, 16, 16, 16, 16, 16, None, 16, 16, None)
+    d, _ = desc()
+    with pytest.raises(RuntimeError, match="row_states is null"):
+        _lib.fwd_rows(d, 16, 16, 16, 16, 16, None, 16, None, None)
+

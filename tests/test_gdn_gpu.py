@@ -226,6 +226,46 @@ def test_decode_steps_carry_the_state(torch_dev, oracle, design):
                  label=f"decode vs oracle, design {design}")
 
 
+@pytest.mark.parametrize("packed", [False, True], ids=["batch", "packed"])
+def test_row_states(torch_dev, oracle, packed):
+    """qb_gdn_fwd_rows keeps the state after every token (the reference's rows pass for exact drafts,
+    src/deltanet.cpp:101-117; keep_rows rolls back to one, src/exact.cpp:152-162): each row equals the oracle's state
+    after that token (its checkpoints at stride 1, shifted by one, then its final state), y and the last row equal
+    the plain forward's bit for bit, and one-token calls chained from a row's state reach the next rows' states."""
+    torch = torch_dev
+    from quotebound_amd import gdn
+    from quotebound_amd.synthetic import Workload, make_inputs, to_device
+
+    w = Workload("rows", 2, 37, 2, 4, 64, 64, seed=29, s0_std=0.02)
+    inp = make_inputs(w)
+    f = inp.f32
+    cu = [0, 37, 74] if packed else None
+    shape = lambda x: x.reshape(1, 74, *x.shape[2:]) if packed else x  # noqa: E731
+    q, k, v, g, beta = (shape(f[n]) for n in ("q", "k", "v", "g", "beta"))
+    y_ref, s_ref, ck = oracle.fwd(q, k, v, g, beta, f["s0"], chunk=1, cu_seqlens=cu, dtype=np.float32)
+    d = {n: (t.reshape(1, 74, *t.shape[2:]) if packed and n != "s0" else t) for n, t in to_device(inp).items()
+         if t is not None}
+    y, rows = gdn.forward_rows(d["q"], d["k"], d["v"], d["g"], d["beta"], d["s0"], log_decay=True, cu_seqlens=cu)
+    y1, s1, _ = gdn.forward(d["q"], d["k"], d["v"], d["g"], d["beta"], d["s0"], log_decay=True,
+                            design=_lib.RECURRENT, cu_seqlens=cu, save_ckpt=False)
+    torch.cuda.synchronize()
+    rows = rows.reshape(2, 37, *rows.shape[-3:]).cpu().numpy()
+    ck = np.asarray(ck).reshape(2, 37, *ck.shape[-3:])  # state before each token, per sequence
+    s_ref = np.asarray(s_ref)
+    for b in range(2):
+        want = np.concatenate([ck[b, 1:], s_ref[b][None]], 0)
+        assert normwise(rows[b], want) <= F32_TOL, b
+        assert np.array_equal(rows[b, -1], s1[b].cpu().numpy())
+    assert torch.equal(y, y1)
+    # Roll back to row 20 of the first sequence and step one token at a time from there.
+    state = torch.tensor(rows[0, 20][None]).cuda()
+    for t in range(21, 25):
+        sl = slice(t, t + 1)
+        _, state, _ = gdn.forward(d["q"][:1, sl], d["k"][:1, sl], d["v"][:1, sl], d["g"][:1, sl],
+                                  d["beta"][:1, sl], state, log_decay=True, design=_lib.RECURRENT, save_ckpt=False)
+        assert np.array_equal(state[0].cpu().numpy(), rows[0, t]), t
+
+
 @pytest.mark.parametrize("design", DESIGNS, ids=DESIGN_IDS.get)
 def test_deterministic(torch_dev, design):
     """Same inputs, same bits: every sum runs in a fixed order (the reference's resume bit-identity relies on it,
