@@ -8,7 +8,7 @@ divided by its mean duration. cpu_baseline times the oracle (the CPU restatement
 the same inputs.
 
 python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--design auto|1|2] [--workload qwen35_4b] [--no-cpu]
-                [--copy-probe-mib N]
+                [--copy-probe-mib N] [--path-only]
 
 roofline.traffic is the dominant kernel's HBM bytes per launch as rocprofv3 counted them (FETCH_SIZE + WRITE_SIZE,
 each scaled by what the counter reads for a plain device copy of known size), read from profiles/traffic.json
@@ -345,6 +345,9 @@ def main():
     ap.add_argument("--workload", default="qwen35_4b")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-probe-mib", type=int, default=0)
+    ap.add_argument("--path-only", action="store_true",
+                    help="skip the legs outside the headline step (decode, neighbours, LoRA step), as profiler "
+                         "counter passes need")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported (the recurrence shards "
@@ -409,13 +412,14 @@ def main():
         "designs": {k: ({kk: vv for kk, vv in v.items() if kk != "nc"} if "ms_per_step" in v else v)
                     for k, v in results.items()},
     }
-    out["decode"] = {"unit": "us per one-token call (state carried, host clock, launch included)",
-                     "config": f"B={w.B} Hk={w.Hk} Hv={w.Hv} Dk={w.Dk} Dv={w.Dv}, {w.dtype} I/O, fp32 state"}
-    for d in designs:
-        name = {lib.RECURRENT: "recurrent", lib.CHUNKED: "chunked"}[d]
-        out["decode"][name] = run_decode(torch, lib, w, d)
-    out["neighbours"] = run_neighbours(torch, lib, w)
-    out["lora_step"] = run_lora_step(torch)
+    if not args.path_only:
+        out["decode"] = {"unit": "us per one-token call (state carried, host clock, launch included)",
+                         "config": f"B={w.B} Hk={w.Hk} Hv={w.Hv} Dk={w.Dk} Dv={w.Dv}, {w.dtype} I/O, fp32 state"}
+        for d in designs:
+            name = {lib.RECURRENT: "recurrent", lib.CHUNKED: "chunked"}[d]
+            out["decode"][name] = run_decode(torch, lib, w, d)
+        out["neighbours"] = run_neighbours(torch, lib, w)
+        out["lora_step"] = run_lora_step(torch)
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(w, inp)
     print(json.dumps(out))

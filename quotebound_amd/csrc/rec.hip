@@ -88,7 +88,8 @@ __device__ __forceinline__ void stage_scalars(float* Gs, float* Bs, const float*
   }
 }
 
-template <int NPT, typename InT, typename OutT>
+// kKeepRows: also store the state after every token (a.p.rows), for the per-token-state forward.
+template <int NPT, typename InT, typename OutT, bool kKeepRows>
 __global__ __launch_bounds__(kThreads) void rec_fwd_kernel(RecFwdArgs a) {
   constexpr int Dk = 16 * NPT;
   __shared__ float Ks[kChunk][Dk];
@@ -154,7 +155,7 @@ __global__ __launch_bounds__(kThreads) void rec_fwd_kernel(RecFwdArgs a) {
 #pragma unroll
       for (int i = 0; i < NPT; ++i) s[i] = gt * s[i] + d * kk[i];
       if (cl == 0) Ys[tt][rl] = yv;
-      if (a.p.rows && live) {  // the state after this token
+      if (kKeepRows && live) {  // the state after this token
         float* dst = a.p.rows + ((tok + tt) * a.Hv + hv) * SS + int64_t(row) * Dk + cl * NPT;
 #pragma unroll
         for (int i = 0; i < NPT; ++i) dst[i] = s[i];
@@ -416,10 +417,20 @@ hipError_t launch_fwd(const Problem& p, const FwdPtrs& ptrs, hipStream_t s, Trac
   a.tab = p.tab;
   const dim3 grid(a.total), block(kThreads);
   tr.mark();
+  const bool rows = ptrs.rows != nullptr;
   switch (p.Dk) {
-    case 32: hipLaunchKernelGGL((rec_fwd_kernel<2, InT, OutT>), grid, block, 0, s, a); break;
-    case 64: hipLaunchKernelGGL((rec_fwd_kernel<4, InT, OutT>), grid, block, 0, s, a); break;
-    case 128: hipLaunchKernelGGL((rec_fwd_kernel<8, InT, OutT>), grid, block, 0, s, a); break;
+    case 32:
+      if (rows) hipLaunchKernelGGL((rec_fwd_kernel<2, InT, OutT, true>), grid, block, 0, s, a);
+      else hipLaunchKernelGGL((rec_fwd_kernel<2, InT, OutT, false>), grid, block, 0, s, a);
+      break;
+    case 64:
+      if (rows) hipLaunchKernelGGL((rec_fwd_kernel<4, InT, OutT, true>), grid, block, 0, s, a);
+      else hipLaunchKernelGGL((rec_fwd_kernel<4, InT, OutT, false>), grid, block, 0, s, a);
+      break;
+    case 128:
+      if (rows) hipLaunchKernelGGL((rec_fwd_kernel<8, InT, OutT, true>), grid, block, 0, s, a);
+      else hipLaunchKernelGGL((rec_fwd_kernel<8, InT, OutT, false>), grid, block, 0, s, a);
+      break;
     default: return hipErrorInvalidValue;
   }
   tr.mark();
