@@ -89,6 +89,10 @@ std::string resolve(const qb_gdn_desc* d, Problem& p) {
     }
     p.tab.tok0[d->n_seqs] = cu[d->n_seqs];
     p.tab.slot0[d->n_seqs] = int32_t(slots);
+    int order[QB_GDN_MAX_SEQS];
+    for (int i = 0; i < d->n_seqs; ++i) order[i] = i;
+    std::stable_sort(order, order + d->n_seqs, [&](int x, int y) { return cu[x + 1] - cu[x] > cu[y + 1] - cu[y]; });
+    for (int i = 0; i < d->n_seqs; ++i) p.tab.longest[i] = uint8_t(order[i]);
     p.N = d->n_seqs;
     p.NC = slots;
   } else {

@@ -44,8 +44,8 @@ __global__ __launch_bounds__(kThreads) void chunk_fwd_kernel(ChunkArgs a) {
   __shared__ __align__(16) float Gs[2][256];             // exp G [64], D [64] (the rest padding)
 
   const int total = a.nblk * a.Hv * a.N;
-  const int wid = xcd_remap(blockIdx.x, total);
-  const int blk = wid % a.nblk, hv = (wid / a.nblk) % a.Hv, n = wid / (a.nblk * a.Hv);
+  const StateItem item = state_item(a.tab, blockIdx.x, a.nblk, a.Hv, a.Hk, total);
+  const int blk = item.blk, hv = item.hv, n = item.n;
   const int hk = hv / (a.Hv / a.Hk), row0 = 16 * blk;
   const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, li = lane & 15;
   // The wave index, made visibly uniform so that its branches are scalar and buffer resources stay in scalar

@@ -139,6 +139,7 @@ struct SeqTable {
   int32_t nc;
   int32_t tok0[kMaxSeqs + 1];
   int32_t slot0[kMaxSeqs + 1];
+  uint8_t longest[kMaxSeqs];  // n > 0: the sequences by decreasing length (ties by index)
 };
 
 struct Seq {
@@ -150,6 +151,34 @@ struct Seq {
 __device__ __forceinline__ Seq seq_of(const SeqTable& tab, int i) {
   if (tab.n == 0) return Seq{int64_t(i) * tab.T, tab.T, int64_t(i) * tab.nc};
   return Seq{tab.tok0[i], tab.tok0[i + 1] - tab.tok0[i], tab.slot0[i]};
+}
+
+// The work item of block `id` in the passes that walk a sequence's chunks in order (the state passes, the
+// recurrent design): row block `blk` of value head `hv` of sequence `n`, among total = nblk * Hv * N items. The
+// items of one (sequence, key head) form a group of G = nblk * (Hv / Hk) blocks reading the same q and k rows.
+// Batch mode: XCD x takes a contiguous range of items (xcd_remap), so groups stay on one XCD. Packed mode: the
+// groups, longest sequence first, are dealt to the XCDs in turn, every block of a group on one XCD (blocks id,
+// id + 8, id + 16, ... run on XCD id % 8). Long sequences start first and every XCD gets its share of each length,
+// where a contiguous range would give one XCD the longest sequence's every item. A bijection on [0, total).
+struct StateItem {
+  int blk, hv, n;
+};
+__device__ __forceinline__ StateItem state_item(const SeqTable& tab, int id, int nblk, int Hv, int Hk, int total) {
+  if (tab.n == 0) {
+    const int w = xcd_remap(id, total);
+    return StateItem{w % nblk, (w / nblk) % Hv, w / (nblk * Hv)};
+  }
+  const int per_hk = Hv / Hk, G = nblk * per_hk, ngroups = total / G, full = ngroups >> 3;
+  int rank, j;  // the group's place in the order, the item within the group
+  const int sb = id / (8 * G);
+  if (sb < full) {  // 8 whole groups, group 8 sb + x on XCD x
+    const int t = id - sb * 8 * G;
+    rank = 8 * sb + (t & 7), j = t >> 3;
+  } else {  // the last 1..7 groups
+    const int rest = ngroups - 8 * full, t = id - full * 8 * G;
+    rank = 8 * full + t % rest, j = t / rest;
+  }
+  return StateItem{j % nblk, (rank % Hk) * per_hk + j / nblk, int(tab.longest[rank / Hk])};
 }
 
 }  // namespace qbgdn

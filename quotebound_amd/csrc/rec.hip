@@ -42,13 +42,13 @@ struct RecBwdArgs {
   SeqTable tab;
 };
 
-// Work item -> (row block, value head, sequence), row block fastest, placed by xcd_remap.
+// Work item -> (row block, value head, sequence), placed by state_item.
 struct Item {
   int blk, hv, n;
 };
-__device__ __forceinline__ Item item_of(int nblk, int Hv, int total) {
-  const int w = xcd_remap(blockIdx.x, total);
-  return Item{w % nblk, (w / nblk) % Hv, w / (nblk * Hv)};
+__device__ __forceinline__ Item item_of(const SeqTable& tab, int nblk, int Hv, int Hk, int total) {
+  const StateItem it = state_item(tab, blockIdx.x, nblk, Hv, Hk, total);
+  return Item{it.blk, it.hv, it.n};
 }
 
 // Stages rows [t0, t0 + L) of the key head's k and q into LDS as float32, 8 elements per access.
@@ -98,7 +98,7 @@ __global__ __launch_bounds__(kThreads) void rec_fwd_kernel(RecFwdArgs a) {
   __shared__ float Ys[kChunk][kRows];
   __shared__ float Gs[kChunk], Bs[kChunk], KQs[kChunk];
 
-  const Item it = item_of(a.nblk, a.Hv, a.total);
+  const Item it = item_of(a.tab, a.nblk, a.Hv, a.Hk, a.total);
   const int tid = threadIdx.x, lane = tid & 63;
   const int cl = lane & 15, rl = (tid >> 6) * 4 + (lane >> 4);
   const int row0 = it.blk * kRows, row = row0 + rl;
@@ -217,7 +217,7 @@ __global__ __launch_bounds__(kThreads) void rec_bwd_kernel(RecBwdArgs a) {
   __shared__ float red[kSub][kWaves][2 * Dk];  // per step and wave: column sums of (dq | dk) over the wave's rows
   __shared__ float rowv[kSub][3][kRows];       // per step and row: dv, dbeta, dg (factor)
 
-  const Item it = item_of(a.nblk, a.Hv, a.total);
+  const Item it = item_of(a.tab, a.nblk, a.Hv, a.Hk, a.total);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int cl = lane & 15, rl = wave * 4 + (lane >> 4);
   const int row0 = it.blk * kRows, row = row0 + rl;
