@@ -267,6 +267,49 @@ def test_row_states(torch_dev, oracle, packed):
 
 
 @pytest.mark.parametrize("design", DESIGNS, ids=DESIGN_IDS.get)
+@pytest.mark.parametrize("case", ["empty_sequences", "max_sequences"])
+def test_packed_edge_cases(torch_dev, oracle, design, case):
+    """Packed batches at the edges: empty sequences among others (their final state is S0 and their dS0 is the
+    final state's cotangent), and the maximum of 255 sequences of 0 to 40 tokens, every output against the oracle."""
+    torch = torch_dev
+    from quotebound_amd.synthetic import Workload, make_inputs, to_device
+
+    if case == "empty_sequences":
+        lens = [5, 64, 0, 130, 1, 0, 63]
+    else:
+        lens = np.random.default_rng(7).integers(0, 41, _lib.MAX_SEQS).tolist()
+    w = Workload(case, 1, int(sum(lens)), 2, 4, 128, 128, seed=31, s0_std=0.02, ds_out=True, seq_lens=lens)
+    inp = make_inputs(w)
+    exp = oracle.fwd_bwd(inp.f32, cu_seqlens=w.cu_seqlens, dtype=np.float32)
+    d = to_device(inp)
+    got = run(torch, dict(d, dy=d["dy"].float()), design, cu=w.cu_seqlens, out_f32=True)
+    assert_close(got, exp, BF16_TOL, label=f"{case} design {design}")
+    for i, n in enumerate(lens):
+        if n == 0:
+            assert np.array_equal(got["s_out"][i], inp.f32["s0"][i])
+            assert np.array_equal(got["ds0"][i], inp.f32["ds_out"][i])
+
+
+@pytest.mark.parametrize("design", DESIGNS, ids=DESIGN_IDS.get)
+def test_empty_batch(torch_dev, design):
+    """T = 0: nothing to compute; the final state is S0 and dS0 is the final state's cotangent."""
+    torch = torch_dev
+    from quotebound_amd import gdn
+
+    B, Hk, Hv, D = 2, 2, 4, 128
+    e = lambda *s: torch.empty(*s, dtype=torch.bfloat16, device="cuda")  # noqa: E731
+    q, k, v, beta, dy = e(B, 0, Hk, D), e(B, 0, Hk, D), e(B, 0, Hv, D), e(B, 0, Hv), e(B, 0, Hv, D)
+    g = torch.empty(B, 0, Hv, device="cuda")
+    s0 = torch.randn(B, Hv, D, D, device="cuda")
+    ds_out = torch.randn(B, Hv, D, D, device="cuda")
+    y, s_out, ckpt = gdn.forward(q, k, v, g, beta, s0, log_decay=True, design=design)
+    grads = gdn.backward(q, k, v, g, beta, ckpt, dy, ds_out, log_decay=True, design=design)
+    torch.cuda.synchronize()
+    assert y.shape == v.shape and torch.equal(s_out, s0)
+    assert torch.equal(grads[5], ds_out) and all(t.numel() == 0 for t in grads[:5])
+
+
+@pytest.mark.parametrize("design", DESIGNS, ids=DESIGN_IDS.get)
 def test_deterministic(torch_dev, design):
     """Same inputs, same bits: every sum runs in a fixed order (the reference's resume bit-identity relies on it,
     reference src/delta_grad.cpp:19-22)."""
