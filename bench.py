@@ -267,28 +267,30 @@ def run_lora_step(torch, steps=5, warmup=2):
     """One LoRA training step of the tiny Qwen3.5-architecture model (quotebound_amd.lora.Config: 8 layers 3
     DeltaNet : 1 attention, hidden 1024, bf16 base, rank 16 on q/k/v/o and the DeltaNet in/out projections) on 4
     sequences of 1024 random tokens with the loss on the last half: forward, adapter gradients, AdamW. Timed with
-    device synchronisations around `steps` steps."""
+    device synchronisations around `steps` steps, run eagerly and replayed from a captured HIP graph."""
     from quotebound_amd import lora
 
     cfg = lora.Config()
     host = lora.init_weights(cfg, seed=31)
     w = lora.to_device(host, "cuda", torch.bfloat16)
     ads = lora.adapters_to(lora.init_adapters(cfg, host, seed=32, b_std=0.05), "cuda")
-    tokens, positions, targets = (t.cuda() for t in lora.last_half_batch(4, 1024, cfg.vocab, seed=33))
-    opt = lora.AdamW(lr=1e-4)
-    state = opt.init(lora.adapter_list(ads))
-    for _ in range(warmup):
-        loss, norm, ads = lora.train_step(w, ads, opt, state, tokens, positions, targets, cfg)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        loss, norm, ads = lora.train_step(w, ads, opt, state, tokens, positions, targets, cfg)
-    torch.cuda.synchronize()
-    ms = (time.perf_counter() - t0) * 1e3 / steps
-    return {"ms_per_step": ms, "tokens_per_s": 4 * 1024 / (ms * 1e-3), "loss": float(loss),
-            "config": "8 layers (3 Gated DeltaNet : 1 attention), hidden 1024, DeltaNet Hk=4 Hv=8 D=128, vocab 32000,"
-                      " bf16 base, LoRA rank 16 on q/k/v/o + in_proj_qkv/out_proj; batch 4 x 1024, loss on the last"
-                      " half; forward + adapter gradients + AdamW"}
+    batch = tuple(t.cuda() for t in lora.last_half_batch(4, 1024, cfg.vocab, seed=33))
+    out = {"config": "8 layers (3 Gated DeltaNet : 1 attention), hidden 1024, DeltaNet Hk=4 Hv=8 D=128, vocab 32000,"
+                     " bf16 base, LoRA rank 16 on q/k/v/o + in_proj_qkv/out_proj; batch 4 x 1024, loss on the last"
+                     " half; forward + adapter gradients + AdamW"}
+    for mode in ("eager", "graph"):
+        step = lora.GraphStep(w, ads, lora.AdamW(lr=1e-4), cfg, batch, capture=(mode == "graph"))
+        for _ in range(warmup):
+            loss, _ = step(*batch)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            loss, _ = step(*batch)
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) * 1e3 / steps
+        out[mode] = {"ms_per_step": ms, "tokens_per_s": 4 * 1024 / (ms * 1e-3), "loss": float(loss)}
+        del step
+    return out
 
 
 def traffic_of(w, kernel):

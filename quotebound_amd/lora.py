@@ -337,6 +337,75 @@ class AdamW:
         return out
 
 
+def adamw_update_(opt: AdamW, params, grads, norm, m, v, count):
+    """opt's update in place on device tensors, its step count a device scalar (count), so that the update can be
+    captured in a graph and replayed: the bias corrections are computed on the device from the count."""
+    count.add_(1.0)
+    bc1 = 1.0 - torch.pow(opt.beta1, count)
+    bc2_sqrt = torch.sqrt(1.0 - torch.pow(opt.beta2, count))
+    coef = torch.clamp(opt.clip / (norm + 1e-6), max=1.0) if opt.clip > 0 else None
+    for p, g, mi, vi in zip(params, grads, m, v):
+        if coef is not None:
+            g = g * coef
+        mi.mul_(opt.beta1).add_(g, alpha=1.0 - opt.beta1)
+        vi.mul_(opt.beta2).addcmul_(g, g, value=1.0 - opt.beta2)
+        p.mul_(1.0 - opt.lr * opt.weight_decay)
+        p.sub_((opt.lr / bc1) * (mi / (torch.sqrt(vi) / bc2_sqrt + opt.eps)))
+
+
+class GraphStep:
+    """The training step (loss, adapter gradients, AdamW) on static device tensors: the adapters, the moments and
+    the step count are updated in place, and each call copies its batch into static inputs. With capture=True the
+    step is recorded once in a HIP graph (torch.cuda.graph) and each call replays it, so the ~1,500 launches of a
+    step cost one; with capture=False each call runs the same step eagerly. example = (tokens, positions, targets)
+    fixes the batch shapes."""
+
+    def __init__(self, w, adapters, opt: AdamW, cfg: Config, example, capture=True, warmup=2):
+        self.w, self.opt, self.cfg, self.scale = w, opt, cfg, adapters["scale"]
+        self.names = list(adapters["adapters"])
+        self.params = [t.detach().clone() for t in adapter_list(adapters)]
+        self.m = [torch.zeros_like(p) for p in self.params]
+        self.v = [torch.zeros_like(p) for p in self.params]
+        self.count = torch.zeros((), dtype=torch.float32, device=self.params[0].device)
+        self.inputs = [t.clone() for t in example]
+        self.graph = None
+        if not capture:
+            return
+        start = [t.clone() for t in self.params + self.m + self.v + [self.count]]
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):  # the first runs set up libraries and the allocator outside the capture
+            for _ in range(warmup):
+                self._step()
+        torch.cuda.current_stream().wait_stream(side)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self.out = self._step()
+        for t, s0 in zip(self.params + self.m + self.v + [self.count], start):  # undo the warm-up steps
+            t.copy_(s0)
+
+    def _step(self):
+        ads = {"scale": self.scale,
+               "adapters": {n: (self.params[2 * i], self.params[2 * i + 1]) for i, n in enumerate(self.names)}}
+        loss, grads, norm = loss_and_grads(self.w, ads, *self.inputs, self.cfg)
+        adamw_update_(self.opt, self.params, grads, norm, self.m, self.v, self.count)
+        return loss, norm
+
+    def __call__(self, tokens, positions, targets):
+        """One step on this batch; returns (loss, gradient norm) as device scalars (overwritten by the next call
+        when captured)."""
+        for dst, src in zip(self.inputs, (tokens, positions, targets)):
+            dst.copy_(src)
+        if self.graph is None:
+            return self._step()
+        self.graph.replay()
+        return self.out
+
+    def adapters(self) -> dict:
+        return {"scale": self.scale,
+                "adapters": {n: (self.params[2 * i], self.params[2 * i + 1]) for i, n in enumerate(self.names)}}
+
+
 def train_step(w, adapters, opt: AdamW, opt_state, tokens, positions, targets, cfg):
     """One step: loss and adapter gradients, then the AdamW update. Returns (loss, norm, new adapters)."""
     loss, grads, norm = loss_and_grads(w, adapters, tokens, positions, targets, cfg)

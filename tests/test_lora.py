@@ -240,3 +240,28 @@ def test_train_step_runs_and_moves_the_adapters(dev):
     moved = [not torch.equal(a, b) for a, b in zip(lora.adapter_list(ads), lora.adapter_list(ads1))]
     assert all(moved[1::2])  # every b moves off zero on the first step
     assert float(loss1) < float(loss0)
+
+
+@pytest.mark.gpu
+def test_graph_step_replays_match_eager(dev):
+    """The step captured in a HIP graph, replayed on three batches with eager work and synchronisations between the
+    replays, equals the same step run eagerly, bit for bit: loss, gradient norm, adapters and both moments after
+    every replay."""
+    cfg = SMALL
+    host = lora.init_weights(cfg, seed=71)
+    w = lora.to_device(host, "cuda", torch.bfloat16)
+    ads = lora.adapters_to(lora.init_adapters(cfg, host, seed=72, b_std=0.05), "cuda")
+    opt = lora.AdamW(lr=1e-3, weight_decay=0.01)
+    batches = [tuple(t.cuda() for t in lora.last_half_batch(2, 128, cfg.vocab, seed=73 + i)) for i in range(3)]
+    eager = lora.GraphStep(w, ads, opt, cfg, batches[0], capture=False)
+    graph = lora.GraphStep(w, ads, opt, cfg, batches[0], capture=True)
+    for i, b in enumerate(batches):
+        le, ne = eager(*b)
+        lg, ng = graph(*b)
+        torch.cuda.synchronize()
+        torch.randn(4096, device="cuda").sum().item()  # eager work between the replays
+        assert torch.equal(le, lg) and torch.equal(ne, ng), i
+        for name, x, y in (("params", eager.params, graph.params), ("m", eager.m, graph.m), ("v", eager.v, graph.v)):
+            assert all(torch.equal(p, q) for p, q in zip(x, y)), (i, name)
+        assert math.isfinite(float(lg))
+
