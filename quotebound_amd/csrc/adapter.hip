@@ -10,6 +10,7 @@
 #include "gdn_common.h"
 #include "qb/delta_grad.h"
 #include "qb/deltanet.h"
+#include "qb/neighbours.h"
 #include "qb_gdn.h"
 
 namespace qb {
@@ -123,6 +124,35 @@ void run_fwd(const qb_gdn_desc& d, const array& q, const array& k, const array& 
                  g_stream, err, sizeof err) != 0)
     throw std::runtime_error(err);
 }
+
+// The neighbours' descriptor: B, T, heads and widths, the activations' dtype (the other fields are unused).
+qb_gdn_desc nb_desc(int B, int T, int Hk, int Hv, int Dk, int Dv, Dtype act) {
+  qb_gdn_desc d{};
+  d.B = B, d.T = T, d.Hk = Hk, d.Hv = Hv, d.Dk = Dk, d.Dv = Dv;
+  d.chunk = 64;
+  d.dtype = int(act);
+  return d;
+}
+
+Dtype act_dtype(std::initializer_list<const array*> xs) {
+  for (const array* x : xs)
+    if (x->dtype() != bfloat16) return float32;
+  return bfloat16;
+}
+
+void need(bool ok, const char* who, const std::string& why, std::initializer_list<const array*> xs) {
+  if (ok) return;
+  std::string m = std::string(who) + ": " + why + " (shapes";
+  for (const array* x : xs) m += " " + shape_str(x->shape());
+  throw std::runtime_error(m + ")");
+}
+
+void abi(int rc, const char* err) {
+  if (rc != 0) throw std::runtime_error(err);
+}
+
+const float* fp(const array& x) { return static_cast<const float*>(x.data()); }
+float* fp(array& x) { return static_cast<float*>(x.data()); }
 
 }  // namespace
 
@@ -244,6 +274,101 @@ std::vector<array> gated_delta_vjp(const std::vector<array>& in, const array& dy
     throw std::runtime_error(err);
   return {astype(dq, q.dtype()), astype(dk, k.dtype()),  astype(dv, v.dtype()),
           astype(dg, g.dtype()), astype(db, beta.dtype()), astype(ds0, state.dtype())};
+}
+
+Prologue deltanet_prologue(const array& q_raw, const array& k_raw, const array& a, const array& b,
+                           const array& a_log, const array& dt_bias) {
+  const char* who = "deltanet prologue";
+  need(q_raw.ndim() == 4 && k_raw.shape() == q_raw.shape() && a.ndim() == 3 && b.shape() == a.shape(), who,
+       "q_raw, k_raw must be [B, T, Hk, Dk] and a, b [B, T, Hv]", {&q_raw, &k_raw, &a, &b});
+  const int B = q_raw.shape(0), T = q_raw.shape(1), Hk = q_raw.shape(2), Dk = q_raw.shape(3), Hv = a.shape(2);
+  need(a.shape(0) == B && a.shape(1) == T && a_log.shape() == Shape{Hv} && dt_bias.shape() == Shape{Hv}, who,
+       "a, b must match q_raw in batch and time, and a_log, dt_bias be [Hv]", {&q_raw, &a, &a_log, &dt_bias});
+  const Dtype act = act_dtype({&q_raw, &k_raw, &a, &b});
+  const qb_gdn_desc d = nb_desc(B, T, Hk, Hv, Dk, Dk, act);
+  const array qr = astype(q_raw, act), kr = astype(k_raw, act), aa = astype(a, act), bb = astype(b, act);
+  const array al = astype(a_log, float32), dt = astype(dt_bias, float32);
+  Prologue r{array(q_raw.shape(), act), array(q_raw.shape(), act), array(a.shape(), act), array(a.shape(), float32)};
+  char err[512];
+  abi(qb_gdn_prologue_fwd(&d, qr.data(), kr.data(), aa.data(), bb.data(), fp(al), fp(dt), r.q.data(), r.k.data(),
+                          r.beta.data(), fp(r.log_decay), g_stream, err, sizeof err),
+      err);
+  return r;
+}
+
+PrologueGrads deltanet_prologue_vjp(const array& q_raw, const array& k_raw, const array& a, const array& b,
+                                    const array& a_log, const array& dt_bias, const array& dq, const array& dk,
+                                    const array& dbeta, const array& dlog_decay) {
+  const char* who = "deltanet prologue backward";
+  need(q_raw.ndim() == 4 && k_raw.shape() == q_raw.shape() && dq.shape() == q_raw.shape() &&
+           dk.shape() == q_raw.shape() && a.ndim() == 3 && b.shape() == a.shape() && dbeta.shape() == a.shape() &&
+           dlog_decay.shape() == a.shape(),
+       who, "cotangents must have their primals' shapes", {&q_raw, &k_raw, &a, &b, &dq, &dk, &dbeta, &dlog_decay});
+  const int B = q_raw.shape(0), T = q_raw.shape(1), Hk = q_raw.shape(2), Dk = q_raw.shape(3), Hv = a.shape(2);
+  need(a.shape(0) == B && a.shape(1) == T && a_log.shape() == Shape{Hv} && dt_bias.shape() == Shape{Hv}, who,
+       "a, b must match q_raw in batch and time, and a_log, dt_bias be [Hv]", {&q_raw, &a, &a_log, &dt_bias});
+  const Dtype act = act_dtype({&q_raw, &k_raw, &a, &b});
+  const qb_gdn_desc d = nb_desc(B, T, Hk, Hv, Dk, Dk, act);
+  const array qr = astype(q_raw, act), kr = astype(k_raw, act), aa = astype(a, act), bb = astype(b, act);
+  const array al = astype(a_log, float32), dt = astype(dt_bias, float32);
+  const array gq = astype(dq, act), gk = astype(dk, act), gb = astype(dbeta, act), gl = astype(dlog_decay, float32);
+  PrologueGrads r{array(q_raw.shape(), act), array(q_raw.shape(), act), array(a.shape(), act),
+                  array(a.shape(), act),     array({Hv}, float32),      array({Hv}, float32)};
+  Scratch ws(qb_gdn_neighbours_workspace_bytes(&d));
+  char err[512];
+  abi(qb_gdn_prologue_bwd(&d, qr.data(), kr.data(), aa.data(), bb.data(), fp(al), fp(dt), gq.data(), gk.data(),
+                          gb.data(), fp(gl), r.dq_raw.data(), r.dk_raw.data(), r.da.data(), r.db.data(),
+                          fp(r.da_log), fp(r.ddt_bias), ws.p, g_stream, err, sizeof err),
+      err);
+  return r;
+}
+
+array deltanet_epilogue(const array& y, const array& z, const array& norm_w, float eps) {
+  const char* who = "deltanet epilogue";
+  need(y.ndim() == 4 && z.shape() == y.shape() && norm_w.shape() == Shape{y.shape(3)}, who,
+       "y, z must be [B, T, Hv, Dv] and norm_w [Dv]", {&y, &z, &norm_w});
+  const Dtype act = act_dtype({&y, &z});
+  const int Hv = y.shape(2), Dv = y.shape(3);
+  const qb_gdn_desc d = nb_desc(y.shape(0), y.shape(1), Hv, Hv, Dv, Dv, act);
+  const array yy = astype(y, act), zz = astype(z, act), w = astype(norm_w, float32);
+  array o(y.shape(), act);
+  char err[512];
+  abi(qb_gdn_epilogue_fwd(&d, yy.data(), zz.data(), fp(w), eps, o.data(), g_stream, err, sizeof err), err);
+  return o;
+}
+
+EpilogueGrads deltanet_epilogue_vjp(const array& y, const array& z, const array& norm_w, float eps,
+                                    const array& dout) {
+  const char* who = "deltanet epilogue backward";
+  need(y.ndim() == 4 && z.shape() == y.shape() && dout.shape() == y.shape() && norm_w.shape() == Shape{y.shape(3)},
+       who, "y, z, dout must be [B, T, Hv, Dv] and norm_w [Dv]", {&y, &z, &dout, &norm_w});
+  const Dtype act = act_dtype({&y, &z});
+  const int Hv = y.shape(2), Dv = y.shape(3);
+  const qb_gdn_desc d = nb_desc(y.shape(0), y.shape(1), Hv, Hv, Dv, Dv, act);
+  const array yy = astype(y, act), zz = astype(z, act), w = astype(norm_w, float32), go = astype(dout, act);
+  EpilogueGrads r{array(y.shape(), act), array(y.shape(), act), array({Dv}, float32)};
+  Scratch ws(qb_gdn_neighbours_workspace_bytes(&d));
+  char err[512];
+  abi(qb_gdn_epilogue_bwd(&d, yy.data(), zz.data(), fp(w), eps, go.data(), r.dy.data(), r.dz.data(), fp(r.dnorm_w),
+                          ws.p, g_stream, err, sizeof err),
+      err);
+  return r;
+}
+
+std::pair<array, array> gated_delta_rows(const array& q, const array& k, const array& v, const array& g,
+                                         const array& beta, const array& state) {
+  const Problem p = check_shapes("gated delta rows", q, k, v, g, beta, state);
+  const Dtype io = io_dtype(q, k, v, beta);
+  qb_gdn_desc d = make_desc(p, io, false);
+  d.design = QB_GDN_RECURRENT;
+  array y({p.B, p.T, p.Hv, p.Dv}, io), rows({p.B, p.T, p.Hv, p.Dv, p.Dk}, float32);
+  const array qq = astype(q, io), kk = astype(k, io), vv = astype(v, io), gg = astype(g, float32);
+  const array bb = astype(beta, io), s0 = astype(state, float32);
+  char err[512];
+  abi(qb_gdn_fwd_rows(&d, qq.data(), kk.data(), vv.data(), fp(gg), bb.data(), fp(s0), y.data(), fp(rows), g_stream,
+                      err, sizeof err),
+      err);
+  return {astype(y, q.dtype()), rows};
 }
 
 }  // namespace qb

@@ -1,4 +1,6 @@
-// Checks the C++ adapters of include/qb (gated_delta, gated_delta_trainable, gated_delta_vjp) against the oracle,
+// Checks the C++ adapters of include/qb (gated_delta, gated_delta_trainable, gated_delta_vjp, gated_delta_rows)
+// against the oracle, and the neighbours' adapters (deltanet_prologue / _epilogue and their vjps) in float32
+// against a float64 statement of their formulas here,
 // the way the reference's tests check its entry points (tests/test_deltanet.cpp:25-154): seeded inputs, the
 // forward and every cotangent compared normwise, max|X - X_ref| / max|X_ref|. float32 outputs must be within 2e-3;
 // a bfloat16 output may in addition differ by half a bfloat16 ulp of each reference element (its own rounding).
@@ -14,6 +16,7 @@
 #include "../../oracle/gdn_ref.h"
 #include "qb/delta_grad.h"
 #include "qb/deltanet.h"
+#include "qb/neighbours.h"
 
 namespace {
 
@@ -141,6 +144,118 @@ void run_case(const char* name, int B, int T, int Hk, int Hv, int Dk, int Dv, qb
   const char* names[6] = {"dq", "dk", "dv", "dg", "dbeta", "dS0"};
   const std::vector<float>* refs[6] = {&dq, &dk, &dv, &dg, &db, &ds0};
   for (int i = 0; i < 6; ++i) compare(names[i], gr[i], *refs[i], 2e-3);
+
+  // The state after every token: the oracle's checkpoints at stride 1 (the state before each token), shifted by one.
+  std::printf(" gated_delta_rows\n");
+  gdn_ref_shape sh1{B, T, Hk, Hv, Dk, Dv, 1, 0, nullptr, 0};
+  std::vector<float> y1(nv), st1(ns), ck1(size_t(gdn_ref_num_chunks(&sh1)) * Hv * Dv * Dk);
+  gdn_ref_fwd_f32(&sh1, tq.host.data(), tk.host.data(), tv.host.data(), tg.host.data(), tb.host.data(),
+                  ts.host.data(), y1.data(), st1.data(), ck1.data());
+  const size_t S = size_t(Hv) * Dv * Dk;
+  std::vector<float> rows_ref(size_t(B) * T * S);
+  for (int b = 0; b < B; ++b)
+    for (int t = 0; t < T; ++t) {
+      const float* src = t + 1 < T ? &ck1[(size_t(b) * T + t + 1) * S] : &st1[size_t(b) * S];
+      std::memcpy(&rows_ref[(size_t(b) * T + t) * S], src, S * sizeof(float));
+    }
+  auto [yr, rows] = qb::gated_delta_rows(tq.dev, tk.dev, tv.dev, tg.dev, tb.dev, ts.dev);
+  compare("y", yr, y1, 2e-3);
+  compare("rows", rows, rows_ref, 2e-3);
+}
+
+double sig(double x) { return 1.0 / (1.0 + std::exp(-x)); }
+
+// The neighbours in float32 against their formulas in float64 (src/deltanet.cpp:22-45, 94-100, 122).
+void neighbours_case() {
+  const int B = 2, T = 37, Hk = 2, Hv = 4, D = 64;
+  std::printf("case neighbours: B=%d T=%d Hk=%d Hv=%d D=%d f32\n", B, T, Hk, Hv, D);
+  Rng r{21};
+  const size_t nqk = size_t(B) * T * Hk * D, ng = size_t(B) * T * Hv, ny = size_t(B) * T * Hv * D;
+  auto fill = [&](size_t n, double sc, double mean = 0.0) {
+    std::vector<float> x(n);
+    for (auto& e : x) e = float(mean + sc * r.normal());
+    return x;
+  };
+  const std::vector<float> qr = fill(nqk, 1), kr = fill(nqk, 1), a = fill(ng, 1), b = fill(ng, 1);
+  std::vector<float> alog(Hv), dt = fill(Hv, 0.5);
+  for (auto& e : alog) e = float(std::log(1.0 + 15.0 * r.uniform()));
+  const std::vector<float> gq = fill(nqk, 1), gk = fill(nqk, 1), gb = fill(ng, 1), gl = fill(ng, 1);
+  const std::vector<float> y = fill(ny, 0.05), z = fill(ny, 2), w = fill(D, 0.2, 1.0), go = fill(ny, 1);
+  const qb::Dtype f = qb::float32;
+  auto dev = [&](const std::vector<float>& x, qb::Shape s) { return qb::array::from_host(x.data(), s, f); };
+  const qb::Shape sqk{B, T, Hk, D}, sg{B, T, Hv}, sy{B, T, Hv, D};
+  // Row statistics: rho = (mean x^2 + eps)^-1/2 per row of D.
+  auto rho = [&](const std::vector<float>& x, size_t row, double eps) {
+    double ss = 0;
+    for (int c = 0; c < D; ++c) ss += double(x[row * D + c]) * x[row * D + c];
+    return 1.0 / std::sqrt(ss / D + eps);
+  };
+  const double s_q = float(1.0 / D), s_k = float(1.0 / std::sqrt(double(D)));
+  std::vector<float> q(nqk), k(nqk), dqr(nqk), dkr(nqk), beta(ng), ld(ng), da(ng), db(ng), dal(Hv, 0.f), ddt(Hv, 0.f);
+  for (size_t row = 0; row < nqk / D; ++row)
+    for (int which = 0; which < 2; ++which) {
+      const std::vector<float>& x = which ? kr : qr;
+      const std::vector<float>& gx = which ? gk : gq;
+      const double s = which ? s_k : s_q, rh = rho(x, row, 1e-6);
+      double sgx = 0;
+      for (int c = 0; c < D; ++c) sgx += s * gx[row * D + c] * x[row * D + c];
+      for (int c = 0; c < D; ++c) {
+        const size_t i = row * D + c;
+        (which ? k : q)[i] = float(s * x[i] * rh);
+        (which ? dkr : dqr)[i] = float(rh * s * gx[i] - rh * rh * rh * x[i] * sgx / D);
+      }
+    }
+  std::vector<double> dal64(Hv, 0.0), ddt64(Hv, 0.0);
+  for (size_t i = 0; i < ng; ++i) {
+    const int h = int(i % Hv);
+    const double x = double(a[i]) + dt[h], sp = std::log1p(std::exp(-std::fabs(x))) + std::fmax(x, 0.0);
+    const double ea = std::exp(double(alog[h])), sb = sig(b[i]);
+    beta[i] = float(sb), ld[i] = float(-ea * sp);
+    db[i] = float(gb[i] * sb * (1 - sb));
+    const double dx = -double(gl[i]) * ea * sig(x);
+    da[i] = float(dx);
+    dal64[h] += double(gl[i]) * (-ea * sp), ddt64[h] += dx;
+  }
+  for (int h = 0; h < Hv; ++h) dal[h] = float(dal64[h]), ddt[h] = float(ddt64[h]);
+  std::vector<float> o(ny), dy(ny), dz(ny), dw(D, 0.f);
+  std::vector<double> dw64(D, 0.0);
+  for (size_t row = 0; row < ny / D; ++row) {
+    const double rh = rho(y, row, 1e-6);
+    double sgy = 0;
+    for (int c = 0; c < D; ++c) {
+      const size_t i = row * D + c;
+      const double zz = z[i], sz = sig(zz), nh = y[i] * rh, dn = go[i] * zz * sz;
+      o[i] = float(zz * sz * w[c] * nh);
+      dz[i] = float(go[i] * nh * w[c] * sz * (1 + zz * (1 - sz)));
+      dw64[c] += dn * nh;
+      sgy += dn * w[c] * y[i];
+    }
+    for (int c = 0; c < D; ++c) {
+      const size_t i = row * D + c;
+      const double dn = go[i] * double(z[i]) * sig(z[i]);
+      dy[i] = float(rh * dn * w[c] - rh * rh * rh * y[i] * sgy / D);
+    }
+  }
+  for (int c = 0; c < D; ++c) dw[c] = float(dw64[c]);
+
+  const qb::array Aqr = dev(qr, sqk), Akr = dev(kr, sqk), Aa = dev(a, sg), Ab = dev(b, sg);
+  const qb::array Aal = dev(alog, {Hv}), Adt = dev(dt, {Hv});
+  std::printf(" deltanet_prologue\n");
+  const qb::Prologue P = qb::deltanet_prologue(Aqr, Akr, Aa, Ab, Aal, Adt);
+  compare("q", P.q, q, 1e-5), compare("k", P.k, k, 1e-5), compare("beta", P.beta, beta, 1e-5);
+  compare("logdec", P.log_decay, ld, 1e-5);
+  std::printf(" deltanet_prologue_vjp\n");
+  const qb::PrologueGrads G =
+      qb::deltanet_prologue_vjp(Aqr, Akr, Aa, Ab, Aal, Adt, dev(gq, sqk), dev(gk, sqk), dev(gb, sg), dev(gl, sg));
+  compare("dq_raw", G.dq_raw, dqr, 1e-5), compare("dk_raw", G.dk_raw, dkr, 1e-5);
+  compare("da", G.da, da, 1e-5), compare("db", G.db, db, 1e-5);
+  compare("dA_log", G.da_log, dal, 1e-4), compare("ddt", G.ddt_bias, ddt, 1e-4);
+  const qb::array Ay = dev(y, sy), Az = dev(z, sy), Aw = dev(w, {D});
+  std::printf(" deltanet_epilogue\n");
+  compare("o", qb::deltanet_epilogue(Ay, Az, Aw, 1e-6f), o, 1e-5);
+  std::printf(" deltanet_epilogue_vjp\n");
+  const qb::EpilogueGrads E = qb::deltanet_epilogue_vjp(Ay, Az, Aw, 1e-6f, dev(go, sy));
+  compare("dy", E.dy, dy, 1e-5), compare("dz", E.dz, dz, 1e-5), compare("dw", E.dnorm_w, dw, 1e-4);
 }
 
 void expect_throw(const char* what, void (*fn)()) {
@@ -158,6 +273,7 @@ void expect_throw(const char* what, void (*fn)()) {
 int main() {
   run_case("chunked", 2, 150, 2, 4, 128, 64, qb::bfloat16, 11);
   run_case("recurrent", 1, 100, 2, 4, 64, 32, qb::float32, 12);
+  neighbours_case();
   std::printf("errors\n");
   expect_throw("k shape", [] {
     const qb::array q = qb::array::zeros({1, 8, 2, 64}, qb::float32), k = qb::array::zeros({1, 8, 2, 32}, qb::float32);
@@ -171,6 +287,15 @@ int main() {
     qb::gated_delta(q, q, v, g, g, s);
   });
   expect_throw("vjp primals", [] { qb::gated_delta_vjp({}, qb::array(), qb::array()); });
+  expect_throw("prologue Dk", [] {
+    const qb::array x = qb::array::zeros({1, 8, 2, 32}, qb::float32), a = qb::array::zeros({1, 8, 4}, qb::float32);
+    const qb::array p = qb::array::zeros({4}, qb::float32);
+    qb::deltanet_prologue(x, x, a, a, p, p);
+  });
+  expect_throw("epilogue weight", [] {
+    const qb::array y = qb::array::zeros({1, 8, 4, 64}, qb::float32), w = qb::array::zeros({32}, qb::float32);
+    qb::deltanet_epilogue(y, y, w, 1e-6f);
+  });
   std::printf(failures ? "FAIL (%d)\n" : "PASS\n", failures);
   return failures ? 1 : 0;
 }

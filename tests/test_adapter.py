@@ -17,6 +17,11 @@ CXX_SYMBOLS = [
     "_ZN2qb11gated_deltaERKNS_5arrayES2_S2_S2_S2_S2_b",
     "_ZN2qb21gated_delta_trainableERKNS_5arrayES2_S2_S2_S2_S2_",
     "_ZN2qb15gated_delta_vjpERKSt6vectorINS_5arrayESaIS1_EERKS1_S7_",
+    "_ZN2qb16gated_delta_rowsERKNS_5arrayES2_S2_S2_S2_S2_",
+    "_ZN2qb17deltanet_prologueERKNS_5arrayES2_S2_S2_S2_S2_",
+    "_ZN2qb21deltanet_prologue_vjpERKNS_5arrayES2_S2_S2_S2_S2_S2_S2_S2_S2_",
+    "_ZN2qb17deltanet_epilogueERKNS_5arrayES2_S2_f",
+    "_ZN2qb21deltanet_epilogue_vjpERKNS_5arrayES2_S2_fS2_",
     "_ZN2qb5arrayC1ESt6vectorIiSaIiEENS_5DtypeE",
     "_ZN2qb5array9from_hostEPKvSt6vectorIiSaIiEENS_5DtypeE",
     "_ZN2qb5array5zerosESt6vectorIiSaIiEENS_5DtypeE",
