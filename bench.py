@@ -352,7 +352,7 @@ def main():
                          "counter passes need")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported (the recurrence shards "
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the recurrence shards "
               "by key-head groups with no exchange, so per-GPU work is the one-GPU run at Hk/N, Hv/N).",
               file=sys.stderr)
         sys.exit(2)

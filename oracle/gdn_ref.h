@@ -1,8 +1,8 @@
 /*
  * CPU restatement of quotebound's gated delta rule: the forward recurrence and its hand-written backward.
  *
- * TEST INFRASTRUCTURE ONLY. This is the checker: the parity tests, __graft_entry__.smoke() and bench.py's
- * CPU-baseline leg load it. The product (quotebound_amd, libqb_gdn.so) never links, loads or calls it, and has no
+ * TEST INFRASTRUCTURE ONLY. The kernels' results are compared with it: the parity tests, __graft_entry__.smoke()
+ * and bench.py's CPU-baseline leg load it. The product (quotebound_amd, libqb_gdn.so) never links, loads or calls it, and has no
  * CPU fallback of any kind.
  *
  * What it restates (reference paths are relative to the quotebound checkout):

@@ -1,6 +1,7 @@
 """ctypes binding of the oracle (libgdn_ref.so), the CPU restatement of quotebound's gated delta rule.
 
-Test infrastructure only: tests/, __graft_entry__.smoke() and bench.py's CPU-baseline leg use it as the checker.
+Test infrastructure only: tests/, __graft_entry__.smoke() and bench.py's CPU-baseline leg compare the kernels'
+results with it.
 Arrays are numpy, float32 or float64, in the layouts of gdn_ref.h; g is the log-decay unless g_is_log=False.
 """
 from __future__ import annotations

@@ -2,7 +2,7 @@
 with torch's own CPU library ops in float32 or float64, its recurrence the oracle's (gdn_ref: the C restatement of
 the gated delta rule, forward and hand-written backward) inside an autograd function.
 
-Test infrastructure only: tests/ and bench.py's checks use it as the checker. It does not round to bf16 anywhere:
+Test infrastructure only: tests/ compare the GPU step with it. It does not round to bf16 anywhere:
 given the bf16 base weights' values it computes the step in the arithmetic it is called with.
 
 Ops, each from torch's library rather than restated by hand:

@@ -1,6 +1,6 @@
 """The oracle of the layer's pointwise neighbours of the recurrence (reference src/deltanet.cpp), in numpy.
 
-Test infrastructure only: tests/ and bench.py's checks use it as the checker.
+Test infrastructure only: tests/ and __graft_entry__.smoke() compare the kernels' results with it.
 
 Forward, following the reference's ops in order (arithmetic in float64; with bf16 activations every op's output
 is rounded to bf16 where the reference's op rounds it, each op returning its input's dtype):
