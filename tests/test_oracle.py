@@ -183,7 +183,8 @@ def _loss(oracle, inp, chunk=4):
 @pytest.mark.parametrize("name", ["q", "k", "v", "g", "beta", "s0"])
 def test_finite_differences(oracle, name):
     """Central differences in float64 along random directions, one input at a time (the method of reference
-    tests/test_train.cpp:105-181, applied to the recurrence)."""
+    tests/test_train.cpp:105-181, applied to the recurrence). With the loss <dy, y> + <dS_out, S_T> this is the
+    dot-product (adjoint) test: <dy, J d> by differences against <J^T dy, d> from the backward."""
     inp = small_case(1, 11, 1, 2, 6, 5, seed=10)
     grads = oracle.fwd_bwd(inp, chunk=4)
     gname = {"s0": "ds0"}.get(name, "d" + name)
