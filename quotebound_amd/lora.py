@@ -343,14 +343,20 @@ def adamw_update_(opt: AdamW, params, grads, norm, m, v, count):
     count.add_(1.0)
     bc1 = 1.0 - torch.pow(opt.beta1, count)
     bc2_sqrt = torch.sqrt(1.0 - torch.pow(opt.beta2, count))
-    coef = torch.clamp(opt.clip / (norm + 1e-6), max=1.0) if opt.clip > 0 else None
-    for p, g, mi, vi in zip(params, grads, m, v):
-        if coef is not None:
-            g = g * coef
-        mi.mul_(opt.beta1).add_(g, alpha=1.0 - opt.beta1)
-        vi.mul_(opt.beta2).addcmul_(g, g, value=1.0 - opt.beta2)
-        p.mul_(1.0 - opt.lr * opt.weight_decay)
-        p.sub_((opt.lr / bc1) * (mi / (torch.sqrt(vi) / bc2_sqrt + opt.eps)))
+    g = list(grads)
+    if opt.clip > 0:  # one multi-tensor launch per op over all adapter arrays instead of one per array
+        g = torch._foreach_mul(g, torch.clamp(opt.clip / (norm + 1e-6), max=1.0))
+    torch._foreach_mul_(m, opt.beta1)
+    torch._foreach_add_(m, g, alpha=1.0 - opt.beta1)
+    torch._foreach_mul_(v, opt.beta2)
+    torch._foreach_addcmul_(v, g, g, value=1.0 - opt.beta2)
+    torch._foreach_mul_(params, 1.0 - opt.lr * opt.weight_decay)
+    denom = torch._foreach_sqrt(v)
+    torch._foreach_div_(denom, bc2_sqrt)
+    torch._foreach_add_(denom, opt.eps)
+    step = torch._foreach_div(m, denom)
+    torch._foreach_mul_(step, opt.lr / bc1)
+    torch._foreach_sub_(params, step)
 
 
 class GraphStep:
