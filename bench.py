@@ -2,8 +2,9 @@
 
 One step = one forward (qb_gdn_fwd, writing the 64-token checkpoints) and one backward (qb_gdn_bwd) over the
 workload's tokens, inputs resident in HBM before the timed region. value = tokens / (wall time per step), the best
-design's. Each kernel's duration comes from HIP events the library records on its launch stream (the descriptor's
-trace_events); the roofline object is for the kernel with the most time per step, its algorithmic work per launch
+design's, timed with nothing between the kernels. Each kernel's duration comes from a second run of as many steps
+with HIP events the library records on its launch stream around each kernel (the descriptor's trace_events);
+the roofline object is for the kernel with the most time per step, its algorithmic work per launch
 divided by its mean duration. cpu_baseline times the oracle (the CPU restatement, float32, OpenMP) on the host on
 the same inputs.
 
@@ -113,7 +114,8 @@ def roofline_of(kind, amount, ms):
 
 
 def run_design(torch, hip, lib, w, dev, design, steps, warmup):
-    """Times `steps` fwd+bwd steps after `warmup`; returns wall ms/step and per-kernel mean ms."""
+    """Times `steps` fwd+bwd steps after `warmup`, then runs as many with the library's trace events for each
+    kernel's duration; returns wall ms/step (of the uninstrumented steps) and per-kernel mean ms."""
     B, T, Hk, Hv, Dk, Dv = w.B, w.T, w.Hk, w.Hv, w.Dk, w.Dv
     cu = w.cu_seqlens
     dt = lib.BF16 if w.dtype == "bf16" else lib.F32
@@ -156,11 +158,14 @@ def run_design(torch, hip, lib, w, dev, design, steps, warmup):
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for i in range(steps):
-        step(i)
+    t0 = time.perf_counter()  # the step as a caller runs it: no events between the kernels
+    for _ in range(steps):
+        step()
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3 / steps
+    for i in range(steps):  # the same steps again with an event before and after each kernel, for their durations
+        step(i)
+    torch.cuda.synchronize()
     per = {}
     for i in range(steps):
         e = evs[i]
