@@ -429,3 +429,39 @@ def last_half_batch(batch: int, seq: int, vocab: int, seed: int = 0, device="cpu
     positions = (torch.arange(batch)[:, None] * seq + t[None, :]).reshape(-1)
     targets = tokens[:, seq // 2:].reshape(-1)
     return tokens.to(device), positions.to(device), targets.to(device)
+
+
+def main(argv=None) -> None:
+    """python -m quotebound_amd.lora [--steps K] [--warmup W] [--graph]: the LoRA workload's training step (the
+    default Config, bf16 base, 4 sequences of 1024 random tokens, loss on the last half) on cuda:0, timed over K
+    steps after W; prints one JSON line."""
+    import argparse
+    import json
+    import time
+
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--steps", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--graph", action="store_true", help="replay the step from a captured HIP graph")
+    args = ap.parse_args(argv)
+    cfg = Config()
+    host = init_weights(cfg, seed=31)
+    w = to_device(host, "cuda", torch.bfloat16)
+    ads = adapters_to(init_adapters(cfg, host, seed=32, b_std=0.05), "cuda")
+    batch = tuple(t.cuda() for t in last_half_batch(4, 1024, cfg.vocab, seed=33))
+    step = GraphStep(w, ads, AdamW(lr=1e-4), cfg, batch, capture=args.graph)
+    for _ in range(args.warmup):
+        step(*batch)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        loss, norm = step(*batch)
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    print(json.dumps({"ms_per_step": ms, "tokens_per_s": 4 * 1024 / (ms * 1e-3), "loss": float(loss),
+                      "grad_norm": float(norm), "graph": args.graph}))
+
+
+if __name__ == "__main__":
+    main()
+
