@@ -7,9 +7,9 @@
 // and their backward. With bf16 activations the forward rounds where the reference's ops do, each op's output
 // taking its inputs' dtype: rms_norm's normalised row, then its product with the scale; a + dt_bias, then its
 // softplus; and o once (the gated rms_norm's weight is float32, so its output is float32 until the product with
-// silu(z) takes the activation dtype). Arithmetic inside an op is float32. The backward is float32 throughout, with one rounding of each output; the parameter
-// gradients (A_log, dt_bias per value head, w per column) are summed over tokens in a fixed order: per-block
-// partials, then one pass over the blocks in order.
+// silu(z) takes the activation dtype). Arithmetic inside an op is float32. The backward is float32 throughout, with
+// one rounding of each output; the parameter gradients (A_log, dt_bias per value head, w per column) are summed over
+// tokens in a fixed order: per-block partials, then one pass over the blocks in order.
 //
 // Rows of D = 64, 128 or 256 elements: a lane holds 8 consecutive elements (one 16-byte load in bf16), a row takes
 // D / 8 consecutive lanes and a group of 64 / (D / 8) rows fills a wave; a wave of the one-pass kernels takes two
@@ -145,9 +145,9 @@ __global__ __launch_bounds__(256) void prologue_fwd_kernel(const T* __restrict__
 
 // The backward. Row blocks: g = scale * dout, dx = rho g - rho^3 x (sum g x) / D. The blocks after them each take a
 // tile of kGateSteps k tokens (k = 256 / Hv): thread t < k Hv handles value head t % Hv of tokens t / Hv,
-// t / Hv + k, ..., so each step reads k Hv contiguous (token, head) elements. It writes db and da, and the tile's partial sums
-// of dA_log = sum dlog_decay * log_decay and ddt_bias = sum da per head (the k threads of a head in order) at
-// part[(tile * Hv + h) * 2 + {0, 1}].
+// t / Hv + k, ..., so each step reads k Hv contiguous (token, head) elements. It writes db and da, and the tile's
+// partial sums of dA_log = sum dlog_decay * log_decay and ddt_bias = sum da per head (the k threads of a head in
+// order) at part[(tile * Hv + h) * 2 + {0, 1}].
 template <typename T, int D>
 __global__ __launch_bounds__(256) void prologue_bwd_kernel(
     const T* __restrict__ qr, const T* __restrict__ kr, const T* __restrict__ dq, const T* __restrict__ dk,

@@ -232,7 +232,8 @@ PROLOGUE_CASES = [  # (B, T, Hk, Hv, Dk, bf16)
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("case", PROLOGUE_CASES, ids=lambda c: "B%dT%dHk%dHv%dDk%d_%s" % (*c[:5], "bf16" if c[5] else "f32"))
+@pytest.mark.parametrize("case", PROLOGUE_CASES,
+                         ids=lambda c: "B%dT%dHk%dHv%dDk%d_%s" % (*c[:5], "bf16" if c[5] else "f32"))
 def test_prologue_parity(dev, case):
     torch = dev
     from quotebound_amd import neighbours
@@ -279,7 +280,8 @@ EPILOGUE_CASES = [  # (B, T, Hv, Dv, bf16)
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("case", EPILOGUE_CASES, ids=lambda c: "B%dT%dHv%dDv%d_%s" % (*c[:4], "bf16" if c[4] else "f32"))
+@pytest.mark.parametrize("case", EPILOGUE_CASES,
+                         ids=lambda c: "B%dT%dHv%dDv%d_%s" % (*c[:4], "bf16" if c[4] else "f32"))
 def test_epilogue_parity(dev, case):
     torch = dev
     from quotebound_amd import neighbours
