@@ -1,8 +1,8 @@
 // The DeltaNet layer's pointwise neighbours of the recurrence (reference src/deltanet.cpp:22-45, 94-100, 122), on
 // qb::array and the HIP kernels of qb_gdn.h. Activations (q_raw, k_raw, a, b, y, z and their cotangents) run in
 // bfloat16 when all of a call's activations are bfloat16, else in float32, with the reference's bf16 roundings in
-// the former case; parameters (a_log, dt_bias, norm_w) and the log-decay are float32. Dk and Dv must be 64, 128 or
-// 256. Throws std::runtime_error naming the shapes when they do not fit.
+// the former case; parameters (a_log, dt_bias, norm_w) and the log-decay are float32. The prologue needs Dk, the
+// epilogue Dv, of 64, 128 or 256. Throws std::runtime_error naming the shapes when they do not fit.
 #pragma once
 #include "qb/array.h"
 

@@ -113,7 +113,8 @@ int qb_gdn_bwd(const qb_gdn_desc* desc, const void* q, const void* k, const void
                float* dg, void* dbeta, float* ds0, void* workspace, void* stream, char* err, int errlen);
 
 /* The layer's pointwise neighbours of the recurrence, each one pass over its rows (reference src/deltanet.cpp). They
- * read B, T, Hk, Hv, Dk, Dv and dtype from desc (the other fields are not used; Dk and Dv must be 64, 128 or 256)
+ * read B, T, Hk, Hv, Dk, Dv and dtype from desc (the other fields are not used; the prologue needs Dk, the epilogue
+ * Dv, of 64, 128 or 256, and Hv at most 256)
  * and take the activations in dtype and the parameters in float32. With bf16 activations each op's output is
  * rounded to bf16 where the reference's op rounds it; arithmetic inside an op is float32. The backward entry points
  * are float32 inside with one rounding of each output, and sum the parameter gradients over tokens in a fixed order

@@ -343,7 +343,8 @@ float round_bf16_host(float x) {
   return r;
 }
 
-std::string nb_resolve(const qb_gdn_desc* d, qbgdn::NbProblem& p) {
+// uses_dk / uses_dv: which of the widths the entry point runs on (the prologue Dk, the epilogue Dv).
+std::string nb_resolve(const qb_gdn_desc* d, qbgdn::NbProblem& p, bool uses_dk, bool uses_dv) {
   if (!d) return "gated delta neighbours: null descriptor";
   const std::string sh = shape_of(*d);
   if (d->B < 1 || d->T < 0 || d->Hk < 1 || d->Hv < 1 || d->Dk < 1 || d->Dv < 1)
@@ -361,7 +362,8 @@ std::string nb_resolve(const qb_gdn_desc* d, qbgdn::NbProblem& p) {
   const double inv = 1.0 / std::sqrt(double(d->Dk));
   p.scale_q = float(inv * inv), p.scale_k = float(inv);
   if (p.bf16) p.scale_q = round_bf16_host(p.scale_q), p.scale_k = round_bf16_host(p.scale_k);
-  if (const char* why = qbgdn::nb_supports(p)) return std::string("gated delta neighbours: ") + why + " " + sh;
+  if (const char* why = qbgdn::nb_supports(p, uses_dk, uses_dv))
+    return std::string("gated delta neighbours: ") + why + " " + sh;
   return {};
 }
 
@@ -372,7 +374,7 @@ extern "C" {
 size_t qb_gdn_neighbours_workspace_bytes(const qb_gdn_desc* desc) {
   try {
     qbgdn::NbProblem p;
-    if (!nb_resolve(desc, p).empty()) return 0;
+    if (!nb_resolve(desc, p, false, false).empty()) return 0;
     return qbgdn::nb_workspace_bytes(p);
   } catch (...) {
     return 0;
@@ -384,7 +386,7 @@ int qb_gdn_prologue_fwd(const qb_gdn_desc* desc, const void* q_raw, const void* 
                         void* stream, char* err, int errlen) {
   return guarded(err, errlen, [&] {
     qbgdn::NbProblem p;
-    std::string why = nb_resolve(desc, p);
+    std::string why = nb_resolve(desc, p, true, false);
     const bool any = why.empty() && p.BT > 0;
     const size_t el = why.empty() && p.bf16 ? 2 : 4;
     const PtrCheck c[] = {{"q_raw", q_raw, any, 16}, {"k_raw", k_raw, any, 16}, {"a", a, any, el},
@@ -412,7 +414,7 @@ int qb_gdn_prologue_bwd(const qb_gdn_desc* desc, const void* q_raw, const void* 
                         float* ddt_bias, void* workspace, void* stream, char* err, int errlen) {
   return guarded(err, errlen, [&] {
     qbgdn::NbProblem p;
-    std::string why = nb_resolve(desc, p);
+    std::string why = nb_resolve(desc, p, true, false);
     const bool any = why.empty() && p.BT > 0;
     const size_t el = why.empty() && p.bf16 ? 2 : 4;
     const PtrCheck c[] = {{"q_raw", q_raw, any, 16},   {"k_raw", k_raw, any, 16},     {"a", a, any, el},
@@ -442,7 +444,7 @@ int qb_gdn_epilogue_fwd(const qb_gdn_desc* desc, const void* y, const void* z, c
                         void* stream, char* err, int errlen) {
   return guarded(err, errlen, [&] {
     qbgdn::NbProblem p;
-    std::string why = nb_resolve(desc, p);
+    std::string why = nb_resolve(desc, p, false, true);
     if (why.empty() && !(eps > 0.f)) why = "gated delta neighbours: eps must be positive";
     const bool any = why.empty() && p.BT > 0;
     const PtrCheck c[] = {{"y", y, any, 16}, {"z", z, any, 16}, {"norm_w", norm_w, true, 16}, {"o", o, any, 16}};
@@ -466,7 +468,7 @@ int qb_gdn_epilogue_bwd(const qb_gdn_desc* desc, const void* y, const void* z, c
                         int errlen) {
   return guarded(err, errlen, [&] {
     qbgdn::NbProblem p;
-    std::string why = nb_resolve(desc, p);
+    std::string why = nb_resolve(desc, p, false, true);
     if (why.empty() && !(eps > 0.f)) why = "gated delta neighbours: eps must be positive";
     const bool any = why.empty() && p.BT > 0;
     const PtrCheck c[] = {{"y", y, any, 16},       {"z", z, any, 16},   {"norm_w", norm_w, true, 16},

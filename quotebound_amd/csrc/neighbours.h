@@ -66,7 +66,9 @@ struct NbEpilogueGrad {
   float* dw;  // [Dv]
 };
 
-const char* nb_supports(const NbProblem& p);
+// Why the kernels cannot run p (nullptr when they can): the prologue uses Dk, the epilogue Dv; with neither flag,
+// at least one of the two must be a width they take.
+const char* nb_supports(const NbProblem& p, bool uses_dk, bool uses_dv);
 size_t nb_workspace_bytes(const NbProblem& p);
 hipError_t nb_prologue_fwd(const NbProblem& p, const NbPrologue& x, hipStream_t s);
 hipError_t nb_prologue_bwd(const NbProblem& p, const NbPrologueGrad& x, void* ws, hipStream_t s);

@@ -447,9 +447,11 @@ hipError_t by_width(int D, F&& f) {
 
 }  // namespace
 
-const char* nb_supports(const NbProblem& p) {
-  if (p.Dk != 64 && p.Dk != 128 && p.Dk != 256) return "the neighbour kernels need Dk of 64, 128 or 256";
-  if (p.Dv != 64 && p.Dv != 128 && p.Dv != 256) return "the neighbour kernels need Dv of 64, 128 or 256";
+const char* nb_supports(const NbProblem& p, bool uses_dk, bool uses_dv) {
+  auto ok = [](int D) { return D == 64 || D == 128 || D == 256; };
+  if (uses_dk && !ok(p.Dk)) return "the neighbour kernels need Dk of 64, 128 or 256";
+  if (uses_dv && !ok(p.Dv)) return "the neighbour kernels need Dv of 64, 128 or 256";
+  if (!uses_dk && !uses_dv && !ok(p.Dk) && !ok(p.Dv)) return "the neighbour kernels need Dk or Dv of 64, 128 or 256";
   if (p.Hv > 256) return "the neighbour kernels need at most 256 value heads";
   return nullptr;
 }

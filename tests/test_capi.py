@@ -125,6 +125,11 @@ def test_neighbours_errors_before_any_gpu_work(lib):
     with pytest.raises(RuntimeError, match="Dk of 64, 128 or 256"):
         _lib.prologue_fwd(d, 16, 16, 16, 16, 16, 16, 16, 16, 16, 16, None)
     assert _lib.neighbours_workspace_bytes(d) == 0
+    d, _ = desc(Dk=128, Dv=32)  # the prologue runs on Dk alone, the epilogue on Dv alone
+    with pytest.raises(RuntimeError, match="a_log is null"):
+        _lib.prologue_fwd(d, 16, 16, 16, 16, None, 16, 16, 16, 16, 16, None)
+    with pytest.raises(RuntimeError, match="Dv of 64, 128 or 256"):
+        _lib.epilogue_fwd(d, 16, 16, 16, 1e-6, 16, None)
     d, _ = desc()
     assert _lib.neighbours_workspace_bytes(d) > 0
     with pytest.raises(RuntimeError, match="a_log is null"):
