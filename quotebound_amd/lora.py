@@ -303,7 +303,8 @@ def loss_and_grads(w, adapters, tokens, positions, targets, cfg):
     params = [t.detach().requires_grad_(True) for t in adapter_list(adapters)]
     loss = mean_loss(w, with_adapter_list(adapters, params), tokens, positions, targets, cfg)
     grads = torch.autograd.grad(loss, params)
-    norm = torch.sqrt(sum((g.double() * g.double()).sum() for g in grads)).float()
+    # The global norm in float32 (src/adamw.cpp:17-21), from one multi-tensor launch of per-array norms.
+    norm = torch.linalg.vector_norm(torch.stack(torch._foreach_norm(grads)))
     return loss.detach(), list(grads), norm
 
 
