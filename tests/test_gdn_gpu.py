@@ -12,7 +12,7 @@ import os
 import numpy as np
 import pytest
 
-from helpers import GRAD_NAMES, normwise, reference_case
+from helpers import GRAD_NAMES, normwise, reference_case, small_case
 from quotebound_amd import _lib
 
 pytestmark = pytest.mark.gpu
@@ -307,6 +307,64 @@ def test_empty_batch(torch_dev, design):
     torch.cuda.synchronize()
     assert y.shape == v.shape and torch.equal(s_out, s0)
     assert torch.equal(grads[5], ds_out) and all(t.numel() == 0 for t in grads[:5])
+
+
+def _random_shape(seed):
+    """A seeded draw of an odd shape: B 1-3 (or 2-6 packed sequences of 0-150 tokens), T 1-300, 1-4 value heads per
+    key head, Dk 32/64/128, Dv 32/64/96/128, bf16 or float32, with or without S0 and dS_out."""
+    r = np.random.default_rng(1000 + seed)
+    Hk = int(r.choice([1, 2, 4]))
+    Hv = Hk * int(r.integers(1, 5))
+    Dk = int(r.choice([32, 64, 128, 128]))
+    Dv = int(r.choice([32, 64, 96, 128]))
+    bf16 = bool(r.integers(0, 4) > 0)
+    if r.integers(0, 3) == 0:
+        lens = r.integers(0, 151, int(r.integers(2, 7))).tolist()
+        return dict(B=1, T=int(sum(lens)), Hk=Hk, Hv=Hv, Dk=Dk, Dv=Dv, bf16=bf16, lens=lens,
+                    s0=bool(r.integers(0, 2)), ds_out=bool(r.integers(0, 2)))
+    return dict(B=int(r.integers(1, 4)), T=int(r.integers(1, 301)), Hk=Hk, Hv=Hv, Dk=Dk, Dv=Dv, bf16=bf16, lens=None,
+                s0=bool(r.integers(0, 2)), ds_out=bool(r.integers(0, 2)))
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_random_shapes(torch_dev, oracle, seed):
+    """Both designs, wherever they take the shape, against the oracle on seeded odd shapes: forward and every
+    cotangent normwise within 2e-3 (bf16 inputs, float32 outputs) or 1e-5 (float32)."""
+    torch = torch_dev
+    from quotebound_amd.synthetic import round_bf16
+
+    c = _random_shape(seed)
+    B, T, Hk, Hv, Dk, Dv = c["B"], c["T"], c["Hk"], c["Hv"], c["Dk"], c["Dv"]
+    inp = small_case(B, T, Hk, Hv, Dk, Dv, seed=seed, s0=c["s0"], ds_out=c["ds_out"])
+    cu = None
+    if c["lens"] is not None:
+        cu = np.concatenate([[0], np.cumsum(c["lens"])]).astype(np.int32)
+        N = len(c["lens"])
+        r = np.random.default_rng(seed)
+        inp["s0"] = r.normal(0.0, 0.1, (N, Hv, Dv, Dk)) if c["s0"] else None
+        inp["ds_out"] = r.standard_normal((N, Hv, Dv, Dk)) if c["ds_out"] else None
+    for n in ("q", "k", "v", "beta", "dy"):
+        x = np.asarray(inp[n], np.float32)
+        inp[n] = round_bf16(x) if c["bf16"] else x
+    for n in ("g", "s0", "ds_out"):
+        if inp[n] is not None:
+            inp[n] = np.asarray(inp[n], np.float32)
+    exp = oracle.fwd_bwd(inp, cu_seqlens=cu, dtype=np.float32)
+    d = host_to_dev(torch, inp, torch.bfloat16 if c["bf16"] else torch.float32)
+    if c["bf16"]:
+        d["dy"] = d["dy"].float()
+    ran = 0
+    for design in DESIGNS:
+        desc, _ = _lib.make_desc(B, T, Hk, Hv, Dk, Dv, dtype=_lib.BF16 if c["bf16"] else _lib.F32, design=design,
+                                 cu_seqlens=cu)
+        if _lib.validate(desc):
+            continue
+        ran += 1
+        got = run(torch, d, design, cu=cu, need_s0_grad=True, out_f32=c["bf16"])
+        names = [n for n in OUT_NAMES if not (n == "ds0" and inp["s0"] is None and inp["ds_out"] is None)]
+        assert_close(got, exp, BF16_TOL if c["bf16"] else F32_TOL, names=names,
+                     label=f"seed {seed} {c} design {design}")
+    assert ran >= 1, c
 
 
 @pytest.mark.parametrize("design", DESIGNS, ids=DESIGN_IDS.get)
