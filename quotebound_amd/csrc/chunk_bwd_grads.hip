@@ -56,6 +56,12 @@ constexpr int ex1c = edbA + 2 * kC, etq = ex1c + 4 * kC;
 constexpr int kEndBytes = (etq + 2 * kC) * 4;
 constexpr int kSmemBytes = kLoopBytes > kEndBytes ? kLoopBytes : kEndBytes;
 
+// The key tile (16 positions j) that accumulator mi of the wave at position tile pw, half hw holds in dP^T and
+// dTb^T. Only tiles m <= pw carry work. For each pw the two halves together hold all four tiles; positions 0..31
+// alternate the tiles between halves so each half works on one of the tiles 0..pw, positions 32..63 split them in
+// halves. The busiest wave of the phase that accumulates them then runs 5 products in place of 6.
+__device__ __forceinline__ int key_tile(int pw, int hw, int mi) { return pw < 2 ? hw + 2 * mi : 2 * hw + mi; }
+
 template <typename OutT>
 __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) {
   constexpr int Dk = 128;
@@ -93,6 +99,60 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
   // Rows past the chunk's last row read as zeros.
   const auto krs = buffer_rsrc(kbase, uint32_t(L * sk) * 2u), qrs = buffer_rsrc(qbase, uint32_t(L * sk) * 2u);
 
+  // Global reads, kept in registers from issue to staging. A value head's tile (Tb and P rows hi and lo, thread ->
+  // row lt / 8, columns 8 (lt % 8) .. + 7, zeros above the diagonal blocks; and the per-position scalars, thread lt <
+  // 64) and one 32-row block of its state (S0 and dS rows, dY, v). dy and v go through buffer resources that end at
+  // the chunk's last row, so rows past it read as zeros without a branch.
+  struct TileIn {
+    bf16x8 tp[4];  // Tb hi, Tb lo, P hi, P lo
+    float sc[4];   // exp G, exp(G_63 - G), beta, G
+  };
+  struct BlockIn {
+    float4 xs[2], ys[2];  // S0, dS: thread -> row tid / 16, columns 8 (tid % 16) .. + 7
+    uint4 yraw;           // dY: thread -> position tid / 8, rows 4 (tid % 8) .. + 3
+    uint16_t vraw[4];     // v at the wave's accumulator positions (16 pw + 4g + jj, column 16 hw + li)
+  };
+  auto load_tile = [&](TileIn& ti, int hv, int lt) {
+    const Tile* tl = a.tiles + slot * a.Hv + hv;
+    if (lt < kC) ti.sc[0] = tl->gam[lt], ti.sc[1] = tl->dec[lt], ti.sc[2] = tl->beta[lt], ti.sc[3] = tl->G[lt];
+    const auto tr = buffer_rsrc(tl->tb[0], 4 * kTri * 2);  // tb[0], tb[1], p[0], p[1] are contiguous
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4) ti.tp[q4] = tri_ld8(tr, q4 * kTri, lt >> 3, (lt & 7) * 8);
+  };
+  auto load_rows = [&](float4 (&x)[2], const float* base, int hv, int r0, int lt) {
+    const float* p = base + ((slot * a.Hv + hv) * a.Dv + r0) * Dk + (lt >> 4) * Dk + (lt & 15) * 8;
+    x[0] = *reinterpret_cast<const float4*>(p);
+    x[1] = *reinterpret_cast<const float4*>(p + 4);
+  };
+  auto load_dy_v = [&](BlockIn& b, int hv, int r0, int lt) {
+    const int g = (lt >> 4) & 3, li = lt & 15, pw = (lt >> 6) & 3, hw = lt >> 8;
+    const auto yr = buffer_rsrc(dy + (tok * a.Hv + hv) * a.Dv + r0, uint32_t(L * sv) * uint32_t(sizeof(OutT)));
+    const auto vr = buffer_rsrc(a.v + (tok * a.Hv + hv) * a.Dv + r0, uint32_t(L * sv) * 2u);
+    const int iy = lt >> 3, r4 = (lt & 7) * 4;
+    if constexpr (kExactDy) {
+      const auto t2 = __builtin_amdgcn_raw_buffer_load_b64(yr, int(uint32_t(iy * sv + r4) * 2), 0, 0);
+      b.yraw = uint4{t2[0], t2[1], 0u, 0u};
+    } else {
+      b.yraw = buf_ld16(yr, uint32_t(iy * sv + r4) * 4);
+    }
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj)
+      b.vraw[jj] = buf_ld2(vr, uint32_t((16 * pw + 4 * g + jj) * sv + 16 * hw + li) * 2);
+  };
+  // A value head's tile and first block, issued one value head ahead (the first at the start, the others during
+  // the previous head's end phase), so no head waits on a global read before its first block.
+  auto load_head = [&](TileIn& ti, BlockIn& b, int hv) {
+    int lt = tid;
+    asm volatile("" : "+v"(lt));
+    load_tile(ti, hv, lt);
+    load_rows(b.xs, a.ckpt, hv, 0, lt);
+    load_rows(b.ys, a.dsend, hv, 0, lt);
+    load_dy_v(b, hv, 0, lt);
+  };
+  TileIn ti;
+  BlockIn nb;
+  load_head(ti, nb, hk * grp);
+
   // The chunk's K rows (A operands of K S0^T, K dS^T, K K^T; B of the K products of the end phase).
   for (int e = tid; e < kC * 16; e += kThreads) {
     const int t = e >> 4, c8 = (e & 15) * 8;
@@ -110,18 +170,15 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
     const int64_t sh = slot * a.Hv + hv;
     const Tile* tl = a.tiles + sh;
     __syncthreads();
-    if (tid < kC) gam[tid] = tl->gam[tid], dec[tid] = tl->dec[tid], bet[tid] = tl->beta[tid], Gf[tid] = tl->G[tid];
-    {  // Tb and P, hi and lo: thread -> row tid / 8, columns 8 (tid % 8) ..; zeros above the diagonal blocks
-      const int i = tid >> 3, c8 = (tid & 7) * 8, lt8 = swz(i, c8, kLT);
-      const auto tr = buffer_rsrc(tl->tb[0], 4 * kTri * 2);  // tb[0], tb[1], p[0], p[1] are contiguous
-      const bf16x8 v0 = tri_ld8(tr, 0, i, c8), v1 = tri_ld8(tr, kTri, i, c8);
-      const bf16x8 v2 = tri_ld8(tr, 2 * kTri, i, c8), v3 = tri_ld8(tr, 3 * kTri, i, c8);
-      *reinterpret_cast<bf16x8*>(TbL[0] + lt8) = v0;
-      *reinterpret_cast<bf16x8*>(TbL[1] + lt8) = v1;
-      *reinterpret_cast<bf16x8*>(PL[0] + lt8) = v2;
-      *reinterpret_cast<bf16x8*>(PL[1] + lt8) = v3;
+    if (tid < kC) gam[tid] = ti.sc[0], dec[tid] = ti.sc[1], bet[tid] = ti.sc[2], Gf[tid] = ti.sc[3];
+    {  // Tb and P, hi and lo
+      const int lt8 = swz(tid >> 3, (tid & 7) * 8, kLT);
+      *reinterpret_cast<bf16x8*>(TbL[0] + lt8) = ti.tp[0];
+      *reinterpret_cast<bf16x8*>(TbL[1] + lt8) = ti.tp[1];
+      *reinterpret_cast<bf16x8*>(PL[0] + lt8) = ti.tp[2];
+      *reinterpret_cast<bf16x8*>(PL[1] + lt8) = ti.tp[3];
     }
-    f32x4 dPt[2], dTbt[2], dQi[4];  // dPt, dTbt: key tiles m = 2 hw + mi; lane -> column i = ip, rows j
+    f32x4 dPt[2], dTbt[2], dQi[4];  // dPt, dTbt: key tiles m = key_tile(pw, hw, mi); lane -> column i = ip, rows j
 #pragma unroll
     for (int t = 0; t < 2; ++t) dPt[t] = zero4(), dTbt[t] = zero4();
 #pragma unroll
@@ -129,35 +186,6 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
     float gpart[4] = {0.f, 0.f, 0.f, 0.f}, hD[4] = {0.f, 0.f, 0.f, 0.f}, sds = 0.f;
     __syncthreads();
 
-    // One block's global reads (S0 and dS rows, dY, v), kept in registers from issue to staging. They are issued in
-    // three groups at three points of the previous block's work, so no wave stalls long on a full load queue. dy
-    // and v go through buffer resources that end at the chunk's last row, so rows past it read as zeros without a
-    // branch.
-    struct BlockIn {
-      float4 xs[2], ys[2];  // S0, dS: thread -> row tid / 16, columns 8 (tid % 16) .. + 7
-      uint4 yraw;           // dY: thread -> position tid / 8, rows 4 (tid % 8) .. + 3
-      uint16_t vraw[4];     // v at the wave's accumulator positions (16 pw + 4g + jj, column 16 hw + li)
-    };
-    auto load_rows = [&](float4 (&x)[2], const float* base, int r0, int lt) {
-      const float* p = base + (sh * a.Dv + r0) * Dk + (lt >> 4) * Dk + (lt & 15) * 8;
-      x[0] = *reinterpret_cast<const float4*>(p);
-      x[1] = *reinterpret_cast<const float4*>(p + 4);
-    };
-    auto load_dy_v = [&](BlockIn& b, int r0, int lt) {
-      const int g = (lt >> 4) & 3, li = lt & 15, pw = (lt >> 6) & 3, hw = lt >> 8;
-      const auto yr = buffer_rsrc(dy + (tok * a.Hv + hv) * a.Dv + r0, uint32_t(L * sv) * uint32_t(sizeof(OutT)));
-      const auto vr = buffer_rsrc(a.v + (tok * a.Hv + hv) * a.Dv + r0, uint32_t(L * sv) * 2u);
-      const int iy = lt >> 3, r4 = (lt & 7) * 4;
-      if constexpr (kExactDy) {
-        const auto t2 = __builtin_amdgcn_raw_buffer_load_b64(yr, int(uint32_t(iy * sv + r4) * 2), 0, 0);
-        b.yraw = uint4{t2[0], t2[1], 0u, 0u};
-      } else {
-        b.yraw = buf_ld16(yr, uint32_t(iy * sv + r4) * 4);
-      }
-#pragma unroll
-      for (int jj = 0; jj < 4; ++jj)
-        b.vraw[jj] = buf_ld2(vr, uint32_t((16 * pw + 4 * g + jj) * sv + 16 * hw + li) * 2);
-    };
     // The end phase's inputs (T rows hi and lo, Q rows, as bf16 bits), loaded during the value head's last block
     // into the registers the next block's reads would use: thread -> T row tid / 8, columns 8 (tid % 8) .. + 7
     // (zeros above the diagonal blocks), and Q row e / 16, columns 8 (e % 16) .. + 7 for e = tid, tid + 512.
@@ -171,14 +199,6 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
         b.ys[q2] = __builtin_bit_cast(float4, buf_ld16(qrs, uint32_t(t * sk + c8) * 2));
       }
     };
-    BlockIn nb;
-    {
-      int lt0 = tid;
-      asm volatile("" : "+v"(lt0));
-      load_rows(nb.xs, a.ckpt, 0, lt0);
-      load_rows(nb.ys, a.dsend, 0, lt0);
-      load_dy_v(nb, 0, lt0);
-    }
 
     // One 32-row block of the state. The last block of the value head (more = false) loads the end phase's inputs
     // instead of the next block's: it is a separate copy of the code, so that every copy issues the same loads in
@@ -219,7 +239,7 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
       for (int jj = 0; jj < 4; ++jj) vv[jj] = bf16_to_f32(nb.vraw[jj]);
       __syncthreads();
       if constexpr (more)
-        load_rows(nb.xs, a.ckpt, r0 + 32, lt);  // the next block's reads, first group
+        load_rows(nb.xs, a.ckpt, hv, r0 + 32, lt);  // the next block's reads, first group
       else
         load_end(nb, lt);
 
@@ -246,15 +266,17 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
       }
       put4(sb + oRh, sb + oRl, swz(r, i0, kLP), rv[0], rv[1], rv[2], rv[3]);
       __syncthreads();
-      if constexpr (more) load_rows(nb.ys, a.dsend, r0 + 32, lt);
+      if constexpr (more) load_rows(nb.ys, a.dsend, hv, r0 + 32, lt);
 
       // Phase 2: Delta = Tb R and dDelta = P^T dY + D KdS (rows: the wave's positions; lane: row r).
       f32x4 dl = zero4(), dd;
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
-        const int at = swz(r, 32 * s + 8 * g, kLP), atb = swz(ip, 32 * s + 8 * g, kLT);
-        const Split8 TbA{lds8(TbL[0] + atb), lds8(TbL[1] + atb)};
-        dl = mma3(dl, TbA, Split8{lds8(sb + oRh + at), lds8(sb + oRl + at)});
+        if (s == 0 || pw >= 2) {  // Tb is zero above the diagonal blocks: rows 0..31 end at column 31
+          const int at = swz(r, 32 * s + 8 * g, kLP), atb = swz(ip, 32 * s + 8 * g, kLT);
+          const Split8 TbA{lds8(TbL[0] + atb), lds8(TbL[1] + atb)};
+          dl = mma3(dl, TbA, Split8{lds8(sb + oRh + at), lds8(sb + oRl + at)});
+        }
       }
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj) dd[jj] = dec[i0 + jj] * kds[jj];
@@ -282,7 +304,7 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
         put4(sb + odDh, sb + odDl, swz(r, i0, kLP), dd[0], dd[1], dd[2], dd[3]);
       }
       __syncthreads();
-      if constexpr (more) load_dy_v(nb, r0 + 32, lt);
+      if constexpr (more) load_dy_v(nb, hv, r0 + 32, lt);
 
       // Phase 3: dR = Tb^T dDelta; dP^T += Delta dY^T and dTb^T += R dDelta^T over this half's key tiles.
       {
@@ -310,7 +332,7 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
         const Split8 BdD{lds_tr8s(sb + odDh + 16 * pw, kLP, lt), lds_tr8s(sb + odDl + 16 * pw, kLP, lt)};
 #pragma unroll
         for (int mi = 0; mi < 2; ++mi) {
-          const int m = 2 * hw + mi;
+          const int m = key_tile(pw, hw, mi);
           if (m <= pw) {
             // Delta and R rows j of key tile m as A (m = j, k = r).
             const Split8 AD{lds_tr8s(sb + oDh + 16 * m, kLP, lt), lds_tr8s(sb + oDl + 16 * m, kLP, lt)};
@@ -365,10 +387,10 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
     }
     __syncthreads();
 
-    // E1: Q rows and T (hi, lo) into the end-phase region. Per lane, at i = ip and j = 16 (2 hw + mi) + 4g + jj (dP
-    // and dTb masked to j <= i): the row and column sums of dP * P (the P factor's part of dG), P * M with
-    // M_ij = exp(G_i - G_j) over P's entries, and dTb diag(beta), both as hi and lo in place of Tb and P (each lane
-    // rewrites only the P entries it has just read).
+    // E1: Q rows and T (hi, lo) into the end-phase region. Per lane, at i = ip and
+    // j = 16 key_tile(pw, hw, mi) + 4g + jj (dP and dTb masked to j <= i): the row and column sums of dP * P (the P
+    // factor's part of dG), P * M with M_ij = exp(G_i - G_j) over P's entries, and dTb diag(beta), both as hi and lo
+    // in place of Tb and P (each lane rewrites only the P entries it has just read).
     {
       {
         const int at = swz(lt >> 3, (lt & 7) * 8, kLT);
@@ -380,12 +402,13 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
           *reinterpret_cast<uint4*>(sb + eQb + swz(e >> 4, (e & 15) * 8, kLK)) = __builtin_bit_cast(uint4, nb.ys[q2]);
         }
       }
+      if (e + 1 < grp) load_head(ti, nb, hv + 1);  // nb is free from here
       // Row sums (over j) add up over g here and over hw in dG; column sums (over i) over li here and over pw in dG.
       float prow = 0.f;
       const float gi = Gf[ip];
 #pragma unroll
       for (int mi = 0; mi < 2; ++mi) {
-        const int j0 = 16 * (2 * hw + mi) + 4 * g, at = swz(ip, j0, kLT);
+        const int j0 = 16 * key_tile(pw, hw, mi) + 4 * g, at = swz(ip, j0, kLT);
         const uint2 ph = *reinterpret_cast<const uint2*>(PL[0] + at);
         const uint2 pl = *reinterpret_cast<const uint2*>(PL[1] + at);
         const uint32_t hw4[2] = {ph.x, ph.y}, lw4[2] = {pl.x, pl.y};
@@ -419,7 +442,7 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
     {
 #pragma unroll
       for (int mi = 0; mi < 2; ++mi) {
-        const int j0 = 16 * (2 * hw + mi) + 4 * g, at = swz(ip, j0, kLT);
+        const int j0 = 16 * key_tile(pw, hw, mi) + 4 * g, at = swz(ip, j0, kLT);
         const uint2 th = *reinterpret_cast<const uint2*>(sb + eTh + at);
         const uint2 tlo = *reinterpret_cast<const uint2*>(sb + eTl + at);
         const uint32_t hw4[2] = {th.x, th.y}, lw4[2] = {tlo.x, tlo.y};
