@@ -161,8 +161,8 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
   f32x4 dQ[4], dK[4];  // columns 16 (4 hw + t) + li, rows 16 pw + 4 g + jj
 #pragma unroll
   for (int t = 0; t < 4; ++t) dQ[t] = zero4(), dK[t] = zero4();
-  // (K K^T)[p][m], rows p = 16 pw + 4g + jj, columns m = 16 (2 hw + mi) + li; zero above tile pw. The same for every
-  // value head of the group: formed in the first one's end phase.
+  // (K K^T)[p][m], rows p = 16 pw + 4g + jj, columns m = 16 key_tile(pw, hw, mi) + li; zero above tile pw. The same
+  // for every value head of the group: formed in the first one's end phase.
   f32x4 kk[2];
 
   for (int e = 0; e < grp; ++e) {
@@ -473,7 +473,7 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
       if (e == 0) {
 #pragma unroll
         for (int mi = 0; mi < 2; ++mi) {
-          const int m = 2 * hw + mi;
+          const int m = key_tile(pw, hw, mi);
           kk[mi] = zero4();
           if (m <= pw) {
 #pragma unroll
@@ -482,16 +482,22 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
           }
         }
       }
+      // P * M is zero above the diagonal: rows i < 32 end at column 31, and columns j >= 32 start at row 32.
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
-        const int at = swz(ip, 32 * s + 8 * g, kLT);
-        const Split8 Apm{lds8(TbL[0] + at), lds8(TbL[1] + at)};  // (P * M) rows i = ip, k = j
-        const Split8 Apmt{lds_tr8s(TbL[0] + 32 * s * kLT + 16 * pw, kLT, lt),
-                          lds_tr8s(TbL[1] + 32 * s * kLT + 16 * pw, kLT, lt)};  // (P * M)^T rows j = ip, k = i
+        if (s == 0 || pw >= 2) {
+          const int at = swz(ip, 32 * s + 8 * g, kLT);
+          const Split8 Apm{lds8(TbL[0] + at), lds8(TbL[1] + at)};  // (P * M) rows i = ip, k = j
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          dQ[t] = mma2(dQ[t], Apm, lds_tr8s(Kres + 32 * s * kLK + 16 * (4 * hw + t), kLK, lt));
-          dK[t] = mma2(dK[t], Apmt, lds_tr8s(sb + eQb + 32 * s * kLK + 16 * (4 * hw + t), kLK, lt));
+          for (int t = 0; t < 4; ++t)
+            dQ[t] = mma2(dQ[t], Apm, lds_tr8s(Kres + 32 * s * kLK + 16 * (4 * hw + t), kLK, lt));
+        }
+        if (s == 1 || pw < 2) {
+          const Split8 Apmt{lds_tr8s(TbL[0] + 32 * s * kLT + 16 * pw, kLT, lt),
+                            lds_tr8s(TbL[1] + 32 * s * kLT + 16 * pw, kLT, lt)};  // (P * M)^T rows j = ip, k = i
+#pragma unroll
+          for (int t = 0; t < 4; ++t)
+            dK[t] = mma2(dK[t], Apmt, lds_tr8s(sb + eQb + 32 * s * kLK + 16 * (4 * hw + t), kLK, lt));
         }
       }
 #pragma unroll
@@ -508,23 +514,29 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
     }
     __syncthreads();
 
-    // E3: dA = -T^T Z below the diagonal (rows p = i0 + jj, columns m = 16 (2 hw + mi) + li, as kk), and at once
-    // its products with E = exp(G_p - G_m) and K K^T: the A part of dbeta (row sums), of dG (row and column sums),
-    // and dKK = diag(beta) (dA * E), stored as dKK^T.
+    // E3: dA = -T^T Z below the diagonal (rows p = i0 + jj, columns m = 16 key_tile(pw, hw, mi) + li, as kk), and at
+    // once its products with E = exp(G_p - G_m) and K K^T: the A part of dbeta (row sums), of dG (row and column
+    // sums), and dKK = diag(beta) (dA * E), stored as dKK^T.
     {
+      // Only tiles mt <= pw are kept (mcol < p), and T^T rows p >= 32 are zero below column 32.
       Split8 AT[2];  // T^T rows p = ip, k = i
 #pragma unroll
       for (int s = 0; s < 2; ++s)
-        AT[s] = Split8{lds_tr8s(sb + eTh + 32 * s * kLT + 16 * pw, kLT, lt), lds_tr8s(sb + eTl + 32 * s * kLT + 16 * pw, kLT, lt)};
+        AT[s] = Split8{lds_tr8s(sb + eTh + 32 * s * kLT + 16 * pw, kLT, lt),
+                       lds_tr8s(sb + eTl + 32 * s * kLT + 16 * pw, kLT, lt)};
       float rowp[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int mi = 0; mi < 2; ++mi) {
-        const int mt = 2 * hw + mi, mcol = 16 * mt + li;
+        const int mt = key_tile(pw, hw, mi), mcol = 16 * mt + li;
         f32x4 da = zero4();
+        if (mt <= pw) {
 #pragma unroll
-        for (int s = 0; s < 2; ++s) {
-          const int ab = swz(mcol, 32 * s + 8 * g, kLT);
-          da = mma3(da, AT[s], Split8{lds8(sb + eZh + ab), lds8(sb + eZl + ab)});
+          for (int s = 0; s < 2; ++s) {
+            if (s == 1 || pw < 2) {
+              const int ab = swz(mcol, 32 * s + 8 * g, kLT);
+              da = mma3(da, AT[s], Split8{lds8(sb + eZh + ab), lds8(sb + eZl + ab)});
+            }
+          }
         }
         float colp = 0.f, kkt[4];
 #pragma unroll
@@ -560,7 +572,9 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
         const bf16x8 B = lds_tr8s(Kres + 32 * s * kLK + 16 * (4 * hw + t), kLK, lt);
-        dK[t] = mma2(mma2(dK[t], A1, B), A2, B);
+        // dKK is strictly lower: dKK[j][i] needs i < j, dKK[i][j] needs i > j.
+        if (s == 0 || pw >= 2) dK[t] = mma2(dK[t], A1, B);
+        if (s == 1 || pw < 2) dK[t] = mma2(dK[t], A2, B);
       }
     }
     // E5 (one wave): dG per position, dg = its reverse cumulative sum (a suffix scan over the wave), and dbeta.
