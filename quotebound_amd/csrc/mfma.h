@@ -28,15 +28,24 @@ struct Split8 {
   bf16x8 hi, lo;
 };
 
+typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
+typedef float f32x2v __attribute__((ext_vector_type(2)));
+
+// x0, x1 as packed bf16 pairs hi = rne(x) and lo = rne(x - hi) (x = hi + lo to about 16 bits): two values per
+// v_cvt_pk_bf16_f32, so neither pair needs packing, and hi widens back to float by a shift or a mask.
+__device__ __forceinline__ void split2(float x0, float x1, uint32_t& hi, uint32_t& lo) {
+  hi = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2v{x0, x1}, bf16x2v));
+  const float h0 = __uint_as_float(hi << 16), h1 = __uint_as_float(hi & 0xffff0000u);
+  lo = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2v{x0 - h0, x1 - h1}, bf16x2v));
+}
+
 __device__ __forceinline__ Split8 split8(const float* x) {
-  Split8 s;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const __bf16 h = (__bf16)x[j];
-    s.hi[j] = h;
-    s.lo[j] = (__bf16)(x[j] - (float)h);
-  }
-  return s;
+  uint4 h, l;
+  split2(x[0], x[1], h.x, l.x);
+  split2(x[2], x[3], h.y, l.y);
+  split2(x[4], x[5], h.z, l.z);
+  split2(x[6], x[7], h.w, l.w);
+  return Split8{__builtin_bit_cast(bf16x8, h), __builtin_bit_cast(bf16x8, l)};
 }
 
 __device__ __forceinline__ bf16x8 round8(const float* x) {
@@ -128,13 +137,10 @@ struct Split4 {
   uint2 hi, lo;
 };
 __device__ __forceinline__ Split4 split4(float x0, float x1, float x2, float x3) {
-  const __bf16 h0 = (__bf16)x0, h1 = (__bf16)x1, h2 = (__bf16)x2, h3 = (__bf16)x3;
-  const __bf16 l0 = (__bf16)(x0 - (float)h0), l1 = (__bf16)(x1 - (float)h1);
-  const __bf16 l2 = (__bf16)(x2 - (float)h2), l3 = (__bf16)(x3 - (float)h3);
-  auto pack = [](__bf16 a, __bf16 b) {
-    return uint32_t(__builtin_bit_cast(uint16_t, a)) | (uint32_t(__builtin_bit_cast(uint16_t, b)) << 16);
-  };
-  return Split4{uint2{pack(h0, h1), pack(h2, h3)}, uint2{pack(l0, l1), pack(l2, l3)}};
+  Split4 s;
+  split2(x0, x1, s.hi.x, s.lo.x);
+  split2(x2, x3, s.hi.y, s.lo.y);
+  return s;
 }
 
 }  // namespace qbgdn
