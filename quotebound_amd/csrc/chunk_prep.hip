@@ -172,20 +172,19 @@ __global__ __launch_bounds__(kThreads) void chunk_prep_kernel(ChunkArgs a) {
         }
         W = mma3(W, split8(x), split8(y));
       }
-      s16x4 th, tl, wh, wl;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float t = Tm[tri_off(16 * I + li, 16 * I + 4 * g + j)];  // T_II rows li, k = 4g + j
-        const __bf16 a = (__bf16)t, b = (__bf16)W[j];
-        th[j] = __builtin_bit_cast(short, a);
-        tl[j] = __builtin_bit_cast(short, (__bf16)(t - (float)a));
-        wh[j] = __builtin_bit_cast(short, b);
-        wl[j] = __builtin_bit_cast(short, (__bf16)(W[j] - (float)b));
+      uint2 th, tl, wh, wl;  // T_II rows li, k = 4g + j, and W, as packed hi / lo pairs
+      {
+        const int r = 16 * I + li, c = 16 * I + 4 * g;
+        split2(Tm[tri_off(r, c)], Tm[tri_off(r, c + 1)], th.x, tl.x);
+        split2(Tm[tri_off(r, c + 2)], Tm[tri_off(r, c + 3)], th.y, tl.y);
+        split2(W[0], W[1], wh.x, wl.x);
+        split2(W[2], W[3], wh.y, wl.y);
       }
       f32x4 R = zero4();
-      R = mma16(R, th, wh);
-      R = mma16(R, th, wl);
-      R = mma16(R, tl, wh);
+      const auto v4 = [](uint2 x) { return __builtin_bit_cast(s16x4, x); };
+      R = mma16(R, v4(th), v4(wh));
+      R = mma16(R, v4(th), v4(wl));
+      R = mma16(R, v4(tl), v4(wh));
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj) Tm[tri_off(16 * I + 4 * g + jj, 16 * J + li)] = -R[jj];
     }
@@ -197,23 +196,22 @@ __global__ __launch_bounds__(kThreads) void chunk_prep_kernel(ChunkArgs a) {
   {
     const int i = tid >> 2, j0 = (tid & 3) * 16;
     if ((j0 >> 4) <= (i >> 4)) {
-      bf16x8 th[2], tl[2], bh[2], bl[2];
+      uint32_t th[8], tl[8], bh[8], bl[8];  // packed bf16 pairs, columns j0 + 2p, j0 + 2p + 1
 #pragma unroll
-      for (int u = 0; u < 16; ++u) {
-        const float t = Tm[tri_off(i, j0 + u)], x = t * Bs[j0 + u];
-        const __bf16 ht = (__bf16)t, hx = (__bf16)x;
-        th[u >> 3][u & 7] = ht;
-        tl[u >> 3][u & 7] = (__bf16)(t - (float)ht);
-        bh[u >> 3][u & 7] = hx;
-        bl[u >> 3][u & 7] = (__bf16)(x - (float)hx);
+      for (int p2 = 0; p2 < 8; ++p2) {
+        const int j = j0 + 2 * p2;
+        const float t0 = Tm[tri_off(i, j)], t1 = Tm[tri_off(i, j + 1)];
+        split2(t0, t1, th[p2], tl[p2]);
+        split2(t0 * Bs[j], t1 * Bs[j + 1], bh[p2], bl[p2]);
       }
       const int at = tri_off(i, j0);
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
-        *reinterpret_cast<bf16x8*>(tile->t[0] + at + 8 * h) = th[h];
-        *reinterpret_cast<bf16x8*>(tile->t[1] + at + 8 * h) = tl[h];
-        *reinterpret_cast<bf16x8*>(tile->tb[0] + at + 8 * h) = bh[h];
-        *reinterpret_cast<bf16x8*>(tile->tb[1] + at + 8 * h) = bl[h];
+        const int q = 4 * h;
+        *reinterpret_cast<uint4*>(tile->t[0] + at + 8 * h) = uint4{th[q], th[q + 1], th[q + 2], th[q + 3]};
+        *reinterpret_cast<uint4*>(tile->t[1] + at + 8 * h) = uint4{tl[q], tl[q + 1], tl[q + 2], tl[q + 3]};
+        *reinterpret_cast<uint4*>(tile->tb[0] + at + 8 * h) = uint4{bh[q], bh[q + 1], bh[q + 2], bh[q + 3]};
+        *reinterpret_cast<uint4*>(tile->tb[1] + at + 8 * h) = uint4{bl[q], bl[q + 1], bl[q + 2], bl[q + 3]};
       }
     }
   }

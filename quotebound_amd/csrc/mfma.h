@@ -48,13 +48,6 @@ __device__ __forceinline__ Split8 split8(const float* x) {
   return Split8{__builtin_bit_cast(bf16x8, h), __builtin_bit_cast(bf16x8, l)};
 }
 
-__device__ __forceinline__ bf16x8 round8(const float* x) {
-  bf16x8 r;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) r[j] = (__bf16)x[j];
-  return r;
-}
-
 // acc += A * B for split operands (three MFMAs).
 __device__ __forceinline__ f32x4 mma3(f32x4 c, const Split8& a, const Split8& b) {
   c = mma(c, a.hi, b.hi);
