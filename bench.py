@@ -5,8 +5,15 @@ workload's tokens, inputs resident in HBM before the timed region. value = token
 design's, timed with nothing between the kernels. Each kernel's duration comes from a second run of as many steps
 with HIP events the library records on its launch stream around each kernel (the descriptor's trace_events);
 the roofline object is for the kernel with the most time per step, its algorithmic work per launch
-divided by its mean duration. cpu_baseline times the oracle (the CPU restatement, float32, OpenMP) on the host on
-the same inputs.
+divided by its mean duration. A kernel's algorithmic bytes are the compulsory tensors it reads or writes in the
+caller's buffers plus the 64-token checkpoints it writes or reads (KERNEL_IO); the design's own intermediates it
+moves (chunk tiles, chunk-end cotangents) are reported apart as design_bytes_per_launch. step_roofline is the whole
+step against the compulsory I/O plus the checkpoints written once and read once. cpu_baseline times the oracle (the
+CPU restatement, float32, OpenMP) on the host on the same inputs.
+
+The line also carries the 9B and packed 4B layer shapes (workloads, each with its own rooflines), the reference
+bench's T sweep at the 4B head shape (t_sweep), the one-token inference step (decode), the layer's pointwise
+neighbours and the LoRA training step; --path-only leaves those out.
 
 python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--design auto|1|2] [--workload qwen35_4b] [--no-cpu]
                 [--copy-probe-mib N] [--path-only]
@@ -55,34 +62,59 @@ class Hip:
         return ms.value
 
 
-def algorithmic_work(w, kernel, nc, design):
-    """(kind, amount per launch) for a kernel: "bytes" of the HBM traffic the kernel cannot avoid (each input read
-    once, each output written once, at their storage types), or "flops" of the recurrent algorithm (7 Dk Dv per
-    token and value head forward, 15 backward; recompute not credited)."""
+def _sizes(w, nc):
+    """Byte sizes of the path's tensors at their storage types (bf16 or float32 I/O, float32 g and states)."""
     BT, Hk, Hv, Dk, Dv = w.B * w.T, w.Hk, w.Hv, w.Dk, w.Dv
     io = 2 if w.dtype == "bf16" else 4
-    qk = 2 * BT * Hk * Dk * io
-    vv = BT * Hv * Dv * io
-    scal = BT * Hv * (4 + io)
-    states = nc * Hv * Dv * Dk * 4
-    tg = nc * Hv * (64 * 64 * 4 + 64 * 8)
-    fin = w.n_states * Hv * Dv * Dk * 4
-    s0 = fin if w.s0_std > 0 else 0
-    if kernel == "chunk_prep":
-        return "bytes", qk / 2 + scal + tg
-    if kernel == "chunk_fwd":
-        return "bytes", qk + vv + BT * Hv * io + tg + vv + states + s0 + fin
-    if kernel == "chunk_bwd_state":
-        return "bytes", qk + vv + BT * Hv * io + tg + states + vv + fin
-    if kernel == "chunk_bwd_grads":
-        return "bytes", qk + 2 * vv + scal + tg + 2 * states + qk + BT * Hv * (4 + io)
+    state = Hv * Dv * Dk * 4
+    return {
+        "q": BT * Hk * Dk * io, "k": BT * Hk * Dk * io, "v": BT * Hv * Dv * io, "y": BT * Hv * Dv * io,
+        "dy": BT * Hv * Dv * io, "dq": BT * Hk * Dk * io, "dk": BT * Hk * Dk * io, "dv": BT * Hv * Dv * io,
+        "g": BT * Hv * 4, "dg": BT * Hv * 4, "beta": BT * Hv * io, "dbeta": BT * Hv * io,
+        "s0": w.n_states * state if w.s0_std > 0 else 0, "s_out": w.n_states * state,
+        "ds_out": w.n_states * state if w.ds_out else 0, "ds0": w.n_states * state,
+        # the checkpoints: every chunk-start state read once by the backward, written by the forward except each
+        # sequence's first (its initial state)
+        "ckpt_read": nc * state, "ckpt_write": (nc - w.n_states) * state,
+    }
+
+
+# Each kernel's share of the step's algorithmic bytes: the compulsory tensors it reads or writes in the caller's
+# buffers, plus the checkpoints it writes or reads, each counted once. Tensors a kernel only sees through the
+# design's own intermediates (the chunk tiles, the chunk-end cotangents) are not counted here but in DESIGN_IO.
+KERNEL_IO = {
+    "chunk_prep": ("q", "k", "g", "beta"),
+    "chunk_fwd": ("q", "k", "v", "s0", "y", "s_out", "ckpt_write"),
+    "chunk_bwd_state": ("q", "k", "dy", "ds_out", "dv", "ds0"),
+    "chunk_bwd_grads": ("q", "k", "v", "dy", "g", "beta", "ckpt_read", "dq", "dk", "dg", "dbeta"),
+}
+# The design's own intermediates each kernel writes or reads: "tiles" (the per-chunk records prep writes after the
+# states in ckpt) and "dsend" (the chunk-end state cotangents the backward state pass hands to the gradient kernel).
+DESIGN_IO = {
+    "chunk_prep": ("tiles",),
+    "chunk_fwd": ("tiles",),
+    "chunk_bwd_state": ("tiles", "dsend"),
+    "chunk_bwd_grads": ("tiles", "dsend"),
+}
+
+
+def algorithmic_work(w, kernel, nc, tiles_bytes=0):
+    """(kind, amount per launch, design bytes per launch) for a kernel. kind "bytes": its share of the step's
+    algorithmic HBM bytes (KERNEL_IO), with the design's intermediates it moves reported apart. kind "flops" (the
+    recurrent design): the recurrent algorithm's flops, 7 Dk Dv per token and value head forward, 15 backward
+    (recompute not credited)."""
+    s = _sizes(w, nc)
+    BT, Hv, Dk, Dv = w.B * w.T, w.Hv, w.Dk, w.Dv
+    if kernel in KERNEL_IO:
+        design = {"tiles": tiles_bytes, "dsend": s["ckpt_read"]}
+        return "bytes", sum(s[n] for n in KERNEL_IO[kernel]), sum(design[n] for n in DESIGN_IO[kernel])
     if kernel == "rec_fwd":
-        return "flops", 7.0 * Dk * Dv * BT * Hv
+        return "flops", 7.0 * Dk * Dv * BT * Hv, 0
     if kernel == "rec_bwd":
-        return "flops", 15.0 * Dk * Dv * BT * Hv
+        return "flops", 15.0 * Dk * Dv * BT * Hv, 0
     if kernel == "rec_reduce":
         nblk = (Dv + 15) // 16
-        return "bytes", 2 * BT * Hv * nblk * (Dk + 1) * 4 + qk + BT * Hv * (4 + io)
+        return "bytes", sum(s[n] for n in ("g", "dq", "dk", "dg", "dbeta")), 2 * BT * Hv * nblk * (Dk + 1) * 4
     raise KeyError(kernel)
 
 
@@ -90,16 +122,13 @@ def step_roof_us(w, nc):
     """The whole fwd+bwd step's roofline time: max(bytes_alg / HBM peak, flops_alg / MFMA peak), bytes_alg = the
     compulsory bf16/f32 I/O plus the 64-token fp32 checkpoints written once and read once, flops_alg = 22 Dk Dv per
     token and value head."""
-    BT, Hk, Hv, Dk, Dv = w.B * w.T, w.Hk, w.Hv, w.Dk, w.Dv
-    io = 2 if w.dtype == "bf16" else 4
-    fin = w.n_states * Hv * Dv * Dk * 4
-    s0 = fin if w.s0_std > 0 else 0
-    fwd = 2 * BT * Hk * Dk * io + BT * Hv * Dv * io + BT * Hv * (4 + io) + s0 + BT * Hv * Dv * io + fin
-    bwd = 2 * BT * Hk * Dk * io + BT * Hv * Dv * io + BT * Hv * (4 + io) + BT * Hv * Dv * io \
-        + 2 * BT * Hk * Dk * io + BT * Hv * Dv * io + BT * Hv * (4 + io) + s0
-    ckpt = (nc - w.n_states) * Hv * Dv * Dk * 4 + nc * Hv * Dv * Dk * 4
-    nbytes = fwd + bwd + ckpt
-    flops = 22.0 * Dk * Dv * BT * Hv
+    s = _sizes(w, nc)
+    fwd = ("q", "k", "v", "g", "beta", "s0", "y", "s_out")
+    bwd = ("q", "k", "v", "g", "beta", "dy", "ds_out", "dq", "dk", "dv", "dg", "dbeta", "ds0")
+    nbytes = sum(s[n] for n in fwd) + sum(s[n] for n in bwd) + s["ckpt_write"] + s["ckpt_read"]
+    if w.s0_std <= 0 and not w.ds_out:
+        nbytes -= s["ds0"]  # no initial state and no final-state cotangent: dS0 is not asked for
+    flops = 22.0 * w.Dk * w.Dv * w.B * w.T * w.Hv
     return max(nbytes / (HBM_PEAK_GBS * 1e9), flops / (BF16_MFMA_PEAK_TFLOPS * 1e12)) * 1e6, nbytes, flops
 
 
@@ -180,8 +209,10 @@ def run_design(torch, hip, lib, w, dev, design, steps, warmup):
             hip.lib.hipEventDestroy(ctypes.c_void_p(e))
     del keep_f, keep_b
     kernels = {n: sum(v) / len(v) for n, v in per.items()}
-    return {"ms_per_step": wall_ms, "fwd_ms": fwd_ms, "bwd_ms": bwd_ms, "kernels_ms": kernels,
-            "nc": lib.num_chunks(desc_f)}, None
+    nc = lib.num_chunks(desc_f)
+    tiles = lib.ckpt_bytes(desc_f) - nc * Hv * Dv * Dk * 4
+    return {"ms_per_step": wall_ms, "fwd_ms": fwd_ms, "bwd_ms": bwd_ms, "kernels_ms": kernels, "nc": nc,
+            "tiles_bytes": tiles}, None
 
 
 def run_decode(torch, lib, w, design, calls=200, warmup=20):
@@ -343,6 +374,70 @@ def cpu_baseline(w, inp, budget_s=12.0, max_reps=60):
                       f"{reps} run(s), {per:.2f} s each"}
 
 
+DESIGN_NAMES = {1: "recurrent", 2: "chunked"}
+
+
+def measure_workload(torch, hip, lib, w, designs, steps, warmup):
+    """Every design in `designs` on workload w: ms per step, per-kernel durations, and for the fastest the roofline
+    of its dominant kernel and of the whole step. Returns (summary, inputs) or (None, reasons)."""
+    from quotebound_amd.synthetic import make_inputs, to_device
+
+    inp = make_inputs(w)
+    dev = to_device(inp, "cuda")
+    torch.cuda.synchronize()
+    results = {}
+    for d in designs:
+        r, why = run_design(torch, hip, lib, w, dev, d, steps, warmup)
+        if r is None:
+            results[DESIGN_NAMES[d]] = {"unavailable": why}
+            continue
+        r["tokens_per_s"] = w.tokens / (r["ms_per_step"] * 1e-3)
+        results[DESIGN_NAMES[d]] = r
+    del dev
+    ok = {k: v for k, v in results.items() if "ms_per_step" in v}
+    if not ok:
+        return None, results
+    best = max(ok, key=lambda k: ok[k]["tokens_per_s"])
+    r = ok[best]
+    dom = max(r["kernels_ms"], key=r["kernels_ms"].get)
+    kind, amount, design_bytes = algorithmic_work(w, dom, r["nc"], r["tiles_bytes"])
+    roof = roofline_of(kind, amount, r["kernels_ms"][dom])
+    roof.update({"kernel": dom, "mean_ms": r["kernels_ms"][dom], "algorithmic_" + kind + "_per_launch": amount,
+                 "design_bytes_per_launch": design_bytes, "traffic": traffic_of(w, dom)})
+    t_roof, nbytes, nflops = step_roof_us(w, r["nc"])
+    summary = {
+        "workload": f"{w.name}: B={w.B} T={w.T} Hk={w.Hk} Hv={w.Hv} Dk={w.Dk} Dv={w.Dv}"
+                    + (f" ({len(w.seq_lens)} packed sequences)" if w.seq_lens else "")
+                    + (", nonzero initial state" if w.s0_std > 0 else "")
+                    + f", {w.dtype} I/O, fp32 state, 64-token checkpoints, fwd+bwd",
+        "tokens": w.tokens, "design": best, "ms_per_step": r["ms_per_step"], "tokens_per_s": r["tokens_per_s"],
+        "roofline": roof,
+        "step_roofline": {"t_roof_us": t_roof, "bytes_alg": nbytes, "flops_alg": nflops,
+                          "t_step_us": r["ms_per_step"] * 1e3, "frac": t_roof / (r["ms_per_step"] * 1e3)},
+        "designs": {k: ({kk: vv for kk, vv in v.items() if kk not in ("nc", "tiles_bytes")} if "ms_per_step" in v
+                        else v) for k, v in results.items()},
+    }
+    return summary, inp
+
+
+def run_t_sweep(torch, hip, lib, design, steps=10, warmup=2):
+    """The reference bench's sweep (reference tests/bench_grad.cpp:38-68, 124-130): the recurrence at the 4B head
+    shape (B=1, Hk=16, Hv=32, Dk=Dv=128) for T in 128, 512, 1024, 2048, forward and forward + backward."""
+    from quotebound_amd.synthetic import Workload, make_inputs, to_device
+
+    out = {"unit": "ms (HIP events around the library's kernels)", "design": DESIGN_NAMES[design]}
+    for T in (128, 512, 1024, 2048):
+        w = Workload(f"sweep_{T}", 1, T, 16, 32, 128, 128, seed=40 + T)
+        dev = to_device(make_inputs(w), "cuda")
+        r, why = run_design(torch, hip, lib, w, dev, design, steps, warmup)
+        if r is None:
+            out[str(T)] = {"unavailable": why}
+            continue
+        out[str(T)] = {"fwd_ms": r["fwd_ms"], "fwd_bwd_ms": r["ms_per_step"],
+                       "tokens_per_s": T / (r["ms_per_step"] * 1e-3)}
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -353,8 +448,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-probe-mib", type=int, default=0)
     ap.add_argument("--path-only", action="store_true",
-                    help="skip the legs outside the headline step (decode, neighbours, LoRA step), as profiler "
-                         "counter passes need")
+                    help="time only the named workload's step (no other shapes, decode, neighbours or LoRA step), as "
+                         "profiler counter passes need")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the recurrence shards "
@@ -365,66 +460,48 @@ def main():
     import torch
 
     from quotebound_amd import _lib as lib
-    from quotebound_amd.synthetic import make_inputs, to_device, workload
+    from quotebound_amd.synthetic import workload
 
-    w = workload(args.workload)
-    inp = make_inputs(w)
-    dev = to_device(inp, "cuda")
-    torch.cuda.synchronize()
     if args.copy_probe_mib > 0:
         copy_probe(torch, args.copy_probe_mib)
     hip = Hip()
     designs = [lib.RECURRENT, lib.CHUNKED] if args.design == "auto" else [int(args.design)]
-    results = {}
-    for d in designs:
-        r, why = run_design(torch, hip, lib, w, dev, d, args.steps, args.warmup)
-        name = {lib.RECURRENT: "recurrent", lib.CHUNKED: "chunked"}[d]
-        if r is None:
-            results[name] = {"unavailable": why}
-            continue
-        r["tokens_per_s"] = w.tokens / (r["ms_per_step"] * 1e-3)
-        results[name] = r
-    ok = {k: v for k, v in results.items() if "ms_per_step" in v}
-    if not ok:
-        print(json.dumps({"metric": METRIC, "error": results}))
+    w = workload(args.workload)
+    head, inp = measure_workload(torch, hip, lib, w, designs, args.steps, args.warmup)
+    if head is None:
+        print(json.dumps({"metric": METRIC, "error": inp}))
         sys.exit(1)
-    best = max(ok, key=lambda k: ok[k]["tokens_per_s"])
-    r = ok[best]
-    dom = max(r["kernels_ms"], key=r["kernels_ms"].get)
-    kind, amount = algorithmic_work(w, dom, r["nc"], best)
-    roof = roofline_of(kind, amount, r["kernels_ms"][dom])
-    roof.update({"kernel": dom, "mean_ms": r["kernels_ms"][dom], "algorithmic_" + kind + "_per_launch": amount,
-                 "traffic": traffic_of(w, dom)})
-    t_roof, nbytes, nflops = step_roof_us(w, r["nc"])
     out = {
         "metric": METRIC,
-        "value": r["tokens_per_s"],
+        "value": head["tokens_per_s"],
         "unit": "tokens/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": r["ms_per_step"],
+        "ms_per_step": head["ms_per_step"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32" if best == "recurrent" else "bf16x3-mfma/f32",
+        "dtype": "f32" if head["design"] == "recurrent" else "bf16x3-mfma/f32",
         "data": "synthetic (seeded numpy: unit-norm q/k, N(0,1) v, log-decay -softplus(N) clipped to [-8,0], "
                 "beta sigmoid(N), dy N(0,1))",
-        "config": {"workload": f"{w.name}: B={w.B} T={w.T} Hk={w.Hk} Hv={w.Hv} Dk={w.Dk} Dv={w.Dv}, "
-                               f"{w.dtype} I/O, fp32 state, 64-token checkpoints, fwd+bwd",
-                   "design": best, "io_dtype": w.dtype},
-        "roofline": roof,
-        "step_roofline": {"t_roof_us": t_roof, "bytes_alg": nbytes, "flops_alg": nflops,
-                          "t_step_us": r["ms_per_step"] * 1e3, "frac": t_roof / (r["ms_per_step"] * 1e3)},
-        "designs": {k: ({kk: vv for kk, vv in v.items() if kk != "nc"} if "ms_per_step" in v else v)
-                    for k, v in results.items()},
+        "config": {"workload": head["workload"], "design": head["design"], "io_dtype": w.dtype},
+        "roofline": head["roofline"],
+        "step_roofline": head["step_roofline"],
+        "designs": head["designs"],
     }
     if not args.path_only:
+        # The other layer shapes of the same metric, each with its own rooflines.
+        out["workloads"] = {}
+        for name in ("qwen35_9b", "qwen35_4b_varlen"):
+            summary, _ = measure_workload(torch, hip, lib, workload(name), designs, args.steps, args.warmup)
+            out["workloads"][name] = summary
+        best = lib.CHUNKED if head["design"] == "chunked" else lib.RECURRENT
+        out["t_sweep"] = run_t_sweep(torch, hip, lib, best)
         out["decode"] = {"unit": "us per one-token call (state carried, host clock, launch included)",
                          "config": f"B={w.B} Hk={w.Hk} Hv={w.Hv} Dk={w.Dk} Dv={w.Dv}, {w.dtype} I/O, fp32 state"}
         for d in designs:
-            name = {lib.RECURRENT: "recurrent", lib.CHUNKED: "chunked"}[d]
-            out["decode"][name] = run_decode(torch, lib, w, d)
+            out["decode"][DESIGN_NAMES[d]] = run_decode(torch, lib, w, d)
         out["neighbours"] = run_neighbours(torch, lib, w)
         out["lora_step"] = run_lora_step(torch)
     if not args.no_cpu:

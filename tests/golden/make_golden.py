@@ -4,7 +4,7 @@
 The expected values come from autodiff in float64 through the plain-ops recurrence (tests/plain_ops.py, the form of
 reference tests/gated_delta_ref.h:100-120), not from the oracle, so the fixture checks the oracle independently.
 A second case (tiny_fp32_s0) adds a nonzero initial state ~N(0, 0.1), a final-state cotangent and GQA (Hk=1, Hv=2),
-as the reference's gradient tests do (reference tests/test_deltanet.cpp:226-233).
+as the reference's gradient tests do (reference tests/test_deltanet.cpp:106-112).
 
 Run from the repository root: python tests/golden/make_golden.py
 """

@@ -19,14 +19,14 @@ def normwise(x, ref) -> float:
 
 
 def unit_rows(rng, shape, scale):
-    """Unit-RMS rows times scale: the reference's test inputs (reference tests/test_deltanet.cpp:150-153)."""
+    """Unit-RMS rows times scale: the reference's test inputs (reference tests/test_deltanet.cpp:29-32, 106-107)."""
     x = rng.standard_normal(shape)
     x = x / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + 1e-6)
     return x * scale
 
 
 def reference_case(B, T, Hk, Hv, Dk, Dv, g_lo, seed):
-    """Inputs as the reference's trainable-gradient test draws them (reference tests/test_deltanet.cpp:226-234):
+    """Inputs as the reference's trainable-gradient test draws them (reference tests/test_deltanet.cpp:106-112):
     q, k unit RMS scaled by 1/Dk and 1/sqrt(Dk); g uniform in [g_lo, 1) as the decay factor; beta uniform in [0, 1);
     state ~N(0, 0.1); cotangents on y and on the final state."""
     rng = np.random.default_rng(seed)

@@ -91,7 +91,7 @@ def test_golden_vectors(torch_dev, design, name):
 
 
 @pytest.mark.parametrize("design", DESIGNS, ids=DESIGN_IDS.get)
-@pytest.mark.parametrize("case", [  # reference tests/test_deltanet.cpp:266-275
+@pytest.mark.parametrize("case", [  # reference tests/test_deltanet.cpp:145-154
     (1, 19, 16, 32, 128, 128, 0.5), (1, 64, 16, 32, 128, 128, 0.9), (2, 150, 16, 32, 128, 128, 0.99),
     (1, 129, 16, 32, 128, 128, 0.9), (1, 70, 2, 8, 32, 32, 0.9), (2, 33, 4, 4, 64, 64, 0.99),
     (1, 70, 2, 4, 128, 4, 0.9), (1, 40, 2, 4, 256, 64, 0.9)], ids=lambda c: "B%dT%dHk%dHv%dDk%dDv%d" % c[:6])
@@ -101,10 +101,8 @@ def test_reference_gradient_cases(torch_dev, oracle, design, case):
     inp = reference_case(B, T, Hk, Hv, Dk, Dv, g_lo, seed=100 + T)
     d, _ = _lib.make_desc(B, T, Hk, Hv, Dk, Dv, dtype=_lib.F32, g_is_log=False, design=design)
     why = _lib.validate(d)
-    if why is not None:  # a shape the design does not take must be refused with a reason, never run
-        with pytest.raises(RuntimeError, match="gated delta"):
-            run(torch, host_to_dev(torch, inp, torch.float32), design, log_decay=False)
-        return
+    if why is not None:  # no parity evidence for a shape the design refuses (the refusal is tested in test_capi)
+        pytest.skip(f"design {design} refuses this shape: {why}")
     y, s, ck = oracle.fwd(inp["q"], inp["k"], inp["v"], inp["g"], inp["beta"], inp["s0"], g_is_log=False)
     grads = oracle.bwd(inp["q"], inp["k"], inp["v"], inp["g"], inp["beta"], ck, inp["dy"], inp["ds_out"],
                        g_is_log=False)
@@ -113,7 +111,7 @@ def test_reference_gradient_cases(torch_dev, oracle, design, case):
     assert_close(got, exp, F32_TOL, label=f"case {case} design {design}")
 
 
-REF_SHAPES_BF16 = [c for c in [  # the reference's gradient cases, bf16 inputs (reference tests/test_deltanet.cpp:266-275)
+REF_SHAPES_BF16 = [c for c in [  # the reference's gradient cases, bf16 inputs (reference tests/test_deltanet.cpp:145-154)
     (1, 19, 16, 32, 128, 128, 0.5), (1, 64, 16, 32, 128, 128, 0.9), (2, 150, 16, 32, 128, 128, 0.99),
     (1, 129, 16, 32, 128, 128, 0.9)]]
 

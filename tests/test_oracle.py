@@ -39,7 +39,7 @@ def test_golden_vectors(oracle, name):
         assert normwise(got32[key], exp[key]) <= 2e-6, key
 
 
-REFERENCE_CASES = [  # (B, T, Hk, Hv, Dk, Dv, g_lo): reference tests/test_deltanet.cpp:266-275
+REFERENCE_CASES = [  # (B, T, Hk, Hv, Dk, Dv, g_lo): reference tests/test_deltanet.cpp:145-154
     (1, 19, 16, 32, 128, 128, 0.5),
     (1, 64, 16, 32, 128, 128, 0.9),
     (2, 150, 16, 32, 128, 128, 0.99),
@@ -120,7 +120,7 @@ def test_gqa_equals_duplicated_key_heads(oracle):
 
 
 def test_split_invariance(oracle):
-    """Carrying the state across calls equals one call (reference tests/test_deltanet.cpp:168-173)."""
+    """Carrying the state across calls equals one call (reference tests/test_deltanet.cpp:47-52)."""
     inp = small_case(2, 70, 2, 4, 16, 8, seed=5)
     y, s, _ = oracle.fwd(inp["q"], inp["k"], inp["v"], inp["g"], inp["beta"], inp["s0"])
     cut = lambda x, a, b: x[:, a:b]  # noqa: E731
