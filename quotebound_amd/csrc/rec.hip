@@ -1,8 +1,10 @@
 // Design 1: the recurrent form. Rows of the state S [Dv, Dk] evolve independently (reference
-// src/delta_grad.cpp:13-18), so each row is owned by 16 lanes of a wave (one DPP row), each lane holding Dk/16
-// columns in VGPRs for all T steps. The two mat-vecs per step are 16-lane DPP reductions. A block is 4 waves =
-// 16 state rows of one value head; the chunk's keys, queries and scalars are staged in LDS once per 64 steps and
-// read by all 16 rows.
+// src/delta_grad.cpp:13-18), so each row is owned by LPR lanes of a wave, each lane holding NPT = Dk / LPR columns in
+// VGPRs for all T steps: LPR = 16 (one DPP row) for Dk up to 128, LPR = 32 for Dk of 160 to 256, so a lane never
+// holds more than 8 columns. The two mat-vecs per step are LPR-lane reductions (DPP within 16 lanes, one swizzle
+// across two rows). A block is 4 waves = 4 * 64 / LPR state rows of one value head; the chunk's keys, queries and
+// scalars are staged in LDS once per 64 steps and read by all its rows (the backward of the wide variant reads the
+// queries from global memory instead, to stay within LDS).
 //
 // Forward (per row, per step), the same recurrence as reference tests/gated_delta_ref.h:46-67 but with both dot
 // products taken on the previous state, so one reduction latency per step sits on the dependency chain:
@@ -12,8 +14,10 @@
 // Backward: reference src/delta_grad.cpp:23-145 re-derived for this layout. Per chunk in reverse: pass A replays
 // the chunk from its checkpoint (one reduction per step) keeping delta and v - u per step in LDS and the state at
 // every 8th step in registers; pass B re-forms 8 states at a time from those without reductions and runs the reverse
-// steps. dq and dk sum over rows: over a wave's 4 rows with lane shuffles, over the block's 4 waves in LDS, over the
-// Dv/16 row blocks and the GQA group in rec_reduce_kernel, always in the same order (no atomics).
+// steps. dq and dk sum over rows: over a wave's rows with lane shuffles, over the block's 4 waves in LDS, over the
+// row blocks and the GQA group in rec_reduce_kernel, always in the same order (no atomics).
+#include <type_traits>
+
 #include "gdn_common.h"
 #include "gdn_kernels.h"
 
@@ -22,9 +26,25 @@ namespace {
 
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
-constexpr int kRows = 4 * kWaves;  // state rows per block
-constexpr int kSub = 8;            // states re-formed at a time in the backward
+constexpr int kSub = 8;  // states re-formed at a time in the backward
 constexpr int kNSub = kChunk / kSub;
+
+// The lane layout for a key width: LPR lanes per state row, NPT columns per lane, rows per block.
+template <int LPR>
+struct Layout {
+  static constexpr int kRowsPerWave = 64 / LPR;
+  static constexpr int kRows = kWaves * kRowsPerWave;
+};
+// Rows per block for a key width (the host side's view of the same layout).
+inline int rec_rows(int Dk) { return Dk <= 128 ? Layout<16>::kRows : Layout<32>::kRows; }
+
+// Sum over each group of LPR lanes; every lane of the group gets the same bits.
+template <int LPR>
+__device__ __forceinline__ float sum_lanes(float x) {
+  x = sum16(x);
+  if constexpr (LPR == 32) x += __shfl_xor(x, 16);
+  return x;
+}
 
 struct RecFwdArgs {
   FwdPtrs p;
@@ -51,7 +71,8 @@ __device__ __forceinline__ Item item_of(const SeqTable& tab, int nblk, int Hv, i
   return Item{it.blk, it.hv, it.n};
 }
 
-// Stages rows [t0, t0 + L) of the key head's k and q into LDS as float32, 8 elements per access.
+// Stages rows [t0, t0 + L) of the key head's k (and q, when Qs is not null) into LDS as float32, 8 elements per
+// access.
 template <int Dk, typename InT>
 __device__ __forceinline__ void stage_kq(float (*Ks)[Dk], float (*Qs)[Dk], const InT* k, const InT* q,
                                          int64_t tok, int Hk, int hk, int L) {
@@ -61,13 +82,13 @@ __device__ __forceinline__ void stage_kq(float (*Ks)[Dk], float (*Qs)[Dk], const
     if (tt < L) {
       const int64_t off = ((tok + tt) * Hk + hk) * Dk + c8;
       IO<InT>::ld8(k + off, &Ks[tt][c8]);
-      IO<InT>::ld8(q + off, &Qs[tt][c8]);
+      if (Qs) IO<InT>::ld8(q + off, &Qs[tt][c8]);
     }
   }
 }
 
-// Stages a [T, Hv, Dv] tensor's 16-row slice of rows [t0, t0 + L) (zeros past Dv).
-template <typename InT>
+// Stages a [T, Hv, Dv] tensor's kRows-row slice of rows [t0, t0 + L) (zeros past Dv).
+template <int kRows, typename InT>
 __device__ __forceinline__ void stage_rows(float (*Xs)[kRows], const InT* x, int64_t tok, int Hv, int hv, int Dv,
                                            int row0, int L) {
   for (int e = threadIdx.x; e < kChunk * kRows; e += kThreads) {
@@ -89,9 +110,10 @@ __device__ __forceinline__ void stage_scalars(float* Gs, float* Bs, const float*
 }
 
 // kKeepRows: also store the state after every token (a.p.rows), for the per-token-state forward.
-template <int NPT, typename InT, typename OutT, bool kKeepRows>
+template <int NPT, int LPR, typename InT, typename OutT, bool kKeepRows>
 __global__ __launch_bounds__(kThreads) void rec_fwd_kernel(RecFwdArgs a) {
-  constexpr int Dk = 16 * NPT;
+  constexpr int Dk = LPR * NPT;
+  constexpr int kRows = Layout<LPR>::kRows;
   __shared__ float Ks[kChunk][Dk];
   __shared__ float Qs[kChunk][Dk];
   __shared__ float Vs[kChunk][kRows];
@@ -100,7 +122,7 @@ __global__ __launch_bounds__(kThreads) void rec_fwd_kernel(RecFwdArgs a) {
 
   const Item it = item_of(a.tab, a.nblk, a.Hv, a.Hk, a.total);
   const int tid = threadIdx.x, lane = tid & 63;
-  const int cl = lane & 15, rl = (tid >> 6) * 4 + (lane >> 4);
+  const int cl = lane % LPR, rl = (tid >> 6) * Layout<LPR>::kRowsPerWave + lane / LPR;
   const int row0 = it.blk * kRows, row = row0 + rl;
   const bool live = row < a.Dv;
   const int hv = it.hv, hk = hv / (a.Hv / a.Hk);
@@ -131,12 +153,12 @@ __global__ __launch_bounds__(kThreads) void rec_fwd_kernel(RecFwdArgs a) {
     stage_rows(Vs, v, tok, a.Hv, hv, a.Dv, row0, L);
     stage_scalars(Gs, Bs, a.p.g, beta, tok, a.Hv, hv, L, a.g_is_log);
     __syncthreads();
-    // k.q per step: 16 row groups of 16 lanes, 4 steps each.
-    for (int tt = tid >> 4; tt < kChunk; tt += kThreads / 16) {
+    // k.q per step: groups of LPR lanes, one step each at a time.
+    for (int tt = tid / LPR; tt < kChunk; tt += kThreads / LPR) {
       float kq = 0.f;
 #pragma unroll
       for (int i = 0; i < NPT; ++i) kq += Ks[tt][cl * NPT + i] * Qs[tt][cl * NPT + i];
-      kq = sum16(kq);
+      kq = sum_lanes<LPR>(kq);
       if (cl == 0) KQs[tt] = kq;
     }
     __syncthreads();
@@ -147,8 +169,8 @@ __global__ __launch_bounds__(kThreads) void rec_fwd_kernel(RecFwdArgs a) {
       float pa = 0.f, pb = 0.f;
 #pragma unroll
       for (int i = 0; i < NPT; ++i) pa += s[i] * kk[i], pb += s[i] * qq[i];
-      pa = sum16(pa);
-      pb = sum16(pb);
+      pa = sum_lanes<LPR>(pa);
+      pb = sum_lanes<LPR>(pb);
       const float gt = Gs[tt], bt = Bs[tt];
       const float d = bt * (Vs[tt][rl] - gt * pa);
       const float yv = gt * pb + d * KQs[tt];
@@ -173,13 +195,14 @@ __global__ __launch_bounds__(kThreads) void rec_fwd_kernel(RecFwdArgs a) {
   }
 }
 
-// Sums NPT per-lane column values over the wave's 4 row groups (lanes l, l^16, l^32, l^48 hold the same columns of
-// different rows) and writes each column's sum once into dst[0, Dk). With NPT >= 4 the values are halved at each
-// exchange so each lane ends with NPT/4 finished columns; with NPT == 2 a plain butterfly is used.
-template <int NPT>
+// Sums NPT per-lane column values over the wave's rows and writes each column's sum once into dst[0, Dk). LPR = 16:
+// lanes l, l^16, l^32, l^48 hold the same columns of the wave's 4 rows; with NPT a multiple of 4 the values are
+// halved at each exchange so each lane ends with NPT/4 finished columns, otherwise a plain butterfly is used. LPR = 32:
+// lanes l and l^32 hold the same columns of the wave's 2 rows.
+template <int NPT, int LPR>
 __device__ __forceinline__ void wave_rows_sum(const float* p, float* dst, int lane) {
-  const int cl = lane & 15;
-  if constexpr (NPT >= 4) {
+  const int cl = lane % LPR;
+  if constexpr (LPR == 16 && NPT % 4 == 0) {
     constexpr int H = NPT / 2, Q = NPT / 4;
     const bool h32 = lane & 32, h16 = lane & 16;
     float w[H], x[Q];
@@ -201,17 +224,21 @@ __device__ __forceinline__ void wave_rows_sum(const float* p, float* dst, int la
     for (int j = 0; j < NPT; ++j) {
       float x = p[j];
       x += __shfl_xor(x, 32);
-      x += __shfl_xor(x, 16);
-      if (lane < 16) dst[cl * NPT + j] = x;
+      if constexpr (LPR == 16) x += __shfl_xor(x, 16);
+      if (lane < LPR) dst[cl * NPT + j] = x;
     }
   }
 }
 
-template <int NPT, typename InT, typename OutT>
+// The wide variant (LPR = 32) reads q from global memory in its reverse steps rather than staging it: its k, red and
+// the per-row arrays take about 137 KB of LDS at Dk = 256.
+template <int NPT, int LPR, typename InT, typename OutT>
 __global__ __launch_bounds__(kThreads) void rec_bwd_kernel(RecBwdArgs a) {
-  constexpr int Dk = 16 * NPT;
+  constexpr int Dk = LPR * NPT;
+  constexpr int kRows = Layout<LPR>::kRows;
+  constexpr bool kQGlobal = LPR == 32;
   __shared__ float Ks[kChunk][Dk];
-  __shared__ float Qs[kChunk][Dk];
+  __shared__ float Qs[kQGlobal ? 1 : kChunk][Dk];
   __shared__ float Vs[kChunk][kRows], DYs[kChunk][kRows], Ds[kChunk][kRows], Es[kChunk][kRows];
   __shared__ float Gs[kChunk], Bs[kChunk];
   __shared__ float red[kSub][kWaves][2 * Dk];  // per step and wave: column sums of (dq | dk) over the wave's rows
@@ -219,7 +246,7 @@ __global__ __launch_bounds__(kThreads) void rec_bwd_kernel(RecBwdArgs a) {
 
   const Item it = item_of(a.tab, a.nblk, a.Hv, a.Hk, a.total);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int cl = lane & 15, rl = wave * 4 + (lane >> 4);
+  const int cl = lane % LPR, rl = wave * Layout<LPR>::kRowsPerWave + lane / LPR;
   const int row0 = it.blk * kRows, row = row0 + rl;
   const bool live = row < a.Dv;
   const int hv = it.hv, hk = hv / (a.Hv / a.Hk);
@@ -242,9 +269,9 @@ __global__ __launch_bounds__(kThreads) void rec_bwd_kernel(RecBwdArgs a) {
     const int t0 = c * kChunk, L = min(kChunk, sq.len - t0);
     const int64_t tok = sq.tok0 + t0;
     __syncthreads();
-    stage_kq<Dk>(Ks, Qs, k, q, tok, a.Hk, hk, L);
-    stage_rows(Vs, v, tok, a.Hv, hv, a.Dv, row0, L);
-    stage_rows(DYs, dy, tok, a.Hv, hv, a.Dv, row0, L);
+    stage_kq<Dk>(Ks, kQGlobal ? nullptr : Qs, k, q, tok, a.Hk, hk, L);
+    stage_rows<kRows>(Vs, v, tok, a.Hv, hv, a.Dv, row0, L);
+    stage_rows<kRows>(DYs, dy, tok, a.Hv, hv, a.Dv, row0, L);
     stage_scalars(Gs, Bs, a.p.g, beta, tok, a.Hv, hv, L, a.g_is_log);
     float st[NPT];
     {
@@ -273,7 +300,7 @@ __global__ __launch_bounds__(kThreads) void rec_bwd_kernel(RecBwdArgs a) {
           float pa = 0.f;
 #pragma unroll
           for (int i = 0; i < NPT; ++i) pa += st[i] * kk[i];
-          pa = sum16(pa);
+          pa = sum_lanes<LPR>(pa);
           const float gt = Gs[tt];
           const float e = Vs[tt][rl] - gt * pa;
           const float d = Bs[tt] * e;
@@ -316,7 +343,10 @@ __global__ __launch_bounds__(kThreads) void rec_bwd_kernel(RecBwdArgs a) {
         if (tt >= L) continue;
         float kk[NPT], qq[NPT], pq[NPT], pk[NPT];
 #pragma unroll
-        for (int i = 0; i < NPT; ++i) kk[i] = Ks[tt][cl * NPT + i], qq[i] = Qs[tt][cl * NPT + i];
+        for (int i = 0; i < NPT; ++i) {
+          kk[i] = Ks[tt][cl * NPT + i];
+          qq[i] = kQGlobal ? IO<InT>::ld(q, ((tok + tt) * a.Hk + hk) * Dk + cl * NPT + i) : Qs[tt][cl * NPT + i];
+        }
         const float gt = Gs[tt], bt = Bs[tt], dyt = DYs[tt][rl], d = Ds[tt][rl], e = Es[tt][rl];
         float dd = 0.f;
 #pragma unroll
@@ -325,7 +355,7 @@ __global__ __launch_bounds__(kThreads) void rec_bwd_kernel(RecBwdArgs a) {
           pq[i] = dyt * S[j + 1][i];
           dd += ds[i] * kk[i];
         }
-        dd = sum16(dd);
+        dd = sum_lanes<LPR>(dd);
         const float du = -bt * dd;
         float dg = 0.f;
 #pragma unroll
@@ -335,10 +365,10 @@ __global__ __launch_bounds__(kThreads) void rec_bwd_kernel(RecBwdArgs a) {
           dg += ds[i] * S[j][i];
           ds[i] *= gt;
         }
-        dg = sum16(dg);
+        dg = sum_lanes<LPR>(dg);
         if (cl == 0) rowv[j][0][rl] = bt * dd, rowv[j][1][rl] = dd * e, rowv[j][2][rl] = dg;
-        wave_rows_sum<NPT>(pq, red[j][wave], lane);
-        wave_rows_sum<NPT>(pk, red[j][wave] + Dk, lane);
+        wave_rows_sum<NPT, LPR>(pq, red[j][wave], lane);
+        wave_rows_sum<NPT, LPR>(pk, red[j][wave] + Dk, lane);
       }
       __syncthreads();
       const int Ls = min(kSub, L - ts);
@@ -407,32 +437,48 @@ __global__ __launch_bounds__(128) void rec_reduce_kernel(const float* dq_part, c
   }
 }
 
+// Calls f(NPT, LPR) (as integral constants) for the key widths the kernels are built for: every multiple of 32 up to
+// 256. Returns false for any other width.
+template <class F>
+bool with_width(int Dk, F&& f) {
+  using std::integral_constant;
+  switch (Dk) {
+    case 32: f(integral_constant<int, 2>{}, integral_constant<int, 16>{}); return true;
+    case 64: f(integral_constant<int, 4>{}, integral_constant<int, 16>{}); return true;
+    case 96: f(integral_constant<int, 6>{}, integral_constant<int, 16>{}); return true;
+    case 128: f(integral_constant<int, 8>{}, integral_constant<int, 16>{}); return true;
+    case 160: f(integral_constant<int, 5>{}, integral_constant<int, 32>{}); return true;
+    case 192: f(integral_constant<int, 6>{}, integral_constant<int, 32>{}); return true;
+    case 224: f(integral_constant<int, 7>{}, integral_constant<int, 32>{}); return true;
+    case 256: f(integral_constant<int, 8>{}, integral_constant<int, 32>{}); return true;
+    default: return false;
+  }
+}
+
+int row_blocks(const Problem& p) {
+  const int rows = rec_rows(p.Dk);
+  return (p.Dv + rows - 1) / rows;
+}
+
 template <typename InT, typename OutT>
 hipError_t launch_fwd(const Problem& p, const FwdPtrs& ptrs, hipStream_t s, Tracer& tr) {
   RecFwdArgs a;
   a.p = ptrs;
   a.Hk = p.Hk, a.Hv = p.Hv, a.Dv = p.Dv, a.g_is_log = p.g_is_log;
-  a.nblk = (p.Dv + kRows - 1) / kRows;
+  a.nblk = row_blocks(p);
   a.total = a.nblk * p.Hv * p.N;
   a.tab = p.tab;
   const dim3 grid(a.total), block(kThreads);
   tr.mark();
   const bool rows = ptrs.rows != nullptr;
-  switch (p.Dk) {
-    case 32:
-      if (rows) hipLaunchKernelGGL((rec_fwd_kernel<2, InT, OutT, true>), grid, block, 0, s, a);
-      else hipLaunchKernelGGL((rec_fwd_kernel<2, InT, OutT, false>), grid, block, 0, s, a);
-      break;
-    case 64:
-      if (rows) hipLaunchKernelGGL((rec_fwd_kernel<4, InT, OutT, true>), grid, block, 0, s, a);
-      else hipLaunchKernelGGL((rec_fwd_kernel<4, InT, OutT, false>), grid, block, 0, s, a);
-      break;
-    case 128:
-      if (rows) hipLaunchKernelGGL((rec_fwd_kernel<8, InT, OutT, true>), grid, block, 0, s, a);
-      else hipLaunchKernelGGL((rec_fwd_kernel<8, InT, OutT, false>), grid, block, 0, s, a);
-      break;
-    default: return hipErrorInvalidValue;
-  }
+  const bool ok = with_width(p.Dk, [&](auto npt, auto lpr) {
+    constexpr int NPT = decltype(npt)::value, LPR = decltype(lpr)::value;
+    if (rows)
+      hipLaunchKernelGGL((rec_fwd_kernel<NPT, LPR, InT, OutT, true>), grid, block, 0, s, a);
+    else
+      hipLaunchKernelGGL((rec_fwd_kernel<NPT, LPR, InT, OutT, false>), grid, block, 0, s, a);
+  });
+  if (!ok) return hipErrorInvalidValue;
   tr.mark();
   return hipGetLastError();
 }
@@ -442,7 +488,7 @@ struct BwdWs {
 };
 
 BwdWs carve(const Problem& p, void* ws) {
-  const int64_t nblk = (p.Dv + kRows - 1) / kRows;
+  const int64_t nblk = row_blocks(p);
   const int64_t big = p.BT * p.Hv * nblk * p.Dk, small = p.BT * p.Hv * nblk;
   float* f = static_cast<float*>(ws);
   return BwdWs{f, f + big, f + 2 * big, f + 2 * big + small};
@@ -453,19 +499,18 @@ hipError_t launch_bwd(const Problem& p, const BwdPtrs& ptrs, void* ws, hipStream
   RecBwdArgs a;
   a.p = ptrs;
   a.Hk = p.Hk, a.Hv = p.Hv, a.Dv = p.Dv, a.g_is_log = p.g_is_log;
-  a.nblk = (p.Dv + kRows - 1) / kRows;
+  a.nblk = row_blocks(p);
   a.total = a.nblk * p.Hv * p.N;
   const BwdWs w = carve(p, ws);
   a.dq_part = w.dq_part, a.dk_part = w.dk_part, a.dg_part = w.dg_part, a.db_part = w.db_part;
   a.tab = p.tab;
   const dim3 grid(a.total), block(kThreads);
   tr.mark();
-  switch (p.Dk) {
-    case 32: hipLaunchKernelGGL((rec_bwd_kernel<2, InT, OutT>), grid, block, 0, s, a); break;
-    case 64: hipLaunchKernelGGL((rec_bwd_kernel<4, InT, OutT>), grid, block, 0, s, a); break;
-    case 128: hipLaunchKernelGGL((rec_bwd_kernel<8, InT, OutT>), grid, block, 0, s, a); break;
-    default: return hipErrorInvalidValue;
-  }
+  const bool ok = with_width(p.Dk, [&](auto npt, auto lpr) {
+    constexpr int NPT = decltype(npt)::value, LPR = decltype(lpr)::value;
+    hipLaunchKernelGGL((rec_bwd_kernel<NPT, LPR, InT, OutT>), grid, block, 0, s, a);
+  });
+  if (!ok) return hipErrorInvalidValue;
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   tr.mark();
@@ -484,14 +529,14 @@ hipError_t launch_bwd(const Problem& p, const BwdPtrs& ptrs, void* ws, hipStream
 }  // namespace
 
 const char* rec_supports(const Problem& p) {
-  if (p.Dk != 32 && p.Dk != 64 && p.Dk != 128) return "the recurrent design needs Dk of 32, 64 or 128";
+  if (p.Dk % 32 || p.Dk > 256) return "the recurrent design needs Dk a multiple of 32 of at most 256";
   return nullptr;
 }
 
 size_t rec_ckpt_bytes(const Problem& p) { return size_t(p.NC) * p.Hv * p.Dv * p.Dk * sizeof(float); }
 
 size_t rec_workspace_bytes(const Problem& p) {
-  const size_t nblk = (p.Dv + kRows - 1) / kRows;
+  const size_t nblk = row_blocks(p);
   return (2 * size_t(p.BT) * p.Hv * nblk * p.Dk + 2 * size_t(p.BT) * p.Hv * nblk) * sizeof(float);
 }
 

@@ -365,6 +365,34 @@ def test_random_shapes(torch_dev, oracle, seed):
     assert ran >= 1, c
 
 
+@pytest.mark.parametrize("Dk", [96, 160, 192, 224, 256])
+@pytest.mark.parametrize("bf16", [False, True], ids=["f32", "bf16"])
+def test_recurrent_key_widths(torch_dev, oracle, Dk, bf16):
+    """The recurrent design at the key widths beyond 32/64/128 (the wide variant, 32 lanes per state row, from 160):
+    a packed batch with a nonzero initial state and a final-state cotangent, every output against the oracle."""
+    torch = torch_dev
+    from quotebound_amd.synthetic import round_bf16
+
+    lens = [70, 0, 131, 1]
+    Hk, Hv, Dv = 2, 4, 64
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    inp = small_case(1, int(cu[-1]), Hk, Hv, Dk, Dv, seed=Dk)
+    r = np.random.default_rng(Dk)
+    inp["s0"] = r.normal(0.0, 0.1, (len(lens), Hv, Dv, Dk))
+    inp["ds_out"] = r.standard_normal((len(lens), Hv, Dv, Dk))
+    for n in ("q", "k", "v", "beta", "dy"):
+        x = np.asarray(inp[n], np.float32)
+        inp[n] = round_bf16(x) if bf16 else x
+    for n in ("g", "s0", "ds_out"):
+        inp[n] = np.asarray(inp[n], np.float32)
+    exp = oracle.fwd_bwd(inp, cu_seqlens=cu, dtype=np.float32)
+    d = host_to_dev(torch, inp, torch.bfloat16 if bf16 else torch.float32)
+    if bf16:
+        d["dy"] = d["dy"].float()
+    got = run(torch, d, _lib.RECURRENT, cu=cu, out_f32=bf16)
+    assert_close(got, exp, BF16_TOL if bf16 else F32_TOL, label=f"Dk {Dk} {'bf16' if bf16 else 'f32'}")
+
+
 @pytest.mark.parametrize("design", DESIGNS, ids=DESIGN_IDS.get)
 def test_deterministic(torch_dev, design):
     """Same inputs, same bits: every sum runs in a fixed order (the reference's resume bit-identity relies on it,
