@@ -13,7 +13,8 @@
  * Conventions (those of the reference's C library, src/constrain_capi.h:8-9): every call that can fail returns -1
  * and writes why into err (cut to errlen, NUL-terminated); nothing throws across the ABI. All data pointers are
  * caller-owned DEVICE buffers, row-major, in the layouts below. Work is queued on `stream` (a hipStream_t; NULL is
- * the default stream) and the calls return without waiting for it. The library keeps no mutable global state:
+ * the default stream) and the calls return without waiting for it. The library keeps no mutable global state apart
+ * from qb_gdn_bwd_static's per-GPU scratch array (and that array's address on each device, looked up once): the other
  * calls on different streams may overlap as long as they do not share output or workspace buffers.
  *
  * Layouts (N = B, or n_seqs with cu_seqlens; NC = chunk slots, see qb_gdn_num_chunks):
@@ -111,6 +112,23 @@ int qb_gdn_fwd_rows(const qb_gdn_desc* desc, const void* q, const void* k, const
 int qb_gdn_bwd(const qb_gdn_desc* desc, const void* q, const void* k, const void* v, const float* g,
                const void* beta, const float* ckpt, const void* dy, const float* ds_out, void* dq, void* dk, void* dv,
                float* dg, void* dbeta, float* ds0, void* workspace, void* stream, char* err, int errlen);
+
+/* Size of the device array qb_gdn_bwd_static uses as its workspace, per GPU: 256 MiB, which holds the chunked
+ * design's workspace up to NC * Hv * Dv * Dk = 2^26 (the 4B and 9B layer shapes at T = 4096). */
+#define QB_GDN_STATIC_SCRATCH_BYTES (256u << 20)
+
+/* qb_gdn_bwd without a workspace argument, for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). No counterpart in the reference. Its workspace is
+ * a file-scope device array of QB_GDN_STATIC_SCRATCH_BYTES that each GPU the library runs on holds until the
+ * process ends; a desc whose qb_gdn_workspace_bytes exceeds that is refused with -1 and the reason in err, before any
+ * GPU work. It calls no hipMalloc, hipFree or allocating routine. The first call on a device looks up that device's
+ * address of the array (with the device current). Every call on one GPU shares that GPU's array: calls that overlap
+ * on one GPU (on different streams, or unordered across host threads) race on it and must not be issued. Nothing in
+ * the array needs to start at zero (the backward writes every byte of its workspace before reading it), and it keeps
+ * the last call's contents. Otherwise as qb_gdn_bwd, with the same outputs bit for bit. */
+int qb_gdn_bwd_static(const qb_gdn_desc* desc, const void* q, const void* k, const void* v, const float* g,
+                      const void* beta, const float* ckpt, const void* dy, const float* ds_out, void* dq, void* dk,
+                      void* dv, float* dg, void* dbeta, float* ds0, void* stream, char* err, int errlen);
 
 /* The layer's pointwise neighbours of the recurrence, each one pass over its rows (reference src/deltanet.cpp). They
  * read B, T, Hk, Hv, Dk, Dv and dtype from desc (the other fields are not used; the prologue needs Dk, the epilogue

@@ -67,6 +67,8 @@ def load():
     L.qb_gdn_fwd_rows.restype = ctypes.c_int
     L.qb_gdn_bwd.argtypes = [D] + [P] * 16 + [ctypes.c_char_p, ctypes.c_int]
     L.qb_gdn_bwd.restype = ctypes.c_int
+    L.qb_gdn_bwd_static.argtypes = [D] + [P] * 15 + [ctypes.c_char_p, ctypes.c_int]
+    L.qb_gdn_bwd_static.restype = ctypes.c_int
     L.qb_gdn_neighbours_workspace_bytes.argtypes = [D]
     L.qb_gdn_neighbours_workspace_bytes.restype = ctypes.c_size_t
     L.qb_gdn_prologue_fwd.argtypes = [D] + [P] * 11 + [ctypes.c_char_p, ctypes.c_int]
@@ -153,6 +155,14 @@ def bwd(desc, q, k, v, g, beta, ckpt, dy, ds_out, dq, dk, dv, dg, dbeta, ds0, wo
                            workspace, stream, err, len(err))
     if rc != 0:
         raise RuntimeError(err.value.decode())
+
+
+def bwd_static(desc, q, k, v, g, beta, ckpt, dy, ds_out, dq, dk, dv, dg, dbeta, ds0, stream) -> None:
+    """qb_gdn_bwd with the library's static per-GPU scratch in place of a workspace (no allocation)."""
+    _call(load().qb_gdn_bwd_static, desc, q, k, v, g, beta, ckpt, dy, ds_out, dq, dk, dv, dg, dbeta, ds0, stream)
+
+
+STATIC_SCRATCH_BYTES = 256 << 20  # QB_GDN_STATIC_SCRATCH_BYTES
 
 
 def neighbours_workspace_bytes(desc) -> int:

@@ -6,11 +6,13 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
 #include <exception>
+#include <mutex>
 #include <string>
 
 #include "gdn_kernels.h"
@@ -289,14 +291,53 @@ int qb_gdn_fwd_rows(const qb_gdn_desc* desc, const void* q, const void* k, const
   });
 }
 
-int qb_gdn_bwd(const qb_gdn_desc* desc, const void* q, const void* k, const void* v, const float* g,
-               const void* beta, const float* ckpt, const void* dy, const float* ds_out, void* dq, void* dk, void* dv,
-               float* dg, void* dbeta, float* ds0, void* workspace, void* stream, char* err, int errlen) {
+}  // extern "C"
+
+namespace {
+
+// The backward's scratch for callers that cannot allocate (qb_gdn_bwd_static): one array per GPU, which each GPU
+// the library runs on holds until the process ends. In host code the name `scratch` is not a device address: the
+// array's address on a device comes from hipGetSymbolAddress, looked up once per device (the first call on it,
+// with that device current) and kept in scratch_ptr.
+static __device__ __align__(256) unsigned char scratch[QB_GDN_STATIC_SCRATCH_BYTES];
+constexpr int kMaxDevices = 64;
+std::atomic<void*> scratch_ptr[kMaxDevices];
+std::mutex scratch_mu;
+
+// The current device's address of the scratch array.
+std::string scratch_of_current_device(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail("hipGetDevice", e);
+  if (dev < 0 || dev >= kMaxDevices) return "gated delta: device index " + std::to_string(dev) + " out of range";
+  void* p = scratch_ptr[dev].load(std::memory_order_acquire);
+  if (!p) {
+    std::lock_guard<std::mutex> lock(scratch_mu);
+    p = scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (!p) {
+      e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (e != hipSuccess || !p) return hip_fail("hipGetSymbolAddress of the static scratch", e);
+      scratch_ptr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return {};
+}
+
+// qb_gdn_bwd's body; with use_static the workspace is the current device's static scratch.
+int bwd_impl(const qb_gdn_desc* desc, const void* q, const void* k, const void* v, const float* g, const void* beta,
+             const float* ckpt, const void* dy, const float* ds_out, void* dq, void* dk, void* dv, float* dg,
+             void* dbeta, float* ds0, void* workspace, bool use_static, void* stream, char* err, int errlen) {
   return guarded(err, errlen, [&] {
-    Problem p;
+    Problem p{};
     std::string why = resolve(desc, p);
     const size_t el = p.in_bf16 ? 2 : 4, eo = p.out_bf16 ? 2 : 4;
     const bool any = p.BT > 0;
+    const size_t need = why.empty() ? ws_bytes(desc, p) : 0;
+    if (why.empty() && use_static && need > QB_GDN_STATIC_SCRATCH_BYTES)
+      why = "gated delta: the backward without allocation needs " + std::to_string(need) +
+            " bytes of scratch, more than its static " + std::to_string(size_t(QB_GDN_STATIC_SCRATCH_BYTES)) + " " +
+            shape_of(*desc);
     const struct {
       const char* name;
       const void* ptr;
@@ -307,12 +348,20 @@ int qb_gdn_bwd(const qb_gdn_desc* desc, const void* q, const void* k, const void
                 {"dy", dy, any, eo},       {"ds_out", ds_out, false, 4}, {"dq", dq, any, eo},
                 {"dk", dk, any, eo},       {"dv", dv, any, eo},         {"dg", dg, any, 4},
                 {"dbeta", dbeta, any, eo}, {"ds0", ds0, false, 4},
-                {"workspace", workspace, why.empty() && any && ws_bytes(desc, p) > 0, 16}};
+                {"workspace", workspace, !use_static && why.empty() && any && need > 0, 16}};
     for (const auto& c : ptrs)
       if (why.empty()) why = check_ptr(c.name, c.ptr, c.req, c.align);
     if (!why.empty()) {
       set_err(err, errlen, why);
       return -1;
+    }
+    if (use_static) {
+      workspace = nullptr;
+      if (any && need > 0) why = scratch_of_current_device(&workspace);
+      if (!why.empty()) {
+        set_err(err, errlen, why);
+        return -1;
+      }
     }
     const qbgdn::BwdPtrs a{q, k, v, g, beta, ckpt, dy, ds_out, dq, dk, dv, dg, dbeta, ds0};
     hipStream_t s = static_cast<hipStream_t>(stream);
@@ -325,6 +374,24 @@ int qb_gdn_bwd(const qb_gdn_desc* desc, const void* q, const void* k, const void
     }
     return 0;
   });
+}
+
+}  // namespace
+
+extern "C" {
+
+int qb_gdn_bwd(const qb_gdn_desc* desc, const void* q, const void* k, const void* v, const float* g,
+               const void* beta, const float* ckpt, const void* dy, const float* ds_out, void* dq, void* dk, void* dv,
+               float* dg, void* dbeta, float* ds0, void* workspace, void* stream, char* err, int errlen) {
+  return bwd_impl(desc, q, k, v, g, beta, ckpt, dy, ds_out, dq, dk, dv, dg, dbeta, ds0, workspace, false, stream, err,
+                  errlen);
+}
+
+int qb_gdn_bwd_static(const qb_gdn_desc* desc, const void* q, const void* k, const void* v, const float* g,
+                      const void* beta, const float* ckpt, const void* dy, const float* ds_out, void* dq, void* dk,
+                      void* dv, float* dg, void* dbeta, float* ds0, void* stream, char* err, int errlen) {
+  return bwd_impl(desc, q, k, v, g, beta, ckpt, dy, ds_out, dq, dk, dv, dg, dbeta, ds0, nullptr, true, stream, err,
+                  errlen);
 }
 
 }  // extern "C"

@@ -160,3 +160,15 @@ def test_fwd_rows_errors_before_any_gpu_work(lib):
         _lib.fwd_rows(d, 16, 16, 16, 16, 16, None, 16, None, None)
 
 
+
+def test_bwd_static_refuses_before_any_gpu_work(lib):
+    """The backward without allocation refuses a shape whose workspace exceeds its static array, and checks its
+    pointers, before it touches the GPU."""
+    d, _ = desc(T=4096, design=_lib.RECURRENT)
+    assert _lib.workspace_bytes(d) > _lib.STATIC_SCRATCH_BYTES
+    with pytest.raises(RuntimeError, match="without allocation needs"):
+        _lib.bwd_static(d, *([16] * 14), None)
+    d, _ = desc(T=4096, design=_lib.CHUNKED)
+    assert _lib.workspace_bytes(d) <= _lib.STATIC_SCRATCH_BYTES
+    with pytest.raises(RuntimeError, match="ckpt is null"):
+        _lib.bwd_static(d, 16, 16, 16, 16, 16, None, 16, None, 16, 16, 16, 16, 16, None, None)
