@@ -1,6 +1,7 @@
 // Chunked design: the host side. The forward is prep (T, G per chunk) then the sequential state pass (states,
 // y, final state); the backward is the reverse state pass (dv, ds0 and each chunk's end-state cotangent) then the
-// per-chunk gradient kernel (dq, dk, dg, dbeta).
+// per-chunk gradient kernel (dq, dk, dg, dbeta), and, when g is given as the decay factor, the exact dL/dg at tiny
+// factors.
 #include "chunk_kernels.h"
 #include "gdn_kernels.h"
 
@@ -93,6 +94,9 @@ hipError_t chunk_bwd(const Problem& p, const BwdPtrs& b, void* ws, hipStream_t s
   tr.mark();
   e = launch_chunk_bwd_grads(a, p.out_bf16, s);
   tr.mark();
+  // With g given as the factor, dL/dg at tiny or zero factors comes from an exact replay (chunk_dgfix.hip); chunks
+  // without one return at once.
+  if (e == hipSuccess && !p.g_is_log) e = launch_chunk_dgfix(a, p.out_bf16, s);
   return e;
 }
 

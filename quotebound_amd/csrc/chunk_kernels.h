@@ -1,5 +1,5 @@
 // Arguments and launchers of the chunked design's kernels (chunk_prep.hip, chunk_fwd.hip, chunk_bwd_state.hip,
-// chunk_bwd_grads.hip); chunk.hip sequences them.
+// chunk_bwd_grads.hip, chunk_dgfix.hip); chunk.hip sequences them.
 #pragma once
 #include "chunk_common.h"
 
@@ -36,5 +36,6 @@ hipError_t launch_chunk_prep(const ChunkArgs& a, hipStream_t s);
 hipError_t launch_chunk_fwd(const ChunkArgs& a, bool out_bf16, hipStream_t s);
 hipError_t launch_chunk_bwd_state(const ChunkArgs& a, bool out_bf16, hipStream_t s);
 hipError_t launch_chunk_bwd_grads(const ChunkArgs& a, bool out_bf16, hipStream_t s);
+hipError_t launch_chunk_dgfix(const ChunkArgs& a, bool out_bf16, hipStream_t s);
 
 }  // namespace qbgdn

@@ -15,6 +15,7 @@ namespace qbgdn {
 namespace {
 
 constexpr int kThreads = 256;
+constexpr double kLogFloor = -150.0;
 constexpr int kLDK = 144;  // bf16 row stride for Dk = 128: 16-byte aligned rows on staggered banks
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
@@ -81,7 +82,9 @@ __global__ __launch_bounds__(kThreads) void chunk_prep_kernel(ChunkArgs a) {
   // keeps its bits when |G| is large).
   if (tid < kC) {
     const int t = tid;
-    double G = uint32_t(t) < L ? (a.g_is_log ? double(gx) : double(logf(gx))) : 0.0;
+    // The log-decay floored at -150: a factor of 0 (or a log-decay of -inf) would make G_i - G_j NaN on every pair
+    // across it; at -150 each exp(.) across it is 0 in float32, as the factor 0 makes it.
+    double G = uint32_t(t) < L ? fmax(a.g_is_log ? double(gx) : double(logf(gx)), kLogFloor) : 0.0;
 #pragma unroll
     for (int off = 1; off < kC; off <<= 1) {
       const double u = __shfl_up(G, off);

@@ -365,6 +365,48 @@ def test_random_shapes(torch_dev, oracle, seed):
     assert ran >= 1, c
 
 
+@pytest.mark.parametrize("design", DESIGNS, ids=DESIGN_IDS.get)
+@pytest.mark.parametrize("mode", ["factor", "log"])
+def test_zero_and_tiny_decays(torch_dev, oracle, design, mode):
+    """Decay factors of 0 (a log-decay of -inf) and tiny ones: at a chunk's first and last step, twice in a row,
+    mid-chunk and at the sequence's last step, beside ordinary ones. Every output finite and within the bf16
+    tolerance of the oracle. (The chunked design floors the log-decay at -150 and, with g given as the factor, takes
+    dL/dg at factors below 2^-10 from its exact replay of the chunk.)"""
+    torch = torch_dev
+    from quotebound_amd.synthetic import round_bf16
+
+    B, T, Hk, Hv, Dk, Dv = 1, 200, 2, 4, 128, 64
+    inp = small_case(B, T, Hk, Hv, Dk, Dv, seed=21, s0=True, ds_out=True, log_decay=False)
+    g = inp["g"]
+    g[0, [0, 63, 64, 100, 101, 150], 0] = 0.0
+    g[0, 70, 1], g[0, 71, 1], g[0, 72, 1] = 1e-30, 2.0 ** -12, 2.0 ** -9
+    g[0, 199, 2] = 0.0
+    g[0, 128, 3] = 1e-42  # subnormal in float32
+    for n in ("q", "k", "v", "beta", "dy"):
+        inp[n] = round_bf16(np.asarray(inp[n], np.float32))
+    for n in ("s0", "ds_out"):
+        inp[n] = np.asarray(inp[n], np.float32)
+    log = mode == "log"
+    with np.errstate(divide="ignore"):
+        inp["g"] = np.log(np.asarray(g, np.float32)) if log else np.asarray(g, np.float32)
+    y, s, ck = oracle.fwd(inp["q"], inp["k"], inp["v"], inp["g"], inp["beta"], inp["s0"], g_is_log=log,
+                          dtype=np.float32)
+    grads = oracle.bwd(inp["q"], inp["k"], inp["v"], inp["g"], inp["beta"], ck, inp["dy"], inp["ds_out"],
+                       g_is_log=log, dtype=np.float32)
+    exp = {"y": y, "s_out": s}
+    exp.update(zip(GRAD_NAMES, grads))
+    for n, x in exp.items():
+        assert np.all(np.isfinite(x)), n
+    desc, _ = _lib.make_desc(B, T, Hk, Hv, Dk, Dv, dtype=_lib.BF16, g_is_log=log, design=design)
+    assert not _lib.validate(desc)
+    d = host_to_dev(torch, inp, torch.bfloat16)
+    d["dy"] = d["dy"].float()
+    got = run(torch, d, design, log_decay=log, out_f32=True)
+    for n in OUT_NAMES:
+        assert np.all(np.isfinite(got[n])), n
+    assert_close(got, exp, BF16_TOL, label=f"{mode} design {design}")
+
+
 @pytest.mark.parametrize("Dk", [96, 160, 192, 224, 256])
 @pytest.mark.parametrize("bf16", [False, True], ids=["f32", "bf16"])
 def test_recurrent_key_widths(torch_dev, oracle, Dk, bf16):

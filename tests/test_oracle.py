@@ -221,6 +221,31 @@ def test_zero_decay_cuts_the_gradient(oracle):
             assert np.array_equal(x[:, :25], z[:, :25]), name
 
 
+def test_decay_factor_gradient_is_an_exact_difference(oracle):
+    """The loss <dy, y> + <ds_out, s_out> is affine in each decay factor g_t (the decayed state g_t S_{t-1} enters
+    every later quantity linearly), so dL/dg_t = L(g_t = 1) - L(g_t = 0) exactly, at g_t = 0 as anywhere else. Zeros
+    at a chunk start, mid-chunk, twice in a row and at the last step."""
+    inp = small_case(1, 40, 1, 2, 8, 4, seed=15, s0=True, ds_out=True, log_decay=False)
+    zeros = (0, 16, 21, 22, 39)
+    for t in zeros:
+        inp["g"][0, t, 0] = 0.0
+    inp["g"][0, 9, 1] = 0.0
+
+    def loss(g):
+        y, s, _ = oracle.fwd(inp["q"], inp["k"], inp["v"], g, inp["beta"], inp["s0"], chunk=16, g_is_log=False)
+        return float(np.sum(inp["dy"] * y) + np.sum(inp["ds_out"] * s))
+
+    y, s, ck = oracle.fwd(inp["q"], inp["k"], inp["v"], inp["g"], inp["beta"], inp["s0"], chunk=16, g_is_log=False)
+    dg = oracle.bwd(inp["q"], inp["k"], inp["v"], inp["g"], inp["beta"], ck, inp["dy"], inp["ds_out"], chunk=16,
+                    g_is_log=False)[3]
+    assert np.all(np.isfinite(dg))
+    for t, h in [(t, 0) for t in zeros] + [(9, 1), (5, 0), (30, 1)]:
+        g1, g0 = inp["g"].copy(), inp["g"].copy()
+        g1[0, t, h], g0[0, t, h] = 1.0, 0.0
+        diff = loss(g1) - loss(g0)
+        assert abs(dg[0, t, h] - diff) <= 1e-11 * max(1.0, abs(diff)), (t, h, dg[0, t, h], diff)
+
+
 def test_log_decay_chain_rule(oracle):
     inp = small_case(1, 30, 1, 2, 8, 4, seed=14)
     log = oracle.fwd_bwd(inp, chunk=8)
