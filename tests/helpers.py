@@ -18,6 +18,12 @@ def normwise(x, ref) -> float:
     return float(diff / scale)
 
 
+def bf16_half_ulp(x):
+    """Half the bf16 spacing at |x| (x in [2^(e-1), 2^e) has spacing 2^(e-8)): the most that rounding to nearest
+    can move it."""
+    return np.ldexp(1.0, np.frexp(np.asarray(x, np.float64))[1] - 9)
+
+
 def unit_rows(rng, shape, scale):
     """Unit-RMS rows times scale: the reference's test inputs (reference tests/test_deltanet.cpp:29-32, 106-107)."""
     x = rng.standard_normal(shape)

@@ -12,7 +12,7 @@ import os
 import numpy as np
 import pytest
 
-from helpers import GRAD_NAMES, normwise, reference_case, small_case
+from helpers import GRAD_NAMES, bf16_half_ulp, normwise, reference_case, small_case
 from quotebound_amd import _lib
 
 pytestmark = pytest.mark.gpu
@@ -66,12 +66,6 @@ def assert_close(got, ref, tol, names=OUT_NAMES, label=""):
     print(label, report)
     for n in names:
         assert errs[n] <= tol, f"{label}: {n} normwise error {errs[n]:.3g} > {tol}; {report}"
-
-
-def bf16_half_ulp(x):
-    """Half the bf16 spacing at |x| (x in [2^(e-1), 2^e) has spacing 2^(e-8)): the most that rounding to nearest
-    can move it."""
-    return np.ldexp(1.0, np.frexp(np.asarray(x, np.float64))[1] - 9)
 
 
 def _golden(name):

@@ -20,7 +20,10 @@ On the GPU, the step's loss and every adapter gradient against the reference run
     reference run in bf16 on the same inputs sets it. The GPU's whole-gradient relative error ||g - ref|| / ||ref||
     must be at most 1.25 times the bf16 reference's, with a cosine of at least 0.98. The loss must agree to 1e-3
     relative (the bf16 reference's loss is off by about 2e-3, the GPU's by about 3e-6: its low-rank path,
-    attention, convolution accumulations and recurrence state stay in float32).
+    attention, convolution accumulations and recurrence state stay in float32);
+  * inside that bf16 step, each DeltaNet layer's recurrence (the chunked kernels) on the activations and cotangents
+    the step fed it: the same kernels with float32 outputs within 1e-4 of the oracle, and the step's bf16 tensors
+    those results rounded once.
 """
 import math
 
@@ -223,6 +226,80 @@ def test_lora_step_workload_bf16(dev, oracle):
     assert lrel <= 1e-3
     assert rel <= 1.25 * floor[0], (rel, floor)
     assert cos >= 0.98
+
+
+@pytest.mark.gpu
+def test_lora_step_recurrence_layers_match_oracle(dev, oracle, monkeypatch):
+    """The chunked kernels inside the LoRA workload's bf16 step, held to the recurrence's own bar. Every DeltaNet
+    layer's call of the trainable recurrence is recorded: its bf16 inputs (q, k, v, beta; the float32 log-decay), its
+    output y and the cotangents the step's backward fed it (dy) and got from it (dq, dk, dv, dg, dbeta). The oracle
+    (float32) then runs each layer on exactly those inputs:
+      * the same kernels rerun on those inputs with float32 outputs within 1e-4 normwise (the split-bf16 products'
+        level; a kernel bug worth a fraction of a percent shows here, not under the whole-gradient noise bar);
+      * the step's own tensors equal to those float32 results rounded once to bf16 (dg, float32, bit-equal), and so
+        within 2e-3 of the oracle plus their own half-ulp, the rule of the layer-shape tests."""
+    from helpers import bf16_half_ulp
+    from quotebound_amd import _lib, gdn
+    from quotebound_amd.synthetic import round_bf16
+
+    cfg = lora.Config()
+    w = lora.init_weights(cfg, seed=31)
+    ads = lora.init_adapters(cfg, w, seed=32, b_std=0.05)
+    tokens, positions, targets = lora.last_half_batch(4, 1024, cfg.vocab, seed=33)
+    calls = []
+    real = gdn.gated_delta_trainable
+
+    def spy(q, k, v, g, beta, state, **kw):
+        assert state is None and kw.get("log_decay") is True
+        y, s = real(q, k, v, g, beta, state, **kw)
+        rec = {"in": [t.detach().clone() for t in (q, k, v, g, beta)], "y": y.detach().clone()}
+
+        def keep(name):
+            def hook(grad):
+                rec[name] = grad.detach().clone()
+            return hook
+
+        y.register_hook(keep("dy"))
+        for name, t in zip(("dq", "dk", "dv", "dg", "dbeta"), (q, k, v, g, beta)):
+            t.register_hook(keep(name))
+        calls.append(rec)
+        return y, s
+
+    monkeypatch.setattr(lora.gdn, "gated_delta_trainable", spy)
+    lora.loss_and_grads(lora.to_device(w, "cuda", torch.bfloat16), lora.adapters_to(ads, "cuda"), tokens.cuda(),
+                        positions.cuda(), targets.cuda(), cfg)
+    torch.cuda.synchronize()
+    assert len(calls) == sum(cfg.is_linear(i) for i in range(cfg.layers))
+    names = ("y", "dq", "dk", "dv", "dg", "dbeta")
+    for li, rec in enumerate(calls):
+        q, k, v, g, beta = rec["in"]
+        B, T, Hk, Dk = q.shape
+        Hv, Dv = v.shape[2], v.shape[3]
+        desc, _ = gdn._desc(q, v, torch.bfloat16, True, None, None, False)  # the step's own choice of design
+        assert desc.design == _lib.CHUNKED
+        host = {n: t.float().cpu().numpy() for n, t in zip(("q", "k", "v", "g", "beta"), (q, k, v, g, beta))}
+        host["dy"] = rec["dy"].float().cpu().numpy()
+        exp = oracle.fwd_bwd(host, dtype=np.float32)
+        y32, _, ckpt = gdn.forward(q, k, v, g, beta, None, log_decay=True, design=_lib.CHUNKED, out_f32=True)
+        g32 = gdn.backward(q, k, v, g, beta, ckpt, rec["dy"].float(), None, log_decay=True, design=_lib.CHUNKED,
+                           want_ds0=False, out_f32=True)
+        torch.cuda.synchronize()
+        f32 = {n: t.float().cpu().numpy() for n, t in zip(names, [y32] + list(g32[:5]))}
+        step = {n: rec[n].float().cpu().numpy() for n in names}
+        errs32 = {n: normwise(f32[n], exp[n]) for n in names}
+        errs = {n: normwise(step[n], exp[n]) for n in names}
+        print(f"layer call {li}: float32 outputs " + ", ".join(f"{n} {e:.1e}" for n, e in errs32.items())
+              + "; the step's own " + ", ".join(f"{n} {e:.1e}" for n, e in errs.items()))
+        for n in names:
+            assert errs32[n] <= 1e-4, (li, n, errs32)
+            if n == "dg":  # float32 in the step too
+                assert np.array_equal(step[n], f32[n]), (li, n)
+                continue
+            # The step's bf16 tensors are the float32 results rounded once, and so within the criterion plus their
+            # own half-ulp of the oracle.
+            assert np.array_equal(step[n], round_bf16(f32[n])), (li, n)
+            slack = np.abs(step[n] - exp[n]) - bf16_half_ulp(np.maximum(np.abs(exp[n]), np.abs(f32[n])))
+            assert slack.max() <= 2e-3 * np.max(np.abs(exp[n])), (li, n)
 
 
 @pytest.mark.gpu
