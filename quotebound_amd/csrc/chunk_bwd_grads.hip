@@ -1,6 +1,8 @@
-// Chunked design, kernel 4: the per-chunk gradients. One block (8 waves) per (chunk slot, key head); the value heads
-// of the key head's GQA group run in order and their dq, dk contributions add up in registers, so the sums over
-// value heads have a fixed order (reference src/delta_grad.cpp:194-198) and need no atomics.
+// Chunked design, kernel 4: the per-chunk gradients. One work item (8 waves) per (chunk slot, key head); the value
+// heads of the key head's GQA group run in order and their dq, dk contributions add up in registers, so the sums
+// over value heads have a fixed order (reference src/delta_grad.cpp:194-198) and need no atomics. The grid is one
+// resident block per CU looping over items, so the next item's first value head is read during this item's last
+// end phase, as a value head's is during the previous head's.
 //
 // Per value head, with S0 the chunk's start state (checkpoint), dS its end-state cotangent (from the backward state
 // pass) and the chunk's tile (Tb, P, T, exp G, D from prep), the state rows are streamed in blocks of 32:
@@ -83,21 +85,23 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
   Row* x1cp = reinterpret_cast<Row*>(sf + ex1c);
   Row* tpos = reinterpret_cast<Row*>(sf + etq);
 
-  const int total = int(a.lay.NC) * a.Hk;
-  const int wid = xcd_remap(blockIdx.x, total);
-  const int64_t slot = wid / a.Hk;
-  const int hk = wid % a.Hk, grp = a.Hv / a.Hk;
-  const SlotPos sp = slot_pos(a.tab, slot);
-  const int L = sp.L;
-  const int64_t tok = sp.tok;
+  const int total = int(a.lay.NC) * a.Hk, grp = a.Hv / a.Hk;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 4, li = lane & 15;
   const int pw = w & 3, hw = w >> 2;  // position tile, half
   const OutT* dy = static_cast<const OutT*>(a.dy);
   const int sk = a.Hk * Dk, sv = a.Hv * a.Dv;  // token strides of k/q/dq/dk and v/dy
-  const bf16_t* kbase = a.k + tok * sk + hk * Dk;
-  const bf16_t* qbase = a.q + tok * sk + hk * Dk;
-  // Rows past the chunk's last row read as zeros.
-  const auto krs = buffer_rsrc(kbase, uint32_t(L * sk) * 2u), qrs = buffer_rsrc(qbase, uint32_t(L * sk) * 2u);
+  // A work item: a chunk slot and key head. The grid is persistent: block b takes items b, b + gridDim.x, ..., and
+  // gridDim.x is a multiple of 8, so all of a block's items fall in its own XCD's range of xcd_remap.
+  struct Item {
+    int64_t slot, tok;
+    int hk, L;
+  };
+  auto item_at = [&](int id) {
+    const int wid = xcd_remap(id, total);
+    const int64_t slot = wid / a.Hk;
+    const SlotPos sp = slot_pos(a.tab, slot);
+    return Item{slot, sp.tok, wid % a.Hk, sp.L};
+  };
 
   // Global reads, kept in registers from issue to staging. A value head's tile (Tb and P rows hi and lo, thread ->
   // row lt / 8, columns 8 (lt % 8) .. + 7, zeros above the diagonal blocks; and the per-position scalars, thread lt <
@@ -112,22 +116,22 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
     uint4 yraw;           // dY: thread -> position tid / 8, rows 4 (tid % 8) .. + 3
     uint16_t vraw[4];     // v at the wave's accumulator positions (16 pw + 4g + jj, column 16 hw + li)
   };
-  auto load_tile = [&](TileIn& ti, int hv, int lt) {
-    const Tile* tl = a.tiles + slot * a.Hv + hv;
+  auto load_tile = [&](TileIn& ti, const Item& it, int hv, int lt) {
+    const Tile* tl = a.tiles + it.slot * a.Hv + hv;
     if (lt < kC) ti.sc[0] = tl->gam[lt], ti.sc[1] = tl->dec[lt], ti.sc[2] = tl->beta[lt], ti.sc[3] = tl->G[lt];
     const auto tr = buffer_rsrc(tl->tb[0], 4 * kTri * 2);  // tb[0], tb[1], p[0], p[1] are contiguous
 #pragma unroll
     for (int q4 = 0; q4 < 4; ++q4) ti.tp[q4] = tri_ld8(tr, q4 * kTri, lt >> 3, (lt & 7) * 8);
   };
-  auto load_rows = [&](float4 (&x)[2], const float* base, int hv, int r0, int lt) {
-    const float* p = base + ((slot * a.Hv + hv) * a.Dv + r0) * Dk + (lt >> 4) * Dk + (lt & 15) * 8;
+  auto load_rows = [&](float4 (&x)[2], const float* base, const Item& it, int hv, int r0, int lt) {
+    const float* p = base + ((it.slot * a.Hv + hv) * a.Dv + r0) * Dk + (lt >> 4) * Dk + (lt & 15) * 8;
     x[0] = *reinterpret_cast<const float4*>(p);
     x[1] = *reinterpret_cast<const float4*>(p + 4);
   };
-  auto load_dy_v = [&](BlockIn& b, int hv, int r0, int lt) {
+  auto load_dy_v = [&](BlockIn& b, const Item& it, int hv, int r0, int lt) {
     const int g = (lt >> 4) & 3, li = lt & 15, pw = (lt >> 6) & 3, hw = lt >> 8;
-    const auto yr = buffer_rsrc(dy + (tok * a.Hv + hv) * a.Dv + r0, uint32_t(L * sv) * uint32_t(sizeof(OutT)));
-    const auto vr = buffer_rsrc(a.v + (tok * a.Hv + hv) * a.Dv + r0, uint32_t(L * sv) * 2u);
+    const auto yr = buffer_rsrc(dy + (it.tok * a.Hv + hv) * a.Dv + r0, uint32_t(it.L * sv) * uint32_t(sizeof(OutT)));
+    const auto vr = buffer_rsrc(a.v + (it.tok * a.Hv + hv) * a.Dv + r0, uint32_t(it.L * sv) * 2u);
     const int iy = lt >> 3, r4 = (lt & 7) * 4;
     if constexpr (kExactDy) {
       const auto t2 = __builtin_amdgcn_raw_buffer_load_b64(yr, int(uint32_t(iy * sv + r4) * 2), 0, 0);
@@ -140,487 +144,511 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
       b.vraw[jj] = buf_ld2(vr, uint32_t((16 * pw + 4 * g + jj) * sv + 16 * hw + li) * 2);
   };
   // A value head's tile and first block, issued one value head ahead (the first at the start, the others during
-  // the previous head's end phase), so no head waits on a global read before its first block.
-  auto load_head = [&](TileIn& ti, BlockIn& b, int hv) {
+  // the previous head's end phase, the next item's first head during this item's last end phase), so no head
+  // waits on a global read before its first block.
+  auto load_head = [&](TileIn& ti, BlockIn& b, const Item& it, int hv) {
     int lt = tid;
     asm volatile("" : "+v"(lt));
-    load_tile(ti, hv, lt);
-    load_rows(b.xs, a.ckpt, hv, 0, lt);
-    load_rows(b.ys, a.dsend, hv, 0, lt);
-    load_dy_v(b, hv, 0, lt);
+    load_tile(ti, it, hv, lt);
+    load_rows(b.xs, a.ckpt, it, hv, 0, lt);
+    load_rows(b.ys, a.dsend, it, hv, 0, lt);
+    load_dy_v(b, it, hv, 0, lt);
   };
   TileIn ti;
   BlockIn nb;
-  load_head(ti, nb, hk * grp);
-
-  // The chunk's K rows (A operands of K S0^T, K dS^T, K K^T; B of the K products of the end phase).
-  for (int e = tid; e < kC * 16; e += kThreads) {
-    const int t = e >> 4, c8 = (e & 15) * 8;
-    *reinterpret_cast<uint4*>(Kres + swz(t, c8, kLK)) = buf_ld16(krs, uint32_t(t * sk + c8) * 2);
+  {
+    const Item first = item_at(blockIdx.x);
+    load_head(ti, nb, first, first.hk * grp);
   }
-  f32x4 dQ[4], dK[4];  // columns 16 (4 hw + t) + li, rows 16 pw + 4 g + jj
-#pragma unroll
-  for (int t = 0; t < 4; ++t) dQ[t] = zero4(), dK[t] = zero4();
-  // (K K^T)[p][m], rows p = 16 pw + 4g + jj, columns m = 16 key_tile(pw, hw, mi) + li; zero above tile pw. The same
-  // for every value head of the group: formed in the first one's end phase.
-  f32x4 kk[2];
+  for (int id = blockIdx.x; id < total; id += gridDim.x) {
+    const Item cur = item_at(id);
+    const int64_t slot = cur.slot, tok = cur.tok;
+    const int hk = cur.hk, L = cur.L;
+    const bf16_t* kbase = a.k + tok * sk + hk * Dk;
+    const bf16_t* qbase = a.q + tok * sk + hk * Dk;
+    // Rows past the chunk's last row read as zeros.
+    const auto krs = buffer_rsrc(kbase, uint32_t(L * sk) * 2u), qrs = buffer_rsrc(qbase, uint32_t(L * sk) * 2u);
+    __syncthreads();  // the previous item's readers of the K rows and the per-position arrays are done
 
-  for (int e = 0; e < grp; ++e) {
-    const int hv = hk * grp + e;
-    const int64_t sh = slot * a.Hv + hv;
-    const Tile* tl = a.tiles + sh;
-    __syncthreads();
-    if (tid < kC) gam[tid] = ti.sc[0], dec[tid] = ti.sc[1], bet[tid] = ti.sc[2], Gf[tid] = ti.sc[3];
-    {  // Tb and P, hi and lo
-      const int lt8 = swz(tid >> 3, (tid & 7) * 8, kLT);
-      *reinterpret_cast<bf16x8*>(TbL[0] + lt8) = ti.tp[0];
-      *reinterpret_cast<bf16x8*>(TbL[1] + lt8) = ti.tp[1];
-      *reinterpret_cast<bf16x8*>(PL[0] + lt8) = ti.tp[2];
-      *reinterpret_cast<bf16x8*>(PL[1] + lt8) = ti.tp[3];
+    // The chunk's K rows (A operands of K S0^T, K dS^T, K K^T; B of the K products of the end phase).
+    for (int e = tid; e < kC * 16; e += kThreads) {
+      const int t = e >> 4, c8 = (e & 15) * 8;
+      *reinterpret_cast<uint4*>(Kres + swz(t, c8, kLK)) = buf_ld16(krs, uint32_t(t * sk + c8) * 2);
     }
-    f32x4 dPt[2], dTbt[2], dQi[4];  // dPt, dTbt: key tiles m = key_tile(pw, hw, mi); lane -> column i = ip, rows j
+    f32x4 dQ[4], dK[4];  // columns 16 (4 hw + t) + li, rows 16 pw + 4 g + jj
 #pragma unroll
-    for (int t = 0; t < 2; ++t) dPt[t] = zero4(), dTbt[t] = zero4();
-#pragma unroll
-    for (int t = 0; t < 4; ++t) dQi[t] = zero4();
-    float gpart[4] = {0.f, 0.f, 0.f, 0.f}, hD[4] = {0.f, 0.f, 0.f, 0.f}, sds = 0.f;
-    __syncthreads();
+    for (int t = 0; t < 4; ++t) dQ[t] = zero4(), dK[t] = zero4();
+    // (K K^T)[p][m], rows p = 16 pw + 4g + jj, columns m = 16 key_tile(pw, hw, mi) + li; zero above tile pw. The same
+    // for every value head of the group: formed in the first one's end phase.
+    f32x4 kk[2];
 
-    // The end phase's inputs (T rows hi and lo, Q rows, as bf16 bits), loaded during the value head's last block
-    // into the registers the next block's reads would use: thread -> T row tid / 8, columns 8 (tid % 8) .. + 7
-    // (zeros above the diagonal blocks), and Q row e / 16, columns 8 (e % 16) .. + 7 for e = tid, tid + 512.
-    auto load_end = [&](BlockIn& b, int lt) {
-      const auto trr = buffer_rsrc(tl->t[0], 2 * kTri * 2);
-      b.xs[0] = __builtin_bit_cast(float4, tri_ld8(trr, 0, lt >> 3, (lt & 7) * 8));
-      b.xs[1] = __builtin_bit_cast(float4, tri_ld8(trr, kTri, lt >> 3, (lt & 7) * 8));
-#pragma unroll
-      for (int q2 = 0; q2 < 2; ++q2) {
-        const int e = lt + kThreads * q2, t = e >> 4, c8 = (e & 15) * 8;
-        b.ys[q2] = __builtin_bit_cast(float4, buf_ld16(qrs, uint32_t(t * sk + c8) * 2));
+    for (int e = 0; e < grp; ++e) {
+      const int hv = hk * grp + e;
+      const int64_t sh = slot * a.Hv + hv;
+      const Tile* tl = a.tiles + sh;
+      __syncthreads();
+      if (tid < kC) gam[tid] = ti.sc[0], dec[tid] = ti.sc[1], bet[tid] = ti.sc[2], Gf[tid] = ti.sc[3];
+      {  // Tb and P, hi and lo
+        const int lt8 = swz(tid >> 3, (tid & 7) * 8, kLT);
+        *reinterpret_cast<bf16x8*>(TbL[0] + lt8) = ti.tp[0];
+        *reinterpret_cast<bf16x8*>(TbL[1] + lt8) = ti.tp[1];
+        *reinterpret_cast<bf16x8*>(PL[0] + lt8) = ti.tp[2];
+        *reinterpret_cast<bf16x8*>(PL[1] + lt8) = ti.tp[3];
       }
-    };
+      f32x4 dPt[2], dTbt[2], dQi[4];  // dPt, dTbt: key tiles m = key_tile(pw, hw, mi); lane -> column i = ip, rows j
+#pragma unroll
+      for (int t = 0; t < 2; ++t) dPt[t] = zero4(), dTbt[t] = zero4();
+#pragma unroll
+      for (int t = 0; t < 4; ++t) dQi[t] = zero4();
+      float gpart[4] = {0.f, 0.f, 0.f, 0.f}, hD[4] = {0.f, 0.f, 0.f, 0.f}, sds = 0.f;
+      __syncthreads();
 
-    // One 32-row block of the state. The last block of the value head (more = false) loads the end phase's inputs
-    // instead of the next block's: it is a separate copy of the code, so that every copy issues the same loads in
-    // the same order whatever the path, and the compiler's count of outstanding loads stays exact.
-    auto block = [&](const int r0, auto more_tag) {
-      constexpr bool more = decltype(more_tag)::value;
-      // Lane indices re-derived from an opaque copy, so their many address expressions are recomputed here instead
-      // of being hoisted out of both loops and held (spilled) for the whole kernel.
+      // The end phase's inputs (T rows hi and lo, Q rows, as bf16 bits), loaded during the value head's last block
+      // into the registers the next block's reads would use: thread -> T row tid / 8, columns 8 (tid % 8) .. + 7
+      // (zeros above the diagonal blocks), and Q row e / 16, columns 8 (e % 16) .. + 7 for e = tid, tid + 512.
+      auto load_end = [&](BlockIn& b, int lt) {
+        const auto trr = buffer_rsrc(tl->t[0], 2 * kTri * 2);
+        b.xs[0] = __builtin_bit_cast(float4, tri_ld8(trr, 0, lt >> 3, (lt & 7) * 8));
+        b.xs[1] = __builtin_bit_cast(float4, tri_ld8(trr, kTri, lt >> 3, (lt & 7) * 8));
+#pragma unroll
+        for (int q2 = 0; q2 < 2; ++q2) {
+          const int e = lt + kThreads * q2, t = e >> 4, c8 = (e & 15) * 8;
+          b.ys[q2] = __builtin_bit_cast(float4, buf_ld16(qrs, uint32_t(t * sk + c8) * 2));
+        }
+      };
+
+      // One 32-row block of the state. The last block of the value head (more = false) loads the end phase's inputs
+      // instead of the next block's: it is a separate copy of the code, so that every copy issues the same loads in
+      // the same order whatever the path, and the compiler's count of outstanding loads stays exact.
+      auto block = [&](const int r0, auto more_tag) {
+        constexpr bool more = decltype(more_tag)::value;
+        // Lane indices re-derived from an opaque copy, so their many address expressions are recomputed here instead
+        // of being hoisted out of both loops and held (spilled) for the whole kernel.
+        int lt = tid;
+        asm volatile("" : "+v"(lt));
+        const int g = (lt >> 4) & 3, li = lt & 15, pw = (lt >> 6) & 3, hw = lt >> 8, ip = 16 * pw + li;
+        const int sr = lt >> 4, sc = (lt & 15) * 8, iy = lt >> 3, r4 = (lt & 7) * 4;
+        const float4* xs = nb.xs;
+        const float4* ys = nb.ys;
+        const uint4 yraw = nb.yraw;
+        __syncthreads();  // the previous block's readers of LDS are done
+
+        {  // Stage S0, dS rows and dY rows as hi / lo.
+          const float x[8] = {xs[0].x, xs[0].y, xs[0].z, xs[0].w, xs[1].x, xs[1].y, xs[1].z, xs[1].w};
+          const float y[8] = {ys[0].x, ys[0].y, ys[0].z, ys[0].w, ys[1].x, ys[1].y, ys[1].z, ys[1].w};
+#pragma unroll
+          for (int u = 0; u < 8; ++u) sds += x[u] * y[u];
+          const Split8 xsp = split8(x), ysp = split8(y);
+          const int at = swz(sr, sc, kLS);
+          *reinterpret_cast<bf16x8*>(sb + oS0h + at) = xsp.hi;
+          *reinterpret_cast<bf16x8*>(sb + oS0l + at) = xsp.lo;
+          *reinterpret_cast<bf16x8*>(sb + odSh + at) = ysp.hi;
+          *reinterpret_cast<bf16x8*>(sb + odSl + at) = ysp.lo;
+          if constexpr (kExactDy) {
+            *reinterpret_cast<uint2*>(sb + odYh + swz(iy, r4, kLY)) = uint2{yraw.x, yraw.y};
+          } else {
+            put4(sb + odYh, sb + odYl, swz(iy, r4, kLY), __uint_as_float(yraw.x), __uint_as_float(yraw.y),
+                 __uint_as_float(yraw.z), __uint_as_float(yraw.w));
+          }
+        }
+        float vv[4];
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) vv[jj] = bf16_to_f32(nb.vraw[jj]);
+        __syncthreads();
+        if constexpr (more)
+          load_rows(nb.xs, a.ckpt, cur, hv, r0 + 32, lt);  // the next block's reads, first group
+        else
+          load_end(nb, lt);
+
+        // The wave's own dY rows (i = ip, k = r = 8g..): A of dY S0, B of Delta dY^T.
+        Split8 dYo;
+        dYo.hi = lds8(sb + odYh + swz(ip, 8 * g, kLY));
+        if constexpr (!kExactDy) dYo.lo = lds8(sb + odYl + swz(ip, 8 * g, kLY));
+
+        // Phase 1: KS and KdS for positions i = 16 pw + 4g + jj, state rows r = 16 hw + li.
+        const int r = 16 * hw + li, i0 = 16 * pw + 4 * g;
+        f32x4 ks = zero4(), kds = zero4();
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          const int at = swz(r, 32 * s + 8 * g, kLS);
+          const bf16x8 ka = lds8(Kres + swz(ip, 32 * s + 8 * g, kLK));
+          ks = mma(mma(ks, ka, lds8(sb + oS0h + at)), ka, lds8(sb + oS0l + at));
+          kds = mma(mma(kds, ka, lds8(sb + odSh + at)), ka, lds8(sb + odSl + at));
+        }
+        float gks[4], rv[4];
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          gks[jj] = gam[i0 + jj] * ks[jj];
+          rv[jj] = vv[jj] - gks[jj];
+        }
+        put4(sb + oRh, sb + oRl, swz(r, i0, kLP), rv[0], rv[1], rv[2], rv[3]);
+        __syncthreads();
+        if constexpr (more) load_rows(nb.ys, a.dsend, cur, hv, r0 + 32, lt);
+
+        // Phase 2: Delta = Tb R and dDelta = P^T dY + D KdS (rows: the wave's positions; lane: row r).
+        f32x4 dl = zero4(), dd;
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+          if (s == 0 || pw >= 2) {  // Tb is zero above the diagonal blocks: rows 0..31 end at column 31
+            const int at = swz(r, 32 * s + 8 * g, kLP), atb = swz(ip, 32 * s + 8 * g, kLT);
+            const Split8 TbA{lds8(TbL[0] + atb), lds8(TbL[1] + atb)};
+            dl = mma3(dl, TbA, Split8{lds8(sb + oRh + at), lds8(sb + oRl + at)});
+          }
+        }
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) dd[jj] = dec[i0 + jj] * kds[jj];
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+          if (32 * s + 31 >= 16 * pw) {  // P^T is zero below the diagonal
+            const int at = 32 * s * kLY + 16 * hw;
+            // P^T rows ip (k = i): P's rows 32s.., column ip.
+            const Split8 PA{lds_tr8s(PL[0] + 32 * s * kLT + 16 * pw, kLT, lt), lds_tr8s(PL[1] + 32 * s * kLT + 16 * pw, kLT, lt)};
+            if constexpr (kExactDy)
+              dd = mma2(dd, PA, lds_tr8s(sb + odYh + at, kLY, lt));
+            else
+              dd = mma3(dd, PA, Split8{lds_tr8s(sb + odYh + at, kLY, lt), lds_tr8s(sb + odYl + at, kLY, lt)});
+          }
+        }
+        {
+          float ddl[4];
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) {
+            hD[jj] += dec[i0 + jj] * dl[jj] * kds[jj];
+            ddl[jj] = dec[i0 + jj] * dl[jj];
+          }
+          put4(sb + oDh, sb + oDl, swz(r, i0, kLP), dl[0], dl[1], dl[2], dl[3]);
+          put4(sb + oDDh, sb + oDDl, swz(r, i0, kLP), ddl[0], ddl[1], ddl[2], ddl[3]);
+          put4(sb + odDh, sb + odDl, swz(r, i0, kLP), dd[0], dd[1], dd[2], dd[3]);
+        }
+        __syncthreads();
+        if constexpr (more) load_dy_v(nb, cur, hv, r0 + 32, lt);
+
+        // Phase 3: dR = Tb^T dDelta; dP^T += Delta dY^T and dTb^T += R dDelta^T over this half's key tiles.
+        {
+          f32x4 dr = zero4();
+#pragma unroll
+          for (int s = 0; s < 2; ++s) {
+            if (32 * s + 31 >= 16 * pw) {  // Tb^T is zero below the diagonal
+              const int at = swz(r, 32 * s + 8 * g, kLP);
+              // Tb^T rows ip (k = j): Tb's rows 32s.., column ip.
+              const Split8 TbtA{lds_tr8s(TbL[0] + 32 * s * kLT + 16 * pw, kLT, lt),
+                                lds_tr8s(TbL[1] + 32 * s * kLT + 16 * pw, kLT, lt)};
+              dr = mma3(dr, TbtA, Split8{lds8(sb + odDh + at), lds8(sb + odDl + at)});
+            }
+          }
+          float gdr[4];
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) {
+            gpart[jj] -= dr[jj] * gks[jj];
+            gdr[jj] = -gam[i0 + jj] * dr[jj];
+          }
+          put4(sb + oGdRh, sb + oGdRl, swz(r, i0, kLP), gdr[0], gdr[1], gdr[2], gdr[3]);
+        }
+        {
+          // dDelta[i][r] of the wave's positions as B (k = r, n = i).
+          const Split8 BdD{lds_tr8s(sb + odDh + 16 * pw, kLP, lt), lds_tr8s(sb + odDl + 16 * pw, kLP, lt)};
+#pragma unroll
+          for (int mi = 0; mi < 2; ++mi) {
+            const int m = key_tile(pw, hw, mi);
+            if (m <= pw) {
+              // Delta and R rows j of key tile m as A (m = j, k = r).
+              const Split8 AD{lds_tr8s(sb + oDh + 16 * m, kLP, lt), lds_tr8s(sb + oDl + 16 * m, kLP, lt)};
+              if constexpr (kExactDy)
+                dPt[mi] = mma2(dPt[mi], AD, dYo.hi);
+              else
+                dPt[mi] = mma3(dPt[mi], AD, dYo);
+              const Split8 AR{lds_tr8s(sb + oRh + 16 * m, kLP, lt), lds_tr8s(sb + oRl + 16 * m, kLP, lt)};
+              dTbt[mi] = mma3(dTbt[mi], AR, BdD);
+            }
+          }
+        }
+        __syncthreads();
+
+        // Phase 4: dQ_inter += dY S0; dK += -diag(exp G) dR S0 + D Delta dS (columns of this half).
+        {
+          const Split8 AGdR{lds_tr8s(sb + oGdRh + 16 * pw, kLP, lt), lds_tr8s(sb + oGdRl + 16 * pw, kLP, lt)};
+          const Split8 ADD{lds_tr8s(sb + oDDh + 16 * pw, kLP, lt), lds_tr8s(sb + oDDl + 16 * pw, kLP, lt)};
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const int c0 = 16 * (4 * hw + t);
+            const Split8 B0{lds_tr8s(sb + oS0h + c0, kLS, lt), lds_tr8s(sb + oS0l + c0, kLS, lt)};
+            const Split8 B1{lds_tr8s(sb + odSh + c0, kLS, lt), lds_tr8s(sb + odSl + c0, kLS, lt)};
+            if constexpr (kExactDy)
+              dQi[t] = mma2(dQi[t], dYo.hi, B0);
+            else
+              dQi[t] = mma3(dQi[t], dYo, B0);
+            dK[t] = mma3(dK[t], AGdR, B0);
+            dK[t] = mma3(dK[t], ADD, B1);
+          }
+        }
+      };
+      int r0 = 0;
+      for (; r0 + 32 < a.Dv; r0 += 32) block(r0, std::true_type{});
+      block(r0, std::false_type{});
+
+      // End of the state rows for this value head: per-position partials, then the 64 x 64 part.
       int lt = tid;
       asm volatile("" : "+v"(lt));
       const int g = (lt >> 4) & 3, li = lt & 15, pw = (lt >> 6) & 3, hw = lt >> 8, ip = 16 * pw + li;
-      const int sr = lt >> 4, sc = (lt & 15) * 8, iy = lt >> 3, r4 = (lt & 7) * 4;
-      const float4* xs = nb.xs;
-      const float4* ys = nb.ys;
-      const uint4 yraw = nb.yraw;
-      __syncthreads();  // the previous block's readers of LDS are done
-
-      {  // Stage S0, dS rows and dY rows as hi / lo.
-        const float x[8] = {xs[0].x, xs[0].y, xs[0].z, xs[0].w, xs[1].x, xs[1].y, xs[1].z, xs[1].w};
-        const float y[8] = {ys[0].x, ys[0].y, ys[0].z, ys[0].w, ys[1].x, ys[1].y, ys[1].z, ys[1].w};
-#pragma unroll
-        for (int u = 0; u < 8; ++u) sds += x[u] * y[u];
-        const Split8 xsp = split8(x), ysp = split8(y);
-        const int at = swz(sr, sc, kLS);
-        *reinterpret_cast<bf16x8*>(sb + oS0h + at) = xsp.hi;
-        *reinterpret_cast<bf16x8*>(sb + oS0l + at) = xsp.lo;
-        *reinterpret_cast<bf16x8*>(sb + odSh + at) = ysp.hi;
-        *reinterpret_cast<bf16x8*>(sb + odSl + at) = ysp.lo;
-        if constexpr (kExactDy) {
-          *reinterpret_cast<uint2*>(sb + odYh + swz(iy, r4, kLY)) = uint2{yraw.x, yraw.y};
-        } else {
-          put4(sb + odYh, sb + odYl, swz(iy, r4, kLY), __uint_as_float(yraw.x), __uint_as_float(yraw.y),
-               __uint_as_float(yraw.z), __uint_as_float(yraw.w));
-        }
-      }
-      float vv[4];
-#pragma unroll
-      for (int jj = 0; jj < 4; ++jj) vv[jj] = bf16_to_f32(nb.vraw[jj]);
-      __syncthreads();
-      if constexpr (more)
-        load_rows(nb.xs, a.ckpt, hv, r0 + 32, lt);  // the next block's reads, first group
-      else
-        load_end(nb, lt);
-
-      // The wave's own dY rows (i = ip, k = r = 8g..): A of dY S0, B of Delta dY^T.
-      Split8 dYo;
-      dYo.hi = lds8(sb + odYh + swz(ip, 8 * g, kLY));
-      if constexpr (!kExactDy) dYo.lo = lds8(sb + odYl + swz(ip, 8 * g, kLY));
-
-      // Phase 1: KS and KdS for positions i = 16 pw + 4g + jj, state rows r = 16 hw + li.
-      const int r = 16 * hw + li, i0 = 16 * pw + 4 * g;
-      f32x4 ks = zero4(), kds = zero4();
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const int at = swz(r, 32 * s + 8 * g, kLS);
-        const bf16x8 ka = lds8(Kres + swz(ip, 32 * s + 8 * g, kLK));
-        ks = mma(mma(ks, ka, lds8(sb + oS0h + at)), ka, lds8(sb + oS0l + at));
-        kds = mma(mma(kds, ka, lds8(sb + odSh + at)), ka, lds8(sb + odSl + at));
-      }
-      float gks[4], rv[4];
+      const int i0 = 16 * pw + 4 * g;  // first of the lane's accumulator rows
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj) {
-        gks[jj] = gam[i0 + jj] * ks[jj];
-        rv[jj] = vv[jj] - gks[jj];
-      }
-      put4(sb + oRh, sb + oRl, swz(r, i0, kLP), rv[0], rv[1], rv[2], rv[3]);
-      __syncthreads();
-      if constexpr (more) load_rows(nb.ys, a.dsend, hv, r0 + 32, lt);
-
-      // Phase 2: Delta = Tb R and dDelta = P^T dY + D KdS (rows: the wave's positions; lane: row r).
-      f32x4 dl = zero4(), dd;
-#pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        if (s == 0 || pw >= 2) {  // Tb is zero above the diagonal blocks: rows 0..31 end at column 31
-          const int at = swz(r, 32 * s + 8 * g, kLP), atb = swz(ip, 32 * s + 8 * g, kLT);
-          const Split8 TbA{lds8(TbL[0] + atb), lds8(TbL[1] + atb)};
-          dl = mma3(dl, TbA, Split8{lds8(sb + oRh + at), lds8(sb + oRl + at)});
-        }
-      }
-#pragma unroll
-      for (int jj = 0; jj < 4; ++jj) dd[jj] = dec[i0 + jj] * kds[jj];
-#pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        if (32 * s + 31 >= 16 * pw) {  // P^T is zero below the diagonal
-          const int at = 32 * s * kLY + 16 * hw;
-          // P^T rows ip (k = i): P's rows 32s.., column ip.
-          const Split8 PA{lds_tr8s(PL[0] + 32 * s * kLT + 16 * pw, kLT, lt), lds_tr8s(PL[1] + 32 * s * kLT + 16 * pw, kLT, lt)};
-          if constexpr (kExactDy)
-            dd = mma2(dd, PA, lds_tr8s(sb + odYh + at, kLY, lt));
-          else
-            dd = mma3(dd, PA, Split8{lds_tr8s(sb + odYh + at, kLY, lt), lds_tr8s(sb + odYl + at, kLY, lt)});
-        }
+        const float v = sum16(gpart[jj]), h = sum16(hD[jj]);
+        if (li == 0) gpos[hw][i0 + jj] = v, hpos[hw][i0 + jj] = h;
       }
       {
-        float ddl[4];
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-          hD[jj] += dec[i0 + jj] * dl[jj] * kds[jj];
-          ddl[jj] = dec[i0 + jj] * dl[jj];
-        }
-        put4(sb + oDh, sb + oDl, swz(r, i0, kLP), dl[0], dl[1], dl[2], dl[3]);
-        put4(sb + oDDh, sb + oDDl, swz(r, i0, kLP), ddl[0], ddl[1], ddl[2], ddl[3]);
-        put4(sb + odDh, sb + odDl, swz(r, i0, kLP), dd[0], dd[1], dd[2], dd[3]);
+        float v = sum16(sds);
+        v += __shfl_xor(v, 16);
+        v += __shfl_xor(v, 32);
+        if ((tid & 63) == 0) red[tid >> 6] = v;
       }
       __syncthreads();
-      if constexpr (more) load_dy_v(nb, hv, r0 + 32, lt);
 
-      // Phase 3: dR = Tb^T dDelta; dP^T += Delta dY^T and dTb^T += R dDelta^T over this half's key tiles.
+      // E1: Q rows and T (hi, lo) into the end-phase region. Per lane, at i = ip and
+      // j = 16 key_tile(pw, hw, mi) + 4g + jj (dP and dTb masked to j <= i): the row and column sums of dP * P (the P
+      // factor's part of dG), P * M with M_ij = exp(G_i - G_j) over P's entries, and dTb diag(beta), both as hi and lo
+      // in place of Tb and P (each lane rewrites only the P entries it has just read).
       {
-        f32x4 dr = zero4();
+        {
+          const int at = swz(lt >> 3, (lt & 7) * 8, kLT);
+          *reinterpret_cast<float4*>(sb + eTh + at) = nb.xs[0];
+          *reinterpret_cast<float4*>(sb + eTl + at) = nb.xs[1];
 #pragma unroll
-        for (int s = 0; s < 2; ++s) {
-          if (32 * s + 31 >= 16 * pw) {  // Tb^T is zero below the diagonal
-            const int at = swz(r, 32 * s + 8 * g, kLP);
-            // Tb^T rows ip (k = j): Tb's rows 32s.., column ip.
-            const Split8 TbtA{lds_tr8s(TbL[0] + 32 * s * kLT + 16 * pw, kLT, lt),
-                              lds_tr8s(TbL[1] + 32 * s * kLT + 16 * pw, kLT, lt)};
-            dr = mma3(dr, TbtA, Split8{lds8(sb + odDh + at), lds8(sb + odDl + at)});
+          for (int q2 = 0; q2 < 2; ++q2) {
+            const int e = lt + kThreads * q2;
+            *reinterpret_cast<uint4*>(sb + eQb + swz(e >> 4, (e & 15) * 8, kLK)) = __builtin_bit_cast(uint4, nb.ys[q2]);
           }
         }
-        float gdr[4];
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-          gpart[jj] -= dr[jj] * gks[jj];
-          gdr[jj] = -gam[i0 + jj] * dr[jj];
+        if (e + 1 < grp) {  // nb is free from here
+          load_head(ti, nb, cur, hv + 1);
+        } else if (id + int(gridDim.x) < total) {  // the next item's first head
+          const Item nx = item_at(id + gridDim.x);
+          load_head(ti, nb, nx, nx.hk * grp);
         }
-        put4(sb + oGdRh, sb + oGdRl, swz(r, i0, kLP), gdr[0], gdr[1], gdr[2], gdr[3]);
-      }
-      {
-        // dDelta[i][r] of the wave's positions as B (k = r, n = i).
-        const Split8 BdD{lds_tr8s(sb + odDh + 16 * pw, kLP, lt), lds_tr8s(sb + odDl + 16 * pw, kLP, lt)};
+        // Row sums (over j) add up over g here and over hw in dG; column sums (over i) over li here and over pw in dG.
+        float prow = 0.f;
+        const float gi = Gf[ip];
 #pragma unroll
         for (int mi = 0; mi < 2; ++mi) {
-          const int m = key_tile(pw, hw, mi);
-          if (m <= pw) {
-            // Delta and R rows j of key tile m as A (m = j, k = r).
-            const Split8 AD{lds_tr8s(sb + oDh + 16 * m, kLP, lt), lds_tr8s(sb + oDl + 16 * m, kLP, lt)};
-            if constexpr (kExactDy)
-              dPt[mi] = mma2(dPt[mi], AD, dYo.hi);
-            else
-              dPt[mi] = mma3(dPt[mi], AD, dYo);
-            const Split8 AR{lds_tr8s(sb + oRh + 16 * m, kLP, lt), lds_tr8s(sb + oRl + 16 * m, kLP, lt)};
-            dTbt[mi] = mma3(dTbt[mi], AR, BdD);
+          const int j0 = 16 * key_tile(pw, hw, mi) + 4 * g, at = swz(ip, j0, kLT);
+          const uint2 ph = *reinterpret_cast<const uint2*>(PL[0] + at);
+          const uint2 pl = *reinterpret_cast<const uint2*>(PL[1] + at);
+          const uint32_t hw4[2] = {ph.x, ph.y}, lw4[2] = {pl.x, pl.y};
+          float pm[4], db[4];
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) {
+            const int j = j0 + jj;
+            const float dp = j <= ip ? dPt[mi][jj] : 0.f;
+            const uint32_t hb = hw4[jj >> 1], lb = lw4[jj >> 1];
+            const float pv = jj & 1 ? __uint_as_float(hb & 0xffff0000u) + __uint_as_float(lb & 0xffff0000u)
+                                    : __uint_as_float(hb << 16) + __uint_as_float(lb << 16);
+            const float x = dp * pv;
+            prow += x;
+            const float col = sum16(x);
+            if (li == 0) x2c[pw][j] = col;
+            // Where j > i, dp is zero and the exponent positive: clamped at 0 to keep the product finite.
+            pm[jj] = dp * __expf(fminf(gi - Gf[j], 0.f));
+            db[jj] = (j <= ip ? dTbt[mi][jj] : 0.f) * bet[j];
           }
+          put4(TbL[0], TbL[1], at, pm[0], pm[1], pm[2], pm[3]);
+          put4(PL[0], PL[1], at, db[0], db[1], db[2], db[3]);
+        }
+        prow += __shfl_xor(prow, 16);
+        prow += __shfl_xor(prow, 32);
+        if (g == 0) x2r[hw][ip] = prow;
+      }
+      __syncthreads();
+
+      // E2: the column sums of dTb * T (dbeta's T part); dQ += diag(exp G) dQ_inter and its dG term; K K^T (the first
+      // value head only, kept in registers); dQ += (P * M) K; dK += (P * M)^T Q; Z = dTb diag(beta) T^T, stored as Z^T.
+      {
+#pragma unroll
+        for (int mi = 0; mi < 2; ++mi) {
+          const int j0 = 16 * key_tile(pw, hw, mi) + 4 * g, at = swz(ip, j0, kLT);
+          const uint2 th = *reinterpret_cast<const uint2*>(sb + eTh + at);
+          const uint2 tlo = *reinterpret_cast<const uint2*>(sb + eTl + at);
+          const uint32_t hw4[2] = {th.x, th.y}, lw4[2] = {tlo.x, tlo.y};
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) {
+            const int j = j0 + jj;
+            const uint32_t hb = hw4[jj >> 1], lb = lw4[jj >> 1];
+            const float tv = jj & 1 ? __uint_as_float(hb & 0xffff0000u) + __uint_as_float(lb & 0xffff0000u)
+                                    : __uint_as_float(hb << 16) + __uint_as_float(lb << 16);
+            const float colb = sum16((j <= ip ? dTbt[mi][jj] : 0.f) * tv);
+            if (li == 0) dbTp[pw][j] = colb;
+          }
+        }
+        float tq[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) {
+            const int i = i0 + jj, c = 16 * (4 * hw + t) + li;
+            tq[jj] += (float)sb[eQb + swz(i, c, kLK)] * dQi[t][jj];
+            dQ[t][jj] += gam[i] * dQi[t][jj];
+          }
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          const float v = sum16(tq[jj]);
+          if (li == 0) tpos[hw][i0 + jj] = v;
+        }
+        if (e == 0) {
+#pragma unroll
+          for (int mi = 0; mi < 2; ++mi) {
+            const int m = key_tile(pw, hw, mi);
+            kk[mi] = zero4();
+            if (m <= pw) {
+#pragma unroll
+              for (int s = 0; s < 4; ++s)
+                kk[mi] = mma(kk[mi], lds8(Kres + swz(ip, 32 * s + 8 * g, kLK)), lds8(Kres + swz(16 * m + li, 32 * s + 8 * g, kLK)));
+            }
+          }
+        }
+        // P * M is zero above the diagonal: rows i < 32 end at column 31, and columns j >= 32 start at row 32.
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+          if (s == 0 || pw >= 2) {
+            const int at = swz(ip, 32 * s + 8 * g, kLT);
+            const Split8 Apm{lds8(TbL[0] + at), lds8(TbL[1] + at)};  // (P * M) rows i = ip, k = j
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+              dQ[t] = mma2(dQ[t], Apm, lds_tr8s(Kres + 32 * s * kLK + 16 * (4 * hw + t), kLK, lt));
+          }
+          if (s == 1 || pw < 2) {
+            const Split8 Apmt{lds_tr8s(TbL[0] + 32 * s * kLT + 16 * pw, kLT, lt),
+                              lds_tr8s(TbL[1] + 32 * s * kLT + 16 * pw, kLT, lt)};  // (P * M)^T rows j = ip, k = i
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+              dK[t] = mma2(dK[t], Apmt, lds_tr8s(sb + eQb + 32 * s * kLK + 16 * (4 * hw + t), kLK, lt));
+          }
+        }
+#pragma unroll
+        for (int mi = 0; mi < 2; ++mi) {
+          const int mr = 16 * (2 * hw + mi) + li;  // this lane's column m of Z
+          f32x4 z = zero4();
+#pragma unroll
+          for (int s = 0; s < 2; ++s) {
+            const int aa = swz(ip, 32 * s + 8 * g, kLT), ab = swz(mr, 32 * s + 8 * g, kLT);
+            z = mma3(z, Split8{lds8(PL[0] + aa), lds8(PL[1] + aa)}, Split8{lds8(sb + eTh + ab), lds8(sb + eTl + ab)});
+          }
+          put4(sb + eZh, sb + eZl, swz(mr, i0, kLT), z[0], z[1], z[2], z[3]);
         }
       }
       __syncthreads();
 
-      // Phase 4: dQ_inter += dY S0; dK += -diag(exp G) dR S0 + D Delta dS (columns of this half).
+      // E3: dA = -T^T Z below the diagonal (rows p = i0 + jj, columns m = 16 key_tile(pw, hw, mi) + li, as kk), and at
+      // once its products with E = exp(G_p - G_m) and K K^T: the A part of dbeta (row sums), of dG (row and column
+      // sums), and dKK = diag(beta) (dA * E), stored as dKK^T.
       {
-        const Split8 AGdR{lds_tr8s(sb + oGdRh + 16 * pw, kLP, lt), lds_tr8s(sb + oGdRl + 16 * pw, kLP, lt)};
-        const Split8 ADD{lds_tr8s(sb + oDDh + 16 * pw, kLP, lt), lds_tr8s(sb + oDDl + 16 * pw, kLP, lt)};
+        // Only tiles mt <= pw are kept (mcol < p), and T^T rows p >= 32 are zero below column 32.
+        Split8 AT[2];  // T^T rows p = ip, k = i
+#pragma unroll
+        for (int s = 0; s < 2; ++s)
+          AT[s] = Split8{lds_tr8s(sb + eTh + 32 * s * kLT + 16 * pw, kLT, lt),
+                         lds_tr8s(sb + eTl + 32 * s * kLT + 16 * pw, kLT, lt)};
+        float rowp[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int mi = 0; mi < 2; ++mi) {
+          const int mt = key_tile(pw, hw, mi), mcol = 16 * mt + li;
+          f32x4 da = zero4();
+          if (mt <= pw) {
+#pragma unroll
+            for (int s = 0; s < 2; ++s) {
+              if (s == 1 || pw < 2) {
+                const int ab = swz(mcol, 32 * s + 8 * g, kLT);
+                da = mma3(da, AT[s], Split8{lds8(sb + eZh + ab), lds8(sb + eZl + ab)});
+              }
+            }
+          }
+          float colp = 0.f, kkt[4];
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) {
+            const int pr = i0 + jj;
+            const float e = __expf(fminf(Gf[pr] - Gf[mcol], 0.f));  // finite everywhere; used where mcol < pr
+            const float dae = mcol < pr ? -da[jj] * e : 0.f;           // dA_pm E_pm
+            const float prod = dae * kk[mi][jj];
+            rowp[jj] += prod;
+            colp += bet[pr] * prod;
+            kkt[jj] = bet[pr] * dae;
+          }
+          put4(sb + eKh, sb + eKl, swz(mcol, i0, kLT), kkt[0], kkt[1], kkt[2], kkt[3]);
+          colp += __shfl_xor(colp, 16);
+          colp += __shfl_xor(colp, 32);
+          if (g == 0) x1cp[pw][mcol] = colp;
+        }
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          const float v = sum16(rowp[jj]);
+          if (li == 0) dbAp[hw][i0 + jj] = v;
+        }
+      }
+      __syncthreads();
+
+      // E4: dK += (dKK + dKK^T) K for rows j = ip, this half's columns: dKK rows j through the transposing read of
+      // dKK^T, dKK^T rows j directly.
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        const int at = swz(ip, 32 * s + 8 * g, kLT);
+        const Split8 A1{lds_tr8s(sb + eKh + 32 * s * kLT + 16 * pw, kLT, lt), lds_tr8s(sb + eKl + 32 * s * kLT + 16 * pw, kLT, lt)};
+        const Split8 A2{lds8(sb + eKh + at), lds8(sb + eKl + at)};
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
-          const int c0 = 16 * (4 * hw + t);
-          const Split8 B0{lds_tr8s(sb + oS0h + c0, kLS, lt), lds_tr8s(sb + oS0l + c0, kLS, lt)};
-          const Split8 B1{lds_tr8s(sb + odSh + c0, kLS, lt), lds_tr8s(sb + odSl + c0, kLS, lt)};
-          if constexpr (kExactDy)
-            dQi[t] = mma2(dQi[t], dYo.hi, B0);
-          else
-            dQi[t] = mma3(dQi[t], dYo, B0);
-          dK[t] = mma3(dK[t], AGdR, B0);
-          dK[t] = mma3(dK[t], ADD, B1);
+          const bf16x8 B = lds_tr8s(Kres + 32 * s * kLK + 16 * (4 * hw + t), kLK, lt);
+          // dKK is strictly lower: dKK[j][i] needs i < j, dKK[i][j] needs i > j.
+          if (s == 0 || pw >= 2) dK[t] = mma2(dK[t], A1, B);
+          if (s == 1 || pw < 2) dK[t] = mma2(dK[t], A2, B);
         }
       }
-    };
-    int r0 = 0;
-    for (; r0 + 32 < a.Dv; r0 += 32) block(r0, std::true_type{});
-    block(r0, std::false_type{});
-
-    // End of the state rows for this value head: per-position partials, then the 64 x 64 part.
-    int lt = tid;
-    asm volatile("" : "+v"(lt));
-    const int g = (lt >> 4) & 3, li = lt & 15, pw = (lt >> 6) & 3, hw = lt >> 8, ip = 16 * pw + li;
-    const int i0 = 16 * pw + 4 * g;  // first of the lane's accumulator rows
+      // E5 (one wave): dG per position, dg = its reverse cumulative sum (a suffix scan over the wave), and dbeta.
+      if (tid < kC) {
+        const int t = tid;
+        const float hs = hpos[0][t] + hpos[1][t];
+        float hsum = sum16(hs);
+        hsum += __shfl_xor(hsum, 16);
+        hsum += __shfl_xor(hsum, 32);
+        float sds_all = 0.f;
 #pragma unroll
-    for (int jj = 0; jj < 4; ++jj) {
-      const float v = sum16(gpart[jj]), h = sum16(hD[jj]);
-      if (li == 0) gpos[hw][i0 + jj] = v, hpos[hw][i0 + jj] = h;
+        for (int u = 0; u < kThreads / 64; ++u) sds_all += red[u];
+        const float dbA = dbAp[0][t] + dbAp[1][t];
+        float v = gam[t] * (tpos[0][t] + tpos[1][t]) + gpos[0][t] + gpos[1][t] - hs + bet[t] * dbA -
+                  (x1cp[0][t] + x1cp[1][t] + x1cp[2][t] + x1cp[3][t]) + x2r[0][t] + x2r[1][t] -
+                  (x2c[0][t] + x2c[1][t] + x2c[2][t] + x2c[3][t]);
+        if (t == kC - 1) v += hsum + gam[kC - 1] * sds_all;
+#pragma unroll
+        for (int off = 1; off < kC; off <<= 1) {
+          const float u = __shfl_down(v, off);
+          if (t + off < kC) v += u;
+        }
+        if (t < L) {
+          const int64_t g0 = tok * a.Hv + hv;
+          const uint32_t gi = uint32_t(t * a.Hv);
+          a.dg[g0 + gi] = a.g_is_log ? v : v / a.g[g0 + gi];
+          const float dbT = dbTp[0][t] + dbTp[1][t] + dbTp[2][t] + dbTp[3][t];
+          IO<OutT>::st(static_cast<OutT*>(a.dbeta) + g0, gi, dbT + dbA);
+        }
+      }
     }
-    {
-      float v = sum16(sds);
-      v += __shfl_xor(v, 16);
-      v += __shfl_xor(v, 32);
-      if ((tid & 63) == 0) red[tid >> 6] = v;
-    }
-    __syncthreads();
 
-    // E1: Q rows and T (hi, lo) into the end-phase region. Per lane, at i = ip and
-    // j = 16 key_tile(pw, hw, mi) + 4g + jj (dP and dTb masked to j <= i): the row and column sums of dP * P (the P
-    // factor's part of dG), P * M with M_ij = exp(G_i - G_j) over P's entries, and dTb diag(beta), both as hi and lo
-    // in place of Tb and P (each lane rewrites only the P entries it has just read).
+    // dq, dk for the wave's positions and columns (lane -> column 16 (4 hw + t) + li, rows 16 pw + 4g + jj), through
+    // buffer resources that end at the chunk's last row; lane indices from an opaque copy, so their addresses are
+    // formed here rather than hoisted out of the item loop.
     {
-      {
-        const int at = swz(lt >> 3, (lt & 7) * 8, kLT);
-        *reinterpret_cast<float4*>(sb + eTh + at) = nb.xs[0];
-        *reinterpret_cast<float4*>(sb + eTl + at) = nb.xs[1];
-#pragma unroll
-        for (int q2 = 0; q2 < 2; ++q2) {
-          const int e = lt + kThreads * q2;
-          *reinterpret_cast<uint4*>(sb + eQb + swz(e >> 4, (e & 15) * 8, kLK)) = __builtin_bit_cast(uint4, nb.ys[q2]);
-        }
-      }
-      if (e + 1 < grp) load_head(ti, nb, hv + 1);  // nb is free from here
-      // Row sums (over j) add up over g here and over hw in dG; column sums (over i) over li here and over pw in dG.
-      float prow = 0.f;
-      const float gi = Gf[ip];
-#pragma unroll
-      for (int mi = 0; mi < 2; ++mi) {
-        const int j0 = 16 * key_tile(pw, hw, mi) + 4 * g, at = swz(ip, j0, kLT);
-        const uint2 ph = *reinterpret_cast<const uint2*>(PL[0] + at);
-        const uint2 pl = *reinterpret_cast<const uint2*>(PL[1] + at);
-        const uint32_t hw4[2] = {ph.x, ph.y}, lw4[2] = {pl.x, pl.y};
-        float pm[4], db[4];
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-          const int j = j0 + jj;
-          const float dp = j <= ip ? dPt[mi][jj] : 0.f;
-          const uint32_t hb = hw4[jj >> 1], lb = lw4[jj >> 1];
-          const float pv = jj & 1 ? __uint_as_float(hb & 0xffff0000u) + __uint_as_float(lb & 0xffff0000u)
-                                  : __uint_as_float(hb << 16) + __uint_as_float(lb << 16);
-          const float x = dp * pv;
-          prow += x;
-          const float col = sum16(x);
-          if (li == 0) x2c[pw][j] = col;
-          // Where j > i, dp is zero and the exponent positive: clamped at 0 to keep the product finite.
-          pm[jj] = dp * __expf(fminf(gi - Gf[j], 0.f));
-          db[jj] = (j <= ip ? dTbt[mi][jj] : 0.f) * bet[j];
-        }
-        put4(TbL[0], TbL[1], at, pm[0], pm[1], pm[2], pm[3]);
-        put4(PL[0], PL[1], at, db[0], db[1], db[2], db[3]);
-      }
-      prow += __shfl_xor(prow, 16);
-      prow += __shfl_xor(prow, 32);
-      if (g == 0) x2r[hw][ip] = prow;
-    }
-    __syncthreads();
-
-    // E2: the column sums of dTb * T (dbeta's T part); dQ += diag(exp G) dQ_inter and its dG term; K K^T (the first
-    // value head only, kept in registers); dQ += (P * M) K; dK += (P * M)^T Q; Z = dTb diag(beta) T^T, stored as Z^T.
-    {
-#pragma unroll
-      for (int mi = 0; mi < 2; ++mi) {
-        const int j0 = 16 * key_tile(pw, hw, mi) + 4 * g, at = swz(ip, j0, kLT);
-        const uint2 th = *reinterpret_cast<const uint2*>(sb + eTh + at);
-        const uint2 tlo = *reinterpret_cast<const uint2*>(sb + eTl + at);
-        const uint32_t hw4[2] = {th.x, th.y}, lw4[2] = {tlo.x, tlo.y};
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-          const int j = j0 + jj;
-          const uint32_t hb = hw4[jj >> 1], lb = lw4[jj >> 1];
-          const float tv = jj & 1 ? __uint_as_float(hb & 0xffff0000u) + __uint_as_float(lb & 0xffff0000u)
-                                  : __uint_as_float(hb << 16) + __uint_as_float(lb << 16);
-          const float colb = sum16((j <= ip ? dTbt[mi][jj] : 0.f) * tv);
-          if (li == 0) dbTp[pw][j] = colb;
-        }
-      }
-      float tq[4] = {0.f, 0.f, 0.f, 0.f};
+      int lt = tid;
+      asm volatile("" : "+v"(lt));
+      const int g = (lt >> 4) & 3, li = lt & 15, pw = (lt >> 6) & 3, hw = lt >> 8;
+      const uint32_t bytes = uint32_t(L * sk) * uint32_t(sizeof(OutT));
+      const auto dqr = buffer_rsrc(static_cast<OutT*>(a.dq) + (tok * a.Hk + hk) * Dk, bytes);
+      const auto dkr = buffer_rsrc(static_cast<OutT*>(a.dk) + (tok * a.Hk + hk) * Dk, bytes);
 #pragma unroll
       for (int t = 0; t < 4; ++t)
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) {
-          const int i = i0 + jj, c = 16 * (4 * hw + t) + li;
-          tq[jj] += (float)sb[eQb + swz(i, c, kLK)] * dQi[t][jj];
-          dQ[t][jj] += gam[i] * dQi[t][jj];
+          const uint32_t at = uint32_t((16 * pw + 4 * g + jj) * sk + 16 * (4 * hw + t) + li);
+          BufIO<OutT>::st(dqr, at, dQ[t][jj]);
+          BufIO<OutT>::st(dkr, at, dK[t][jj]);
         }
-#pragma unroll
-      for (int jj = 0; jj < 4; ++jj) {
-        const float v = sum16(tq[jj]);
-        if (li == 0) tpos[hw][i0 + jj] = v;
-      }
-      if (e == 0) {
-#pragma unroll
-        for (int mi = 0; mi < 2; ++mi) {
-          const int m = key_tile(pw, hw, mi);
-          kk[mi] = zero4();
-          if (m <= pw) {
-#pragma unroll
-            for (int s = 0; s < 4; ++s)
-              kk[mi] = mma(kk[mi], lds8(Kres + swz(ip, 32 * s + 8 * g, kLK)), lds8(Kres + swz(16 * m + li, 32 * s + 8 * g, kLK)));
-          }
-        }
-      }
-      // P * M is zero above the diagonal: rows i < 32 end at column 31, and columns j >= 32 start at row 32.
-#pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        if (s == 0 || pw >= 2) {
-          const int at = swz(ip, 32 * s + 8 * g, kLT);
-          const Split8 Apm{lds8(TbL[0] + at), lds8(TbL[1] + at)};  // (P * M) rows i = ip, k = j
-#pragma unroll
-          for (int t = 0; t < 4; ++t)
-            dQ[t] = mma2(dQ[t], Apm, lds_tr8s(Kres + 32 * s * kLK + 16 * (4 * hw + t), kLK, lt));
-        }
-        if (s == 1 || pw < 2) {
-          const Split8 Apmt{lds_tr8s(TbL[0] + 32 * s * kLT + 16 * pw, kLT, lt),
-                            lds_tr8s(TbL[1] + 32 * s * kLT + 16 * pw, kLT, lt)};  // (P * M)^T rows j = ip, k = i
-#pragma unroll
-          for (int t = 0; t < 4; ++t)
-            dK[t] = mma2(dK[t], Apmt, lds_tr8s(sb + eQb + 32 * s * kLK + 16 * (4 * hw + t), kLK, lt));
-        }
-      }
-#pragma unroll
-      for (int mi = 0; mi < 2; ++mi) {
-        const int mr = 16 * (2 * hw + mi) + li;  // this lane's column m of Z
-        f32x4 z = zero4();
-#pragma unroll
-        for (int s = 0; s < 2; ++s) {
-          const int aa = swz(ip, 32 * s + 8 * g, kLT), ab = swz(mr, 32 * s + 8 * g, kLT);
-          z = mma3(z, Split8{lds8(PL[0] + aa), lds8(PL[1] + aa)}, Split8{lds8(sb + eTh + ab), lds8(sb + eTl + ab)});
-        }
-        put4(sb + eZh, sb + eZl, swz(mr, i0, kLT), z[0], z[1], z[2], z[3]);
-      }
-    }
-    __syncthreads();
-
-    // E3: dA = -T^T Z below the diagonal (rows p = i0 + jj, columns m = 16 key_tile(pw, hw, mi) + li, as kk), and at
-    // once its products with E = exp(G_p - G_m) and K K^T: the A part of dbeta (row sums), of dG (row and column
-    // sums), and dKK = diag(beta) (dA * E), stored as dKK^T.
-    {
-      // Only tiles mt <= pw are kept (mcol < p), and T^T rows p >= 32 are zero below column 32.
-      Split8 AT[2];  // T^T rows p = ip, k = i
-#pragma unroll
-      for (int s = 0; s < 2; ++s)
-        AT[s] = Split8{lds_tr8s(sb + eTh + 32 * s * kLT + 16 * pw, kLT, lt),
-                       lds_tr8s(sb + eTl + 32 * s * kLT + 16 * pw, kLT, lt)};
-      float rowp[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int mi = 0; mi < 2; ++mi) {
-        const int mt = key_tile(pw, hw, mi), mcol = 16 * mt + li;
-        f32x4 da = zero4();
-        if (mt <= pw) {
-#pragma unroll
-          for (int s = 0; s < 2; ++s) {
-            if (s == 1 || pw < 2) {
-              const int ab = swz(mcol, 32 * s + 8 * g, kLT);
-              da = mma3(da, AT[s], Split8{lds8(sb + eZh + ab), lds8(sb + eZl + ab)});
-            }
-          }
-        }
-        float colp = 0.f, kkt[4];
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-          const int pr = i0 + jj;
-          const float e = __expf(fminf(Gf[pr] - Gf[mcol], 0.f));  // finite everywhere; used where mcol < pr
-          const float dae = mcol < pr ? -da[jj] * e : 0.f;           // dA_pm E_pm
-          const float prod = dae * kk[mi][jj];
-          rowp[jj] += prod;
-          colp += bet[pr] * prod;
-          kkt[jj] = bet[pr] * dae;
-        }
-        put4(sb + eKh, sb + eKl, swz(mcol, i0, kLT), kkt[0], kkt[1], kkt[2], kkt[3]);
-        colp += __shfl_xor(colp, 16);
-        colp += __shfl_xor(colp, 32);
-        if (g == 0) x1cp[pw][mcol] = colp;
-      }
-#pragma unroll
-      for (int jj = 0; jj < 4; ++jj) {
-        const float v = sum16(rowp[jj]);
-        if (li == 0) dbAp[hw][i0 + jj] = v;
-      }
-    }
-    __syncthreads();
-
-    // E4: dK += (dKK + dKK^T) K for rows j = ip, this half's columns: dKK rows j through the transposing read of
-    // dKK^T, dKK^T rows j directly.
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      const int at = swz(ip, 32 * s + 8 * g, kLT);
-      const Split8 A1{lds_tr8s(sb + eKh + 32 * s * kLT + 16 * pw, kLT, lt), lds_tr8s(sb + eKl + 32 * s * kLT + 16 * pw, kLT, lt)};
-      const Split8 A2{lds8(sb + eKh + at), lds8(sb + eKl + at)};
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const bf16x8 B = lds_tr8s(Kres + 32 * s * kLK + 16 * (4 * hw + t), kLK, lt);
-        // dKK is strictly lower: dKK[j][i] needs i < j, dKK[i][j] needs i > j.
-        if (s == 0 || pw >= 2) dK[t] = mma2(dK[t], A1, B);
-        if (s == 1 || pw < 2) dK[t] = mma2(dK[t], A2, B);
-      }
-    }
-    // E5 (one wave): dG per position, dg = its reverse cumulative sum (a suffix scan over the wave), and dbeta.
-    if (tid < kC) {
-      const int t = tid;
-      const float hs = hpos[0][t] + hpos[1][t];
-      float hsum = sum16(hs);
-      hsum += __shfl_xor(hsum, 16);
-      hsum += __shfl_xor(hsum, 32);
-      float sds_all = 0.f;
-#pragma unroll
-      for (int u = 0; u < kThreads / 64; ++u) sds_all += red[u];
-      const float dbA = dbAp[0][t] + dbAp[1][t];
-      float v = gam[t] * (tpos[0][t] + tpos[1][t]) + gpos[0][t] + gpos[1][t] - hs + bet[t] * dbA -
-                (x1cp[0][t] + x1cp[1][t] + x1cp[2][t] + x1cp[3][t]) + x2r[0][t] + x2r[1][t] -
-                (x2c[0][t] + x2c[1][t] + x2c[2][t] + x2c[3][t]);
-      if (t == kC - 1) v += hsum + gam[kC - 1] * sds_all;
-#pragma unroll
-      for (int off = 1; off < kC; off <<= 1) {
-        const float u = __shfl_down(v, off);
-        if (t + off < kC) v += u;
-      }
-      if (t < L) {
-        const int64_t g0 = tok * a.Hv + hv;
-        const uint32_t gi = uint32_t(t * a.Hv);
-        a.dg[g0 + gi] = a.g_is_log ? v : v / a.g[g0 + gi];
-        const float dbT = dbTp[0][t] + dbTp[1][t] + dbTp[2][t] + dbTp[3][t];
-        IO<OutT>::st(static_cast<OutT*>(a.dbeta) + g0, gi, dbT + dbA);
-      }
     }
   }
-
-  // dq, dk for the wave's positions and columns (lane -> column 16 (4 hw + t) + li, rows 16 pw + 4g + jj).
-  OutT* dq = static_cast<OutT*>(a.dq) + (tok * a.Hk + hk) * Dk;
-  OutT* dk = static_cast<OutT*>(a.dk) + (tok * a.Hk + hk) * Dk;
-#pragma unroll
-  for (int t = 0; t < 4; ++t)
-#pragma unroll
-    for (int jj = 0; jj < 4; ++jj) {
-      const int i = 16 * pw + 4 * g + jj;
-      if (i < L) {
-        const uint32_t at = uint32_t(i * sk + 16 * (4 * hw + t) + li);
-        IO<OutT>::st(dq, at, dQ[t][jj]);
-        IO<OutT>::st(dk, at, dK[t][jj]);
-      }
-    }
 }
 
 }  // namespace
@@ -628,10 +656,17 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
 hipError_t launch_chunk_bwd_grads(const ChunkArgs& a, bool out_bf16, hipStream_t s) {
   const int total = int(a.lay.NC) * a.Hk;
   if (total == 0) return hipSuccess;
+  // One resident block per CU (the kernel's LDS allows no more), looping over its items; a multiple of 8 blocks, so
+  // each block's items stay on its XCD.
+  int dev = 0, cus = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  if (e != hipSuccess) return e;
+  const int grid = total <= cus ? total : (cus >= 8 ? cus & ~7 : cus);
   if (out_bf16)
-    hipLaunchKernelGGL(chunk_bwd_grads_kernel<bf16_t>, dim3(total), dim3(kThreads), 0, s, a);
+    hipLaunchKernelGGL(chunk_bwd_grads_kernel<bf16_t>, dim3(grid), dim3(kThreads), 0, s, a);
   else
-    hipLaunchKernelGGL(chunk_bwd_grads_kernel<float>, dim3(total), dim3(kThreads), 0, s, a);
+    hipLaunchKernelGGL(chunk_bwd_grads_kernel<float>, dim3(grid), dim3(kThreads), 0, s, a);
   return hipGetLastError();
 }
 
