@@ -158,6 +158,17 @@ int qb_gdn_prologue_bwd(const qb_gdn_desc* desc, const void* q_raw, const void* 
                         const float* dlog_decay, void* dq_raw, void* dk_raw, void* da, void* db, float* da_log,
                         float* ddt_bias, void* workspace, void* stream, char* err, int errlen);
 
+/* qb_gdn_prologue_fwd and qb_gdn_fwd in one: the prologue runs inside the forward's first kernel, which reads q_raw,
+ * k_raw, a and b in place of q, k, g and beta, forms those exactly as qb_gdn_prologue_fwd does (bit for bit), writes
+ * them (q, k, beta, log_decay as there: the backward reads them) and goes on as qb_gdn_fwd with g = log_decay. It saves
+ * the separate pass over q_raw and k_raw and its launch (reference src/deltanet.cpp:94-100 feeding
+ * gated_delta_update, :101-117). The chunked design only: desc->design QB_GDN_CHUNKED, dtype bf16, g_is_log = 1 (the
+ * prologue emits the log-decay); s0, s_out and ckpt as for qb_gdn_fwd. */
+int qb_gdn_fwd_prologue(const qb_gdn_desc* desc, const void* q_raw, const void* k_raw, const void* v, const void* a,
+                        const void* b, const float* a_log, const float* dt_bias, const float* s0, void* q, void* k,
+                        void* beta, float* log_decay, void* y, float* s_out, float* ckpt, void* workspace,
+                        void* stream, char* err, int errlen);
+
 /* Epilogue, after qb_gdn_fwd (src/deltanet.cpp:35-45, 122, the gated RMSNorm): o = silu(z) rms_norm(y, norm_w, eps).
  * y, z, o [B, T, Hv, Dv] in dtype; norm_w [Dv] float32. */
 int qb_gdn_epilogue_fwd(const qb_gdn_desc* desc, const void* y, const void* z, const float* norm_w, float eps, void* o,

@@ -75,6 +75,8 @@ def load():
     L.qb_gdn_prologue_fwd.restype = ctypes.c_int
     L.qb_gdn_prologue_bwd.argtypes = [D] + [P] * 18 + [ctypes.c_char_p, ctypes.c_int]
     L.qb_gdn_prologue_bwd.restype = ctypes.c_int
+    L.qb_gdn_fwd_prologue.argtypes = [D] + [P] * 17 + [ctypes.c_char_p, ctypes.c_int]
+    L.qb_gdn_fwd_prologue.restype = ctypes.c_int
     F = ctypes.c_float
     L.qb_gdn_epilogue_fwd.argtypes = [D, P, P, P, F, P, P, ctypes.c_char_p, ctypes.c_int]
     L.qb_gdn_epilogue_fwd.restype = ctypes.c_int
@@ -173,6 +175,12 @@ def _call(fn, desc, *args) -> None:
     err = ctypes.create_string_buffer(512)
     if fn(ctypes.byref(desc), *args, err, len(err)) != 0:
         raise RuntimeError(err.value.decode())
+
+
+def fwd_prologue(desc, q_raw, k_raw, v, a, b, a_log, dt_bias, s0, q, k, beta, log_decay, y, s_out, ckpt, workspace,
+                 stream) -> None:
+    _call(load().qb_gdn_fwd_prologue, desc, q_raw, k_raw, v, a, b, a_log, dt_bias, s0, q, k, beta, log_decay, y, s_out,
+          ckpt, workspace, stream)
 
 
 def prologue_fwd(desc, q_raw, k_raw, a, b, a_log, dt_bias, q, k, beta, log_decay, stream) -> None:

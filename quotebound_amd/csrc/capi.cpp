@@ -507,6 +507,44 @@ int qb_gdn_prologue_bwd(const qb_gdn_desc* desc, const void* q_raw, const void* 
   });
 }
 
+int qb_gdn_fwd_prologue(const qb_gdn_desc* desc, const void* q_raw, const void* k_raw, const void* v, const void* a,
+                        const void* b, const float* a_log, const float* dt_bias, const float* s0, void* q, void* k,
+                        void* beta, float* log_decay, void* y, float* s_out, float* ckpt, void* workspace,
+                        void* stream, char* err, int errlen) {
+  return guarded(err, errlen, [&] {
+    Problem p;
+    std::string why = resolve(desc, p);
+    qbgdn::NbProblem nb;
+    if (why.empty()) why = nb_resolve(desc, nb, true, false);
+    if (why.empty() && (desc->design != QB_GDN_CHUNKED || !desc->g_is_log || !p.in_bf16))
+      why = "gated delta: the fused prologue runs the chunked design with bf16 inputs and g_is_log = 1 " +
+            shape_of(*desc);
+    const bool any = why.empty() && p.BT > 0;
+    const size_t eo = p.out_bf16 ? 2 : 4;
+    const PtrCheck c[] = {{"q_raw", q_raw, any, 16},      {"k_raw", k_raw, any, 16},     {"v", v, any, 2},
+                          {"a", a, any, 2},               {"b", b, any, 2},              {"a_log", a_log, true, 4},
+                          {"dt_bias", dt_bias, true, 4},  {"s0", s0, false, 4},          {"q", q, any, 16},
+                          {"k", k, any, 16},              {"beta", beta, any, 2},        {"log_decay", log_decay, any, 4},
+                          {"y", y, any, eo},              {"s_out", s_out, false, 4},    {"ckpt", ckpt, false, 16},
+                          {"workspace", workspace, any && ws_bytes(desc, p) > 0, 16}};
+    if (why.empty()) why = check_all(c);
+    if (!why.empty()) {
+      set_err(err, errlen, why);
+      return -1;
+    }
+    const qbgdn::PrologueIn pro{q_raw, k_raw, a, b, a_log, dt_bias, nb.scale_q, nb.scale_k, q, k, beta, log_decay};
+    const qbgdn::FwdPtrs f{q, k, v, log_decay, beta, s0, y, s_out, ckpt};
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    qbgdn::Tracer tr = tracer_of(desc, st);
+    const hipError_t e = qbgdn::chunk_fwd_prologue(p, pro, f, workspace, st, tr);
+    if (e != hipSuccess) {
+      set_err(err, errlen, hip_fail("forward launch", e));
+      return -1;
+    }
+    return 0;
+  });
+}
+
 int qb_gdn_epilogue_fwd(const qb_gdn_desc* desc, const void* y, const void* z, const float* norm_w, float eps, void* o,
                         void* stream, char* err, int errlen) {
   return guarded(err, errlen, [&] {

@@ -49,7 +49,9 @@ size_t chunk_workspace_bytes(const Problem& p) {
   return a > b ? a : b;
 }
 
-hipError_t chunk_fwd(const Problem& p, const FwdPtrs& f, void* ws, hipStream_t s, Tracer& tr) {
+namespace {
+
+hipError_t fwd_impl(const Problem& p, const PrologueIn* pro, const FwdPtrs& f, void* ws, hipStream_t s, Tracer& tr) {
   ChunkArgs a = base_args(p);
   a.q = static_cast<const bf16_t*>(f.q);
   a.k = static_cast<const bf16_t*>(f.k);
@@ -61,13 +63,33 @@ hipError_t chunk_fwd(const Problem& p, const FwdPtrs& f, void* ws, hipStream_t s
   a.s_out = f.s_out;
   a.ckpt = f.ckpt;
   place_extras(p, a, f.ckpt, ws);
+  if (pro) {
+    a.pro = ChunkArgs::Prologue{static_cast<const bf16_t*>(pro->q_raw), static_cast<const bf16_t*>(pro->k_raw),
+                                static_cast<const bf16_t*>(pro->a),     static_cast<const bf16_t*>(pro->b),
+                                pro->a_log,                             pro->dt_bias,
+                                pro->scale_q,                           pro->scale_k,
+                                static_cast<bf16_t*>(pro->q),           static_cast<bf16_t*>(pro->k),
+                                static_cast<bf16_t*>(pro->beta),        pro->log_decay};
+  }
   tr.mark();
-  hipError_t e = launch_chunk_prep(a, s);
+  hipError_t e = launch_chunk_prep(a, s, pro != nullptr);
   if (e != hipSuccess) return e;
   tr.mark();
   e = launch_chunk_fwd(a, p.out_bf16, s);
   tr.mark();
   return e;
+}
+
+}  // namespace
+
+hipError_t chunk_fwd(const Problem& p, const FwdPtrs& f, void* ws, hipStream_t s, Tracer& tr) {
+  return fwd_impl(p, nullptr, f, ws, s, tr);
+}
+
+hipError_t chunk_fwd_prologue(const Problem& p, const PrologueIn& pro, const FwdPtrs& f, void* ws, hipStream_t s,
+                              Tracer& tr) {
+  if (!p.g_is_log || !p.in_bf16) return hipErrorInvalidValue;
+  return fwd_impl(p, &pro, f, ws, s, tr);
 }
 
 hipError_t chunk_bwd(const Problem& p, const BwdPtrs& b, void* ws, hipStream_t s, Tracer& tr) {

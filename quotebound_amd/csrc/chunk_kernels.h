@@ -30,9 +30,24 @@ struct ChunkArgs {
   int nblk;  // Dv / 16 state-row blocks
   int N;     // sequences
   SeqTable tab;
+  // The layer's prologue fused into chunk_prep (qb_gdn_fwd_prologue): the raw inputs, and the prologue's outputs,
+  // which prep writes and the later kernels read as q, k, g (the log-decay) and beta.
+  struct Prologue {
+    const bf16_t* q_raw;
+    const bf16_t* k_raw;
+    const bf16_t* a;
+    const bf16_t* b;
+    const float* a_log;
+    const float* dt_bias;
+    float scale_q, scale_k;
+    bf16_t* q;
+    bf16_t* k;
+    bf16_t* beta;
+    float* log_decay;
+  } pro;
 };
 
-hipError_t launch_chunk_prep(const ChunkArgs& a, hipStream_t s);
+hipError_t launch_chunk_prep(const ChunkArgs& a, hipStream_t s, bool fused_prologue = false);
 hipError_t launch_chunk_fwd(const ChunkArgs& a, bool out_bf16, hipStream_t s);
 hipError_t launch_chunk_bwd_state(const ChunkArgs& a, bool out_bf16, hipStream_t s);
 hipError_t launch_chunk_bwd_grads(const ChunkArgs& a, bool out_bf16, hipStream_t s);

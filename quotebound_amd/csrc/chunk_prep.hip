@@ -10,6 +10,7 @@
 // diagonal block by substitution with the column held in registers, then T_IJ = -T_II sum_K A_IK T_KJ by distance.
 #include "chunk_common.h"
 #include "chunk_kernels.h"
+#include "prologue_math.h"
 
 namespace qbgdn {
 namespace {
@@ -31,6 +32,11 @@ constexpr int kKQBytes = 2 * kC * kLDK * 2;
 constexpr int kAoff = 0, kToff = kTri * 4, kPoff = 2 * kTri * 4;  // byte offsets of A, T, P (hi then lo)
 static_assert(kPoff + 2 * kTri * 2 <= kKQBytes, "A, T and P fit in the k/q staging bytes");
 
+// kFused: the layer's prologue in front (qb_gdn_fwd_prologue). The block reads q_raw, k_raw, a and b in place of
+// q, k, g and beta and forms them as the separate prologue pass does, bit for bit (prologue_math.h; a row's sum of
+// squares is the same in-lane sum over 8 consecutive elements and DPP reduction over its 16 lanes). It writes beta and
+// the log-decay of its value head, and the first value head of each key head's group writes q and k.
+template <bool kFused>
 __global__ __launch_bounds__(kThreads) void chunk_prep_kernel(ChunkArgs a) {
   __shared__ __align__(16) unsigned char smem[kKQBytes];
   __shared__ double Gd[kC];
@@ -55,21 +61,61 @@ __global__ __launch_bounds__(kThreads) void chunk_prep_kernel(ChunkArgs a) {
   float gx = 0.f, bx = 0.f;
   if (tid < kC) {
     const int64_t s0 = sp.tok * a.Hv + hv;
-    const auto gr = buffer_rsrc(a.g + s0, L == 0 ? 0u : ((L - 1) * uint32_t(a.Hv) + 1) * 4u);
-    const auto br = buffer_rsrc(a.beta + s0, L == 0 ? 0u : ((L - 1) * uint32_t(a.Hv) + 1) * 2u);
-    gx = buf_ld4(gr, uint32_t(tid * a.Hv) * 4);
-    bx = bf16_to_f32(buf_ld2(br, uint32_t(tid * a.Hv) * 2));
+    const uint32_t n = L == 0 ? 0u : (L - 1) * uint32_t(a.Hv) + 1;  // elements from s0 to the chunk's last row
+    if constexpr (kFused) {
+      const auto ar = buffer_rsrc(a.pro.a + s0, n * 2u), br = buffer_rsrc(a.pro.b + s0, n * 2u);
+      const float av = bf16_to_f32(buf_ld2(ar, uint32_t(tid * a.Hv) * 2));
+      const float bv = bf16_to_f32(buf_ld2(br, uint32_t(tid * a.Hv) * 2));
+      gx = gate_log_decay<bf16_t>(av, a.pro.a_log[hv], a.pro.dt_bias[hv]);
+      bx = gate_beta<bf16_t>(bv);
+      if (uint32_t(tid) < L) {
+        a.pro.log_decay[s0 + int64_t(tid) * a.Hv] = gx;
+        a.pro.beta[s0 + int64_t(tid) * a.Hv] = f32_to_bf16(bx);
+      }
+    } else {
+      const auto gr = buffer_rsrc(a.g + s0, n * 4u);
+      const auto br = buffer_rsrc(a.beta + s0, n * 2u);
+      gx = buf_ld4(gr, uint32_t(tid * a.Hv) * 4);
+      bx = bf16_to_f32(buf_ld2(br, uint32_t(tid * a.Hv) * 2));
+    }
   }
   {
     const int sk = a.Hk * 128;
     const uint32_t bytes = L * uint32_t(sk) * 2u;
-    const auto kr = buffer_rsrc(a.k + sp.tok * sk + hk * 128, bytes), qr = buffer_rsrc(a.q + sp.tok * sk + hk * 128, bytes);
+    const bf16_t* kb = kFused ? a.pro.k_raw : a.k;
+    const bf16_t* qb = kFused ? a.pro.q_raw : a.q;
+    const auto kr = buffer_rsrc(kb + sp.tok * sk + hk * 128, bytes), qr = buffer_rsrc(qb + sp.tok * sk + hk * 128, bytes);
     uint4 kv[4], qv[4];
 #pragma unroll
     for (int q4 = 0; q4 < 4; ++q4) {
       const int e = tid + kThreads * q4, t = e >> 4, c8 = (e & 15) * 8;
       kv[q4] = buf_ld16(kr, uint32_t(t * sk + c8) * 2);
       qv[q4] = buf_ld16(qr, uint32_t(t * sk + c8) * 2);
+    }
+    if constexpr (kFused) {
+      // Normalise each row (16 lanes of 8 elements); rows past the chunk's end are zeros and stay zeros.
+      const bool writer = hv % (a.Hv / a.Hk) == 0;
+      const auto ko = buffer_rsrc(a.pro.k + sp.tok * sk + hk * 128, bytes);
+      const auto qo = buffer_rsrc(a.pro.q + sp.tok * sk + hk * 128, bytes);
+      auto norm = [&](uint4& u, float s) {
+        float x[8];
+        const uint32_t w4[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) x[2 * j] = __uint_as_float(w4[j] << 16), x[2 * j + 1] = __uint_as_float(w4[j] & 0xffff0000u);
+        norm_row8<bf16_t>(x, sum16(sumsq8(x)), 128, s);
+        u = uint4{f32x2_to_bf16x2(x[0], x[1]), f32x2_to_bf16x2(x[2], x[3]), f32x2_to_bf16x2(x[4], x[5]),
+                  f32x2_to_bf16x2(x[6], x[7])};
+      };
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const int e = tid + kThreads * q4, t = e >> 4, c8 = (e & 15) * 8;
+        norm(kv[q4], a.pro.scale_k);
+        norm(qv[q4], a.pro.scale_q);
+        if (writer) {
+          buf_st16(ko, uint32_t(t * sk + c8) * 2, kv[q4]);
+          buf_st16(qo, uint32_t(t * sk + c8) * 2, qv[q4]);
+        }
+      }
     }
 #pragma unroll
     for (int q4 = 0; q4 < 4; ++q4) {
@@ -84,7 +130,7 @@ __global__ __launch_bounds__(kThreads) void chunk_prep_kernel(ChunkArgs a) {
     const int t = tid;
     // The log-decay floored at -150: a factor of 0 (or a log-decay of -inf) would make G_i - G_j NaN on every pair
     // across it; at -150 each exp(.) across it is 0 in float32, as the factor 0 makes it.
-    double G = uint32_t(t) < L ? fmax(a.g_is_log ? double(gx) : double(logf(gx)), kLogFloor) : 0.0;
+    double G = uint32_t(t) < L ? fmax(kFused || a.g_is_log ? double(gx) : double(logf(gx)), kLogFloor) : 0.0;
 #pragma unroll
     for (int off = 1; off < kC; off <<= 1) {
       const double u = __shfl_up(G, off);
@@ -222,10 +268,13 @@ __global__ __launch_bounds__(kThreads) void chunk_prep_kernel(ChunkArgs a) {
 
 }  // namespace
 
-hipError_t launch_chunk_prep(const ChunkArgs& a, hipStream_t s) {
+hipError_t launch_chunk_prep(const ChunkArgs& a, hipStream_t s, bool fused_prologue) {
   const int total = int(a.lay.NC) * a.Hv;
   if (total == 0) return hipSuccess;
-  hipLaunchKernelGGL(chunk_prep_kernel, dim3(total), dim3(kThreads), 0, s, a);
+  if (fused_prologue)
+    hipLaunchKernelGGL(chunk_prep_kernel<true>, dim3(total), dim3(kThreads), 0, s, a);
+  else
+    hipLaunchKernelGGL(chunk_prep_kernel<false>, dim3(total), dim3(kThreads), 0, s, a);
   return hipGetLastError();
 }
 

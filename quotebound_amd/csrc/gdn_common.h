@@ -14,13 +14,14 @@ typedef uint16_t bf16_t;
 
 __device__ __forceinline__ float bf16_to_f32(bf16_t b) { return __uint_as_float(uint32_t(b) << 16); }
 
-// Round to nearest even; NaN stays NaN.
-__device__ __forceinline__ bf16_t f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return bf16_t((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return bf16_t(u >> 16);
+// Two floats to packed bf16 (x0 in the low half), rounded to nearest even, NaN staying NaN: one
+// v_cvt_pk_bf16_f32.
+__device__ __forceinline__ uint32_t f32x2_to_bf16x2(float x0, float x1) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  typedef float f32x2_t __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{x0, x1}, bf16x2_t));
 }
+__device__ __forceinline__ bf16_t f32_to_bf16(float f) { return bf16_t(f32x2_to_bf16x2(f, 0.f)); }
 
 template <typename T>
 struct IO;
@@ -62,6 +63,11 @@ __device__ __forceinline__ uint4 buf_ld16(__amdgpu_buffer_rsrc_t r, uint32_t byt
   const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, int(byte_off), 0, 0);
   return uint4{v[0], v[1], v[2], v[3]};
 }
+// Stores at byte offsets past the range are dropped.
+__device__ __forceinline__ void buf_st16(__amdgpu_buffer_rsrc_t r, uint32_t byte_off, uint4 v) {
+  typedef __attribute__((__vector_size__(4 * sizeof(uint32_t)))) uint32_t u32x4;
+  __builtin_amdgcn_raw_buffer_store_b128(u32x4{v.x, v.y, v.z, v.w}, r, int(byte_off), 0, 0);
+}
 __device__ __forceinline__ uint2 buf_ld8(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
   const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, int(byte_off), 0, 0);
   return uint2{v[0], v[1]};
@@ -97,8 +103,7 @@ struct BufIO<bf16_t> {
   template <typename V4>
   static __device__ __forceinline__ void st4(__amdgpu_buffer_rsrc_t r, uint32_t i, const V4& x) {
     typedef __attribute__((__vector_size__(2 * sizeof(uint32_t)))) uint32_t u32x2;
-    const u32x2 v = {uint32_t(f32_to_bf16(x[0])) | (uint32_t(f32_to_bf16(x[1])) << 16),
-                     uint32_t(f32_to_bf16(x[2])) | (uint32_t(f32_to_bf16(x[3])) << 16)};
+    const u32x2 v = {f32x2_to_bf16x2(x[0], x[1]), f32x2_to_bf16x2(x[2], x[3])};
     __builtin_amdgcn_raw_buffer_store_b64(v, r, int(i * 2), 0, 0);
   }
 };

@@ -79,6 +79,23 @@ size_t chunk_workspace_bytes(const Problem& p);
 extern const char* const kChunkFwdLaunches;
 extern const char* const kChunkBwdLaunches;
 hipError_t chunk_fwd(const Problem& p, const FwdPtrs& a, void* ws, hipStream_t s, Tracer& tr);
+// The layer's prologue fused into the chunked forward (qb_gdn_fwd_prologue): its raw inputs and its outputs, which
+// the forward writes and then runs on (a.q, a.k, a.g, a.beta must be q, k, log_decay, beta below).
+struct PrologueIn {
+  const void* q_raw;
+  const void* k_raw;
+  const void* a;
+  const void* b;
+  const float* a_log;
+  const float* dt_bias;
+  float scale_q, scale_k;  // 1/Dk and Dk^-1/2 in the activation dtype
+  void* q;
+  void* k;
+  void* beta;
+  float* log_decay;
+};
+hipError_t chunk_fwd_prologue(const Problem& p, const PrologueIn& pro, const FwdPtrs& a, void* ws, hipStream_t s,
+                              Tracer& tr);
 hipError_t chunk_bwd(const Problem& p, const BwdPtrs& a, void* ws, hipStream_t s, Tracer& tr);
 
 }  // namespace qbgdn

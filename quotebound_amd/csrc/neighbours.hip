@@ -22,11 +22,11 @@
 
 #include "gdn_common.h"
 #include "neighbours.h"
+#include "prologue_math.h"
 
 namespace qbgdn {
 namespace {
 
-constexpr float kNormEps = 1e-6f;  // the q/k rms_norm's eps (src/deltanet.cpp:96-97)
 constexpr int kVec = 8;            // elements per lane
 constexpr int kNormBwdBlocks = 256;  // gated-norm backward: at most one block of 16 waves per CU
 constexpr int kGateSteps = 4;      // gates backward: steps per thread, so a tile is 4 (256 / Hv) tokens
@@ -40,12 +40,6 @@ __device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, bf16x2_t));
 }
 
-template <typename T>
-__device__ __forceinline__ float rnd(float x) {  // the activation dtype's rounding
-  if constexpr (sizeof(T) == 2) return float(static_cast<__bf16>(x));
-  return x;
-}
-
 // Sum over aligned groups of L consecutive lanes (L = 8, 16, 32, 64); every lane of a group gets the same bits.
 template <int L>
 __device__ __forceinline__ float group_sum(float x) {
@@ -57,11 +51,6 @@ __device__ __forceinline__ float group_sum(float x) {
   if constexpr (L >= 64) x += __shfl_xor(x, 32);
   return x;
 }
-
-// The hardware exp2 and reciprocal (a few float32 ulps).
-__device__ __forceinline__ float sigmoidf(float x) { return __builtin_amdgcn_rcpf(1.f + __expf(-x)); }
-__device__ __forceinline__ float rsqrt_mean(float ss, int n, float eps) { return __builtin_amdgcn_rsqf(ss / n + eps); }
-__device__ __forceinline__ float softplusf(float x) { return fmaxf(x, 0.f) + log1pf(expf(-fabsf(x))); }
 
 template <typename T>
 __device__ __forceinline__ void ld8(const T* p, float (&x)[kVec]) {
@@ -114,9 +103,8 @@ __global__ __launch_bounds__(256) void prologue_fwd_kernel(const T* __restrict__
     const int64_t i = (int64_t(blockIdx.x) - nrow_blocks) * 256 + threadIdx.x;
     if (i >= n) return;
     const int h = int(i % Hv);
-    IO<T>::st(beta, i, sigmoidf(IO<T>::ld(b, i)));
-    const float x = rnd<T>(IO<T>::ld(a, i) + dt_bias[h]);
-    log_decay[i] = -expf(a_log[h]) * rnd<T>(softplusf(x));
+    IO<T>::st(beta, i, gate_beta<T>(IO<T>::ld(b, i)));
+    log_decay[i] = gate_log_decay<T>(IO<T>::ld(a, i), a_log[h], dt_bias[h]);
     return;
   }
   using RL = RowLane<D>;
@@ -132,13 +120,7 @@ __global__ __launch_bounds__(256) void prologue_fwd_kernel(const T* __restrict__
   }
 #pragma unroll
   for (int j = 0; j < kSlots; ++j) {
-    const float s = isk[j] ? sk : sq;
-    float ss = 0.f;
-#pragma unroll
-    for (int e = 0; e < kVec; ++e) ss += x[j][e] * x[j][e];
-    const float rho = rsqrt_mean(group_sum<RL::L>(ss), D, kNormEps);
-#pragma unroll
-    for (int e = 0; e < kVec; ++e) x[j][e] = rnd<T>(s * rnd<T>(x[j][e] * rho));
+    norm_row8<T>(x[j], group_sum<RL::L>(sumsq8(x[j])), D, isk[j] ? sk : sq);
     if (live[j]) st8((isk[j] ? k : q) + off[j], x[j]);
   }
 }

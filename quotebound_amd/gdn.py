@@ -119,6 +119,38 @@ def backward(q, k, v, g, beta, ckpt, dy, ds_out=None, *, log_decay=False, design
     return dq, dk, dv, dg, dbeta, ds0
 
 
+def forward_prologue(q_raw, k_raw, v, a, b, a_log, dt_bias, state=None, *, cu_seqlens=None, out_f32=False):
+    """The layer's prologue fused into the chunked forward (qb_gdn_fwd_prologue): from the raw q/k rows and gate
+    inputs, (y, s_out, ckpt, q, k, beta, log_decay), the last four exactly what neighbours.prologue_forward returns,
+    y, s_out and ckpt what forward(q, k, v, log_decay, beta, state, log_decay=True, design=CHUNKED) returns on them.
+    bf16 activations; a_log and dt_bias float32."""
+    for t in (q_raw, k_raw, v, a, b):
+        if t.dtype != torch.bfloat16 or not t.is_cuda:
+            raise RuntimeError("gated delta: the fused prologue takes bf16 device tensors")
+    q_raw, k_raw, v, a, b = (t.contiguous() for t in (q_raw, k_raw, v, a, b))
+    a_log, dt_bias = a_log.float().contiguous(), dt_bias.float().contiguous()
+    desc, keep = _desc(q_raw, v, torch.bfloat16, True, _lib.CHUNKED, cu_seqlens, out_f32)
+    why = _lib.validate(desc)
+    if why:
+        raise RuntimeError(why)
+    N = q_raw.shape[0] if cu_seqlens is None else len(cu_seqlens) - 1
+    dev = q_raw.device
+    Hv, Dv, Dk = v.shape[2], v.shape[3], q_raw.shape[3]
+    s0 = None if state is None else state.to(torch.float32).contiguous()
+    q, k = torch.empty_like(q_raw), torch.empty_like(k_raw)
+    beta = torch.empty_like(b)
+    log_decay = torch.empty(a.shape, dtype=torch.float32, device=dev)
+    y = torch.empty(v.shape, dtype=torch.float32 if out_f32 else torch.bfloat16, device=dev)
+    s_out = torch.empty(N, Hv, Dv, Dk, dtype=torch.float32, device=dev)
+    ckpt = torch.empty(max(_lib.ckpt_bytes(desc) // 4, 1), dtype=torch.float32, device=dev)
+    ws = _workspace(desc, dev)
+    _lib.fwd_prologue(desc, _dev_ptr(q_raw), _dev_ptr(k_raw), _dev_ptr(v), _dev_ptr(a), _dev_ptr(b), _dev_ptr(a_log),
+                      _dev_ptr(dt_bias), _dev_ptr(s0), _dev_ptr(q), _dev_ptr(k), _dev_ptr(beta), _dev_ptr(log_decay),
+                      _dev_ptr(y), _dev_ptr(s_out), _dev_ptr(ckpt), _dev_ptr(ws), _stream(dev))
+    del keep
+    return y, s_out, ckpt, q, k, beta, log_decay
+
+
 def forward_rows(q, k, v, g, beta, state=None, *, log_decay=False, cu_seqlens=None):
     """(y, row_states): the forward keeping the state after every token, row_states [B, T, Hv, Dv, Dk] float32 (or
     [total, Hv, Dv, Dk] packed) — the reference's rows pass for exact drafts (src/deltanet.cpp:101-117), whose

@@ -349,3 +349,41 @@ def test_neighbours_autograd_and_empty(dev):
     dy, dz, dw = neighbours.epilogue_backward(yv, yv, torch.ones(64, device="cuda"), 1e-6, yv)
     torch.cuda.synchronize()
     assert dy.numel() == 0 and torch.count_nonzero(dw) == 0
+
+
+FUSED_CASES = [  # (B, T, Hk, Hv, Dv, packed lengths or None, initial state)
+    (2, 150, 2, 4, 64, None, True),
+    (1, 333, 4, 12, 32, [70, 0, 130, 133], False),  # packed, an empty sequence, GQA ratio 3
+    (1, 4096, 16, 32, 128, None, False),             # the 4B layer shape
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("case", FUSED_CASES, ids=lambda c: "B%dT%dHk%dHv%dDv%d%s%s" % (
+    *c[:5], "_packed" if c[5] else "", "_s0" if c[6] else ""))
+def test_fused_prologue_forward_is_the_two_passes(dev, case):
+    """qb_gdn_fwd_prologue (the prologue inside the chunked forward's first kernel) against the separate prologue
+    pass followed by the chunked forward on its outputs: q, k, beta, the log-decay, y, the final state and the whole
+    residual buffer (states and chunk tiles) equal bit for bit."""
+    torch = dev
+    from quotebound_amd import gdn, neighbours
+
+    B, T, Hk, Hv, Dv, lens, with_s0 = case
+    Dk = 128
+    rng = np.random.default_rng(70 + T)
+    x = _prologue_inputs(rng, B, T, Hk, Hv, Dk, bf16=True)
+    x["v"] = nb.round_bf16(rng.standard_normal((B, T, Hv, Dv)))
+    d = _to_dev(torch, x, True, ("q_raw", "k_raw", "a", "b", "v"))
+    cu = None if lens is None else np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    N = B if cu is None else len(lens)
+    s0 = torch.tensor(rng.normal(0.0, 0.1, (N, Hv, Dv, Dk)).astype(np.float32)).cuda() if with_s0 else None
+    fused = gdn.forward_prologue(d["q_raw"], d["k_raw"], d["v"], d["a"], d["b"], d["a_log"], d["dt_bias"], s0,
+                                 cu_seqlens=cu)
+    q, k, beta, ld = neighbours.prologue_forward(d["q_raw"], d["k_raw"], d["a"], d["b"], d["a_log"], d["dt_bias"])
+    y, s_out, ckpt = gdn.forward(q, k, d["v"], ld, beta, s0, log_decay=True, design=2, cu_seqlens=cu)
+    torch.cuda.synchronize()
+    names = ("y", "s_out", "ckpt", "q", "k", "beta", "log_decay")
+    for name, got, ref in zip(names, fused, (y, s_out, ckpt, q, k, beta, ld)):
+        assert got.dtype == ref.dtype and got.shape == ref.shape, name
+        assert torch.equal(got.view(torch.int16) if got.dtype == torch.bfloat16 else got.view(torch.int32),
+                           ref.view(torch.int16) if ref.dtype == torch.bfloat16 else ref.view(torch.int32)), name
