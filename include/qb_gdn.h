@@ -113,9 +113,10 @@ int qb_gdn_bwd(const qb_gdn_desc* desc, const void* q, const void* k, const void
                const void* beta, const float* ckpt, const void* dy, const float* ds_out, void* dq, void* dk, void* dv,
                float* dg, void* dbeta, float* ds0, void* workspace, void* stream, char* err, int errlen);
 
-/* Size of the device array qb_gdn_bwd_static uses as its workspace, per GPU: 256 MiB, which holds the chunked
- * design's workspace up to NC * Hv * Dv * Dk = 2^26 (the 4B and 9B layer shapes at T = 4096). */
-#define QB_GDN_STATIC_SCRATCH_BYTES (256u << 20)
+/* Size of the device array qb_gdn_bwd_static uses as its workspace, per GPU: 257 MiB, which holds the chunked
+ * design's workspace (the chunk-end state cotangents and 8 bytes per chunk and value head) up to
+ * NC * Hv * Dv * Dk = 2^26 (the 4B and 9B layer shapes at T = 4096 hold half that). */
+#define QB_GDN_STATIC_SCRATCH_BYTES (257u << 20)
 
 /* qb_gdn_bwd without a workspace argument, for callers that cannot allocate device memory (code under HIP graph
  * capture, tight serving loops, harnesses that forbid hipMalloc). No counterpart in the reference. Its workspace is
@@ -168,6 +169,20 @@ int qb_gdn_fwd_prologue(const qb_gdn_desc* desc, const void* q_raw, const void* 
                         const void* b, const float* a_log, const float* dt_bias, const float* s0, void* q, void* k,
                         void* beta, float* log_decay, void* y, float* s_out, float* ckpt, void* workspace,
                         void* stream, char* err, int errlen);
+
+/* qb_gdn_bwd and qb_gdn_prologue_bwd in one, after qb_gdn_fwd_prologue: the prologue's backward runs at the end of
+ * the backward's last kernel, which rounds the cotangents of q, k and beta to bf16 as qb_gdn_prologue_bwd would read
+ * them and turns them, with that of the log-decay, into those of q_raw, k_raw, a, b (bf16) and of a_log, dt_bias
+ * ([Hv] float32, summed over every token: per (chunk, value head) in the kernel, then over chunks in order, a
+ * fixed order but not qb_gdn_prologue_bwd's). q, k, beta, log_decay and ckpt are what qb_gdn_fwd_prologue wrote.
+ * It saves the separate pass's reads of dq, dk, q_raw, k_raw and its launch; dq_raw and dk_raw leave as 16-byte
+ * row stores. The chunked design only: desc->design QB_GDN_CHUNKED, dtype bf16, out_f32 = 0, g_is_log = 1. ds_out
+ * and ds0 as for qb_gdn_bwd. */
+int qb_gdn_bwd_prologue(const qb_gdn_desc* desc, const void* q_raw, const void* k_raw, const void* a, const void* b,
+                        const float* a_log, const float* dt_bias, const void* q, const void* k, const void* v,
+                        const void* beta, const float* log_decay, const float* ckpt, const void* dy,
+                        const float* ds_out, void* dq_raw, void* dk_raw, void* dv, void* da, void* db, float* da_log,
+                        float* ddt_bias, float* ds0, void* workspace, void* stream, char* err, int errlen);
 
 /* Epilogue, after qb_gdn_fwd (src/deltanet.cpp:35-45, 122, the gated RMSNorm): o = silu(z) rms_norm(y, norm_w, eps).
  * y, z, o [B, T, Hv, Dv] in dtype; norm_w [Dv] float32. */

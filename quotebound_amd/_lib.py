@@ -77,6 +77,8 @@ def load():
     L.qb_gdn_prologue_bwd.restype = ctypes.c_int
     L.qb_gdn_fwd_prologue.argtypes = [D] + [P] * 17 + [ctypes.c_char_p, ctypes.c_int]
     L.qb_gdn_fwd_prologue.restype = ctypes.c_int
+    L.qb_gdn_bwd_prologue.argtypes = [D] + [P] * 24 + [ctypes.c_char_p, ctypes.c_int]
+    L.qb_gdn_bwd_prologue.restype = ctypes.c_int
     F = ctypes.c_float
     L.qb_gdn_epilogue_fwd.argtypes = [D, P, P, P, F, P, P, ctypes.c_char_p, ctypes.c_int]
     L.qb_gdn_epilogue_fwd.restype = ctypes.c_int
@@ -164,7 +166,7 @@ def bwd_static(desc, q, k, v, g, beta, ckpt, dy, ds_out, dq, dk, dv, dg, dbeta, 
     _call(load().qb_gdn_bwd_static, desc, q, k, v, g, beta, ckpt, dy, ds_out, dq, dk, dv, dg, dbeta, ds0, stream)
 
 
-STATIC_SCRATCH_BYTES = 256 << 20  # QB_GDN_STATIC_SCRATCH_BYTES
+STATIC_SCRATCH_BYTES = 257 << 20  # QB_GDN_STATIC_SCRATCH_BYTES
 
 
 def neighbours_workspace_bytes(desc) -> int:
@@ -181,6 +183,12 @@ def fwd_prologue(desc, q_raw, k_raw, v, a, b, a_log, dt_bias, s0, q, k, beta, lo
                  stream) -> None:
     _call(load().qb_gdn_fwd_prologue, desc, q_raw, k_raw, v, a, b, a_log, dt_bias, s0, q, k, beta, log_decay, y, s_out,
           ckpt, workspace, stream)
+
+
+def bwd_prologue(desc, q_raw, k_raw, a, b, a_log, dt_bias, q, k, v, beta, log_decay, ckpt, dy, ds_out, dq_raw,
+                 dk_raw, dv, da, db, da_log, ddt_bias, ds0, workspace, stream) -> None:
+    _call(load().qb_gdn_bwd_prologue, desc, q_raw, k_raw, a, b, a_log, dt_bias, q, k, v, beta, log_decay, ckpt, dy,
+          ds_out, dq_raw, dk_raw, dv, da, db, da_log, ddt_bias, ds0, workspace, stream)
 
 
 def prologue_fwd(desc, q_raw, k_raw, a, b, a_log, dt_bias, q, k, beta, log_decay, stream) -> None:

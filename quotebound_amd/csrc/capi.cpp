@@ -545,6 +545,51 @@ int qb_gdn_fwd_prologue(const qb_gdn_desc* desc, const void* q_raw, const void* 
   });
 }
 
+int qb_gdn_bwd_prologue(const qb_gdn_desc* desc, const void* q_raw, const void* k_raw, const void* a, const void* b,
+                        const float* a_log, const float* dt_bias, const void* q, const void* k, const void* v,
+                        const void* beta, const float* log_decay, const float* ckpt, const void* dy,
+                        const float* ds_out, void* dq_raw, void* dk_raw, void* dv, void* da, void* db, float* da_log,
+                        float* ddt_bias, float* ds0, void* workspace, void* stream, char* err, int errlen) {
+  return guarded(err, errlen, [&] {
+    Problem p;
+    std::string why = resolve(desc, p);
+    qbgdn::NbProblem nb;
+    if (why.empty()) why = nb_resolve(desc, nb, true, false);
+    if (why.empty() && (desc->design != QB_GDN_CHUNKED || !desc->g_is_log || !p.in_bf16 || !p.out_bf16))
+      why = "gated delta: the fused prologue backward runs the chunked design with bf16 inputs and outputs and "
+            "g_is_log = 1 " + shape_of(*desc);
+    const bool any = why.empty() && p.BT > 0;
+    const PtrCheck c[] = {{"q_raw", q_raw, any, 16},         {"k_raw", k_raw, any, 16},
+                          {"a", a, any, 2},                  {"b", b, any, 2},
+                          {"a_log", a_log, true, 4},         {"dt_bias", dt_bias, true, 4},
+                          {"q", q, any, 16},                 {"k", k, any, 16},
+                          {"v", v, any, 2},                  {"beta", beta, any, 2},
+                          {"log_decay", log_decay, any, 4},  {"ckpt", ckpt, any, 16},
+                          {"dy", dy, any, 2},                {"ds_out", ds_out, false, 4},
+                          {"dq_raw", dq_raw, any, 16},       {"dk_raw", dk_raw, any, 16},
+                          {"dv", dv, any, 2},                {"da", da, any, 2},
+                          {"db", db, any, 2},                {"da_log", da_log, true, 4},
+                          {"ddt_bias", ddt_bias, true, 4},   {"ds0", ds0, false, 4},
+                          {"workspace", workspace, any && ws_bytes(desc, p) > 0, 16}};
+    if (why.empty()) why = check_all(c);
+    if (!why.empty()) {
+      set_err(err, errlen, why);
+      return -1;
+    }
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const qbgdn::PrologueGradIn pro{q_raw, k_raw, a, b, a_log, dt_bias, nb.scale_q, nb.scale_k,
+                                    dq_raw, dk_raw, da, db, da_log, ddt_bias};
+    const qbgdn::BwdPtrs bp{q, k, v, log_decay, beta, ckpt, dy, ds_out, dq_raw, dk_raw, dv, nullptr, nullptr, ds0};
+    qbgdn::Tracer tr = tracer_of(desc, st);
+    const hipError_t e = qbgdn::chunk_bwd_prologue(p, pro, bp, workspace, st, tr);
+    if (e != hipSuccess) {
+      set_err(err, errlen, hip_fail("backward launch", e));
+      return -1;
+    }
+    return 0;
+  });
+}
+
 int qb_gdn_epilogue_fwd(const qb_gdn_desc* desc, const void* y, const void* z, const float* norm_w, float eps, void* o,
                         void* stream, char* err, int errlen) {
   return guarded(err, errlen, [&] {

@@ -12,6 +12,8 @@ ChunkLayout layout_of(const Problem& p) { return ChunkLayout{p.NC, p.Hv, p.Dv, p
 
 size_t extras_bytes(const Problem& p) { return layout_of(p).tiles_bytes(); }
 size_t dsend_bytes(const Problem& p) { return size_t(p.NC) * p.Hv * p.Dv * p.Dk * 4; }
+// The fused prologue backward's per-(chunk slot, value head) sums, after dSend.
+size_t gate_part_bytes(const Problem& p) { return (size_t(p.NC) * p.Hv * 2 * 4 + 255) & ~size_t(255); }
 
 ChunkArgs base_args(const Problem& p) {
   ChunkArgs a{};
@@ -45,7 +47,7 @@ const char* chunk_supports(const Problem& p) {
 size_t chunk_ckpt_bytes(const Problem& p) { return layout_of(p).bytes(); }
 
 size_t chunk_workspace_bytes(const Problem& p) {
-  const size_t a = dsend_bytes(p), b = extras_bytes(p);
+  const size_t a = dsend_bytes(p) + gate_part_bytes(p), b = extras_bytes(p);
   return a > b ? a : b;
 }
 
@@ -92,7 +94,10 @@ hipError_t chunk_fwd_prologue(const Problem& p, const PrologueIn& pro, const Fwd
   return fwd_impl(p, &pro, f, ws, s, tr);
 }
 
-hipError_t chunk_bwd(const Problem& p, const BwdPtrs& b, void* ws, hipStream_t s, Tracer& tr) {
+namespace {
+
+hipError_t bwd_impl(const Problem& p, const PrologueGradIn* pro, const BwdPtrs& b, void* ws, hipStream_t s,
+                    Tracer& tr) {
   ChunkArgs a = base_args(p);
   a.q = static_cast<const bf16_t*>(b.q);
   a.k = static_cast<const bf16_t*>(b.k);
@@ -110,16 +115,38 @@ hipError_t chunk_bwd(const Problem& p, const BwdPtrs& b, void* ws, hipStream_t s
   a.dbeta = b.dbeta;
   a.ds0 = b.ds0;
   a.dsend = static_cast<float*>(ws);
+  if (pro) {
+    a.pro.q_raw = static_cast<const bf16_t*>(pro->q_raw), a.pro.k_raw = static_cast<const bf16_t*>(pro->k_raw);
+    a.pro.a = static_cast<const bf16_t*>(pro->a), a.pro.b = static_cast<const bf16_t*>(pro->b);
+    a.pro.a_log = pro->a_log, a.pro.dt_bias = pro->dt_bias;
+    a.pro.scale_q = pro->scale_q, a.pro.scale_k = pro->scale_k;
+    a.pro.da = static_cast<bf16_t*>(pro->da), a.pro.db = static_cast<bf16_t*>(pro->db);
+    a.pro.part = reinterpret_cast<float*>(static_cast<unsigned char*>(ws) + dsend_bytes(p));
+    a.dq = pro->dq_raw, a.dk = pro->dk_raw;
+  }
   tr.mark();
   hipError_t e = launch_chunk_bwd_state(a, p.out_bf16, s);
   if (e != hipSuccess) return e;
   tr.mark();
-  e = launch_chunk_bwd_grads(a, p.out_bf16, s);
+  e = launch_chunk_bwd_grads(a, p.out_bf16, s, pro != nullptr);
   tr.mark();
+  if (e == hipSuccess && pro) e = launch_chunk_gate_sums(a, pro->da_log, pro->ddt_bias, s);
   // With g given as the factor, dL/dg at tiny or zero factors comes from an exact replay (chunk_dgfix.hip); chunks
   // without one return at once.
   if (e == hipSuccess && !p.g_is_log) e = launch_chunk_dgfix(a, p.out_bf16, s);
   return e;
+}
+
+}  // namespace
+
+hipError_t chunk_bwd(const Problem& p, const BwdPtrs& b, void* ws, hipStream_t s, Tracer& tr) {
+  return bwd_impl(p, nullptr, b, ws, s, tr);
+}
+
+hipError_t chunk_bwd_prologue(const Problem& p, const PrologueGradIn& pro, const BwdPtrs& b, void* ws,
+                              hipStream_t s, Tracer& tr) {
+  if (!p.g_is_log || !p.in_bf16 || !p.out_bf16) return hipErrorInvalidValue;
+  return bwd_impl(p, &pro, b, ws, s, tr);
 }
 
 }  // namespace qbgdn

@@ -22,6 +22,7 @@
 
 #include "chunk_common.h"
 #include "chunk_kernels.h"
+#include "prologue_math.h"
 
 namespace qbgdn {
 namespace {
@@ -64,7 +65,11 @@ constexpr int kSmemBytes = kLoopBytes > kEndBytes ? kLoopBytes : kEndBytes;
 // halves. The busiest wave of the phase that accumulates them then runs 5 products in place of 6.
 __device__ __forceinline__ int key_tile(int pw, int hw, int mi) { return pw < 2 ? hw + 2 * mi : 2 * hw + mi; }
 
-template <typename OutT>
+// kFused: the layer's prologue backward at the end (qb_gdn_bwd_prologue; bf16 only). The cotangents of q, k and
+// beta are rounded to bf16 as the separate pass would read them, then turned into those of q_raw, k_raw, a and b with
+// the separate pass's arithmetic (prologue_math.h); the dA_log and ddt_bias terms are summed per (chunk, value head)
+// into a.pro.part, which chunk_gate_sums_kernel sums over chunks.
+template <typename OutT, bool kFused>
 __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) {
   constexpr int Dk = 128;
   constexpr bool kExactDy = std::is_same<OutT, bf16_t>::value;
@@ -619,7 +624,23 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
           const float u = __shfl_down(v, off);
           if (t + off < kC) v += u;
         }
-        if (t < L) {
+        if constexpr (kFused) {
+          const int64_t g0 = tok * a.Hv + hv;
+          const uint32_t gi = uint32_t(t * a.Hv);
+          const float dbT = dbTp[0][t] + dbTp[1][t] + dbTp[2][t] + dbTp[3][t];
+          float pa = 0.f, pd = 0.f;
+          if (t < L) {
+            float da, db;
+            gate_bwd<bf16_t>(bf16_to_f32(a.pro.a[g0 + gi]), bf16_to_f32(a.pro.b[g0 + gi]), rnd<bf16_t>(dbT + dbA), v,
+                             expf(a.pro.a_log[hv]), a.pro.dt_bias[hv], da, db, pa, pd);
+            a.pro.da[g0 + gi] = f32_to_bf16(da);
+            a.pro.db[g0 + gi] = f32_to_bf16(db);
+          }
+          pa = sum16(pa), pd = sum16(pd);
+          pa += __shfl_xor(pa, 16), pd += __shfl_xor(pd, 16);
+          pa += __shfl_xor(pa, 32), pd += __shfl_xor(pd, 32);
+          if (t == 0) a.pro.part[(slot * a.Hv + hv) * 2] = pa, a.pro.part[(slot * a.Hv + hv) * 2 + 1] = pd;
+        } else if (t < L) {
           const int64_t g0 = tok * a.Hv + hv;
           const uint32_t gi = uint32_t(t * a.Hv);
           a.dg[g0 + gi] = a.g_is_log ? v : v / a.g[g0 + gi];
@@ -629,10 +650,57 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
       }
     }
 
+    if constexpr (kFused) {
+      // dq, dk rounded to bf16 into rows [64][128] in the end phase's bytes (E5's reads of them done), then the
+      // normalisation's backward row by row, 16 lanes of 8 elements per row as in the separate pass: the raw rows,
+      // and the results, through buffer resources that end at the chunk's last row.
+      __syncthreads();
+      {
+        int lt = tid;
+        asm volatile("" : "+v"(lt));
+        const int g = (lt >> 4) & 3, li = lt & 15, pw = (lt >> 6) & 3, hw = lt >> 8;
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) {
+            const int at = (16 * pw + 4 * g + jj) * kLK + 16 * (4 * hw + t) + li;
+            sb[eQb + at] = static_cast<__bf16>(dQ[t][jj]);
+            sb[eQb + kC * kLK + at] = static_cast<__bf16>(dK[t][jj]);
+          }
+      }
+      __syncthreads();
+      {
+        const uint32_t bytes = uint32_t(L * sk) * 2u;
+        const int64_t base = (tok * a.Hk + hk) * Dk;
+        const auto qrr = buffer_rsrc(a.pro.q_raw + base, bytes), krr = buffer_rsrc(a.pro.k_raw + base, bytes);
+        const auto dqo = buffer_rsrc(static_cast<bf16_t*>(a.dq) + base, bytes);
+        const auto dko = buffer_rsrc(static_cast<bf16_t*>(a.dk) + base, bytes);
+        const int c8 = (tid & 15) * 8;
+        for (int rr = tid >> 4; rr < 2 * kC; rr += kThreads / 16) {
+          const bool isk = rr >= kC;
+          const int t = rr & (kC - 1);
+          const uint32_t off = uint32_t(t * sk + c8) * 2u;
+          const uint4 xr = buf_ld16(isk ? krr : qrr, off);
+          const uint4 gr = *reinterpret_cast<const uint4*>(sb + eQb + rr * kLK + c8);
+          float x[8], gg[8];
+          const uint32_t xw[4] = {xr.x, xr.y, xr.z, xr.w}, gw[4] = {gr.x, gr.y, gr.z, gr.w};
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            x[2 * j] = __uint_as_float(xw[j] << 16), x[2 * j + 1] = __uint_as_float(xw[j] & 0xffff0000u);
+            gg[2 * j] = __uint_as_float(gw[j] << 16), gg[2 * j + 1] = __uint_as_float(gw[j] & 0xffff0000u);
+          }
+          float ss, gx;
+          norm_bwd_sums(x, gg, isk ? a.pro.scale_k : a.pro.scale_q, ss, gx);
+          norm_bwd_apply(x, gg, sum16(ss), sum16(gx), Dk);
+          buf_st16(isk ? dko : dqo, off,
+                   uint4{f32x2_to_bf16x2(x[0], x[1]), f32x2_to_bf16x2(x[2], x[3]), f32x2_to_bf16x2(x[4], x[5]),
+                         f32x2_to_bf16x2(x[6], x[7])});
+        }
+      }
+    } else {
     // dq, dk for the wave's positions and columns (lane -> column 16 (4 hw + t) + li, rows 16 pw + 4g + jj), through
     // buffer resources that end at the chunk's last row; lane indices from an opaque copy, so their addresses are
     // formed here rather than hoisted out of the item loop.
-    {
       int lt = tid;
       asm volatile("" : "+v"(lt));
       const int g = (lt >> 4) & 3, li = lt & 15, pw = (lt >> 6) & 3, hw = lt >> 8;
@@ -651,9 +719,21 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
   }
 }
 
+// dA_log and ddt_bias [Hv]: the per-(chunk slot, value head) sums of the fused gradient kernel, summed over the slots
+// in order.
+__global__ __launch_bounds__(256) void chunk_gate_sums_kernel(const float* part, int64_t NC, int Hv, float* da_log,
+                                                              float* ddt_bias) {
+  const int h = blockIdx.x * 256 + threadIdx.x;
+  if (h >= Hv) return;
+  float sa = 0.f, sd = 0.f;
+  for (int64_t c = 0; c < NC; ++c) sa += part[(c * Hv + h) * 2], sd += part[(c * Hv + h) * 2 + 1];
+  da_log[h] = sa;
+  ddt_bias[h] = sd;
+}
+
 }  // namespace
 
-hipError_t launch_chunk_bwd_grads(const ChunkArgs& a, bool out_bf16, hipStream_t s) {
+hipError_t launch_chunk_bwd_grads(const ChunkArgs& a, bool out_bf16, hipStream_t s, bool fused_prologue) {
   const int total = int(a.lay.NC) * a.Hk;
   if (total == 0) return hipSuccess;
   // One resident block per CU (the kernel's LDS allows no more), looping over its items; a multiple of 8 blocks, so
@@ -663,10 +743,20 @@ hipError_t launch_chunk_bwd_grads(const ChunkArgs& a, bool out_bf16, hipStream_t
   if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
   if (e != hipSuccess) return e;
   const int grid = total <= cus ? total : (cus >= 8 ? cus & ~7 : cus);
-  if (out_bf16)
-    hipLaunchKernelGGL(chunk_bwd_grads_kernel<bf16_t>, dim3(grid), dim3(kThreads), 0, s, a);
-  else
-    hipLaunchKernelGGL(chunk_bwd_grads_kernel<float>, dim3(grid), dim3(kThreads), 0, s, a);
+  if (fused_prologue) {
+    if (!out_bf16) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((chunk_bwd_grads_kernel<bf16_t, true>), dim3(grid), dim3(kThreads), 0, s, a);
+  } else if (out_bf16) {
+    hipLaunchKernelGGL((chunk_bwd_grads_kernel<bf16_t, false>), dim3(grid), dim3(kThreads), 0, s, a);
+  } else {
+    hipLaunchKernelGGL((chunk_bwd_grads_kernel<float, false>), dim3(grid), dim3(kThreads), 0, s, a);
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_chunk_gate_sums(const ChunkArgs& a, float* da_log, float* ddt_bias, hipStream_t s) {
+  hipLaunchKernelGGL(chunk_gate_sums_kernel, dim3((a.Hv + 255) / 256), dim3(256), 0, s, a.pro.part, a.lay.NC, a.Hv,
+                     da_log, ddt_bias);
   return hipGetLastError();
 }
 

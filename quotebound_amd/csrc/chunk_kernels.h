@@ -44,13 +44,19 @@ struct ChunkArgs {
     bf16_t* k;
     bf16_t* beta;
     float* log_decay;
+    // The fused backward (chunk_bwd_grads): the cotangents of a and b, and per (chunk slot, value head) the sums
+    // of the dA_log and ddt_bias terms [NC][Hv][2]. dq_raw and dk_raw go to dq and dk.
+    bf16_t* da;
+    bf16_t* db;
+    float* part;
   } pro;
 };
 
 hipError_t launch_chunk_prep(const ChunkArgs& a, hipStream_t s, bool fused_prologue = false);
 hipError_t launch_chunk_fwd(const ChunkArgs& a, bool out_bf16, hipStream_t s);
 hipError_t launch_chunk_bwd_state(const ChunkArgs& a, bool out_bf16, hipStream_t s);
-hipError_t launch_chunk_bwd_grads(const ChunkArgs& a, bool out_bf16, hipStream_t s);
+hipError_t launch_chunk_bwd_grads(const ChunkArgs& a, bool out_bf16, hipStream_t s, bool fused_prologue = false);
+hipError_t launch_chunk_gate_sums(const ChunkArgs& a, float* da_log, float* ddt_bias, hipStream_t s);
 hipError_t launch_chunk_dgfix(const ChunkArgs& a, bool out_bf16, hipStream_t s);
 
 }  // namespace qbgdn

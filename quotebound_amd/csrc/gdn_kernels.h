@@ -96,6 +96,25 @@ struct PrologueIn {
 };
 hipError_t chunk_fwd_prologue(const Problem& p, const PrologueIn& pro, const FwdPtrs& a, void* ws, hipStream_t s,
                               Tracer& tr);
+// The layer's prologue backward fused into the chunked backward (qb_gdn_bwd_prologue): the raw inputs and the
+// prologue's cotangents, which replace those of q, k, g and beta (a.dq, a.dk, a.dg, a.dbeta are not written).
+struct PrologueGradIn {
+  const void* q_raw;
+  const void* k_raw;
+  const void* a;
+  const void* b;
+  const float* a_log;
+  const float* dt_bias;
+  float scale_q, scale_k;
+  void* dq_raw;
+  void* dk_raw;
+  void* da;
+  void* db;
+  float* da_log;
+  float* ddt_bias;
+};
+hipError_t chunk_bwd_prologue(const Problem& p, const PrologueGradIn& pro, const BwdPtrs& a, void* ws,
+                              hipStream_t s, Tracer& tr);
 hipError_t chunk_bwd(const Problem& p, const BwdPtrs& a, void* ws, hipStream_t s, Tracer& tr);
 
 }  // namespace qbgdn

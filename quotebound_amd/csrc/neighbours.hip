@@ -147,14 +147,12 @@ __global__ __launch_bounds__(256) void prologue_bwd_kernel(
       const int64_t tt = int64_t(kGateSteps) * k, end = (tile + 1) * tt < BT ? (tile + 1) * tt : BT;
       for (int64_t tok = tile * tt + t / Hv; tok < end; tok += k) {
         const int64_t i = tok * Hv + h;
-        const float sb = sigmoidf(IO<T>::ld(b, i));
-        IO<T>::st(db, i, IO<T>::ld(dbeta, i) * sb * (1.f - sb));
-        const float x = rnd<T>(IO<T>::ld(a, i) + bias);
-        const float g = dld[i];
-        const float dx = -g * ea * sigmoidf(x);
-        IO<T>::st(da, i, dx);
-        pa += g * (-ea * rnd<T>(softplusf(x)));  // d log_decay / d A_log = log_decay
-        pd += dx;
+        float dxa, dxb, ta, td;  // d log_decay / d A_log = log_decay
+        gate_bwd<T>(IO<T>::ld(a, i), IO<T>::ld(b, i), IO<T>::ld(dbeta, i), dld[i], ea, bias, dxa, dxb, ta, td);
+        IO<T>::st(db, i, dxb);
+        IO<T>::st(da, i, dxa);
+        pa += ta;
+        pd += td;
       }
     }
     red[0][t] = pa, red[1][t] = pd;
@@ -181,18 +179,9 @@ __global__ __launch_bounds__(256) void prologue_bwd_kernel(
   }
 #pragma unroll
   for (int j = 0; j < kSlots; ++j) {
-    const float s = isk[j] ? sk : sq;
-    float ss = 0.f, gx = 0.f;
-#pragma unroll
-    for (int e = 0; e < kVec; ++e) {
-      g[j][e] *= s;
-      ss += x[j][e] * x[j][e];
-      gx += g[j][e] * x[j][e];
-    }
-    const float rho = rsqrt_mean(group_sum<RL::L>(ss), D, kNormEps);
-    const float c = rho * rho * rho * group_sum<RL::L>(gx) / D;
-#pragma unroll
-    for (int e = 0; e < kVec; ++e) x[j][e] = rho * g[j][e] - c * x[j][e];
+    float ss, gx;
+    norm_bwd_sums(x[j], g[j], isk[j] ? sk : sq, ss, gx);
+    norm_bwd_apply(x[j], g[j], group_sum<RL::L>(ss), group_sum<RL::L>(gx), D);
     if (live[j]) st8((isk[j] ? dkr : dqr) + off[j], x[j]);
   }
 }

@@ -39,6 +39,38 @@ __device__ __forceinline__ void norm_row8(float (&x)[8], float ss_row, int D, fl
   for (int e = 0; e < 8; ++e) x[e] = rnd<T>(s * rnd<T>(x[e] * rho));
 }
 
+// The q/k normalisation's backward for one lane's 8 elements of a row: g holds the cotangent of the normalised row
+// (dout) and gets s dout; the lane sums of sum(x^2) and sum(g x) come back, to be reduced over the row's lanes and
+// handed to norm_bwd_apply, which leaves dx = rho g - rho^3 x sum(g x) / D in x.
+__device__ __forceinline__ void norm_bwd_sums(const float (&x)[8], float (&g)[8], float s, float& ss, float& gx) {
+  ss = 0.f, gx = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    g[e] *= s;
+    ss += x[e] * x[e];
+    gx += g[e] * x[e];
+  }
+}
+__device__ __forceinline__ void norm_bwd_apply(float (&x)[8], const float (&g)[8], float ss_row, float gx_row, int D) {
+  const float rho = rsqrt_mean(ss_row, D, kNormEps);
+  const float c = rho * rho * rho * gx_row / D;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) x[e] = rho * g[e] - c * x[e];
+}
+
+// The gates' backward for one (token, value head): db from the cotangent of beta (already in the activation dtype),
+// da from that of the log-decay, and the terms of dA_log (dlog_decay * log_decay) and ddt_bias (da unrounded).
+template <typename T>
+__device__ __forceinline__ void gate_bwd(float a, float b, float dbeta, float dlog, float ea, float dt_bias,
+                                         float& da, float& db, float& pa, float& pd) {
+  const float sb = sigmoidf(b);
+  db = dbeta * sb * (1.f - sb);
+  const float x = rnd<T>(a + dt_bias);
+  da = -dlog * ea * sigmoidf(x);
+  pa = dlog * (-ea * rnd<T>(softplusf(x)));
+  pd = da;
+}
+
 // beta and the log-decay of one (token, value head) from b and a.
 template <typename T>
 __device__ __forceinline__ float gate_beta(float b) { return rnd<T>(sigmoidf(b)); }

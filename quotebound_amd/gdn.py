@@ -151,6 +151,41 @@ def forward_prologue(q_raw, k_raw, v, a, b, a_log, dt_bias, state=None, *, cu_se
     return y, s_out, ckpt, q, k, beta, log_decay
 
 
+def backward_prologue(q_raw, k_raw, a, b, a_log, dt_bias, q, k, v, beta, log_decay, ckpt, dy, ds_out=None, *,
+                      cu_seqlens=None, want_ds0=True):
+    """The chunked backward with the prologue's backward at the end of its last kernel (qb_gdn_bwd_prologue), after
+    forward_prologue (q, k, beta, log_decay, ckpt are what it returned): (dq_raw, dk_raw, dv, da, db, da_log,
+    ddt_bias, ds0). The first five are exactly what backward(q, k, v, log_decay, beta, ckpt, dy, ds_out,
+    log_decay=True, design=CHUNKED) followed by neighbours.prologue_backward on its cotangents returns; da_log and
+    ddt_bias are the same sums taken per chunk and then over chunks. bf16 activations and dy."""
+    for t in (q_raw, k_raw, a, b, q, k, v, beta, dy):
+        if t.dtype != torch.bfloat16 or not t.is_cuda:
+            raise RuntimeError("gated delta: the fused prologue backward takes bf16 device tensors")
+    q_raw, k_raw, a, b, q, k, v, beta, dy = (t.contiguous() for t in (q_raw, k_raw, a, b, q, k, v, beta, dy))
+    a_log, dt_bias = a_log.float().contiguous(), dt_bias.float().contiguous()
+    log_decay = log_decay.float().contiguous()
+    desc, keep = _desc(q_raw, v, torch.bfloat16, True, _lib.CHUNKED, cu_seqlens, False)
+    why = _lib.validate(desc)
+    if why:
+        raise RuntimeError(why)
+    N = q_raw.shape[0] if cu_seqlens is None else len(cu_seqlens) - 1
+    dev = q_raw.device
+    Hv, Dv, Dk = v.shape[2], v.shape[3], q_raw.shape[3]
+    dso = None if ds_out is None else ds_out.to(torch.float32).contiguous()
+    dq_raw, dk_raw, dv = torch.empty_like(q_raw), torch.empty_like(k_raw), torch.empty_like(v)
+    da, db = torch.empty_like(a), torch.empty_like(b)
+    da_log, ddt_bias = torch.empty_like(a_log), torch.empty_like(dt_bias)
+    ds0 = torch.empty(N, Hv, Dv, Dk, dtype=torch.float32, device=dev) if want_ds0 else None
+    ws = _workspace(desc, dev)
+    _lib.bwd_prologue(desc, _dev_ptr(q_raw), _dev_ptr(k_raw), _dev_ptr(a), _dev_ptr(b), _dev_ptr(a_log),
+                      _dev_ptr(dt_bias), _dev_ptr(q), _dev_ptr(k), _dev_ptr(v), _dev_ptr(beta), _dev_ptr(log_decay),
+                      _dev_ptr(ckpt), _dev_ptr(dy), _dev_ptr(dso), _dev_ptr(dq_raw), _dev_ptr(dk_raw), _dev_ptr(dv),
+                      _dev_ptr(da), _dev_ptr(db), _dev_ptr(da_log), _dev_ptr(ddt_bias), _dev_ptr(ds0), _dev_ptr(ws),
+                      _stream(dev))
+    del keep
+    return dq_raw, dk_raw, dv, da, db, da_log, ddt_bias, ds0
+
+
 def forward_rows(q, k, v, g, beta, state=None, *, log_decay=False, cu_seqlens=None):
     """(y, row_states): the forward keeping the state after every token, row_states [B, T, Hv, Dv, Dk] float32 (or
     [total, Hv, Dv, Dk] packed) — the reference's rows pass for exact drafts (src/deltanet.cpp:101-117), whose

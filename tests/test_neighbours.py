@@ -387,3 +387,47 @@ def test_fused_prologue_forward_is_the_two_passes(dev, case):
         assert got.dtype == ref.dtype and got.shape == ref.shape, name
         assert torch.equal(got.view(torch.int16) if got.dtype == torch.bfloat16 else got.view(torch.int32),
                            ref.view(torch.int16) if ref.dtype == torch.bfloat16 else ref.view(torch.int32)), name
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("case", FUSED_CASES, ids=lambda c: "B%dT%dHk%dHv%dDv%d%s%s" % (
+    *c[:5], "_packed" if c[5] else "", "_s0" if c[6] else ""))
+def test_fused_prologue_backward_is_the_two_passes(dev, case):
+    """qb_gdn_bwd_prologue (the prologue's backward at the end of the chunked backward's gradient kernel) against the
+    chunked backward followed by the separate prologue backward on its cotangents: dq_raw, dk_raw, dv, da, db and ds0
+    equal bit for bit; da_log and ddt_bias, summed per chunk and then over chunks instead of per token tile, within
+    1e-5 of the separate pass's sums relative to the sum of the terms' magnitudes."""
+    torch = dev
+    from quotebound_amd import gdn, neighbours
+
+    B, T, Hk, Hv, Dv, lens, with_s0 = case
+    Dk = 128
+    rng = np.random.default_rng(170 + T)
+    x = _prologue_inputs(rng, B, T, Hk, Hv, Dk, bf16=True)
+    x["v"] = nb.round_bf16(rng.standard_normal((B, T, Hv, Dv)))
+    x["dy"] = nb.round_bf16(rng.standard_normal((B, T, Hv, Dv)))
+    d = _to_dev(torch, x, True, ("q_raw", "k_raw", "a", "b", "v", "dy"))
+    cu = None if lens is None else np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    N = B if cu is None else len(lens)
+    s0 = torch.tensor(rng.normal(0.0, 0.1, (N, Hv, Dv, Dk)).astype(np.float32)).cuda() if with_s0 else None
+    dso = torch.tensor(rng.normal(0.0, 0.1, (N, Hv, Dv, Dk)).astype(np.float32)).cuda() if with_s0 else None
+    _, _, ckpt, q, k, beta, ld = gdn.forward_prologue(d["q_raw"], d["k_raw"], d["v"], d["a"], d["b"], d["a_log"],
+                                                      d["dt_bias"], s0, cu_seqlens=cu)
+    fused = gdn.backward_prologue(d["q_raw"], d["k_raw"], d["a"], d["b"], d["a_log"], d["dt_bias"], q, k, d["v"],
+                                  beta, ld, ckpt, d["dy"], dso, cu_seqlens=cu)
+    dq, dk, dv, dld, dbeta, ds0 = gdn.backward(q, k, d["v"], ld, beta, ckpt, d["dy"], dso, log_decay=True, design=2,
+                                               cu_seqlens=cu)
+    dq_raw, dk_raw, da, db, da_log, ddt = neighbours.prologue_backward(d["q_raw"], d["k_raw"], d["a"], d["b"],
+                                                                       d["a_log"], d["dt_bias"], dq, dk, dbeta, dld)
+    torch.cuda.synchronize()
+    names = ("dq_raw", "dk_raw", "dv", "da", "db", "ds0")
+    for name, got, ref in zip(names, fused[:5] + fused[7:], (dq_raw, dk_raw, dv, da, db, ds0)):
+        assert got.dtype == ref.dtype and got.shape == ref.shape, name
+        assert torch.equal(got.view(torch.int16) if got.dtype == torch.bfloat16 else got.view(torch.int32),
+                           ref.view(torch.int16) if ref.dtype == torch.bfloat16 else ref.view(torch.int32)), name
+    # The per-head sums' terms: dlog_decay * log_decay for dA_log, da for ddt_bias.
+    mag_a = (dld.double() * ld.double()).abs().reshape(-1, Hv).sum(0)
+    mag_d = da.double().abs().reshape(-1, Hv).sum(0)
+    for name, got, ref, mag in (("da_log", fused[5], da_log, mag_a), ("ddt_bias", fused[6], ddt, mag_d)):
+        err = ((got.double() - ref.double()).abs() / mag.clamp_min(1e-30)).max().item()
+        assert err <= 1e-5, (name, err)
