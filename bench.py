@@ -296,6 +296,60 @@ def run_neighbours(torch, lib, w, calls=50, warmup=5):
         gbs = nbytes / (us * 1e-6) / 1e9
         out[name] = {"us": us, "bytes_alg": nbytes, "GB/s": gbs, "frac_hbm": gbs / HBM_PEAK_GBS}
     del keep
+    out["prologue_fusion"] = run_prologue_fusion(torch, lib, w, calls=20, warmup=warmup)
+    return out
+
+
+def run_prologue_fusion(torch, lib, w, calls=20, warmup=3):
+    """The recurrence with its prologue, forward and backward, two ways at the workload's shape: the separate
+    prologue pass, chunked forward, chunked backward and prologue backward (four entry points), and the two fused
+    entry points (qb_gdn_fwd_prologue, qb_gdn_bwd_prologue). Microseconds per forward+backward, events around
+    back-to-back calls."""
+    g = torch.Generator(device="cuda").manual_seed(13)
+    r = lambda *shape: torch.randn(*shape, device="cuda", generator=g).to(torch.bfloat16)  # noqa: E731
+    qr, kr, q, k, dq, dk, dqr, dkr = (r(w.B, w.T, w.Hk, w.Dk) for _ in range(8))
+    a, b, beta, dbeta, da, db = (r(w.B, w.T, w.Hv) for _ in range(6))
+    v, dy, y, dv = (r(w.B, w.T, w.Hv, w.Dv) for _ in range(4))
+    ld, dld = (torch.empty(w.B, w.T, w.Hv, device="cuda") for _ in range(2))
+    a_log = torch.rand(w.Hv, device="cuda", generator=g) * 2.7
+    dt_bias = torch.randn(w.Hv, device="cuda", generator=g) * 0.5
+    da_log, ddt = torch.empty_like(a_log), torch.empty_like(dt_bias)
+    desc, keep = lib.make_desc(w.B, w.T, w.Hk, w.Hv, w.Dk, w.Dv, dtype=lib.BF16, design=lib.CHUNKED,
+                               cu_seqlens=w.cu_seqlens)
+    nbd, keep2 = lib.make_desc(w.B, w.T, w.Hk, w.Hv, w.Dk, w.Dv, dtype=lib.BF16)
+    N = w.n_states
+    s_out, ds0 = (torch.empty(N, w.Hv, w.Dv, w.Dk, device="cuda") for _ in range(2))
+    ckpt = torch.empty(lib.ckpt_bytes(desc) // 4, device="cuda")
+    ws = torch.empty(max(lib.workspace_bytes(desc), lib.neighbours_workspace_bytes(nbd), 1), dtype=torch.uint8,
+                     device="cuda")
+    st = torch.cuda.current_stream().cuda_stream
+    P = lambda *ts: [None if t is None else t.data_ptr() for t in ts]  # noqa: E731
+
+    def separate():
+        lib.prologue_fwd(nbd, *P(qr, kr, a, b, a_log, dt_bias, q, k, beta, ld), st)
+        lib.fwd(desc, *P(q, k, v, ld, beta, None, y, s_out, ckpt, ws), st)
+        lib.bwd(desc, *P(q, k, v, ld, beta, ckpt, dy, None, dq, dk, dv, dld, dbeta, ds0, ws), st)
+        lib.prologue_bwd(nbd, *P(qr, kr, a, b, a_log, dt_bias, dq, dk, dbeta, dld, dqr, dkr, da, db, da_log, ddt,
+                                 ws), st)
+
+    def fused():
+        lib.fwd_prologue(desc, *P(qr, kr, v, a, b, a_log, dt_bias, None, q, k, beta, ld, y, s_out, ckpt, ws), st)
+        lib.bwd_prologue(desc, *P(qr, kr, a, b, a_log, dt_bias, q, k, v, beta, ld, ckpt, dy, None, dqr, dkr, dv, da,
+                                  db, da_log, ddt, ds0, ws), st)
+
+    out = {"unit": "us per forward+backward (events around back-to-back calls)"}
+    for name, fn in (("separate", separate), ("fused", fused)):
+        for _ in range(warmup):
+            fn()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(calls):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        out[name] = e0.elapsed_time(e1) * 1e3 / calls
+    out["saved_frac"] = 1.0 - out["fused"] / out["separate"]
+    del keep, keep2
     return out
 
 

@@ -719,16 +719,22 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
   }
 }
 
-// dA_log and ddt_bias [Hv]: the per-(chunk slot, value head) sums of the fused gradient kernel, summed over the slots
-// in order.
+// dA_log and ddt_bias [Hv]: the per-(chunk slot, value head) sums of the fused gradient kernel, summed over the slots.
+// One wave per head: lane l sums slots l, l + 64, ... in order, then the wave's lanes are summed in a fixed order, so
+// the result does not depend on timing.
 __global__ __launch_bounds__(256) void chunk_gate_sums_kernel(const float* part, int64_t NC, int Hv, float* da_log,
                                                               float* ddt_bias) {
-  const int h = blockIdx.x * 256 + threadIdx.x;
+  const int h = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
   if (h >= Hv) return;
   float sa = 0.f, sd = 0.f;
-  for (int64_t c = 0; c < NC; ++c) sa += part[(c * Hv + h) * 2], sd += part[(c * Hv + h) * 2 + 1];
-  da_log[h] = sa;
-  ddt_bias[h] = sd;
+  for (int64_t c = lane; c < NC; c += 64) {
+    const float2 x = *reinterpret_cast<const float2*>(part + (c * Hv + h) * 2);
+    sa += x.x, sd += x.y;
+  }
+  sa = sum16(sa), sd = sum16(sd);
+  sa += __shfl_xor(sa, 16), sd += __shfl_xor(sd, 16);
+  sa += __shfl_xor(sa, 32), sd += __shfl_xor(sd, 32);
+  if (lane == 0) da_log[h] = sa, ddt_bias[h] = sd;
 }
 
 }  // namespace
@@ -755,7 +761,7 @@ hipError_t launch_chunk_bwd_grads(const ChunkArgs& a, bool out_bf16, hipStream_t
 }
 
 hipError_t launch_chunk_gate_sums(const ChunkArgs& a, float* da_log, float* ddt_bias, hipStream_t s) {
-  hipLaunchKernelGGL(chunk_gate_sums_kernel, dim3((a.Hv + 255) / 256), dim3(256), 0, s, a.pro.part, a.lay.NC, a.Hv,
+  hipLaunchKernelGGL(chunk_gate_sums_kernel, dim3((a.Hv + 3) / 4), dim3(256), 0, s, a.pro.part, a.lay.NC, a.Hv,
                      da_log, ddt_bias);
   return hipGetLastError();
 }
