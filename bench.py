@@ -16,7 +16,7 @@ bench's T sweep at the 4B head shape (t_sweep), the one-token inference step (de
 neighbours and the LoRA training step; --path-only leaves those out.
 
 python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--design auto|1|2] [--workload qwen35_4b] [--no-cpu]
-                [--copy-probe-mib N] [--path-only]
+                [--copy-probe-mib N] [--path-only] [--prologue-fusion]
 
 roofline.traffic is the dominant kernel's HBM bytes per launch as rocprofv3 counted them (FETCH_SIZE + WRITE_SIZE,
 each scaled by what the counter reads for a plain device copy of known size), read from profiles/traffic.json
@@ -504,6 +504,9 @@ def main():
     ap.add_argument("--path-only", action="store_true",
                     help="time only the named workload's step (no other shapes, decode, neighbours or LoRA step), as "
                          "profiler counter passes need")
+    ap.add_argument("--prologue-fusion", action="store_true",
+                    help="time only the layer with its prologue, fused and as four separate entry points, at the "
+                         "named workload's shape, and print that object (for kernel traces)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the recurrence shards "
@@ -519,6 +522,10 @@ def main():
     if args.copy_probe_mib > 0:
         copy_probe(torch, args.copy_probe_mib)
     hip = Hip()
+    if args.prologue_fusion:
+        print(json.dumps(run_prologue_fusion(torch, lib, workload(args.workload), calls=args.steps,
+                                             warmup=args.warmup)))
+        return
     designs = [lib.RECURRENT, lib.CHUNKED] if args.design == "auto" else [int(args.design)]
     w = workload(args.workload)
     head, inp = measure_workload(torch, hip, lib, w, designs, args.steps, args.warmup)
