@@ -1,27 +1,30 @@
-// Chunked design, kernel 2: the forward state pass. One block (8 waves) per (sequence, value head, 16 state rows),
+// Chunked design, kernel 2: the forward state pass. One block (12 waves) per (sequence, value head, 16 state rows),
 // sequential over the sequence's chunks; rows of the state evolve independently (reference src/delta_grad.cpp:13),
 // so a 16-row block needs no other block. Per chunk, with S the block's rows of the state at the chunk start, every
 // product is formed transposed, so that a lane holds one position i and four consecutive state rows r (or one
 // state row and four consecutive columns):
 //   write S to LDS and to the chunk's checkpoint slot (the reference's ckpt, src/delta_grad.cpp:172-181)
-//   R^T = V^T - (S K^T) diag(exp G),  Delta^T = R^T Tb^T          waves 0-3, positions 16w..16w+15
+//   R^T = V^T - (S K^T) diag(exp G), and S Q^T                     waves 4-7, positions 16(w-4)..
+//   Delta^T = R^T Tb^T                                             waves 0-3, positions 16w..16w+15
 //   S^T <- exp(G_63) S^T + K^T (D Delta),  D = diag(exp(G_63 - G)) waves 0-3, state columns 32w..32w+31
-//   Y^T = (S Q^T) diag(exp G) + Delta^T P^T                        waves 4-7, positions 16(w-4)..: off the chain
-// Three barriers per chunk. Waves 0-3 carry the recurrence and touch no global memory but the checkpoint stores:
-// waves 4-7 load every input of the next chunk, in two groups issued in the two windows where they would otherwise
-// wait for the chain, keep their own q and P rows in registers, and stage the chain's k rows, packed Tb, v and
-// exp G in LDS (two buffers, by chunk parity); K^T for the state update comes from the staged k rows through the
-// transposing read. The two groups run loops of their own, so that each loop holds only its own group's memory
-// operations: the compiler's waits stay exact and none covers a load issued for a later chunk. All products run
-// on v_mfma_f32_16x16x32_bf16; float32 operands (S, R, Delta, Tb, P) are split into bf16 hi + lo pairs so the state
-// keeps float32 accuracy, while k, q, v enter exactly.
+//   Y^T = (S Q^T) diag(exp G) + Delta^T P^T                        waves 4-7: off the chain
+// Three barriers per chunk. Waves 0-3 carry the state and touch no global memory but the checkpoint stores.
+// Waves 4-7 read S from LDS once for both S K^T and S Q^T, and form y from LDS. Waves 8-11 load every input two chunks ahead, each wave load reading whole cache lines,
+// and stage them in LDS: the chain's k rows, packed Tb, v and exp G (two buffers, by chunk parity), the output
+// group's q rows and packed P (one buffer each); K^T for the state update comes from the staged k rows through the
+// transposing read. The loads and the LDS writes are spread over the chain's phases and the work over two groups,
+// so that neither group, nor the CU's vector memory path or LDS, holds the chain at its barriers. Each group
+// runs a loop of its own, so that each loop holds only its own group's memory operations: the compiler's waits stay
+// exact and none covers a load issued for a later chunk. All products run on v_mfma_f32_16x16x32_bf16; float32
+// operands (S, R, Delta, Tb, P) are split into bf16 hi + lo pairs so the state keeps float32 accuracy, while k, q, v
+// enter exactly.
 #include "chunk_common.h"
 #include "chunk_kernels.h"
 
 namespace qbgdn {
 namespace {
 
-constexpr int kThreads = 512;
+constexpr int kThreads = 768;  // waves 0-3 the chain, 4-7 the output, 8-11 the staging
 // Row pitches (elements) of the swz-placed LDS matrices: 16 x an odd number.
 constexpr int kLS = 144;  // S [16][128]
 constexpr int kLK = 144;  // K [64][128]
@@ -42,6 +45,10 @@ __global__ __launch_bounds__(kThreads) void chunk_fwd_kernel(ChunkArgs a) {
   __shared__ __align__(16) __bf16 Tbp[2][kTbUnits * 8];  // packed Tb (tri_off), hi then lo
   __shared__ __align__(16) bf16_t Vs[2][256 * 8];        // v [64][16] (units 128.. padding)
   __shared__ __align__(16) float Gs[2][256];             // exp G [64], D [64] (the rest padding)
+  // The output group's operands, one buffer each: q rows (written after the chunk's S Q^T, read in the next) and
+  // packed P (written after the previous chunk's y, read in this chunk's).
+  __shared__ __align__(16) __bf16 Qb[kC * kLK];
+  __shared__ __align__(16) __bf16 Pb[kTbUnits * 8];
 
   const int total = a.nblk * a.Hv * a.N;
   const StateItem item = state_item(a.tab, blockIdx.x, a.nblk, a.Hv, a.Hk, total);
@@ -51,33 +58,31 @@ __global__ __launch_bounds__(kThreads) void chunk_fwd_kernel(ChunkArgs a) {
   // The wave index, made visibly uniform so that its branches are scalar and buffer resources stay in scalar
   // registers.
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const bool side = w >= 4;
   const int wp = w & 3, ip = 16 * wp + li;  // position tile; the lane's position in products over positions
-  const int u = tid & 255;                   // waves 4-7: thread index within the loading group
+  const int u = tid & 255;                   // waves 4-11: thread index within the wave's group
   const Seq sq = seq_of(a.tab, n);
   const int nch = (sq.len + kC - 1) / kC;
   OutT* y = static_cast<OutT*>(a.y);
   const int sk = a.Hk * Dk, sv = a.Hv * a.Dv;  // token strides of k/q and v/y
   const int64_t srow = (int64_t(n) * a.Hv + hv) * a.Dv + row0 + li;  // the lane's state row
 
-  // Waves 4-7: one chunk's inputs. q and P rows stay in registers as MFMA operands of the wave's positions (two
-  // register sets in turn); the rest goes to LDS in the same chunk. k, q, v go through buffer resources that end
-  // at the sequence's last row, so rows past it read as zeros without a branch; units past the packed Tb, v or the
-  // two per-position vectors read as zeros and land in padding.
-  struct Own {
-    uint4 q[4];   // q at position ip, columns 32 s + 8 g ..
-    bf16x8 p[4];  // P row ip, columns 8 g.. and 32 + 8 g.., hi and lo
-  };
+  // Waves 8-11 (the staging group) load each chunk's inputs two chunks ahead, in rows of 16-byte units that a wave
+  // reads whole (every cache line it touches in full), and stage them in LDS: k, packed Tb, v and the per-position
+  // vectors for the chain (two buffers, by chunk parity), q and packed P for waves 4-7 (the output group), which
+  // then read no global memory. k, q, v go through buffer resources that end at the sequence's last row, so rows
+  // past it read as zeros without a branch; units past the packed matrices, v or the two per-position vectors read
+  // as zeros, and the waves whose units are all past them (10 and 11) skip those LDS writes.
   struct Stage {
     uint4 k[4];   // k units u + 256 q4: row e / 16, columns 8 (e % 16) ..
+    uint4 q[4];   // q, the same units
     uint4 tb[3];  // packed Tb units u + 256 t
+    uint4 p[3];   // packed P units u + 256 t
     uint4 v;      // v unit u: row u / 2, state rows 8 (u % 2) ..
     float gd;     // exp G_u (u < 64), D_(u - 64) (u < 128)
   };
-  // Two load groups per chunk, each issued where these waves would otherwise wait for the chain: (a) k, packed Tb
-  // and the per-position vectors, staged later in the same chunk; (b) q and P rows for the wave's own products, and
-  // v.
-  auto load_a = [&](Stage& st, int c) {
+  // The loads in two parts, issued in two of the chain's phases so that the CU's vector memory path is not asked
+  // for a whole chunk's bytes at once: k and packed Tb, then q, packed P, v and the per-position vectors.
+  auto load1 = [&](Stage& st, int c) {
     const int64_t slot = sq.slot0 + c, tok = sq.tok0 + int64_t(c) * kC;
     const uint32_t L = uint32_t(min(kC, sq.len - c * kC));
     const Tile* tl = a.tiles + (slot * a.Hv + hv);
@@ -90,88 +95,139 @@ __global__ __launch_bounds__(kThreads) void chunk_fwd_kernel(ChunkArgs a) {
     const auto tr = buffer_rsrc(tl->tb[0], 2 * kTri * 2);
 #pragma unroll
     for (int t = 0; t < 3; ++t) st.tb[t] = buf_ld16(tr, uint32_t(u + 256 * t) * 16);
-    const auto gr = buffer_rsrc(tl->gam, 2 * kC * 4);  // gam, then dec
-    st.gd = buf_ld4(gr, uint32_t(u) * 4);
   };
-  auto load_b = [&](Own& o, Stage& st, int c) {
+  auto load2 = [&](Stage& st, int c) {
     const int64_t slot = sq.slot0 + c, tok = sq.tok0 + int64_t(c) * kC;
     const uint32_t L = uint32_t(min(kC, sq.len - c * kC));
     const Tile* tl = a.tiles + (slot * a.Hv + hv);
     const auto qr = buffer_rsrc(a.q + tok * sk + hk * Dk, L * sk * 2);
 #pragma unroll
-    for (int s = 0; s < 4; ++s) o.q[s] = buf_ld16(qr, uint32_t(ip * sk + 32 * s + 8 * g) * 2);
+    for (int q4 = 0; q4 < 4; ++q4) {
+      const int e = u + 256 * q4;
+      st.q[q4] = buf_ld16(qr, uint32_t((e >> 4) * sk + (e & 15) * 8) * 2);
+    }
+    const auto gr = buffer_rsrc(tl->gam, 2 * kC * 4);  // gam, then dec
+    st.gd = buf_ld4(gr, uint32_t(u) * 4);
     const auto vr = buffer_rsrc(a.v + tok * sv + hv * a.Dv + row0, L * sv * 2);
     st.v = buf_ld16(vr, u < 128 ? uint32_t((u >> 1) * sv + 8 * (u & 1)) * 2 : 0x80000000u);
     const auto pr = buffer_rsrc(tl->p[0], 2 * kTri * 2);  // hi, then lo
-    o.p[0] = tri_ld8(pr, 0, ip, 8 * g), o.p[1] = tri_ld8(pr, kTri, ip, 8 * g);
-    o.p[2] = tri_ld8(pr, 0, ip, 32 + 8 * g), o.p[3] = tri_ld8(pr, kTri, ip, 32 + 8 * g);  // zeros for rows < 32
+#pragma unroll
+    for (int t = 0; t < 3; ++t) st.p[t] = buf_ld16(pr, uint32_t(u + 256 * t) * 16);
   };
-  auto stage_a = [&](const Stage& st, int b) {
+  // k and packed Tb, then v, the per-position vectors and q: to buffer b of the chain and to Qb.
+  auto stage1 = [&](const Stage& st, int b) {
 #pragma unroll
     for (int q4 = 0; q4 < 4; ++q4) {
       const int e = u + 256 * q4;
       *reinterpret_cast<uint4*>(Kb[b] + swz(e >> 4, (e & 15) * 8, kLK)) = st.k[q4];
     }
 #pragma unroll
-    for (int t = 0; t < 3; ++t) *reinterpret_cast<uint4*>(Tbp[b] + 8 * (u + 256 * t)) = st.tb[t];
-    Gs[b][u] = st.gd;
+    for (int t = 0; t < 2; ++t) *reinterpret_cast<uint4*>(Tbp[b] + 8 * (u + 256 * t)) = st.tb[t];
+    if (w < 10) *reinterpret_cast<uint4*>(Tbp[b] + 8 * (u + 512)) = st.tb[2];  // units 640.. are padding
   };
-  auto stage_b = [&](const Stage& st, int b) { *reinterpret_cast<uint4*>(Vs[b] + 8 * u) = st.v; };
+  auto stage2 = [&](const Stage& st, int b) {
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4) {
+      const int e = u + 256 * q4;
+      *reinterpret_cast<uint4*>(Qb + swz(e >> 4, (e & 15) * 8, kLK)) = st.q[q4];
+    }
+    if (w < 10) {  // units 128.. are padding
+      Gs[b][u] = st.gd;
+      *reinterpret_cast<uint4*>(Vs[b] + 8 * u) = st.v;
+    }
+  };
+  auto stage_p = [&](const Stage& st) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t) *reinterpret_cast<uint4*>(Pb + 8 * (u + 256 * t)) = st.p[t];
+    if (w < 10) *reinterpret_cast<uint4*>(Pb + 8 * (u + 512)) = st.p[2];
+  };
 
-  // The two wave groups run loops of their own, with the same three barriers per chunk (a barrier counts waves,
-  // not program points): each loop then holds only its own group's memory operations, and the compiler's waits in
-  // it are exact.
-  if (side) {
-    auto step = [&](int c, Own& f, Own& nxt, Stage& st) {
-      const int b = c & 1, cn = min(c + 1, nch - 1);  // the last chunk loads itself again rather than branch
+  // Each group runs a loop of its own with the chain's three barriers per chunk (a barrier counts waves, not program
+  // points): each loop then holds only its own group's memory operations, and the compiler's waits in it are exact.
+  if (w >= 8) {
+    // Two register sets take turns, cur holding chunk c (staged but for its P) and nxt chunk c + 1, and the LDS
+    // writes go where the chain's phases leave the LDS least busy. After the chain's first barrier of chunk c:
+    // chunk c + 1's k and Tb to the chain's other LDS buffers (their last readers were chunk c - 1's), and the first
+    // part of chunk c + 2 into cur (two chunks ahead, which covers the memory latency). After the second: chunk c's
+    // P to Pb (chunk c - 1's y is formed) and the second part of chunk c + 2. After the third: chunk c + 1's q to Qb
+    // (chunk c's S Q^T is done), its v and per-position vectors.
+    auto step = [&](int c, Stage& cur, Stage& nxt) {
+      const int c2 = min(c + 2, nch - 1);  // the last chunks load the last again rather than branch
+      const int b1 = (c & 1) ^ 1;
       __syncthreads();
-      load_a(st, cn);
-      f32x4 xh = zero4(), xl = zero4();  // the hi and lo halves of S in two independent chains
+      load1(cur, c2);
+      stage1(nxt, b1);
+      __syncthreads();
+      stage_p(cur);
+      load2(cur, c2);
+      __syncthreads();
+      stage2(nxt, b1);
+    };
+    Stage sa, sb;
+    if (nch > 0) {
+      const int c1 = min(1, nch - 1);
+      load1(sa, 0);
+      load2(sa, 0);
+      load1(sb, c1);
+      load2(sb, c1);
+      stage1(sa, 0);
+      stage2(sa, 0);
+    }
+    int c = 0;
+    for (; c + 1 < nch; c += 2) {
+      step(c, sa, sb);
+      step(c + 1, sb, sa);
+    }
+    if (c < nch) step(c, sa, sb);
+    return;
+  }
+  if (w >= 4) {
+    for (int c = 0; c < nch; ++c) {
+      const int b = c & 1;
+      __syncthreads();
+      // S K^T and S Q^T at state rows 4g + jj, position ip, from one read of S (hi and lo); then
+      // R^T = V^T - (S K^T) diag(exp G), which the chain's next phase reads.
+      f32x4 kh = zero4(), kl = zero4(), xh = zero4(), xl = zero4();
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        const int at = swz(li, 32 * s + 8 * g, kLS);
-        const bf16x8 bq = __builtin_bit_cast(bf16x8, f.q[s]);
-        xh = mma(xh, lds8(Sm[0] + at), bq);
-        xl = mma(xl, lds8(Sm[1] + at), bq);
+        const int at = swz(li, 32 * s + 8 * g, kLS), ak = swz(ip, 32 * s + 8 * g, kLK);
+        const bf16x8 sh = lds8(Sm[0] + at), sl = lds8(Sm[1] + at);
+        const bf16x8 bk = lds8(Kb[b] + ak), bq = lds8(Qb + ak);
+        kh = mma(kh, sh, bk);
+        kl = mma(kl, sl, bk);
+        xh = mma(xh, sh, bq);
+        xl = mma(xl, sl, bq);
+      }
+      const float gam = Gs[b][ip];
+      {
+        const uint2 v = *reinterpret_cast<const uint2*>(Vs[b] + 16 * ip + 4 * g);
+        const f32x4 ks = kh + kl;
+        const f32x4 r = {bf16_lo(v.x) - gam * ks[0], bf16_hi(v.x) - gam * ks[1], bf16_lo(v.y) - gam * ks[2],
+                         bf16_hi(v.y) - gam * ks[3]};
+        put4(Rm[0], Rm[1], swz(ip, 4 * g, kLP), r);
       }
       const f32x4 xs = xh + xl;
-      const float gam = Gs[b][ip];
       __syncthreads();
-      // While the chain computes Delta: the second load group, and the first one to the other LDS buffers (their
-      // last readers were the previous chunk's).
-      load_b(nxt, st, cn);
-      stage_a(st, b ^ 1);
       __syncthreads();
-      // Y^T = (S Q^T) diag(exp G) + Delta^T P^T at state rows 4g + jj, position ip.
+      // Y^T = (S Q^T) diag(exp G) + Delta^T P^T at state rows 4g + jj, position ip; P rows ip from the packed copy
+      // (blocks above the diagonal are zeros).
       f32x4 yv = gam * xs;
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
+        const int c8 = 32 * s + 8 * g;
+        const bool in = (c8 >> 4) <= wp;
+        const int at = in ? tri_off(ip, c8) : 0;
+        const bf16x8 z = {};
+        const bf16x8 ph = lds8(Pb + at), pl = lds8(Pb + kTri + at);
         const Split8 A{lds_tr8s(Dm[0] + 32 * s * kLP, kLP, lane), lds_tr8s(Dm[1] + 32 * s * kLP, kLP, lane)};
-        yv = mma3(yv, A, Split8{f.p[2 * s], f.p[2 * s + 1]});
+        yv = mma3(yv, A, Split8{in ? ph : z, in ? pl : z});
       }
       const int64_t tok = sq.tok0 + int64_t(c) * kC;
       const uint32_t L = uint32_t(min(kC, sq.len - c * kC));
       // Positions past the chunk's end fall past the resource and are dropped.
       const auto yr = buffer_rsrc(y + tok * sv + hv * a.Dv + row0, L * sv * uint32_t(sizeof(OutT)));
       BufIO<OutT>::st4(yr, uint32_t(ip * sv + 4 * g), yv);
-      stage_b(st, b ^ 1);
-    };
-    // Chunk 0's inputs, then the chunks in pairs: chunk c computes from one register set while chunk c + 1 loads
-    // into the other.
-    Own oa, ob;
-    Stage st;
-    if (nch > 0) {
-      load_a(st, 0);
-      load_b(oa, st, 0);
-      stage_a(st, 0);
-      stage_b(st, 0);
     }
-    int c = 0;
-    for (; c + 1 < nch; c += 2) {
-      step(c, oa, ob, st);
-      step(c + 1, ob, oa, st);
-    }
-    if (c < nch) step(c, oa, ob, st);
     return;
   }
 
@@ -198,26 +254,8 @@ __global__ __launch_bounds__(kThreads) void chunk_fwd_kernel(ChunkArgs a) {
         BufIO<float>::st4(ck, uint32_t(li * Dk + col), S[t]);
       }
     }
-    __syncthreads();
-
-    // S K^T (k rows from LDS): state rows 4g + jj, position ip; then R[ip][4g + jj].
-    const float gam = Gs[b][ip];
-    const uint2 v = *reinterpret_cast<const uint2*>(Vs[b] + 16 * ip + 4 * g);
-    f32x4 xh = zero4(), xl = zero4();  // the hi and lo halves of S in two independent chains
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const int at = swz(li, 32 * s + 8 * g, kLS);
-      const bf16x8 bk = lds8(Kb[b] + swz(ip, 32 * s + 8 * g, kLK));
-      xh = mma(xh, lds8(Sm[0] + at), bk);
-      xl = mma(xl, lds8(Sm[1] + at), bk);
-    }
-    {
-      const f32x4 xs = xh + xl;
-      const f32x4 r = {bf16_lo(v.x) - gam * xs[0], bf16_hi(v.x) - gam * xs[1], bf16_lo(v.y) - gam * xs[2],
-                       bf16_hi(v.y) - gam * xs[3]};
-      put4(Rm[0], Rm[1], swz(ip, 4 * g, kLP), r);
-    }
-    __syncthreads();
+    __syncthreads();  // S in LDS: the output group forms R from it
+    __syncthreads();  // R in LDS
 
     {  // Delta^T = R^T Tb^T: A = R^T through the transposing read, B = Tb rows ip from the packed copy
       f32x4 d2[2];  // the two k steps in independent chains
