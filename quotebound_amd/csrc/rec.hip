@@ -38,11 +38,23 @@ struct Layout {
 // Rows per block for a key width (the host side's view of the same layout).
 inline int rec_rows(int Dk) { return Dk <= 128 ? Layout<16>::kRows : Layout<32>::kRows; }
 
+// x plus x of lane ^ 16 (swap16_sum) or lane ^ 32 (swap32_sum), each one gfx950 lane swap and an add, no LDS:
+// v_permlane16_swap(x, x) leaves (x, x of lane + 16) in the low 16 lanes of every 32 and (x of lane - 16, x) in the
+// high ones, so the two lanes of a pair add the same two values in the same order and get the same bits.
+__device__ __forceinline__ float swap16_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float swap32_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 // Sum over each group of LPR lanes; every lane of the group gets the same bits.
 template <int LPR>
 __device__ __forceinline__ float sum_lanes(float x) {
   x = sum16(x);
-  if constexpr (LPR == 32) x += __shfl_xor(x, 16);
+  if constexpr (LPR == 32) x = swap16_sum(x);
   return x;
 }
 
@@ -162,6 +174,7 @@ __global__ __launch_bounds__(kThreads) void rec_fwd_kernel(RecFwdArgs a) {
       if (cl == 0) KQs[tt] = kq;
     }
     __syncthreads();
+#pragma unroll 2
     for (int tt = 0; tt < L; ++tt) {
       float kk[NPT], qq[NPT];
 #pragma unroll
@@ -176,7 +189,7 @@ __global__ __launch_bounds__(kThreads) void rec_fwd_kernel(RecFwdArgs a) {
       const float yv = gt * pb + d * KQs[tt];
 #pragma unroll
       for (int i = 0; i < NPT; ++i) s[i] = gt * s[i] + d * kk[i];
-      if (cl == 0) Ys[tt][rl] = yv;
+      Ys[tt][rl] = yv;  // every lane of the row holds the same bits: a store without a branch
       if (kKeepRows && live) {  // the state after this token
         float* dst = a.p.rows + ((tok + tt) * a.Hv + hv) * SS + int64_t(row) * Dk + cl * NPT;
 #pragma unroll
@@ -205,16 +218,19 @@ __device__ __forceinline__ void wave_rows_sum(const float* p, float* dst, int la
   if constexpr (LPR == 16 && NPT % 4 == 0) {
     constexpr int H = NPT / 2, Q = NPT / 4;
     const bool h32 = lane & 32, h16 = lane & 16;
+    // Each exchange is one gfx950 lane swap (VALU, no LDS): v_permlane32_swap(a, b) leaves (a, a of lane + 32) in
+    // lanes 0-31 and (b of lane - 32, b) in lanes 32-63, so the sum of its two results is, in every lane, the lane's
+    // kept value plus its partner's sent one; v_permlane16_swap does the same between the 16-lane halves of each 32.
     float w[H], x[Q];
 #pragma unroll
     for (int j = 0; j < H; ++j) {
-      const float send = h32 ? p[j] : p[j + H], keep = h32 ? p[j + H] : p[j];
-      w[j] = keep + __shfl_xor(send, 32);
+      const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(p[j]), __float_as_uint(p[j + H]), false, false);
+      w[j] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
     }
 #pragma unroll
     for (int j = 0; j < Q; ++j) {
-      const float send = h16 ? w[j] : w[j + Q], keep = h16 ? w[j + Q] : w[j];
-      x[j] = keep + __shfl_xor(send, 16);
+      const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(w[j]), __float_as_uint(w[j + Q]), false, false);
+      x[j] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
     }
     const int base = cl * NPT + (h16 ? Q : 0) + (h32 ? H : 0);
 #pragma unroll
@@ -222,9 +238,8 @@ __device__ __forceinline__ void wave_rows_sum(const float* p, float* dst, int la
   } else {
 #pragma unroll
     for (int j = 0; j < NPT; ++j) {
-      float x = p[j];
-      x += __shfl_xor(x, 32);
-      if constexpr (LPR == 16) x += __shfl_xor(x, 16);
+      float x = swap32_sum(p[j]);
+      if constexpr (LPR == 16) x = swap16_sum(x);
       if (lane < LPR) dst[cl * NPT + j] = x;
     }
   }
@@ -306,7 +321,7 @@ __global__ __launch_bounds__(kThreads) void rec_bwd_kernel(RecBwdArgs a) {
           const float d = Bs[tt] * e;
 #pragma unroll
           for (int i = 0; i < NPT; ++i) st[i] = gt * st[i] + d * kk[i];
-          if (cl == 0) Ds[tt][rl] = d, Es[tt][rl] = e;
+          Ds[tt][rl] = d, Es[tt][rl] = e;  // row-uniform values, stored by every lane of the row
         }
       }
     }
@@ -366,7 +381,7 @@ __global__ __launch_bounds__(kThreads) void rec_bwd_kernel(RecBwdArgs a) {
           ds[i] *= gt;
         }
         dg = sum_lanes<LPR>(dg);
-        if (cl == 0) rowv[j][0][rl] = bt * dd, rowv[j][1][rl] = dd * e, rowv[j][2][rl] = dg;
+        rowv[j][0][rl] = bt * dd, rowv[j][1][rl] = dd * e, rowv[j][2][rl] = dg;  // row-uniform, every lane
         wave_rows_sum<NPT, LPR>(pq, red[j][wave], lane);
         wave_rows_sum<NPT, LPR>(pk, red[j][wave] + Dk, lane);
       }
