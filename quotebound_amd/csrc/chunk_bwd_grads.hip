@@ -403,8 +403,7 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
       }
       {
         float v = sum16(sds);
-        v += __shfl_xor(v, 16);
-        v += __shfl_xor(v, 32);
+        v = swap32_sum(swap16_sum(v));
         if ((tid & 63) == 0) red[tid >> 6] = v;
       }
       __syncthreads();
@@ -458,8 +457,7 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
           put4(TbL[0], TbL[1], at, pm[0], pm[1], pm[2], pm[3]);
           put4(PL[0], PL[1], at, db[0], db[1], db[2], db[3]);
         }
-        prow += __shfl_xor(prow, 16);
-        prow += __shfl_xor(prow, 32);
+        prow = swap32_sum(swap16_sum(prow));
         if (g == 0) x2r[hw][ip] = prow;
       }
       __syncthreads();
@@ -577,8 +575,7 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
             kkt[jj] = bet[pr] * dae;
           }
           put4(sb + eKh, sb + eKl, swz(mcol, i0, kLT), kkt[0], kkt[1], kkt[2], kkt[3]);
-          colp += __shfl_xor(colp, 16);
-          colp += __shfl_xor(colp, 32);
+          colp = swap32_sum(swap16_sum(colp));
           if (g == 0) x1cp[pw][mcol] = colp;
         }
 #pragma unroll
@@ -609,8 +606,7 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
         const int t = tid;
         const float hs = hpos[0][t] + hpos[1][t];
         float hsum = sum16(hs);
-        hsum += __shfl_xor(hsum, 16);
-        hsum += __shfl_xor(hsum, 32);
+        hsum = swap32_sum(swap16_sum(hsum));
         float sds_all = 0.f;
 #pragma unroll
         for (int u = 0; u < kThreads / 64; ++u) sds_all += red[u];
@@ -637,8 +633,7 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
             a.pro.db[g0 + gi] = f32_to_bf16(db);
           }
           pa = sum16(pa), pd = sum16(pd);
-          pa += __shfl_xor(pa, 16), pd += __shfl_xor(pd, 16);
-          pa += __shfl_xor(pa, 32), pd += __shfl_xor(pd, 32);
+          pa = swap32_sum(swap16_sum(pa)), pd = swap32_sum(swap16_sum(pd));
           if (t == 0) a.pro.part[(slot * a.Hv + hv) * 2] = pa, a.pro.part[(slot * a.Hv + hv) * 2 + 1] = pd;
         } else if (t < L) {
           const int64_t g0 = tok * a.Hv + hv;
@@ -732,8 +727,7 @@ __global__ __launch_bounds__(256) void chunk_gate_sums_kernel(const float* part,
     sa += x.x, sd += x.y;
   }
   sa = sum16(sa), sd = sum16(sd);
-  sa += __shfl_xor(sa, 16), sd += __shfl_xor(sd, 16);
-  sa += __shfl_xor(sa, 32), sd += __shfl_xor(sd, 32);
+  sa = swap32_sum(swap16_sum(sa)), sd = swap32_sum(swap16_sum(sd));
   if (lane == 0) da_log[h] = sa, ddt_bias[h] = sd;
 }
 

@@ -125,6 +125,19 @@ __device__ __forceinline__ float sum16(float x) {
   return x;
 }
 
+// x plus x of lane ^ 16 (swap16_sum) or lane ^ 32 (swap32_sum), each one gfx950 lane swap and an add, no LDS:
+// v_permlane16_swap(x, x) leaves (x, x of lane + 16) in the low 16 lanes of every 32 and (x of lane - 16, x) in the
+// high ones (v_permlane32_swap likewise for the two 32-lane halves), so the two lanes of a pair add the same two
+// values and, addition being commutative, get the same bits as x + __shfl_xor(x, 16 or 32) would give.
+__device__ __forceinline__ float swap16_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float swap32_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 // Blocks are dispatched round-robin over the MI355X's 8 XCDs (block id runs on XCD id % 8), each with its own
 // L2. This gives XCD x a contiguous range of work items, so neighbouring items (which read the same key head)
 // share an L2. A bijection on [0, n).

@@ -47,8 +47,8 @@ __device__ __forceinline__ float group_sum(float x) {
   x += dpp_mov<0x4e>(x);   // quad_perm [2,3,0,1]
   x += dpp_mov<0x141>(x);  // row_half_mirror: the two quads of each 8 lanes
   if constexpr (L >= 16) x += dpp_mov<0x140>(x);  // row_mirror: the two halves of each 16 lanes
-  if constexpr (L >= 32) x += __shfl_xor(x, 16);
-  if constexpr (L >= 64) x += __shfl_xor(x, 32);
+  if constexpr (L >= 32) x = swap16_sum(x);
+  if constexpr (L >= 64) x = swap32_sum(x);
   return x;
 }
 
@@ -269,8 +269,11 @@ __global__ __launch_bounds__(1024) void epilogue_bwd_kernel(const T* __restrict_
     }
   }
 #pragma unroll
-  for (int e = 0; e < kVec; ++e)
-    for (int s = RL::L; s < 64; s <<= 1) pw[e] += __shfl_xor(pw[e], s);
+  for (int e = 0; e < kVec; ++e) {  // the sum over the wave's row slots: lanes l ^ L, l ^ 2L, ...
+    if constexpr (RL::L < 16) pw[e] += __shfl_xor(pw[e], 8);
+    if constexpr (RL::L < 32) pw[e] = swap16_sum(pw[e]);
+    pw[e] = swap32_sum(pw[e]);
+  }
   if (lane < RL::L) {
 #pragma unroll
     for (int e = 0; e < kVec; ++e) acc[wv][lane * kVec + e] = pw[e];

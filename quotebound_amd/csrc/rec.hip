@@ -38,18 +38,6 @@ struct Layout {
 // Rows per block for a key width (the host side's view of the same layout).
 inline int rec_rows(int Dk) { return Dk <= 128 ? Layout<16>::kRows : Layout<32>::kRows; }
 
-// x plus x of lane ^ 16 (swap16_sum) or lane ^ 32 (swap32_sum), each one gfx950 lane swap and an add, no LDS:
-// v_permlane16_swap(x, x) leaves (x, x of lane + 16) in the low 16 lanes of every 32 and (x of lane - 16, x) in the
-// high ones, so the two lanes of a pair add the same two values in the same order and get the same bits.
-__device__ __forceinline__ float swap16_sum(float x) {
-  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-__device__ __forceinline__ float swap32_sum(float x) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-
 // Sum over each group of LPR lanes; every lane of the group gets the same bits.
 template <int LPR>
 __device__ __forceinline__ float sum_lanes(float x) {
