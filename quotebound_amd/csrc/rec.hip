@@ -375,16 +375,21 @@ __global__ __launch_bounds__(kThreads) void rec_bwd_kernel(RecBwdArgs a) {
       }
       __syncthreads();
       const int Ls = min(kSub, L - ts);
-      for (int e = tid; e < Ls * 2 * Dk; e += kThreads) {
-        const int j = e / (2 * Dk), col = e % (2 * Dk);
-        float acc = 0.f;
+      // A fixed trip count, unrolled, so that every pass's LDS reads issue together rather than one round trip per
+      // pass; passes past the sub-chunk's last step store nothing.
+      constexpr int kPasses = (kSub * 2 * Dk + kThreads - 1) / kThreads;
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) acc += red[j][w][col];
-        const int64_t at = (((tok + ts + j) * a.Hv + hv) * a.nblk + it.blk) * Dk;
-        if (col < Dk)
-          a.dq_part[at + col] = acc;
-        else
-          a.dk_part[at + col - Dk] = acc;
+      for (int pss = 0; pss < kPasses; ++pss) {
+        const int e = tid + pss * kThreads;
+        if (e < Ls * 2 * Dk) {
+          const int j = e / (2 * Dk), col = e % (2 * Dk);
+          float acc = 0.f;
+#pragma unroll
+          for (int w = 0; w < kWaves; ++w) acc += red[j][w][col];
+          const int64_t at = (((tok + ts + j) * a.Hv + hv) * a.nblk + it.blk) * Dk;
+          float* dst = col < Dk ? a.dq_part + at + col : a.dk_part + at + col - Dk;
+          *dst = acc;
+        }
       }
       for (int e = tid; e < Ls * kRows; e += kThreads) {
         const int j = e / kRows, r = e % kRows;
