@@ -415,25 +415,36 @@ __global__ __launch_bounds__(kThreads) void rec_bwd_kernel(RecBwdArgs a) {
 // src/delta_grad.cpp:194-198 sums row blocks first; both orders are fixed). dg, dbeta [BT, Hv] likewise over row
 // blocks; dg becomes d/d(log-decay) when g_is_log.
 template <typename OutT>
-__global__ __launch_bounds__(128) void rec_reduce_kernel(const float* dq_part, const float* dk_part,
+__global__ __launch_bounds__(256) void rec_reduce_kernel(const float* dq_part, const float* dk_part,
                                                          const float* dg_part, const float* db_part, const float* g,
                                                          OutT* dq, OutT* dk, float* dg, OutT* dbeta, int Hk, int Hv,
-                                                         int Dk, int nblk, int g_is_log) {
-  const int64_t tok = blockIdx.x;
-  const int hk = blockIdx.y, grp = Hv / Hk;
-  for (int col = threadIdx.x; col < Dk; col += blockDim.x) {
-    float aq = 0.f, ak = 0.f;
-    for (int h = 0; h < grp; ++h)
-      for (int b = 0; b < nblk; ++b) {
-        const int64_t at = ((tok * Hv + hk * grp + h) * nblk + b) * Dk + col;
-        aq += dq_part[at];
-        ak += dk_part[at];
-      }
-    IO<OutT>::st(dq, (tok * Hk + hk) * Dk + col, aq);
-    IO<OutT>::st(dk, (tok * Hk + hk) * Dk + col, ak);
+                                                         int Dk, int nblk, int g_is_log, int64_t items) {
+  // Eight (token, key head) items per block, 32 lanes each, four columns per lane: an item's partials are
+  // grp * nblk contiguous rows of Dk floats, read as 16-byte units and summed in row order (value head, then row
+  // block), the fixed order of the reference (src/delta_grad.cpp:194-198 over row blocks).
+  const int64_t item = int64_t(blockIdx.x) * 8 + (threadIdx.x >> 5);
+  if (item >= items) return;
+  const int l32 = threadIdx.x & 31;
+  const int64_t tok = item / Hk;
+  const int hk = int(item % Hk), grp = Hv / Hk, np = grp * nblk;
+  const int64_t base = (tok * Hv + int64_t(hk) * grp) * nblk;  // the item's first partial row
+  for (int c = 4 * l32; c < Dk; c += 128) {
+    float4 aq = {0.f, 0.f, 0.f, 0.f}, ak = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 8
+    for (int pr = 0; pr < np; ++pr) {
+      const float4 xq = *reinterpret_cast<const float4*>(dq_part + (base + pr) * Dk + c);
+      const float4 xk = *reinterpret_cast<const float4*>(dk_part + (base + pr) * Dk + c);
+      aq.x += xq.x, aq.y += xq.y, aq.z += xq.z, aq.w += xq.w;
+      ak.x += xk.x, ak.y += xk.y, ak.z += xk.z, ak.w += xk.w;
+    }
+    const int64_t o = (tok * Hk + hk) * Dk + c;
+    IO<OutT>::st(dq, o, aq.x), IO<OutT>::st(dq, o + 1, aq.y), IO<OutT>::st(dq, o + 2, aq.z);
+    IO<OutT>::st(dq, o + 3, aq.w);
+    IO<OutT>::st(dk, o, ak.x), IO<OutT>::st(dk, o + 1, ak.y), IO<OutT>::st(dk, o + 2, ak.z);
+    IO<OutT>::st(dk, o + 3, ak.w);
   }
-  if (threadIdx.x < grp) {
-    const int hv = hk * grp + threadIdx.x;
+  if (l32 < grp) {
+    const int hv = hk * grp + l32;
     float ag = 0.f, ab = 0.f;
     for (int b = 0; b < nblk; ++b) {
       ag += dg_part[(tok * Hv + hv) * nblk + b];
@@ -526,10 +537,11 @@ hipError_t launch_bwd(const Problem& p, const BwdPtrs& ptrs, void* ws, hipStream
     tr.mark();
     return hipSuccess;
   }
-  const dim3 rgrid(static_cast<unsigned>(p.BT), p.Hk);
-  hipLaunchKernelGGL((rec_reduce_kernel<OutT>), rgrid, dim3(128), 0, s, w.dq_part, w.dk_part, w.dg_part, w.db_part,
-                     ptrs.g, static_cast<OutT*>(ptrs.dq), static_cast<OutT*>(ptrs.dk), ptrs.dg,
-                     static_cast<OutT*>(ptrs.dbeta), p.Hk, p.Hv, p.Dk, a.nblk, p.g_is_log);
+  const int64_t items = p.BT * p.Hk;
+  hipLaunchKernelGGL((rec_reduce_kernel<OutT>), dim3(static_cast<unsigned>((items + 7) / 8)), dim3(256), 0, s,
+                     w.dq_part, w.dk_part, w.dg_part, w.db_part, ptrs.g, static_cast<OutT*>(ptrs.dq),
+                     static_cast<OutT*>(ptrs.dk), ptrs.dg, static_cast<OutT*>(ptrs.dbeta), p.Hk, p.Hv, p.Dk, a.nblk,
+                     p.g_is_log, items);
   tr.mark();
   return hipGetLastError();
 }
