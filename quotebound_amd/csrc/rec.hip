@@ -46,6 +46,16 @@ __device__ __forceinline__ float sum_lanes(float x) {
   return x;
 }
 
+// The state column of lane cl's i-th value. With NPT a multiple of 4 a lane holds runs of four columns, the LPR
+// lanes of a row side by side in each run: a 16-byte LDS read of a step's k or q row by the row's lanes then covers
+// every bank once (a lane's NPT contiguous columns would put lanes 8 apart on the same banks). Otherwise a lane
+// holds NPT contiguous columns.
+template <int NPT, int LPR>
+__device__ __forceinline__ int col_of(int cl, int i) {
+  if constexpr (NPT % 4 == 0) return (i >> 2) * (4 * LPR) + 4 * cl + (i & 3);
+  return cl * NPT + i;
+}
+
 struct RecFwdArgs {
   FwdPtrs p;
   int Hk, Hv, Dv, g_is_log, nblk, total;
@@ -133,20 +143,20 @@ __global__ __launch_bounds__(kThreads) void rec_fwd_kernel(RecFwdArgs a) {
   const InT* beta = static_cast<const InT*>(a.p.beta);
   OutT* y = static_cast<OutT*>(a.p.y);
   const int64_t SS = int64_t(a.Dv) * Dk;
-  const int64_t srow = (int64_t(it.n) * a.Hv + hv) * SS + int64_t(row) * Dk + cl * NPT;
+  const int64_t srow = (int64_t(it.n) * a.Hv + hv) * SS + int64_t(row) * Dk;  // the row's first column
 
   float s[NPT];
 #pragma unroll
-  for (int i = 0; i < NPT; ++i) s[i] = (live && a.p.s0) ? a.p.s0[srow + i] : 0.f;
+  for (int i = 0; i < NPT; ++i) s[i] = (live && a.p.s0) ? a.p.s0[srow + col_of<NPT, LPR>(cl, i)] : 0.f;
 
   const int nch = (sq.len + kChunk - 1) / kChunk;
   for (int c = 0; c < nch; ++c) {
     const int t0 = c * kChunk, L = min(kChunk, sq.len - t0);
     const int64_t tok = sq.tok0 + t0;
     if (a.p.ckpt && live) {
-      float* dst = a.p.ckpt + ((sq.slot0 + c) * a.Hv + hv) * SS + int64_t(row) * Dk + cl * NPT;
+      float* dst = a.p.ckpt + ((sq.slot0 + c) * a.Hv + hv) * SS + int64_t(row) * Dk;
 #pragma unroll
-      for (int i = 0; i < NPT; ++i) dst[i] = s[i];
+      for (int i = 0; i < NPT; ++i) dst[col_of<NPT, LPR>(cl, i)] = s[i];
     }
     __syncthreads();  // the previous chunk's LDS readers are done
     stage_kq<Dk>(Ks, Qs, (const InT*)k, (const InT*)q, tok, a.Hk, hk, L);
@@ -157,7 +167,7 @@ __global__ __launch_bounds__(kThreads) void rec_fwd_kernel(RecFwdArgs a) {
     for (int tt = tid / LPR; tt < kChunk; tt += kThreads / LPR) {
       float kq = 0.f;
 #pragma unroll
-      for (int i = 0; i < NPT; ++i) kq += Ks[tt][cl * NPT + i] * Qs[tt][cl * NPT + i];
+      for (int i = 0; i < NPT; ++i) kq += Ks[tt][col_of<NPT, LPR>(cl, i)] * Qs[tt][col_of<NPT, LPR>(cl, i)];
       kq = sum_lanes<LPR>(kq);
       if (cl == 0) KQs[tt] = kq;
     }
@@ -166,7 +176,7 @@ __global__ __launch_bounds__(kThreads) void rec_fwd_kernel(RecFwdArgs a) {
     for (int tt = 0; tt < L; ++tt) {
       float kk[NPT], qq[NPT];
 #pragma unroll
-      for (int i = 0; i < NPT; ++i) kk[i] = Ks[tt][cl * NPT + i], qq[i] = Qs[tt][cl * NPT + i];
+      for (int i = 0; i < NPT; ++i) kk[i] = Ks[tt][col_of<NPT, LPR>(cl, i)], qq[i] = Qs[tt][col_of<NPT, LPR>(cl, i)];
       float pa = 0.f, pb = 0.f;
 #pragma unroll
       for (int i = 0; i < NPT; ++i) pa += s[i] * kk[i], pb += s[i] * qq[i];
@@ -179,9 +189,9 @@ __global__ __launch_bounds__(kThreads) void rec_fwd_kernel(RecFwdArgs a) {
       for (int i = 0; i < NPT; ++i) s[i] = gt * s[i] + d * kk[i];
       Ys[tt][rl] = yv;  // every lane of the row holds the same bits: a store without a branch
       if (kKeepRows && live) {  // the state after this token
-        float* dst = a.p.rows + ((tok + tt) * a.Hv + hv) * SS + int64_t(row) * Dk + cl * NPT;
+        float* dst = a.p.rows + ((tok + tt) * a.Hv + hv) * SS + int64_t(row) * Dk;
 #pragma unroll
-        for (int i = 0; i < NPT; ++i) dst[i] = s[i];
+        for (int i = 0; i < NPT; ++i) dst[col_of<NPT, LPR>(cl, i)] = s[i];
       }
     }
     __syncthreads();
@@ -192,7 +202,7 @@ __global__ __launch_bounds__(kThreads) void rec_fwd_kernel(RecFwdArgs a) {
   }
   if (a.p.s_out && live) {
 #pragma unroll
-    for (int i = 0; i < NPT; ++i) a.p.s_out[srow + i] = s[i];
+    for (int i = 0; i < NPT; ++i) a.p.s_out[srow + col_of<NPT, LPR>(cl, i)] = s[i];
   }
 }
 
@@ -220,15 +230,15 @@ __device__ __forceinline__ void wave_rows_sum(const float* p, float* dst, int la
       const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(w[j]), __float_as_uint(w[j + Q]), false, false);
       x[j] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
     }
-    const int base = cl * NPT + (h16 ? Q : 0) + (h32 ? H : 0);
+    const int i0 = (h16 ? Q : 0) + (h32 ? H : 0);  // the lane's finished values: i0 .. i0 + Q - 1
 #pragma unroll
-    for (int j = 0; j < Q; ++j) dst[base + j] = x[j];
+    for (int j = 0; j < Q; ++j) dst[col_of<NPT, LPR>(cl, i0 + j)] = x[j];
   } else {
 #pragma unroll
     for (int j = 0; j < NPT; ++j) {
       float x = swap32_sum(p[j]);
       if constexpr (LPR == 16) x = swap16_sum(x);
-      if (lane < LPR) dst[cl * NPT + j] = x;
+      if (lane < LPR) dst[col_of<NPT, LPR>(cl, j)] = x;
     }
   }
 }
@@ -261,11 +271,11 @@ __global__ __launch_bounds__(kThreads) void rec_bwd_kernel(RecBwdArgs a) {
   const InT* beta = static_cast<const InT*>(a.p.beta);
   OutT* dv = static_cast<OutT*>(a.p.dv);
   const int64_t SS = int64_t(a.Dv) * Dk;
-  const int64_t srow = (int64_t(it.n) * a.Hv + hv) * SS + int64_t(row) * Dk + cl * NPT;
+  const int64_t srow = (int64_t(it.n) * a.Hv + hv) * SS + int64_t(row) * Dk;  // the row's first column
 
   float ds[NPT];
 #pragma unroll
-  for (int i = 0; i < NPT; ++i) ds[i] = (live && a.p.ds_out) ? a.p.ds_out[srow + i] : 0.f;
+  for (int i = 0; i < NPT; ++i) ds[i] = (live && a.p.ds_out) ? a.p.ds_out[srow + col_of<NPT, LPR>(cl, i)] : 0.f;
 
   const int nch = (sq.len + kChunk - 1) / kChunk;
   for (int c = nch - 1; c >= 0; --c) {
@@ -278,9 +288,9 @@ __global__ __launch_bounds__(kThreads) void rec_bwd_kernel(RecBwdArgs a) {
     stage_scalars(Gs, Bs, a.p.g, beta, tok, a.Hv, hv, L, a.g_is_log);
     float st[NPT];
     {
-      const float* src = a.p.ckpt + ((sq.slot0 + c) * a.Hv + hv) * SS + int64_t(row) * Dk + cl * NPT;
+      const float* src = a.p.ckpt + ((sq.slot0 + c) * a.Hv + hv) * SS + int64_t(row) * Dk;
 #pragma unroll
-      for (int i = 0; i < NPT; ++i) st[i] = live ? src[i] : 0.f;
+      for (int i = 0; i < NPT; ++i) st[i] = live ? src[col_of<NPT, LPR>(cl, i)] : 0.f;
     }
     __syncthreads();
 
@@ -299,7 +309,7 @@ __global__ __launch_bounds__(kThreads) void rec_bwd_kernel(RecBwdArgs a) {
         if (tt < L) {
           float kk[NPT];
 #pragma unroll
-          for (int i = 0; i < NPT; ++i) kk[i] = Ks[tt][cl * NPT + i];
+          for (int i = 0; i < NPT; ++i) kk[i] = Ks[tt][col_of<NPT, LPR>(cl, i)];
           float pa = 0.f;
 #pragma unroll
           for (int i = 0; i < NPT; ++i) pa += st[i] * kk[i];
@@ -334,7 +344,7 @@ __global__ __launch_bounds__(kThreads) void rec_bwd_kernel(RecBwdArgs a) {
         if (tt < L) {
           const float gt = Gs[tt], d = Ds[tt][rl];
 #pragma unroll
-          for (int i = 0; i < NPT; ++i) S[j + 1][i] = gt * S[j][i] + d * Ks[tt][cl * NPT + i];
+          for (int i = 0; i < NPT; ++i) S[j + 1][i] = gt * S[j][i] + d * Ks[tt][col_of<NPT, LPR>(cl, i)];
         } else {
 #pragma unroll
           for (int i = 0; i < NPT; ++i) S[j + 1][i] = S[j][i];
@@ -347,8 +357,8 @@ __global__ __launch_bounds__(kThreads) void rec_bwd_kernel(RecBwdArgs a) {
         float kk[NPT], qq[NPT], pq[NPT], pk[NPT];
 #pragma unroll
         for (int i = 0; i < NPT; ++i) {
-          kk[i] = Ks[tt][cl * NPT + i];
-          qq[i] = kQGlobal ? IO<InT>::ld(q, ((tok + tt) * a.Hk + hk) * Dk + cl * NPT + i) : Qs[tt][cl * NPT + i];
+          kk[i] = Ks[tt][col_of<NPT, LPR>(cl, i)];
+          qq[i] = kQGlobal ? IO<InT>::ld(q, ((tok + tt) * a.Hk + hk) * Dk + col_of<NPT, LPR>(cl, i)) : Qs[tt][col_of<NPT, LPR>(cl, i)];
         }
         const float gt = Gs[tt], bt = Bs[tt], dyt = DYs[tt][rl], d = Ds[tt][rl], e = Es[tt][rl];
         float dd = 0.f;
@@ -407,7 +417,7 @@ __global__ __launch_bounds__(kThreads) void rec_bwd_kernel(RecBwdArgs a) {
   }
   if (a.p.ds0 && live) {
 #pragma unroll
-    for (int i = 0; i < NPT; ++i) a.p.ds0[srow + i] = ds[i];
+    for (int i = 0; i < NPT; ++i) a.p.ds0[srow + col_of<NPT, LPR>(cl, i)] = ds[i];
   }
 }
 
