@@ -18,6 +18,8 @@
 // key-position tiles, or 64 of the 128 columns). MFMA with split float32 operands as in the forward. Each
 // intermediate crosses between waves through LDS once, written as 8-byte vectors and read either directly or with
 // gfx950's transposing LDS read, whichever index the consuming product reduces over.
+// Sums reduced over a lane group (sum16 and the lane-swap sums give every lane of the group the same bits) are
+// stored by every lane of the group: a store under a lane-0 condition would be an exec-masked branch.
 #include <type_traits>
 
 #include "chunk_common.h"
@@ -399,12 +401,12 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj) {
         const float v = sum16(gpart[jj]), h = sum16(hD[jj]);
-        if (li == 0) gpos[hw][i0 + jj] = v, hpos[hw][i0 + jj] = h;
+        gpos[hw][i0 + jj] = v, hpos[hw][i0 + jj] = h;  // the 16 lanes of a row hold the same bits: no branch
       }
       {
         float v = sum16(sds);
         v = swap32_sum(swap16_sum(v));
-        if ((tid & 63) == 0) red[tid >> 6] = v;
+        red[tid >> 6] = v;  // every lane of the wave holds the same bits
       }
       __syncthreads();
 
@@ -449,7 +451,7 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
             const float x = dp * pv;
             prow += x;
             const float col = sum16(x);
-            if (li == 0) x2c[pw][j] = col;
+            x2c[pw][j] = col;
             // Where j > i, dp is zero and the exponent positive: clamped at 0 to keep the product finite.
             pm[jj] = dp * __expf(fminf(gi - Gf[j], 0.f));
             db[jj] = (j <= ip ? dTbt[mi][jj] : 0.f) * bet[j];
@@ -458,7 +460,7 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
           put4(PL[0], PL[1], at, db[0], db[1], db[2], db[3]);
         }
         prow = swap32_sum(swap16_sum(prow));
-        if (g == 0) x2r[hw][ip] = prow;
+        x2r[hw][ip] = prow;  // the same bits in the four lane groups
       }
       __syncthreads();
 
@@ -478,7 +480,7 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
             const float tv = jj & 1 ? __uint_as_float(hb & 0xffff0000u) + __uint_as_float(lb & 0xffff0000u)
                                     : __uint_as_float(hb << 16) + __uint_as_float(lb << 16);
             const float colb = sum16((j <= ip ? dTbt[mi][jj] : 0.f) * tv);
-            if (li == 0) dbTp[pw][j] = colb;
+            dbTp[pw][j] = colb;
           }
         }
         float tq[4] = {0.f, 0.f, 0.f, 0.f};
@@ -493,7 +495,7 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) {
           const float v = sum16(tq[jj]);
-          if (li == 0) tpos[hw][i0 + jj] = v;
+          tpos[hw][i0 + jj] = v;
         }
         if (e == 0) {
 #pragma unroll
@@ -576,12 +578,12 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
           }
           put4(sb + eKh, sb + eKl, swz(mcol, i0, kLT), kkt[0], kkt[1], kkt[2], kkt[3]);
           colp = swap32_sum(swap16_sum(colp));
-          if (g == 0) x1cp[pw][mcol] = colp;
+          x1cp[pw][mcol] = colp;
         }
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) {
           const float v = sum16(rowp[jj]);
-          if (li == 0) dbAp[hw][i0 + jj] = v;
+          dbAp[hw][i0 + jj] = v;
         }
       }
       __syncthreads();
