@@ -173,7 +173,8 @@ __global__ __launch_bounds__(kThreads) void chunk_prep_kernel(ChunkArgs a) {
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj) {
         const int i = 16 * I + 4 * g + jj, j = 16 * J + li, at = tri_off(i, j);
-        const float e = j <= i ? expf(float(Gd[i] - Gd[j])) : 0.f;
+        // The hardware exponential: its error (a few ulp) is far below the 2^-17 of the hi/lo split that carries E.
+        const float e = j <= i ? __expf(float(Gd[i] - Gd[j])) : 0.f;
         Am[at] = j < i ? Bs[i] * e * kk[u][jj] : 0.f;
         const float x = e * qk[u][jj];
         const __bf16 h = (__bf16)x;
