@@ -150,9 +150,9 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
     for (int jj = 0; jj < 4; ++jj)
       b.vraw[jj] = buf_ld2(vr, uint32_t((16 * pw + 4 * g + jj) * sv + 16 * hw + li) * 2);
   };
-  // A value head's tile and first block, issued one value head ahead (the first at the start, the others during
-  // the previous head's end phase, the next item's first head during this item's last end phase), so no head
-  // waits on a global read before its first block.
+  // A value head's tile and first block, issued one value head ahead (the block's first head here at the start, the
+  // others in pieces during the previous head's end phase, the next item's first head during this item's last end
+  // phase), so no head waits on a global read before its first block.
   auto load_head = [&](TileIn& ti, BlockIn& b, const Item& it, int hv) {
     int lt = tid;
     asm volatile("" : "+v"(lt));
@@ -193,6 +193,18 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
       const int hv = hk * grp + e;
       const int64_t sh = slot * a.Hv + hv;
       const Tile* tl = a.tiles + sh;
+      // The head whose tile and first block the end phase reads ahead, in pieces at the starts of E2, E3 and E4
+      // (beside their products, so that no phase issues them all): the next in the group, the next item's first,
+      // or, for the block's last item, this head again (those reads are unused; they keep every path's loads the
+      // same, so the compiler's waits stay exact).
+      Item nx = cur;
+      int nhv = hv;
+      if (e + 1 < grp) {
+        nhv = hv + 1;
+      } else if (id + int(gridDim.x) < total) {
+        nx = item_at(id + gridDim.x);
+        nhv = nx.hk * grp;
+      }
       __syncthreads();
       if (tid < kC) gam[tid] = ti.sc[0], dec[tid] = ti.sc[1], bet[tid] = ti.sc[2], Gf[tid] = ti.sc[3];
       {  // Tb and P, hi and lo
@@ -425,12 +437,6 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
             *reinterpret_cast<uint4*>(sb + eQb + swz(e >> 4, (e & 15) * 8, kLK)) = __builtin_bit_cast(uint4, nb.ys[q2]);
           }
         }
-        if (e + 1 < grp) {  // nb is free from here
-          load_head(ti, nb, cur, hv + 1);
-        } else if (id + int(gridDim.x) < total) {  // the next item's first head
-          const Item nx = item_at(id + gridDim.x);
-          load_head(ti, nb, nx, nx.hk * grp);
-        }
         // Row sums (over j) add up over g here and over hw in dG; column sums (over i) over li here and over pw in dG.
         float prow = 0.f;
         const float gi = Gf[ip];
@@ -464,6 +470,11 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
       }
       __syncthreads();
 
+      {  // the next head's tile (ti was staged at this head's start)
+        int lq = tid;
+        asm volatile("" : "+v"(lq));
+        load_tile(ti, nx, nhv, lq);
+      }
       // E2: the column sums of dTb * T (dbeta's T part); dQ += diag(exp G) dQ_inter and its dG term; K K^T (the first
       // value head only, kept in registers); dQ += (P * M) K; dK += (P * M)^T Q; Z = dTb diag(beta) T^T, stored as Z^T.
       {
@@ -541,6 +552,7 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
       }
       __syncthreads();
 
+      load_rows(nb.xs, a.ckpt, nx, nhv, 0, lt);  // the next head's first S0 rows (nb.xs went to LDS in E1)
       // E3: dA = -T^T Z below the diagonal (rows p = i0 + jj, columns m = 16 key_tile(pw, hw, mi) + li, as kk), and at
       // once its products with E = exp(G_p - G_m) and K K^T: the A part of dbeta (row sums), of dG (row and column
       // sums), and dKK = diag(beta) (dA * E), stored as dKK^T.
@@ -588,6 +600,8 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
       }
       __syncthreads();
 
+      load_rows(nb.ys, a.dsend, nx, nhv, 0, lt);  // and its first dS rows, dy and v
+      load_dy_v(nb, nx, nhv, 0, lt);
       // E4: dK += (dKK + dKK^T) K for rows j = ip, this half's columns: dKK rows j through the transposing read of
       // dKK^T, dKK^T rows j directly.
 #pragma unroll
