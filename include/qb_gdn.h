@@ -108,7 +108,8 @@ int qb_gdn_fwd_rows(const qb_gdn_desc* desc, const void* q, const void* k, const
                     int errlen);
 
 /* Backward from the forward's ckpt: the cotangents of (q, k, v, g, beta, s0) given dy and ds_out (the cotangent of
- * the final state; NULL is zero). ds0 may be NULL. Deterministic: sums run in a fixed order, no atomics. */
+ * the final state; NULL is zero). ds0 may be NULL. Deterministic: sums run in a fixed order, no atomics. ckpt must
+ * come from a forward of the same desc, design included (past the states each design keeps its own residual). */
 int qb_gdn_bwd(const qb_gdn_desc* desc, const void* q, const void* k, const void* v, const float* g,
                const void* beta, const float* ckpt, const void* dy, const float* ds_out, void* dq, void* dk, void* dv,
                float* dg, void* dbeta, float* ds0, void* workspace, void* stream, char* err, int errlen);

@@ -11,10 +11,12 @@
 //   a = S_prev k, b = S_prev q;  u = g a;  delta = beta (v - u);  y = g b + delta (k.q);  S = g S_prev + delta k^T
 // The chunk-start states (the reference's ckpt, src/delta_grad.cpp:172-181) are written as the forward passes them.
 //
+// The forward also keeps e = v - u per token and state row after the checkpoints in ckpt (4 bytes per token and row).
+//
 // Backward: reference src/delta_grad.cpp:23-145 re-derived for this layout. Per chunk in reverse: pass A replays
-// the chunk from its checkpoint (one reduction per step) keeping delta and v - u per step in LDS and the state at
-// every 8th step in registers; pass B re-forms 8 states at a time from those without reductions and runs the reverse
-// steps. dq and dk sum over rows: over a wave's rows with lane shuffles, over the block's 4 waves in LDS, over the
+// the chunk's states from its checkpoint with the forward's e (delta = beta e, as the forward formed it), so without
+// a reduction, keeping the state at every 8th step in registers; pass B re-forms 8 states at a time from those and
+// runs the reverse steps. dq and dk sum over rows: over a wave's rows with lane shuffles, over the block's 4 waves in LDS, over the
 // row blocks and the GQA group in rec_reduce_kernel, always in the same order (no atomics).
 #include <type_traits>
 
@@ -58,12 +60,14 @@ __device__ __forceinline__ int col_of(int cl, int i) {
 
 struct RecFwdArgs {
   FwdPtrs p;
+  float* e_res;  // v - u per token and state row [tokens, Hv, Dv], after the states in ckpt (null without ckpt)
   int Hk, Hv, Dv, g_is_log, nblk, total;
   SeqTable tab;
 };
 
 struct RecBwdArgs {
   BwdPtrs p;
+  const float* e_res;  // the forward's v - u per token and state row
   int Hk, Hv, Dv, g_is_log, nblk, total;
   float* dq_part;  // [BT, Hv, nblk, Dk]
   float* dk_part;
@@ -127,7 +131,7 @@ __global__ __launch_bounds__(kThreads) void rec_fwd_kernel(RecFwdArgs a) {
   __shared__ float Ks[kChunk][Dk];
   __shared__ float Qs[kChunk][Dk];
   __shared__ float Vs[kChunk][kRows];
-  __shared__ float Ys[kChunk][kRows];
+  __shared__ float Ys[kChunk][kRows], Es[kChunk][kRows];
   __shared__ float Gs[kChunk], Bs[kChunk], KQs[kChunk];
 
   const Item it = item_of(a.tab, a.nblk, a.Hv, a.Hk, a.total);
@@ -183,11 +187,12 @@ __global__ __launch_bounds__(kThreads) void rec_fwd_kernel(RecFwdArgs a) {
       pa = sum_lanes<LPR>(pa);
       pb = sum_lanes<LPR>(pb);
       const float gt = Gs[tt], bt = Bs[tt];
-      const float d = bt * (Vs[tt][rl] - gt * pa);
+      const float e = Vs[tt][rl] - gt * pa;
+      const float d = bt * e;
       const float yv = gt * pb + d * KQs[tt];
 #pragma unroll
       for (int i = 0; i < NPT; ++i) s[i] = gt * s[i] + d * kk[i];
-      Ys[tt][rl] = yv;  // every lane of the row holds the same bits: a store without a branch
+      Ys[tt][rl] = yv, Es[tt][rl] = e;  // every lane of the row holds the same bits: stores without a branch
       if (kKeepRows && live) {  // the state after this token
         float* dst = a.p.rows + ((tok + tt) * a.Hv + hv) * SS + int64_t(row) * Dk;
 #pragma unroll
@@ -197,7 +202,11 @@ __global__ __launch_bounds__(kThreads) void rec_fwd_kernel(RecFwdArgs a) {
     __syncthreads();
     for (int e = tid; e < L * kRows; e += kThreads) {
       const int tt = e / kRows, j = e % kRows;
-      if (row0 + j < a.Dv) IO<OutT>::st(y, ((tok + tt) * a.Hv + hv) * a.Dv + row0 + j, Ys[tt][j]);
+      if (row0 + j < a.Dv) {
+        const int64_t at = ((tok + tt) * a.Hv + hv) * a.Dv + row0 + j;
+        IO<OutT>::st(y, at, Ys[tt][j]);
+        if (a.e_res) a.e_res[at] = Es[tt][j];
+      }
     }
   }
   if (a.p.s_out && live) {
@@ -252,7 +261,7 @@ __global__ __launch_bounds__(kThreads) void rec_bwd_kernel(RecBwdArgs a) {
   constexpr bool kQGlobal = LPR == 32;
   __shared__ float Ks[kChunk][Dk];
   __shared__ float Qs[kQGlobal ? 1 : kChunk][Dk];
-  __shared__ float Vs[kChunk][kRows], DYs[kChunk][kRows], Ds[kChunk][kRows], Es[kChunk][kRows];
+  __shared__ float DYs[kChunk][kRows], Es[kChunk][kRows];
   __shared__ float Gs[kChunk], Bs[kChunk];
   __shared__ float red[kSub][kWaves][2 * Dk];  // per step and wave: column sums of (dq | dk) over the wave's rows
   __shared__ float rowv[kSub][3][kRows];       // per step and row: dv, dbeta, dg (factor)
@@ -266,7 +275,6 @@ __global__ __launch_bounds__(kThreads) void rec_bwd_kernel(RecBwdArgs a) {
   const Seq sq = seq_of(a.tab, it.n);
   const InT* q = static_cast<const InT*>(a.p.q);
   const InT* k = static_cast<const InT*>(a.p.k);
-  const InT* v = static_cast<const InT*>(a.p.v);
   const OutT* dy = static_cast<const OutT*>(a.p.dy);
   const InT* beta = static_cast<const InT*>(a.p.beta);
   OutT* dv = static_cast<OutT*>(a.p.dv);
@@ -283,7 +291,7 @@ __global__ __launch_bounds__(kThreads) void rec_bwd_kernel(RecBwdArgs a) {
     const int64_t tok = sq.tok0 + t0;
     __syncthreads();
     stage_kq<Dk>(Ks, kQGlobal ? nullptr : Qs, k, q, tok, a.Hk, hk, L);
-    stage_rows<kRows>(Vs, v, tok, a.Hv, hv, a.Dv, row0, L);
+    stage_rows<kRows>(Es, a.e_res, tok, a.Hv, hv, a.Dv, row0, L);
     stage_rows<kRows>(DYs, dy, tok, a.Hv, hv, a.Dv, row0, L);
     stage_scalars(Gs, Bs, a.p.g, beta, tok, a.Hv, hv, L, a.g_is_log);
     float st[NPT];
@@ -294,7 +302,7 @@ __global__ __launch_bounds__(kThreads) void rec_bwd_kernel(RecBwdArgs a) {
     }
     __syncthreads();
 
-    // Pass A: replay the chunk, keeping delta and v - u per step and every kSub-th state.
+    // Pass A: replay the chunk's states (delta = beta e, the forward's product), keeping every kSub-th one.
     float sub[kNSub][NPT];
     for (int m = 0; m < kNSub; ++m) {
 #pragma unroll
@@ -307,23 +315,12 @@ __global__ __launch_bounds__(kThreads) void rec_bwd_kernel(RecBwdArgs a) {
       for (int j = 0; j < kSub; ++j) {
         const int tt = m * kSub + j;
         if (tt < L) {
-          float kk[NPT];
+          const float gt = Gs[tt], d = Bs[tt] * Es[tt][rl];
 #pragma unroll
-          for (int i = 0; i < NPT; ++i) kk[i] = Ks[tt][col_of<NPT, LPR>(cl, i)];
-          float pa = 0.f;
-#pragma unroll
-          for (int i = 0; i < NPT; ++i) pa += st[i] * kk[i];
-          pa = sum_lanes<LPR>(pa);
-          const float gt = Gs[tt];
-          const float e = Vs[tt][rl] - gt * pa;
-          const float d = Bs[tt] * e;
-#pragma unroll
-          for (int i = 0; i < NPT; ++i) st[i] = gt * st[i] + d * kk[i];
-          Ds[tt][rl] = d, Es[tt][rl] = e;  // row-uniform values, stored by every lane of the row
+          for (int i = 0; i < NPT; ++i) st[i] = gt * st[i] + d * Ks[tt][col_of<NPT, LPR>(cl, i)];
         }
       }
     }
-    __syncthreads();
 
     // Pass B: 8 states at a time from the kept starts, then the reverse steps (reference :97-141).
     for (int m = kNSub - 1; m >= 0; --m) {
@@ -342,7 +339,7 @@ __global__ __launch_bounds__(kThreads) void rec_bwd_kernel(RecBwdArgs a) {
       for (int j = 0; j < kSub; ++j) {
         const int tt = ts + j;
         if (tt < L) {
-          const float gt = Gs[tt], d = Ds[tt][rl];
+          const float gt = Gs[tt], d = Bs[tt] * Es[tt][rl];
 #pragma unroll
           for (int i = 0; i < NPT; ++i) S[j + 1][i] = gt * S[j][i] + d * Ks[tt][col_of<NPT, LPR>(cl, i)];
         } else {
@@ -360,7 +357,7 @@ __global__ __launch_bounds__(kThreads) void rec_bwd_kernel(RecBwdArgs a) {
           kk[i] = Ks[tt][col_of<NPT, LPR>(cl, i)];
           qq[i] = kQGlobal ? IO<InT>::ld(q, ((tok + tt) * a.Hk + hk) * Dk + col_of<NPT, LPR>(cl, i)) : Qs[tt][col_of<NPT, LPR>(cl, i)];
         }
-        const float gt = Gs[tt], bt = Bs[tt], dyt = DYs[tt][rl], d = Ds[tt][rl], e = Es[tt][rl];
+        const float gt = Gs[tt], bt = Bs[tt], dyt = DYs[tt][rl], e = Es[tt][rl], d = bt * e;
         float dd = 0.f;
 #pragma unroll
         for (int i = 0; i < NPT; ++i) {
@@ -493,6 +490,7 @@ template <typename InT, typename OutT>
 hipError_t launch_fwd(const Problem& p, const FwdPtrs& ptrs, hipStream_t s, Tracer& tr) {
   RecFwdArgs a;
   a.p = ptrs;
+  a.e_res = ptrs.ckpt ? ptrs.ckpt + int64_t(p.NC) * p.Hv * p.Dv * p.Dk : nullptr;
   a.Hk = p.Hk, a.Hv = p.Hv, a.Dv = p.Dv, a.g_is_log = p.g_is_log;
   a.nblk = row_blocks(p);
   a.total = a.nblk * p.Hv * p.N;
@@ -527,6 +525,7 @@ template <typename InT, typename OutT>
 hipError_t launch_bwd(const Problem& p, const BwdPtrs& ptrs, void* ws, hipStream_t s, Tracer& tr) {
   RecBwdArgs a;
   a.p = ptrs;
+  a.e_res = ptrs.ckpt + int64_t(p.NC) * p.Hv * p.Dv * p.Dk;
   a.Hk = p.Hk, a.Hv = p.Hv, a.Dv = p.Dv, a.g_is_log = p.g_is_log;
   a.nblk = row_blocks(p);
   a.total = a.nblk * p.Hv * p.N;
@@ -563,7 +562,10 @@ const char* rec_supports(const Problem& p) {
   return nullptr;
 }
 
-size_t rec_ckpt_bytes(const Problem& p) { return size_t(p.NC) * p.Hv * p.Dv * p.Dk * sizeof(float); }
+// The chunk-start states [NC, Hv, Dv, Dk], then e = v - u [tokens, Hv, Dv].
+size_t rec_ckpt_bytes(const Problem& p) {
+  return (size_t(p.NC) * p.Hv * p.Dv * p.Dk + size_t(p.BT) * p.Hv * p.Dv) * sizeof(float);
+}
 
 size_t rec_workspace_bytes(const Problem& p) {
   const size_t nblk = row_blocks(p);

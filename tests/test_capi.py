@@ -94,7 +94,8 @@ def test_rejects_with_reason(lib, kw, needle):
 def test_chunk_slots_and_sizes(lib):
     d, _ = desc(T=4096)
     assert _lib.num_chunks(d) == 64
-    assert _lib.ckpt_bytes(d) == 64 * 32 * 128 * 128 * 4
+    # The chunk-start states, then the recurrent design's e = v - u per token and state row.
+    assert _lib.ckpt_bytes(d) == (64 * 32 * 128 * 128 + 4096 * 32 * 128) * 4
     d, _ = desc(B=3, T=65, Hv=16)
     assert _lib.num_chunks(d) == 6
     lens = [5, 64, 0, 130, 1]
