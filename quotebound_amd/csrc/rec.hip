@@ -1,10 +1,11 @@
 // Design 1: the recurrent form. Rows of the state S [Dv, Dk] evolve independently (reference
 // src/delta_grad.cpp:13-18), so each row is owned by LPR lanes of a wave, each lane holding NPT = Dk / LPR columns in
-// VGPRs for all T steps: LPR = 16 (one DPP row) for Dk up to 128, LPR = 32 for Dk of 160 to 256, so a lane never
-// holds more than 8 columns. The two mat-vecs per step are LPR-lane reductions (DPP within 16 lanes, one swizzle
-// across two rows). A block is 4 waves = 4 * 64 / LPR state rows of one value head; the chunk's keys, queries and
-// scalars are staged in LDS once per 64 steps and read by all its rows (the backward of the wide variant reads the
-// queries from global memory instead, to stay within LDS).
+// VGPRs for all T steps: LPR = 16 (one DPP row) for Dk up to 96, LPR = 32 from Dk = 128 to 256, so a lane never
+// holds more than 8 columns. The two mat-vecs per step are LPR-lane reductions (DPP within 16 lanes, one lane swap
+// across two). A block holds the state rows of one value head: 16 rows up to Dk = 128 (4 waves of LPR = 16, or at
+// Dk = 128 8 waves of LPR = 32, two waves per SIMD), 8 rows past it (4 waves). The chunk's keys, queries and scalars
+// are staged in LDS once per 64 steps and read by all its rows (the backward past Dk = 128 reads the queries from
+// global memory instead, to stay within LDS).
 //
 // Forward (per row, per step), the same recurrence as reference tests/gated_delta_ref.h:46-67 but with both dot
 // products taken on the previous state, so one reduction latency per step sits on the dependency chain:
@@ -26,19 +27,22 @@
 namespace qbgdn {
 namespace {
 
-constexpr int kWaves = 4;
-constexpr int kThreads = 64 * kWaves;
 constexpr int kSub = 8;  // states re-formed at a time in the backward
 constexpr int kNSub = kChunk / kSub;
 
-// The lane layout for a key width: LPR lanes per state row, NPT columns per lane, rows per block.
-template <int LPR>
+// The lane layout for a key width: LPR lanes per state row, NPT columns per lane, waves and rows per block. Dk = 128
+// takes LPR = 32 in 8-wave blocks: two waves per SIMD at one block per CU, to hide each other's reduction latency
+// (16 rows per block, as with 4 waves of LPR = 16). The wider keys stay at 4 waves for LDS.
+template <int NPT, int LPR>
 struct Layout {
+  static constexpr int kDk = NPT * LPR;
+  static constexpr int kWaves = (LPR == 32 && kDk <= 128) ? 8 : 4;
+  static constexpr int kThreads = 64 * kWaves;
   static constexpr int kRowsPerWave = 64 / LPR;
   static constexpr int kRows = kWaves * kRowsPerWave;
 };
-// Rows per block for a key width (the host side's view of the same layout).
-inline int rec_rows(int Dk) { return Dk <= 128 ? Layout<16>::kRows : Layout<32>::kRows; }
+// Rows per block for a key width (the host side's view of the same layout): 16 up to Dk = 128, 8 past it.
+inline int rec_rows(int Dk) { return Dk <= 128 ? 16 : 8; }
 
 // Sum over each group of LPR lanes; every lane of the group gets the same bits.
 template <int LPR>
@@ -87,11 +91,11 @@ __device__ __forceinline__ Item item_of(const SeqTable& tab, int nblk, int Hv, i
 
 // Stages rows [t0, t0 + L) of the key head's k (and q, when Qs is not null) into LDS as float32, 8 elements per
 // access.
-template <int Dk, typename InT>
+template <int kThr, int Dk, typename InT>
 __device__ __forceinline__ void stage_kq(float (*Ks)[Dk], float (*Qs)[Dk], const InT* k, const InT* q,
                                          int64_t tok, int Hk, int hk, int L) {
   constexpr int V8 = Dk / 8;
-  for (int e = threadIdx.x; e < kChunk * V8; e += kThreads) {
+  for (int e = threadIdx.x; e < kChunk * V8; e += kThr) {
     const int tt = e / V8, c8 = (e % V8) * 8;
     if (tt < L) {
       const int64_t off = ((tok + tt) * Hk + hk) * Dk + c8;
@@ -102,20 +106,20 @@ __device__ __forceinline__ void stage_kq(float (*Ks)[Dk], float (*Qs)[Dk], const
 }
 
 // Stages a [T, Hv, Dv] tensor's kRows-row slice of rows [t0, t0 + L) (zeros past Dv).
-template <int kRows, typename InT>
+template <int kThr, int kRows, typename InT>
 __device__ __forceinline__ void stage_rows(float (*Xs)[kRows], const InT* x, int64_t tok, int Hv, int hv, int Dv,
                                            int row0, int L) {
-  for (int e = threadIdx.x; e < kChunk * kRows; e += kThreads) {
+  for (int e = threadIdx.x; e < kChunk * kRows; e += kThr) {
     const int tt = e / kRows, j = e % kRows;
     if (tt < L) Xs[tt][j] = (row0 + j < Dv) ? IO<InT>::ld(x, ((tok + tt) * Hv + hv) * Dv + row0 + j) : 0.f;
   }
 }
 
 // Per-step scalars: the decay factor (exp of the log-decay when g_is_log) and beta.
-template <typename InT>
+template <int kThr, typename InT>
 __device__ __forceinline__ void stage_scalars(float* Gs, float* Bs, const float* g, const InT* beta, int64_t tok,
                                               int Hv, int hv, int L, int g_is_log) {
-  for (int tt = threadIdx.x; tt < L; tt += kThreads) {
+  for (int tt = threadIdx.x; tt < L; tt += kThr) {
     const int64_t i = (tok + tt) * Hv + hv;
     const float gv = g[i];
     Gs[tt] = g_is_log ? expf(gv) : gv;
@@ -125,18 +129,18 @@ __device__ __forceinline__ void stage_scalars(float* Gs, float* Bs, const float*
 
 // kKeepRows: also store the state after every token (a.p.rows), for the per-token-state forward.
 template <int NPT, int LPR, typename InT, typename OutT, bool kKeepRows>
-__global__ __launch_bounds__(kThreads) void rec_fwd_kernel(RecFwdArgs a) {
-  constexpr int Dk = LPR * NPT;
-  constexpr int kRows = Layout<LPR>::kRows;
+__global__ __launch_bounds__((Layout<NPT, LPR>::kThreads)) void rec_fwd_kernel(RecFwdArgs a) {
+  using Lay = Layout<NPT, LPR>;
+  constexpr int Dk = LPR * NPT, kRows = Lay::kRows, kThreads = Lay::kThreads;
   __shared__ float Ks[kChunk][Dk];
   __shared__ float Qs[kChunk][Dk];
   __shared__ float Vs[kChunk][kRows];
-  __shared__ float Ys[kChunk][kRows], Es[kChunk][kRows];
+  __shared__ float2 YEs[kChunk][kRows];  // y and e = v - u per step and row
   __shared__ float Gs[kChunk], Bs[kChunk], KQs[kChunk];
 
   const Item it = item_of(a.tab, a.nblk, a.Hv, a.Hk, a.total);
   const int tid = threadIdx.x, lane = tid & 63;
-  const int cl = lane % LPR, rl = (tid >> 6) * Layout<LPR>::kRowsPerWave + lane / LPR;
+  const int cl = lane % LPR, rl = (tid >> 6) * Lay::kRowsPerWave + lane / LPR;
   const int row0 = it.blk * kRows, row = row0 + rl;
   const bool live = row < a.Dv;
   const int hv = it.hv, hk = hv / (a.Hv / a.Hk);
@@ -163,9 +167,9 @@ __global__ __launch_bounds__(kThreads) void rec_fwd_kernel(RecFwdArgs a) {
       for (int i = 0; i < NPT; ++i) dst[col_of<NPT, LPR>(cl, i)] = s[i];
     }
     __syncthreads();  // the previous chunk's LDS readers are done
-    stage_kq<Dk>(Ks, Qs, (const InT*)k, (const InT*)q, tok, a.Hk, hk, L);
-    stage_rows(Vs, v, tok, a.Hv, hv, a.Dv, row0, L);
-    stage_scalars(Gs, Bs, a.p.g, beta, tok, a.Hv, hv, L, a.g_is_log);
+    stage_kq<kThreads>(Ks, Qs, (const InT*)k, (const InT*)q, tok, a.Hk, hk, L);
+    stage_rows<kThreads>(Vs, v, tok, a.Hv, hv, a.Dv, row0, L);
+    stage_scalars<kThreads>(Gs, Bs, a.p.g, beta, tok, a.Hv, hv, L, a.g_is_log);
     __syncthreads();
     // k.q per step: groups of LPR lanes, one step each at a time.
     for (int tt = tid / LPR; tt < kChunk; tt += kThreads / LPR) {
@@ -192,7 +196,7 @@ __global__ __launch_bounds__(kThreads) void rec_fwd_kernel(RecFwdArgs a) {
       const float yv = gt * pb + d * KQs[tt];
 #pragma unroll
       for (int i = 0; i < NPT; ++i) s[i] = gt * s[i] + d * kk[i];
-      Ys[tt][rl] = yv, Es[tt][rl] = e;  // every lane of the row holds the same bits: stores without a branch
+      YEs[tt][rl] = float2{yv, e};  // every lane of the row holds the same bits: a store without a branch
       if (kKeepRows && live) {  // the state after this token
         float* dst = a.p.rows + ((tok + tt) * a.Hv + hv) * SS + int64_t(row) * Dk;
 #pragma unroll
@@ -204,8 +208,9 @@ __global__ __launch_bounds__(kThreads) void rec_fwd_kernel(RecFwdArgs a) {
       const int tt = e / kRows, j = e % kRows;
       if (row0 + j < a.Dv) {
         const int64_t at = ((tok + tt) * a.Hv + hv) * a.Dv + row0 + j;
-        IO<OutT>::st(y, at, Ys[tt][j]);
-        if (a.e_res) a.e_res[at] = Es[tt][j];
+        const float2 ye = YEs[tt][j];
+        IO<OutT>::st(y, at, ye.x);
+        if (a.e_res) a.e_res[at] = ye.y;
       }
     }
   }
@@ -242,6 +247,17 @@ __device__ __forceinline__ void wave_rows_sum(const float* p, float* dst, int la
     const int i0 = (h16 ? Q : 0) + (h32 ? H : 0);  // the lane's finished values: i0 .. i0 + Q - 1
 #pragma unroll
     for (int j = 0; j < Q; ++j) dst[col_of<NPT, LPR>(cl, i0 + j)] = x[j];
+  } else if constexpr (LPR == 32 && NPT % 2 == 0) {
+    constexpr int H = NPT / 2;
+    float w[H];
+#pragma unroll
+    for (int j = 0; j < H; ++j) {
+      const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(p[j]), __float_as_uint(p[j + H]), false, false);
+      w[j] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+    const int i0 = lane & 32 ? H : 0;
+#pragma unroll
+    for (int j = 0; j < H; ++j) dst[col_of<NPT, LPR>(cl, i0 + j)] = w[j];
   } else {
 #pragma unroll
     for (int j = 0; j < NPT; ++j) {
@@ -255,10 +271,10 @@ __device__ __forceinline__ void wave_rows_sum(const float* p, float* dst, int la
 // The wide variant (LPR = 32) reads q from global memory in its reverse steps rather than staging it: its k, red and
 // the per-row arrays take about 137 KB of LDS at Dk = 256.
 template <int NPT, int LPR, typename InT, typename OutT>
-__global__ __launch_bounds__(kThreads) void rec_bwd_kernel(RecBwdArgs a) {
-  constexpr int Dk = LPR * NPT;
-  constexpr int kRows = Layout<LPR>::kRows;
-  constexpr bool kQGlobal = LPR == 32;
+__global__ __launch_bounds__((Layout<NPT, LPR>::kThreads)) void rec_bwd_kernel(RecBwdArgs a) {
+  using Lay = Layout<NPT, LPR>;
+  constexpr int Dk = LPR * NPT, kRows = Lay::kRows, kThreads = Lay::kThreads, kWaves = Lay::kWaves;
+  constexpr bool kQGlobal = Dk > 128;
   __shared__ float Ks[kChunk][Dk];
   __shared__ float Qs[kQGlobal ? 1 : kChunk][Dk];
   __shared__ float DYs[kChunk][kRows], Es[kChunk][kRows];
@@ -268,7 +284,7 @@ __global__ __launch_bounds__(kThreads) void rec_bwd_kernel(RecBwdArgs a) {
 
   const Item it = item_of(a.tab, a.nblk, a.Hv, a.Hk, a.total);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int cl = lane % LPR, rl = wave * Layout<LPR>::kRowsPerWave + lane / LPR;
+  const int cl = lane % LPR, rl = wave * Lay::kRowsPerWave + lane / LPR;
   const int row0 = it.blk * kRows, row = row0 + rl;
   const bool live = row < a.Dv;
   const int hv = it.hv, hk = hv / (a.Hv / a.Hk);
@@ -290,10 +306,10 @@ __global__ __launch_bounds__(kThreads) void rec_bwd_kernel(RecBwdArgs a) {
     const int t0 = c * kChunk, L = min(kChunk, sq.len - t0);
     const int64_t tok = sq.tok0 + t0;
     __syncthreads();
-    stage_kq<Dk>(Ks, kQGlobal ? nullptr : Qs, k, q, tok, a.Hk, hk, L);
-    stage_rows<kRows>(Es, a.e_res, tok, a.Hv, hv, a.Dv, row0, L);
-    stage_rows<kRows>(DYs, dy, tok, a.Hv, hv, a.Dv, row0, L);
-    stage_scalars(Gs, Bs, a.p.g, beta, tok, a.Hv, hv, L, a.g_is_log);
+    stage_kq<kThreads>(Ks, kQGlobal ? nullptr : Qs, k, q, tok, a.Hk, hk, L);
+    stage_rows<kThreads>(Es, a.e_res, tok, a.Hv, hv, a.Dv, row0, L);
+    stage_rows<kThreads>(DYs, dy, tok, a.Hv, hv, a.Dv, row0, L);
+    stage_scalars<kThreads>(Gs, Bs, a.p.g, beta, tok, a.Hv, hv, L, a.g_is_log);
     float st[NPT];
     {
       const float* src = a.p.ckpt + ((sq.slot0 + c) * a.Hv + hv) * SS + int64_t(row) * Dk;
@@ -472,7 +488,7 @@ bool with_width(int Dk, F&& f) {
     case 32: f(integral_constant<int, 2>{}, integral_constant<int, 16>{}); return true;
     case 64: f(integral_constant<int, 4>{}, integral_constant<int, 16>{}); return true;
     case 96: f(integral_constant<int, 6>{}, integral_constant<int, 16>{}); return true;
-    case 128: f(integral_constant<int, 8>{}, integral_constant<int, 16>{}); return true;
+    case 128: f(integral_constant<int, 4>{}, integral_constant<int, 32>{}); return true;
     case 160: f(integral_constant<int, 5>{}, integral_constant<int, 32>{}); return true;
     case 192: f(integral_constant<int, 6>{}, integral_constant<int, 32>{}); return true;
     case 224: f(integral_constant<int, 7>{}, integral_constant<int, 32>{}); return true;
@@ -495,11 +511,12 @@ hipError_t launch_fwd(const Problem& p, const FwdPtrs& ptrs, hipStream_t s, Trac
   a.nblk = row_blocks(p);
   a.total = a.nblk * p.Hv * p.N;
   a.tab = p.tab;
-  const dim3 grid(a.total), block(kThreads);
+  const dim3 grid(a.total);
   tr.mark();
   const bool rows = ptrs.rows != nullptr;
   const bool ok = with_width(p.Dk, [&](auto npt, auto lpr) {
     constexpr int NPT = decltype(npt)::value, LPR = decltype(lpr)::value;
+    const dim3 block(Layout<NPT, LPR>::kThreads);
     if (rows)
       hipLaunchKernelGGL((rec_fwd_kernel<NPT, LPR, InT, OutT, true>), grid, block, 0, s, a);
     else
@@ -532,10 +549,11 @@ hipError_t launch_bwd(const Problem& p, const BwdPtrs& ptrs, void* ws, hipStream
   const BwdWs w = carve(p, ws);
   a.dq_part = w.dq_part, a.dk_part = w.dk_part, a.dg_part = w.dg_part, a.db_part = w.db_part;
   a.tab = p.tab;
-  const dim3 grid(a.total), block(kThreads);
+  const dim3 grid(a.total);
   tr.mark();
   const bool ok = with_width(p.Dk, [&](auto npt, auto lpr) {
     constexpr int NPT = decltype(npt)::value, LPR = decltype(lpr)::value;
+    const dim3 block(Layout<NPT, LPR>::kThreads);
     hipLaunchKernelGGL((rec_bwd_kernel<NPT, LPR, InT, OutT>), grid, block, 0, s, a);
   });
   if (!ok) return hipErrorInvalidValue;
