@@ -138,6 +138,18 @@ __device__ __forceinline__ float swap32_sum(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// The sums of a and of b over each group of 32 lanes, both given to every lane of the group, on one 16-lane DPP
+// tree: v_permlane16_swap(a, b) plus an add leaves a + (a of lane + 16) in the low 16 lanes of every 32 and
+// (b of lane - 16) + b in the high ones; sum16 finishes a's sum in the low lanes and b's in the high; a second swap
+// of that value with itself hands each half the other's (first result: a's sum everywhere, second: b's).
+__device__ __forceinline__ void sum32_pair(float& a, float& b) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+  const float x = sum16(__uint_as_float(r[0]) + __uint_as_float(r[1]));
+  const auto t = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  a = __uint_as_float(t[0]);
+  b = __uint_as_float(t[1]);
+}
+
 // Blocks are dispatched round-robin over the MI355X's 8 XCDs (block id runs on XCD id % 8), each with its own
 // L2. This gives XCD x a contiguous range of work items, so neighbouring items (which read the same key head)
 // share an L2. A bijection on [0, n).

@@ -188,8 +188,12 @@ __global__ __launch_bounds__((Layout<NPT, LPR>::kThreads)) void rec_fwd_kernel(R
       float pa = 0.f, pb = 0.f;
 #pragma unroll
       for (int i = 0; i < NPT; ++i) pa += s[i] * kk[i], pb += s[i] * qq[i];
-      pa = sum_lanes<LPR>(pa);
-      pb = sum_lanes<LPR>(pb);
+      if constexpr (LPR == 32) {
+        sum32_pair(pa, pb);
+      } else {
+        pa = sum_lanes<LPR>(pa);
+        pb = sum_lanes<LPR>(pb);
+      }
       const float gt = Gs[tt], bt = Bs[tt];
       const float e = Vs[tt][rl] - gt * pa;
       const float d = bt * e;
@@ -363,6 +367,9 @@ __global__ __launch_bounds__((Layout<NPT, LPR>::kThreads)) void rec_bwd_kernel(R
           for (int i = 0; i < NPT; ++i) S[j + 1][i] = S[j][i];
         }
       }
+      // With LPR = 32, a step's dg is summed over the row's lanes together with the next (lower) step's dd, one
+      // paired reduction for the two (dgp holds it meanwhile).
+      float dgp = 0.f;
 #pragma unroll
       for (int j = kSub - 1; j >= 0; --j) {
         const int tt = ts + j;
@@ -381,7 +388,16 @@ __global__ __launch_bounds__((Layout<NPT, LPR>::kThreads)) void rec_bwd_kernel(R
           pq[i] = dyt * S[j + 1][i];
           dd += ds[i] * kk[i];
         }
-        dd = sum_lanes<LPR>(dd);
+        if constexpr (LPR == 32) {
+          if (j < kSub - 1) {
+            sum32_pair(dd, dgp);
+            rowv[j + 1][2][rl] = dgp;  // step j + 1's dg (not read past the sub-chunk's last step)
+          } else {
+            dd = sum_lanes<LPR>(dd);
+          }
+        } else {
+          dd = sum_lanes<LPR>(dd);
+        }
         const float du = -bt * dd;
         float dg = 0.f;
 #pragma unroll
@@ -391,11 +407,17 @@ __global__ __launch_bounds__((Layout<NPT, LPR>::kThreads)) void rec_bwd_kernel(R
           dg += ds[i] * S[j][i];
           ds[i] *= gt;
         }
-        dg = sum_lanes<LPR>(dg);
-        rowv[j][0][rl] = bt * dd, rowv[j][1][rl] = dd * e, rowv[j][2][rl] = dg;  // row-uniform, every lane
+        if constexpr (LPR == 32) {
+          dgp = dg;
+        } else {
+          dg = sum_lanes<LPR>(dg);
+          rowv[j][2][rl] = dg;
+        }
+        rowv[j][0][rl] = bt * dd, rowv[j][1][rl] = dd * e;  // row-uniform, every lane
         wave_rows_sum<NPT, LPR>(pq, red[j][wave], lane);
         wave_rows_sum<NPT, LPR>(pk, red[j][wave] + Dk, lane);
       }
+      if constexpr (LPR == 32) rowv[0][2][rl] = sum_lanes<LPR>(dgp);  // the sub-chunk's first step (always run)
       __syncthreads();
       const int Ls = min(kSub, L - ts);
       // A fixed trip count, unrolled, so that every pass's LDS reads issue together rather than one round trip per
