@@ -283,7 +283,7 @@ __global__ __launch_bounds__((Layout<NPT, LPR>::kThreads)) void rec_bwd_kernel(R
   __shared__ float Qs[kQGlobal ? 1 : kChunk][Dk];
   __shared__ float DYs[kChunk][kRows], Es[kChunk][kRows];
   __shared__ float Gs[kChunk], Bs[kChunk];
-  __shared__ float red[kSub][kWaves][2 * Dk];  // per step and wave: column sums of (dq | dk) over the wave's rows
+  __shared__ __align__(16) float red[kSub][kWaves][2 * Dk];  // per step and wave: column sums of (dq | dk) over the wave's rows
   __shared__ float rowv[kSub][3][kRows];       // per step and row: dv, dbeta, dg (factor)
 
   const Item it = item_of(a.tab, a.nblk, a.Hv, a.Hk, a.total);
@@ -398,11 +398,11 @@ __global__ __launch_bounds__((Layout<NPT, LPR>::kThreads)) void rec_bwd_kernel(R
         } else {
           dd = sum_lanes<LPR>(dd);
         }
-        const float du = -bt * dd;
+        const float du = -bt * dd, dug = du * gt;
         float dg = 0.f;
 #pragma unroll
         for (int i = 0; i < NPT; ++i) {
-          pk[i] = ds[i] * d + du * (gt * S[j][i]);
+          pk[i] = ds[i] * d + dug * S[j][i];
           ds[i] += du * kk[i];
           dg += ds[i] * S[j][i];
           ds[i] *= gt;
@@ -420,20 +420,25 @@ __global__ __launch_bounds__((Layout<NPT, LPR>::kThreads)) void rec_bwd_kernel(R
       if constexpr (LPR == 32) rowv[0][2][rl] = sum_lanes<LPR>(dgp);  // the sub-chunk's first step (always run)
       __syncthreads();
       const int Ls = min(kSub, L - ts);
-      // A fixed trip count, unrolled, so that every pass's LDS reads issue together rather than one round trip per
-      // pass; passes past the sub-chunk's last step store nothing.
-      constexpr int kPasses = (kSub * 2 * Dk + kThreads - 1) / kThreads;
+      // Four columns per thread and pass (16-byte reads and stores), a fixed trip count, unrolled, so that every
+      // pass's LDS reads issue together rather than one round trip per pass; passes past the sub-chunk's last step
+      // store nothing. The waves' sums add in wave order.
+      constexpr int kU = Dk / 2;  // 4-column units of a step's (dq | dk) row
+      constexpr int kPasses = (kSub * kU + kThreads - 1) / kThreads;
 #pragma unroll
       for (int pss = 0; pss < kPasses; ++pss) {
         const int e = tid + pss * kThreads;
-        if (e < Ls * 2 * Dk) {
-          const int j = e / (2 * Dk), col = e % (2 * Dk);
-          float acc = 0.f;
+        if (e < Ls * kU) {
+          const int j = e / kU, col = (e % kU) * 4;
+          float4 acc = *reinterpret_cast<const float4*>(&red[j][0][col]);
 #pragma unroll
-          for (int w = 0; w < kWaves; ++w) acc += red[j][w][col];
+          for (int w = 1; w < kWaves; ++w) {
+            const float4 x = *reinterpret_cast<const float4*>(&red[j][w][col]);
+            acc.x += x.x, acc.y += x.y, acc.z += x.z, acc.w += x.w;
+          }
           const int64_t at = (((tok + ts + j) * a.Hv + hv) * a.nblk + it.blk) * Dk;
           float* dst = col < Dk ? a.dq_part + at + col : a.dk_part + at + col - Dk;
-          *dst = acc;
+          *reinterpret_cast<float4*>(dst) = acc;
         }
       }
       for (int e = tid; e < Ls * kRows; e += kThreads) {
