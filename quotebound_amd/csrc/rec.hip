@@ -115,15 +115,16 @@ __device__ __forceinline__ void stage_rows(float (*Xs)[kRows], const InT* x, int
   }
 }
 
-// Per-step scalars: the decay factor (exp of the log-decay when g_is_log) and beta.
-template <int kThr, typename InT>
-__device__ __forceinline__ void stage_scalars(float* Gs, float* Bs, const float* g, const InT* beta, int64_t tok,
-                                              int Hv, int hv, int L, int g_is_log) {
+// Per-step scalars: the decay factor (exp of the log-decay when g_is_log) and beta, as the first two of W floats
+// per step (the step's scalars are read together, one vector read at a uniform address).
+template <int kThr, int W, typename InT>
+__device__ __forceinline__ void stage_scalars(float (*GB)[W], const float* g, const InT* beta, int64_t tok, int Hv,
+                                              int hv, int L, int g_is_log) {
   for (int tt = threadIdx.x; tt < L; tt += kThr) {
     const int64_t i = (tok + tt) * Hv + hv;
     const float gv = g[i];
-    Gs[tt] = g_is_log ? expf(gv) : gv;
-    Bs[tt] = IO<InT>::ld(beta, i);
+    GB[tt][0] = g_is_log ? expf(gv) : gv;
+    GB[tt][1] = IO<InT>::ld(beta, i);
   }
 }
 
@@ -136,7 +137,7 @@ __global__ __launch_bounds__((Layout<NPT, LPR>::kThreads)) void rec_fwd_kernel(R
   __shared__ float Qs[kChunk][Dk];
   __shared__ float Vs[kChunk][kRows];
   __shared__ float2 YEs[kChunk][kRows];  // y and e = v - u per step and row
-  __shared__ float Gs[kChunk], Bs[kChunk], KQs[kChunk];
+  __shared__ __align__(16) float GBK[kChunk][4];  // per step: decay factor, beta, k.q
 
   const Item it = item_of(a.tab, a.nblk, a.Hv, a.Hk, a.total);
   const int tid = threadIdx.x, lane = tid & 63;
@@ -169,7 +170,7 @@ __global__ __launch_bounds__((Layout<NPT, LPR>::kThreads)) void rec_fwd_kernel(R
     __syncthreads();  // the previous chunk's LDS readers are done
     stage_kq<kThreads>(Ks, Qs, (const InT*)k, (const InT*)q, tok, a.Hk, hk, L);
     stage_rows<kThreads>(Vs, v, tok, a.Hv, hv, a.Dv, row0, L);
-    stage_scalars<kThreads>(Gs, Bs, a.p.g, beta, tok, a.Hv, hv, L, a.g_is_log);
+    stage_scalars<kThreads>(GBK, a.p.g, beta, tok, a.Hv, hv, L, a.g_is_log);
     __syncthreads();
     // k.q per step: groups of LPR lanes, one step each at a time.
     for (int tt = tid / LPR; tt < kChunk; tt += kThreads / LPR) {
@@ -177,7 +178,7 @@ __global__ __launch_bounds__((Layout<NPT, LPR>::kThreads)) void rec_fwd_kernel(R
 #pragma unroll
       for (int i = 0; i < NPT; ++i) kq += Ks[tt][col_of<NPT, LPR>(cl, i)] * Qs[tt][col_of<NPT, LPR>(cl, i)];
       kq = sum_lanes<LPR>(kq);
-      if (cl == 0) KQs[tt] = kq;
+      if (cl == 0) GBK[tt][2] = kq;
     }
     __syncthreads();
 #pragma unroll 2
@@ -194,10 +195,11 @@ __global__ __launch_bounds__((Layout<NPT, LPR>::kThreads)) void rec_fwd_kernel(R
         pa = sum_lanes<LPR>(pa);
         pb = sum_lanes<LPR>(pb);
       }
-      const float gt = Gs[tt], bt = Bs[tt];
+      const float4 gbk = *reinterpret_cast<const float4*>(GBK[tt]);
+      const float gt = gbk.x, bt = gbk.y;
       const float e = Vs[tt][rl] - gt * pa;
       const float d = bt * e;
-      const float yv = gt * pb + d * KQs[tt];
+      const float yv = gt * pb + d * gbk.z;
 #pragma unroll
       for (int i = 0; i < NPT; ++i) s[i] = gt * s[i] + d * kk[i];
       YEs[tt][rl] = float2{yv, e};  // every lane of the row holds the same bits: a store without a branch
@@ -282,7 +284,7 @@ __global__ __launch_bounds__((Layout<NPT, LPR>::kThreads)) void rec_bwd_kernel(R
   __shared__ float Ks[kChunk][Dk];
   __shared__ float Qs[kQGlobal ? 1 : kChunk][Dk];
   __shared__ float DYs[kChunk][kRows], Es[kChunk][kRows];
-  __shared__ float Gs[kChunk], Bs[kChunk];
+  __shared__ __align__(8) float GB[kChunk][2];  // per step: decay factor, beta
   __shared__ __align__(16) float red[kSub][kWaves][2 * Dk];  // per step and wave: column sums of (dq | dk) over the wave's rows
   __shared__ float rowv[kSub][3][kRows];       // per step and row: dv, dbeta, dg (factor)
 
@@ -313,7 +315,7 @@ __global__ __launch_bounds__((Layout<NPT, LPR>::kThreads)) void rec_bwd_kernel(R
     stage_kq<kThreads>(Ks, kQGlobal ? nullptr : Qs, k, q, tok, a.Hk, hk, L);
     stage_rows<kThreads>(Es, a.e_res, tok, a.Hv, hv, a.Dv, row0, L);
     stage_rows<kThreads>(DYs, dy, tok, a.Hv, hv, a.Dv, row0, L);
-    stage_scalars<kThreads>(Gs, Bs, a.p.g, beta, tok, a.Hv, hv, L, a.g_is_log);
+    stage_scalars<kThreads>(GB, a.p.g, beta, tok, a.Hv, hv, L, a.g_is_log);
     float st[NPT];
     {
       const float* src = a.p.ckpt + ((sq.slot0 + c) * a.Hv + hv) * SS + int64_t(row) * Dk;
@@ -335,7 +337,8 @@ __global__ __launch_bounds__((Layout<NPT, LPR>::kThreads)) void rec_bwd_kernel(R
       for (int j = 0; j < kSub; ++j) {
         const int tt = m * kSub + j;
         if (tt < L) {
-          const float gt = Gs[tt], d = Bs[tt] * Es[tt][rl];
+          const float2 gb = *reinterpret_cast<const float2*>(GB[tt]);
+          const float gt = gb.x, d = gb.y * Es[tt][rl];
 #pragma unroll
           for (int i = 0; i < NPT; ++i) st[i] = gt * st[i] + d * Ks[tt][col_of<NPT, LPR>(cl, i)];
         }
@@ -359,7 +362,8 @@ __global__ __launch_bounds__((Layout<NPT, LPR>::kThreads)) void rec_bwd_kernel(R
       for (int j = 0; j < kSub; ++j) {
         const int tt = ts + j;
         if (tt < L) {
-          const float gt = Gs[tt], d = Bs[tt] * Es[tt][rl];
+          const float2 gb = *reinterpret_cast<const float2*>(GB[tt]);
+          const float gt = gb.x, d = gb.y * Es[tt][rl];
 #pragma unroll
           for (int i = 0; i < NPT; ++i) S[j + 1][i] = gt * S[j][i] + d * Ks[tt][col_of<NPT, LPR>(cl, i)];
         } else {
@@ -380,7 +384,8 @@ __global__ __launch_bounds__((Layout<NPT, LPR>::kThreads)) void rec_bwd_kernel(R
           kk[i] = Ks[tt][col_of<NPT, LPR>(cl, i)];
           qq[i] = kQGlobal ? IO<InT>::ld(q, ((tok + tt) * a.Hk + hk) * Dk + col_of<NPT, LPR>(cl, i)) : Qs[tt][col_of<NPT, LPR>(cl, i)];
         }
-        const float gt = Gs[tt], bt = Bs[tt], dyt = DYs[tt][rl], e = Es[tt][rl], d = bt * e;
+        const float2 gb = *reinterpret_cast<const float2*>(GB[tt]);
+        const float gt = gb.x, bt = gb.y, dyt = DYs[tt][rl], e = Es[tt][rl], d = bt * e;
         float dd = 0.f;
 #pragma unroll
         for (int i = 0; i < NPT; ++i) {
