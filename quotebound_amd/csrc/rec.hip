@@ -181,34 +181,43 @@ __global__ __launch_bounds__((Layout<NPT, LPR>::kThreads)) void rec_fwd_kernel(R
       if (cl == 0) GBK[tt][2] = kq;
     }
     __syncthreads();
-#pragma unroll 2
-    for (int tt = 0; tt < L; ++tt) {
+    auto step = [&](const int tt) {
       float kk[NPT], qq[NPT];
 #pragma unroll
       for (int i = 0; i < NPT; ++i) kk[i] = Ks[tt][col_of<NPT, LPR>(cl, i)], qq[i] = Qs[tt][col_of<NPT, LPR>(cl, i)];
       float pa = 0.f, pb = 0.f;
 #pragma unroll
-      for (int i = 0; i < NPT; ++i) pa += s[i] * kk[i], pb += s[i] * qq[i];
+      for (int i = 0; i < NPT; ++i) pa = fmaf(s[i], kk[i], pa), pb = fmaf(s[i], qq[i], pb);
       if constexpr (LPR == 32) {
         sum32_pair(pa, pb);
       } else {
         pa = sum_lanes<LPR>(pa);
         pb = sum_lanes<LPR>(pb);
       }
+      // Each rounding written out (fmaf), so that both copies of the step below, in every variant of the kernel,
+      // form the same bits: a multi-token call and one-token calls from its per-token states agree exactly.
       const float4 gbk = *reinterpret_cast<const float4*>(GBK[tt]);
       const float gt = gbk.x, bt = gbk.y;
-      const float e = Vs[tt][rl] - gt * pa;
+      const float e = fmaf(-gt, pa, Vs[tt][rl]);
       const float d = bt * e;
-      const float yv = gt * pb + d * gbk.z;
+      const float yv = fmaf(gt, pb, d * gbk.z);
 #pragma unroll
-      for (int i = 0; i < NPT; ++i) s[i] = gt * s[i] + d * kk[i];
+      for (int i = 0; i < NPT; ++i) s[i] = fmaf(gt, s[i], d * kk[i]);
       YEs[tt][rl] = float2{yv, e};  // every lane of the row holds the same bits: a store without a branch
       if (kKeepRows && live) {  // the state after this token
         float* dst = a.p.rows + ((tok + tt) * a.Hv + hv) * SS + int64_t(row) * Dk;
 #pragma unroll
         for (int i = 0; i < NPT; ++i) dst[col_of<NPT, LPR>(cl, i)] = s[i];
       }
+    };
+    // Steps in pairs, written out (the compiler does not unroll a loop of lane swaps with a run-time count), so that
+    // the two copies alternate their registers instead of copying the state at every step.
+    int tt = 0;
+    for (; tt + 1 < L; tt += 2) {
+      step(tt);
+      step(tt + 1);
     }
+    if (tt < L) step(tt);
     __syncthreads();
     for (int e = tid; e < L * kRows; e += kThreads) {
       const int tt = e / kRows, j = e % kRows;
