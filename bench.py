@@ -476,7 +476,8 @@ def measure_workload(torch, hip, lib, w, designs, steps, warmup):
 
 def run_t_sweep(torch, hip, lib, design, steps=10, warmup=2):
     """The reference bench's sweep (reference tests/bench_grad.cpp:38-68, 124-130): the recurrence at the 4B head
-    shape (B=1, Hk=16, Hv=32, Dk=Dv=128) for T in 128, 512, 1024, 2048, forward and forward + backward."""
+    shape (B=1, Hk=16, Hv=32, Dk=Dv=128) for T in 128, 512, 1024, 2048, forward and forward + backward, with each
+    kernel's time (what dominates at short T)."""
     from quotebound_amd.synthetic import Workload, make_inputs, to_device
 
     out = {"unit": "ms (HIP events around the library's kernels)", "design": DESIGN_NAMES[design]}
@@ -488,7 +489,7 @@ def run_t_sweep(torch, hip, lib, design, steps=10, warmup=2):
             out[str(T)] = {"unavailable": why}
             continue
         out[str(T)] = {"fwd_ms": r["fwd_ms"], "fwd_bwd_ms": r["ms_per_step"],
-                       "tokens_per_s": T / (r["ms_per_step"] * 1e-3)}
+                       "tokens_per_s": T / (r["ms_per_step"] * 1e-3), "kernels_ms": r["kernels_ms"]}
     return out
 
 
