@@ -64,12 +64,12 @@ struct Scratch {
   Scratch& operator=(const Scratch&) = delete;
 };
 
-// The design the adapters run: the chunked one where the library supports the shape and T > 16, else the recurrent
-// one, which is the faster at a few steps (a one-token decode call takes about 6.6 us with it and 15 us with the
-// chunked design's two launches at the 4B layer shape).
+// The design the adapters run: the chunked one where the library supports the shape and T > 48, else the recurrent
+// one, which is the faster at a few dozen steps (4B layer shape, launches included: forward + backward 54.8 against
+// 59.7 us at T = 48, 66.5 against 60.0 us at T = 64; a one-token decode call about 6 us against 15 us).
 int pick_design(qb_gdn_desc d) {
   char err[16];
-  if (d.T <= 16) return QB_GDN_RECURRENT;
+  if (d.T <= 48) return QB_GDN_RECURRENT;
   d.design = QB_GDN_CHUNKED;
   if (qb_gdn_validate(&d, err, sizeof err) == 0) return QB_GDN_CHUNKED;
   return QB_GDN_RECURRENT;
