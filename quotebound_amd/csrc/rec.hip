@@ -452,7 +452,9 @@ __global__ __launch_bounds__((Layout<NPT, LPR>::kThreads)) void rec_bwd_kernel(R
           }
           const int64_t at = (((tok + ts + j) * a.Hv + hv) * a.nblk + it.blk) * Dk;
           float* dst = col < Dk ? a.dq_part + at + col : a.dk_part + at + col - Dk;
-          *reinterpret_cast<float4*>(dst) = acc;
+          // Written once and read once by the reduction: streaming stores.
+          typedef float v4f __attribute__((ext_vector_type(4)));
+          __builtin_nontemporal_store(v4f{acc.x, acc.y, acc.z, acc.w}, reinterpret_cast<v4f*>(dst));
         }
       }
       for (int e = tid; e < Ls * kRows; e += kThreads) {
@@ -496,8 +498,10 @@ __global__ __launch_bounds__(256) void rec_reduce_kernel(const float* dq_part, c
     float4 aq = {0.f, 0.f, 0.f, 0.f}, ak = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll 8
     for (int pr = 0; pr < np; ++pr) {
-      const float4 xq = *reinterpret_cast<const float4*>(dq_part + (base + pr) * Dk + c);
-      const float4 xk = *reinterpret_cast<const float4*>(dk_part + (base + pr) * Dk + c);
+      // Read once: streaming loads (the partials are not reused).
+      typedef float v4f __attribute__((ext_vector_type(4)));
+      const v4f xq = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(dq_part + (base + pr) * Dk + c));
+      const v4f xk = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(dk_part + (base + pr) * Dk + c));
       aq.x += xq.x, aq.y += xq.y, aq.z += xq.z, aq.w += xq.w;
       ak.x += xk.x, ak.y += xk.y, ak.z += xk.z, ak.w += xk.w;
     }
