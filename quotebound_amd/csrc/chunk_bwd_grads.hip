@@ -130,14 +130,10 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
 #pragma unroll
     for (int q4 = 0; q4 < 4; ++q4) ti.tp[q4] = tri_ld8(tr, q4 * kTri, lt >> 3, (lt & 7) * 8);
   };
-  // S0 and dS rows, each read once: streaming loads.
   auto load_rows = [&](float4 (&x)[2], const float* base, const Item& it, int hv, int r0, int lt) {
-    typedef float v4f __attribute__((ext_vector_type(4)));
     const float* p = base + ((it.slot * a.Hv + hv) * a.Dv + r0) * Dk + (lt >> 4) * Dk + (lt & 15) * 8;
-    const v4f u0 = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(p));
-    const v4f u1 = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(p + 4));
-    x[0] = float4{u0.x, u0.y, u0.z, u0.w};
-    x[1] = float4{u1.x, u1.y, u1.z, u1.w};
+    x[0] = *reinterpret_cast<const float4*>(p);
+    x[1] = *reinterpret_cast<const float4*>(p + 4);
   };
   auto load_dy_v = [&](BlockIn& b, const Item& it, int hv, int r0, int lt) {
     const int g = (lt >> 4) & 3, li = lt & 15, pw = (lt >> 6) & 3, hw = lt >> 8;

@@ -206,7 +206,7 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_state_kernel(ChunkArgs a) 
       for (int t = 0; t < 2; ++t) {
         const int col = 32 * wp + 16 * t + 4 * g;
         put4(dSm[0], dSm[1], swz(li, col, kLS), dS[t]);
-        BufIO<float>::st4<kStreamNT>(out, uint32_t(li * Dk + col), dS[t]);  // read once, by the gradient kernel
+        BufIO<float>::st4(out, uint32_t(li * Dk + col), dS[t]);
       }
     }
     __syncthreads();

@@ -251,7 +251,7 @@ __global__ __launch_bounds__(kThreads) void chunk_fwd_kernel(ChunkArgs a) {
       for (int t = 0; t < 2; ++t) {
         const int col = 32 * wp + 16 * t + 4 * g;
         put4(Sm[0], Sm[1], swz(li, col, kLS), S[t]);
-        BufIO<float>::st4<kStreamNT>(ck, uint32_t(li * Dk + col), S[t]);  // read once, by the gradient kernel
+        BufIO<float>::st4(ck, uint32_t(li * Dk + col), S[t]);
       }
     }
     __syncthreads();  // S in LDS: the output group forms R from it

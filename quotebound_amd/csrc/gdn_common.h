@@ -81,22 +81,17 @@ __device__ __forceinline__ float buf_ld4(__amdgpu_buffer_rsrc_t r, uint32_t byte
 
 template <typename T>
 struct BufIO;
-// The cache-policy operand of a buffer access that streams (gfx950: the nt bit): for data touched once, so that it
-// does not push data that is reused out of the caches.
-constexpr int kStreamNT = 2;
-
 template <>
 struct BufIO<float> {
   static __device__ __forceinline__ void st(__amdgpu_buffer_rsrc_t r, uint32_t i, float x) {
     __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x), r, int(i * 4), 0, 0);
   }
-  // Elements i .. i + 3 (i a multiple of 4) in one 16-byte store; kAux is the store's cache policy (kStreamNT for data
-  // written once and read once, later).
-  template <int kAux = 0, typename V4>
+  // Elements i .. i + 3 (i a multiple of 4) in one 16-byte store.
+  template <typename V4>
   static __device__ __forceinline__ void st4(__amdgpu_buffer_rsrc_t r, uint32_t i, const V4& x) {
     typedef __attribute__((__vector_size__(4 * sizeof(uint32_t)))) uint32_t u32x4;
     const u32x4 v = {__float_as_uint(x[0]), __float_as_uint(x[1]), __float_as_uint(x[2]), __float_as_uint(x[3])};
-    __builtin_amdgcn_raw_buffer_store_b128(v, r, int(i * 4), 0, kAux);
+    __builtin_amdgcn_raw_buffer_store_b128(v, r, int(i * 4), 0, 0);
   }
 };
 template <>
