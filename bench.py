@@ -144,7 +144,8 @@ def roofline_of(kind, amount, ms):
 
 def run_design(torch, hip, lib, w, dev, design, steps, warmup):
     """Times `steps` fwd+bwd steps after `warmup`, then runs as many with the library's trace events for each
-    kernel's duration; returns wall ms/step (of the uninstrumented steps) and per-kernel mean ms."""
+    kernel's duration, then as many again with the caches flushed before the forward and before the backward;
+    returns wall ms/step (of the uninstrumented steps), per-kernel mean ms, and the cold-cache step and kernels."""
     B, T, Hk, Hv, Dk, Dv = w.B, w.T, w.Hk, w.Hv, w.Dk, w.Dv
     cu = w.cu_seqlens
     dt = lib.BF16 if w.dtype == "bf16" else lib.F32
@@ -170,15 +171,19 @@ def run_design(torch, hip, lib, w, dev, design, steps, warmup):
     nf, nb = len(fnames) + 1, len(bnames) + 1
     evs = [[hip.event() for _ in range(nf + nb)] for _ in range(steps)]
 
-    def step(i=None):
+    def step(i=None, flush=None):
         if i is not None:
             keep1 = lib.set_trace(desc_f, evs[i][:nf])
             keep2 = lib.set_trace(desc_b, evs[i][nf:])
         else:
             desc_f.trace_events, desc_f.n_trace_events = None, 0
             desc_b.trace_events, desc_b.n_trace_events = None, 0
+        if flush is not None:
+            flush.sum()
         lib.fwd(desc_f, p(dev["q"]), p(dev["k"]), p(dev["v"]), p(dev["g"]), p(dev["beta"]), p(dev["s0"]), p(y),
                 p(s_out), p(ckpt), p(ws), stream)
+        if flush is not None:
+            flush.sum()
         lib.bwd(desc_b, p(dev["q"]), p(dev["k"]), p(dev["v"]), p(dev["g"]), p(dev["beta"]), p(ckpt), p(dev["dy"]),
                 p(dev["ds_out"]), p(dq), p(dk), p(dv), p(dg), p(dbeta), p(ds0), p(ws), stream)
         if i is not None:
@@ -204,6 +209,23 @@ def run_design(torch, hip, lib, w, dev, design, steps, warmup):
             per.setdefault(n, []).append(hip.elapsed_ms(e[nf + j], e[nf + j + 1]))
     fwd_ms = sum(hip.elapsed_ms(evs[i][0], evs[i][nf - 1]) for i in range(steps)) / steps
     bwd_ms = sum(hip.elapsed_ms(evs[i][nf], evs[i][nf + nb - 1]) for i in range(steps)) / steps
+    # The same steps with the caches holding none of the step's data: a 512 MB read of an unrelated buffer before the
+    # forward and before the backward (in training, other layers run between them). The kernels' spans, flushes
+    # excluded.
+    flush = torch.ones(128 << 20, dtype=torch.float32, device="cuda")
+    for i in range(steps):
+        step(i, flush)
+    torch.cuda.synchronize()
+    cold = {}
+    for i in range(steps):
+        e = evs[i]
+        for j, n in enumerate(fnames):
+            cold.setdefault(n, []).append(hip.elapsed_ms(e[j], e[j + 1]))
+        for j, n in enumerate(bnames):
+            cold.setdefault(n, []).append(hip.elapsed_ms(e[nf + j], e[nf + j + 1]))
+    cold_ms = sum(hip.elapsed_ms(evs[i][0], evs[i][nf - 1]) + hip.elapsed_ms(evs[i][nf], evs[i][nf + nb - 1])
+                  for i in range(steps)) / steps
+    del flush
     for row in evs:
         for e in row:
             hip.lib.hipEventDestroy(ctypes.c_void_p(e))
@@ -211,7 +233,9 @@ def run_design(torch, hip, lib, w, dev, design, steps, warmup):
     kernels = {n: sum(v) / len(v) for n, v in per.items()}
     nc = lib.num_chunks(desc_f)
     tiles = lib.ckpt_bytes(desc_f) - nc * Hv * Dv * Dk * 4
-    return {"ms_per_step": wall_ms, "fwd_ms": fwd_ms, "bwd_ms": bwd_ms, "kernels_ms": kernels, "nc": nc,
+    return {"ms_per_step": wall_ms, "fwd_ms": fwd_ms, "bwd_ms": bwd_ms, "kernels_ms": kernels,
+            "cold_caches": {"ms_per_step": cold_ms, "kernels_ms": {n: sum(v) / len(v) for n, v in cold.items()}},
+            "nc": nc,
             "tiles_bytes": tiles}, None
 
 
