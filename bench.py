@@ -11,7 +11,8 @@ moves (chunk tiles, chunk-end cotangents) are reported apart as design_bytes_per
 step against the compulsory I/O plus the checkpoints written once and read once. cpu_baseline times the oracle (the
 CPU restatement, float32, OpenMP) on the host on the same inputs.
 
-The line also carries the 9B and packed 4B layer shapes (workloads, each with its own rooflines), the reference
+The line also carries the 9B and packed 4B layer shapes and the 4B shape with float32 activations, the dtype of the
+reference op (workloads, each with its own rooflines; float32 runs on the recurrent design), the reference
 bench's T sweep at the 4B head shape (t_sweep), the one-token inference step (decode), the layer's pointwise
 neighbours and the LoRA training step; --path-only leaves those out.
 
@@ -579,7 +580,7 @@ def main():
     if not args.path_only:
         # The other layer shapes of the same metric, each with its own rooflines.
         out["workloads"] = {}
-        for name in ("qwen35_9b", "qwen35_4b_varlen"):
+        for name in ("qwen35_9b", "qwen35_4b_varlen", "qwen35_4b_f32"):
             summary, _ = measure_workload(torch, hip, lib, workload(name), designs, args.steps, args.warmup)
             out["workloads"][name] = summary
         best = lib.CHUNKED if head["design"] == "chunked" else lib.RECURRENT

@@ -118,7 +118,8 @@ def varlen_lengths(seed: int, n: int = 8, lo: int = 256, hi: int = 2048) -> list
 
 
 def workload(name: str) -> Workload:
-    """The named workloads: the tiny fp32 case, the Qwen3.5-4B and -9B layer shapes and the packed batch."""
+    """The named workloads: the tiny fp32 case, the Qwen3.5-4B and -9B layer shapes, the packed batch, and the 4B
+    shape with float32 activations."""
     if name == "tiny":
         return Workload("tiny", 1, 64, 2, 2, 32, 32, dtype="f32", seed=0, clip_log_decay=None)
     if name == "qwen35_4b":
@@ -128,10 +129,12 @@ def workload(name: str) -> Workload:
     if name == "qwen35_4b_varlen":
         lens = varlen_lengths(3)
         return Workload("qwen35_4b_varlen", 1, sum(lens), 16, 32, 128, 128, seed=3, seq_lens=lens)
+    if name == "qwen35_4b_f32":  # the 4B layer shape with float32 activations, the reference op's own dtype
+        return Workload("qwen35_4b_f32", 1, 4096, 16, 32, 128, 128, dtype="f32", seed=1)
     raise KeyError(name)
 
 
-WORKLOADS = ("tiny", "qwen35_4b", "qwen35_9b", "qwen35_4b_varlen")
+WORKLOADS = ("tiny", "qwen35_4b", "qwen35_9b", "qwen35_4b_varlen", "qwen35_4b_f32")
 
 
 def to_device(inp: Inputs, device="cuda"):
