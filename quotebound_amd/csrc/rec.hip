@@ -133,11 +133,16 @@ template <int NPT, int LPR, typename InT, typename OutT, bool kKeepRows>
 __global__ __launch_bounds__((Layout<NPT, LPR>::kThreads)) void rec_fwd_kernel(RecFwdArgs a) {
   using Lay = Layout<NPT, LPR>;
   constexpr int Dk = LPR * NPT, kRows = Lay::kRows, kThreads = Lay::kThreads;
-  __shared__ float Ks[kChunk][Dk];
-  __shared__ float Qs[kChunk][Dk];
-  __shared__ float Vs[kChunk][kRows];
-  __shared__ float2 YEs[kChunk][kRows];  // y and e = v - u per step and row
-  __shared__ __align__(16) float GBK[kChunk][4];  // per step: decay factor, beta, k.q
+  // One LDS array, the small per-step arrays first: at low addresses every access to them takes an immediate offset
+  // from one base register (a ds_read reaches 64 KB past its address) instead of a materialized address per step.
+  constexpr int oGBK = 0, oV = oGBK + kChunk * 4 * 4, oYE = oV + kChunk * kRows * 4, oK = oYE + kChunk * kRows * 8;
+  constexpr int oQ = oK + kChunk * Dk * 4, kLdsBytes = oQ + kChunk * Dk * 4;
+  __shared__ __align__(16) unsigned char lds[kLdsBytes];
+  auto GBK = reinterpret_cast<float (*)[4]>(lds + oGBK);  // per step: decay factor, beta, k.q
+  auto Vs = reinterpret_cast<float (*)[kRows]>(lds + oV);
+  auto YEs = reinterpret_cast<float2 (*)[kRows]>(lds + oYE);  // y and e = v - u per step and row
+  auto Ks = reinterpret_cast<float (*)[Dk]>(lds + oK);
+  auto Qs = reinterpret_cast<float (*)[Dk]>(lds + oQ);
 
   const Item it = item_of(a.tab, a.nblk, a.Hv, a.Hk, a.total);
   const int tid = threadIdx.x, lane = tid & 63;
@@ -290,12 +295,19 @@ __global__ __launch_bounds__((Layout<NPT, LPR>::kThreads)) void rec_bwd_kernel(R
   using Lay = Layout<NPT, LPR>;
   constexpr int Dk = LPR * NPT, kRows = Lay::kRows, kThreads = Lay::kThreads, kWaves = Lay::kWaves;
   constexpr bool kQGlobal = Dk > 128;
-  __shared__ float Ks[kChunk][Dk];
-  __shared__ float Qs[kQGlobal ? 1 : kChunk][Dk];
-  __shared__ float DYs[kChunk][kRows], Es[kChunk][kRows];
-  __shared__ __align__(8) float GB[kChunk][2];  // per step: decay factor, beta
-  __shared__ __align__(16) float red[kSub][kWaves][2 * Dk];  // per step and wave: column sums of (dq | dk) over the wave's rows
-  __shared__ float rowv[kSub][3][kRows];       // per step and row: dv, dbeta, dg (factor)
+  // One LDS array, the small per-step arrays first (low addresses: immediate offsets from one base register).
+  constexpr int oGB = 0, oDY = oGB + kChunk * 2 * 4, oE = oDY + kChunk * kRows * 4, oRow = oE + kChunk * kRows * 4;
+  constexpr int oRed = (oRow + kSub * 3 * kRows * 4 + 15) / 16 * 16, oK = oRed + kSub * kWaves * 2 * Dk * 4;
+  constexpr int oQ = oK + kChunk * Dk * 4, kLdsBytes = oQ + (kQGlobal ? 1 : kChunk) * Dk * 4;
+  __shared__ __align__(16) unsigned char lds[kLdsBytes];
+  auto GB = reinterpret_cast<float (*)[2]>(lds + oGB);  // per step: decay factor, beta
+  auto DYs = reinterpret_cast<float (*)[kRows]>(lds + oDY);
+  auto Es = reinterpret_cast<float (*)[kRows]>(lds + oE);
+  auto rowv = reinterpret_cast<float (*)[3][kRows]>(lds + oRow);  // per step and row: dv, dbeta, dg (factor)
+  // per step and wave: column sums of (dq | dk) over the wave's rows
+  auto red = reinterpret_cast<float (*)[kWaves][2 * Dk]>(lds + oRed);
+  auto Ks = reinterpret_cast<float (*)[Dk]>(lds + oK);
+  auto Qs = reinterpret_cast<float (*)[Dk]>(lds + oQ);
 
   const Item it = item_of(a.tab, a.nblk, a.Hv, a.Hk, a.total);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
