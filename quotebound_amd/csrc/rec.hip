@@ -89,9 +89,13 @@ __device__ __forceinline__ Item item_of(const SeqTable& tab, int nblk, int Hv, i
   return Item{it.blk, it.hv, it.n};
 }
 
+// The staging of a chunk's steps [0, L). With kPad, the steps [L, 64) past a sequence's end are staged as identity
+// steps (zero k, q, dy and e, decay factor 1, beta 0), which leave the state and its cotangent unchanged bit for bit,
+// so the backward's unrolled steps need no check of their own.
+
 // Stages rows [t0, t0 + L) of the key head's k (and q, when Qs is not null) into LDS as float32, 8 elements per
 // access.
-template <int kThr, int Dk, typename InT>
+template <int kThr, bool kPad = false, int Dk, typename InT>
 __device__ __forceinline__ void stage_kq(float (*Ks)[Dk], float (*Qs)[Dk], const InT* k, const InT* q,
                                          int64_t tok, int Hk, int hk, int L) {
   constexpr int V8 = Dk / 8;
@@ -101,30 +105,43 @@ __device__ __forceinline__ void stage_kq(float (*Ks)[Dk], float (*Qs)[Dk], const
       const int64_t off = ((tok + tt) * Hk + hk) * Dk + c8;
       IO<InT>::ld8(k + off, &Ks[tt][c8]);
       if (Qs) IO<InT>::ld8(q + off, &Qs[tt][c8]);
+    } else if (kPad) {
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        Ks[tt][c8 + u] = 0.f;
+        if (Qs) Qs[tt][c8 + u] = 0.f;
+      }
     }
   }
 }
 
 // Stages a [T, Hv, Dv] tensor's kRows-row slice of rows [t0, t0 + L) (zeros past Dv).
-template <int kThr, int kRows, typename InT>
+template <int kThr, bool kPad = false, int kRows, typename InT>
 __device__ __forceinline__ void stage_rows(float (*Xs)[kRows], const InT* x, int64_t tok, int Hv, int hv, int Dv,
                                            int row0, int L) {
   for (int e = threadIdx.x; e < kChunk * kRows; e += kThr) {
     const int tt = e / kRows, j = e % kRows;
-    if (tt < L) Xs[tt][j] = (row0 + j < Dv) ? IO<InT>::ld(x, ((tok + tt) * Hv + hv) * Dv + row0 + j) : 0.f;
+    if (tt < L)
+      Xs[tt][j] = (row0 + j < Dv) ? IO<InT>::ld(x, ((tok + tt) * Hv + hv) * Dv + row0 + j) : 0.f;
+    else if (kPad)
+      Xs[tt][j] = 0.f;
   }
 }
 
 // Per-step scalars: the decay factor (exp of the log-decay when g_is_log) and beta, as the first two of W floats
 // per step (the step's scalars are read together, one vector read at a uniform address).
-template <int kThr, int W, typename InT>
+template <int kThr, bool kPad = false, int W, typename InT>
 __device__ __forceinline__ void stage_scalars(float (*GB)[W], const float* g, const InT* beta, int64_t tok, int Hv,
                                               int hv, int L, int g_is_log) {
-  for (int tt = threadIdx.x; tt < L; tt += kThr) {
-    const int64_t i = (tok + tt) * Hv + hv;
-    const float gv = g[i];
-    GB[tt][0] = g_is_log ? expf(gv) : gv;
-    GB[tt][1] = IO<InT>::ld(beta, i);
+  for (int tt = threadIdx.x; tt < (kPad ? kChunk : L); tt += kThr) {
+    if (tt < L) {
+      const int64_t i = (tok + tt) * Hv + hv;
+      const float gv = g[i];
+      GB[tt][0] = g_is_log ? expf(gv) : gv;
+      GB[tt][1] = IO<InT>::ld(beta, i);
+    } else {
+      GB[tt][0] = 1.f, GB[tt][1] = 0.f;
+    }
   }
 }
 
@@ -295,6 +312,9 @@ __global__ __launch_bounds__((Layout<NPT, LPR>::kThreads)) void rec_bwd_kernel(R
   using Lay = Layout<NPT, LPR>;
   constexpr int Dk = LPR * NPT, kRows = Lay::kRows, kThreads = Lay::kThreads, kWaves = Lay::kWaves;
   constexpr bool kQGlobal = Dk > 128;
+  // Steps past a sequence's end staged as identity steps (the stage_ helpers), so the unrolled steps run unchecked;
+  // not with kQGlobal, whose reverse steps read q from global memory, where such a step has no row.
+  constexpr bool kPad = !kQGlobal;
   // One LDS array, the small per-step arrays first (low addresses: immediate offsets from one base register).
   constexpr int oGB = 0, oDY = oGB + kChunk * 2 * 4, oE = oDY + kChunk * kRows * 4, oRow = oE + kChunk * kRows * 4;
   constexpr int oRed = (oRow + kSub * 3 * kRows * 4 + 15) / 16 * 16, oK = oRed + kSub * kWaves * 2 * Dk * 4;
@@ -333,10 +353,10 @@ __global__ __launch_bounds__((Layout<NPT, LPR>::kThreads)) void rec_bwd_kernel(R
     const int t0 = c * kChunk, L = min(kChunk, sq.len - t0);
     const int64_t tok = sq.tok0 + t0;
     __syncthreads();
-    stage_kq<kThreads>(Ks, kQGlobal ? nullptr : Qs, k, q, tok, a.Hk, hk, L);
-    stage_rows<kThreads>(Es, a.e_res, tok, a.Hv, hv, a.Dv, row0, L);
-    stage_rows<kThreads>(DYs, dy, tok, a.Hv, hv, a.Dv, row0, L);
-    stage_scalars<kThreads>(GB, a.p.g, beta, tok, a.Hv, hv, L, a.g_is_log);
+    stage_kq<kThreads, kPad>(Ks, kQGlobal ? nullptr : Qs, k, q, tok, a.Hk, hk, L);
+    stage_rows<kThreads, kPad>(Es, a.e_res, tok, a.Hv, hv, a.Dv, row0, L);
+    stage_rows<kThreads, kPad>(DYs, dy, tok, a.Hv, hv, a.Dv, row0, L);
+    stage_scalars<kThreads, kPad>(GB, a.p.g, beta, tok, a.Hv, hv, L, a.g_is_log);
     float st[NPT];
     {
       const float* src = a.p.ckpt + ((sq.slot0 + c) * a.Hv + hv) * SS + int64_t(row) * Dk;
@@ -357,7 +377,7 @@ __global__ __launch_bounds__((Layout<NPT, LPR>::kThreads)) void rec_bwd_kernel(R
 #pragma unroll
       for (int j = 0; j < kSub; ++j) {
         const int tt = m * kSub + j;
-        if (tt < L) {
+        if (kPad || tt < L) {
           const float2 gb = *reinterpret_cast<const float2*>(GB[tt]);
           const float gt = gb.x, d = gb.y * Es[tt][rl];
 #pragma unroll
@@ -382,7 +402,7 @@ __global__ __launch_bounds__((Layout<NPT, LPR>::kThreads)) void rec_bwd_kernel(R
 #pragma unroll
       for (int j = 0; j < kSub; ++j) {
         const int tt = ts + j;
-        if (tt < L) {
+        if (kPad || tt < L) {
           const float2 gb = *reinterpret_cast<const float2*>(GB[tt]);
           const float gt = gb.x, d = gb.y * Es[tt][rl];
 #pragma unroll
@@ -398,7 +418,7 @@ __global__ __launch_bounds__((Layout<NPT, LPR>::kThreads)) void rec_bwd_kernel(R
 #pragma unroll
       for (int j = kSub - 1; j >= 0; --j) {
         const int tt = ts + j;
-        if (tt >= L) continue;
+        if (!kPad && tt >= L) continue;
         float kk[NPT], qq[NPT], pq[NPT], pk[NPT];
 #pragma unroll
         for (int i = 0; i < NPT; ++i) {
