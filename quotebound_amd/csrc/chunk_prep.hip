@@ -1,6 +1,7 @@
-// Chunked design, kernel 1 (prep), one block per (chunk slot, value head): everything about the chunk that does not
-// depend on the state, written once as MFMA-ready operands (the Tile record, chunk_common.h: T, Tb and P as bf16
-// hi/lo pairs of their lower-triangular blocks).
+// Chunked design, kernel 1 (prep), one block per (chunk slot, key head): K K^T and Q K^T once, then for each value
+// head of the key head's group everything about the chunk that does not depend on the state, written once as
+// MFMA-ready operands (the Tile record, chunk_common.h: T, Tb and P as bf16 hi/lo pairs of their lower-triangular
+// blocks).
 //   G = cumsum of the log-decays (fp64, so G_i - G_j keeps its bits when |G| is large)
 //   A = strict_lower(diag(beta) (E * K K^T)),  T = (I + A)^-1,  Tb = T diag(beta)
 //   P = lower_incl(E * Q K^T),  E_ij = exp(G_i - G_j)
@@ -34,8 +35,8 @@ static_assert(kPoff + 2 * kTri * 2 <= kKQBytes, "A, T and P fit in the k/q stagi
 
 // kFused: the layer's prologue in front (qb_gdn_fwd_prologue). The block reads q_raw, k_raw, a and b in place of
 // q, k, g and beta and forms them as the separate prologue pass does, bit for bit (prologue_math.h; a row's sum of
-// squares is the same in-lane sum over 8 consecutive elements and DPP reduction over its 16 lanes). It writes beta and
-// the log-decay of its value head, and the first value head of each key head's group writes q and k.
+// squares is the same in-lane sum over 8 consecutive elements and DPP reduction over its 16 lanes). It writes q and k
+// of its key head and beta and the log-decay of each of its value heads.
 template <bool kFused>
 __global__ __launch_bounds__(kThreads) void chunk_prep_kernel(ChunkArgs a) {
   __shared__ __align__(16) unsigned char smem[kKQBytes];
@@ -47,19 +48,17 @@ __global__ __launch_bounds__(kThreads) void chunk_prep_kernel(ChunkArgs a) {
   float* Tm = reinterpret_cast<float*>(smem + kToff);
   __bf16* Pp = reinterpret_cast<__bf16*>(smem + kPoff);  // hi; lo at + kTri
 
-  const int total = int(a.lay.NC) * a.Hv;
+  const int total = int(a.lay.NC) * a.Hk, grp = a.Hv / a.Hk;
   const int wid = xcd_remap(blockIdx.x, total);
-  const int64_t slot = wid / a.Hv;
-  const int hv = wid % a.Hv, hk = hv / (a.Hv / a.Hk);
+  const int64_t slot = wid / a.Hk;
+  const int hk = wid % a.Hk;
   const SlotPos sp = slot_pos(a.tab, slot);
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 4, li = lane & 15;
-  Tile* tile = a.tiles + (slot * a.Hv + hv);
 
-  // g and beta first (one wave), then the K and Q rows, through buffer resources that end at the chunk's last row
-  // (rows past it read as zeros); all issued before any is used.
+  // A value head's log-decay and beta for the chunk's rows (one wave), through buffer resources that end at the
+  // chunk's last row (rows past it read as zeros).
   const uint32_t L = uint32_t(sp.L);
-  float gx = 0.f, bx = 0.f;
-  if (tid < kC) {
+  auto load_scalars = [&](const int hv, float& gx, float& bx) {
     const int64_t s0 = sp.tok * a.Hv + hv;
     const uint32_t n = L == 0 ? 0u : (L - 1) * uint32_t(a.Hv) + 1;  // elements from s0 to the chunk's last row
     if constexpr (kFused) {
@@ -78,7 +77,10 @@ __global__ __launch_bounds__(kThreads) void chunk_prep_kernel(ChunkArgs a) {
       gx = buf_ld4(gr, uint32_t(tid * a.Hv) * 4);
       bx = bf16_to_f32(buf_ld2(br, uint32_t(tid * a.Hv) * 2));
     }
-  }
+  };
+  float gx = 0.f, bx = 0.f;
+  if (tid < kC) load_scalars(hk * grp, gx, bx);
+  // The key head's K and Q rows, read once for every value head of its group; all issued before any is used.
   {
     const int sk = a.Hk * 128;
     const uint32_t bytes = L * uint32_t(sk) * 2u;
@@ -93,8 +95,8 @@ __global__ __launch_bounds__(kThreads) void chunk_prep_kernel(ChunkArgs a) {
       qv[q4] = buf_ld16(qr, uint32_t(t * sk + c8) * 2);
     }
     if constexpr (kFused) {
-      // Normalise each row (16 lanes of 8 elements); rows past the chunk's end are zeros and stay zeros.
-      const bool writer = hv % (a.Hv / a.Hk) == 0;
+      // Normalise each row (16 lanes of 8 elements) and write it; rows past the chunk's end are zeros and stay
+      // zeros.
       const auto ko = buffer_rsrc(a.pro.k + sp.tok * sk + hk * 128, bytes);
       const auto qo = buffer_rsrc(a.pro.q + sp.tok * sk + hk * 128, bytes);
       auto norm = [&](uint4& u, float s) {
@@ -111,10 +113,8 @@ __global__ __launch_bounds__(kThreads) void chunk_prep_kernel(ChunkArgs a) {
         const int e = tid + kThreads * q4, t = e >> 4, c8 = (e & 15) * 8;
         norm(kv[q4], a.pro.scale_k);
         norm(qv[q4], a.pro.scale_q);
-        if (writer) {
-          buf_st16(ko, uint32_t(t * sk + c8) * 2, kv[q4]);
-          buf_st16(qo, uint32_t(t * sk + c8) * 2, qv[q4]);
-        }
+        buf_st16(ko, uint32_t(t * sk + c8) * 2, kv[q4]);
+        buf_st16(qo, uint32_t(t * sk + c8) * 2, qv[q4]);
       }
     }
 #pragma unroll
@@ -124,31 +124,11 @@ __global__ __launch_bounds__(kThreads) void chunk_prep_kernel(ChunkArgs a) {
       *reinterpret_cast<uint4*>(Qb + t * kLDK + c8) = qv[q4];
     }
   }
-  // One wave: G = the inclusive prefix sum of the log-decays, accumulated in fp64 by a shuffle scan (so G_i - G_j
-  // keeps its bits when |G| is large).
-  if (tid < kC) {
-    const int t = tid;
-    // The log-decay floored at -150: a factor of 0 (or a log-decay of -inf) would make G_i - G_j NaN on every pair
-    // across it; at -150 each exp(.) across it is 0 in float32, as the factor 0 makes it.
-    double G = uint32_t(t) < L ? fmax(kFused || a.g_is_log ? double(gx) : double(logf(gx)), kLogFloor) : 0.0;
-#pragma unroll
-    for (int off = 1; off < kC; off <<= 1) {
-      const double u = __shfl_up(G, off);
-      if (t >= off) G += u;
-    }
-    const double Glast = __shfl(G, kC - 1);
-    Gd[t] = G;
-    Bs[t] = uint32_t(t) < L ? bx : 0.f;
-    tile->beta[t] = Bs[t];
-    tile->gam[t] = expf(float(G));
-    tile->dec[t] = expf(float(Glast - G));
-    tile->G[t] = float(G);
-  }
   __syncthreads();
 
-  // The ten lower-triangular 16 x 16 blocks (I, J) of A and P, block b = tri_off order, round-robin over the waves
-  // (three, three, two, two): K K^T and Q K^T on MFMA, lane -> column j = 16 J + li, rows i = 16 I + 4g + jj. The
-  // results wait in registers until every wave is done with the k and q rows, whose bytes A and P then take.
+  // The ten lower-triangular 16 x 16 blocks (I, J) of K K^T and Q K^T, block b = tri_off order, round-robin over the
+  // waves (three, three, two, two), on MFMA: lane -> column j = 16 J + li, rows i = 16 I + 4g + jj. They stay in
+  // registers for every value head of the group; A and P take the k and q rows' bytes once every wave is done.
   f32x4 kk[3], qk[3];
 #pragma unroll
   for (int u = 0; u < 3; ++u) {
@@ -164,104 +144,138 @@ __global__ __launch_bounds__(kThreads) void chunk_prep_kernel(ChunkArgs a) {
       }
     }
   }
-  __syncthreads();
-#pragma unroll
-  for (int u = 0; u < 3; ++u) {
-    const int b = w + 4 * u;
-    if (b < 10) {
-      const int I = (b >= 1) + (b >= 3) + (b >= 6), J = b - I * (I + 1) / 2;
-#pragma unroll
-      for (int jj = 0; jj < 4; ++jj) {
-        const int i = 16 * I + 4 * g + jj, j = 16 * J + li, at = tri_off(i, j);
-        // The hardware exponential: its error (a few ulp) is far below the 2^-17 of the hi/lo split that carries E.
-        const float e = j <= i ? __expf(float(Gd[i] - Gd[j])) : 0.f;
-        Am[at] = j < i ? Bs[i] * e * kk[u][jj] : 0.f;
-        const float x = e * qk[u][jj];
-        const __bf16 h = (__bf16)x;
-        Pp[at] = h;
-        Pp[kTri + at] = (__bf16)(x - (float)h);
-      }
-    }
-  }
-  __syncthreads();
-  // P, hi and lo, to the tile: the packed bytes as they are, 16 bytes per thread and step.
-  for (int u = tid; u < 2 * kTri / 8; u += kThreads)
-    *reinterpret_cast<uint4*>(tile->p[0] + 8 * u) = *reinterpret_cast<const uint4*>(Pp + 8 * u);
 
-  // Diagonal blocks: thread -> column j of block bd; the column lives in registers through the substitution.
-  if (tid < kC) {
-    const int bd = tid >> 4, jl = tid & 15, b0 = 16 * bd;
-    float x[16];
+  for (int vh = 0; vh < grp; ++vh) {
+    const int hv = hk * grp + vh;
+    Tile* tile = a.tiles + (slot * a.Hv + hv);
+    // The thread's indices re-formed from an opaque copy of its id, so that the compiler does not keep the LDS
+    // addresses of one head's inverse in registers for the next (they would take the registers of two more waves).
+    int tidv = threadIdx.x;
+    asm volatile("" : "+v"(tidv));
+    const int tid = tidv, lane = tid & 63, w = tid >> 6, g = lane >> 4, li = lane & 15;
+    // The first pass: every wave is done with the k and q rows. Later ones: done with the previous head's G, beta,
+    // A, T and P.
+    __syncthreads();
+    // One wave: G = the inclusive prefix sum of the log-decays, accumulated in fp64 by a shuffle scan (so G_i - G_j
+    // keeps its bits when |G| is large). Then the next value head's scalars are read, to arrive during this head.
+    if (tid < kC) {
+      const int t = tid;
+      // The log-decay floored at -150: a factor of 0 (or a log-decay of -inf) would make G_i - G_j NaN on every pair
+      // across it; at -150 each exp(.) across it is 0 in float32, as the factor 0 makes it.
+      double G = uint32_t(t) < L ? fmax(kFused || a.g_is_log ? double(gx) : double(logf(gx)), kLogFloor) : 0.0;
 #pragma unroll
-    for (int il = 0; il < 16; ++il) {
-      float v = il == jl ? 1.f : 0.f;
-#pragma unroll
-      for (int kl = 0; kl < il; ++kl) v -= Am[tri_off(b0 + il, b0 + kl)] * x[kl];  // x[kl] = 0 for kl < jl
-      x[il] = il >= jl ? v : 0.f;
-    }
-#pragma unroll
-    for (int il = 0; il < 16; ++il) Tm[tri_off(b0 + il, b0 + jl)] = x[il];
-  }
-  __syncthreads();
-  // Off-diagonal blocks at distance d = I - J, one wave per block (wave w: I = d + w, J = w), on MFMA with split
-  // float32 operands:
-  //   W = sum_{J <= K < I} A_IK T_KJ    16 x 16 x 16d, k zero-padded to a multiple of 32
-  //   T_IJ = -T_II W                    16 x 16 x 16, with W's result tile as the B operand (k = W's rows)
-  for (int d = 1; d < 4; ++d) {
-    if (w < 4 - d) {
-      const int I = d + w, J = w;
-      f32x4 W = zero4();
-      for (int s = 0; s < (d + 1) / 2; ++s) {
-        const int k0 = 16 * J + 32 * s + 8 * g;
-        const bool in = k0 < 16 * I;  // whole groups of 8 columns are in or out
-        float x[8], y[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          x[j] = in ? Am[tri_off(16 * I + li, k0 + j)] : 0.f;  // A rows 16 I + li, columns k
-          y[j] = in ? Tm[tri_off(k0 + j, 16 * J + li)] : 0.f;  // T rows k, column 16 J + li
-        }
-        W = mma3(W, split8(x), split8(y));
+      for (int off = 1; off < kC; off <<= 1) {
+        const double u = __shfl_up(G, off);
+        if (t >= off) G += u;
       }
-      uint2 th, tl, wh, wl;  // T_II rows li, k = 4g + j, and W, as packed hi / lo pairs
-      {
-        const int r = 16 * I + li, c = 16 * I + 4 * g;
-        split2(Tm[tri_off(r, c)], Tm[tri_off(r, c + 1)], th.x, tl.x);
-        split2(Tm[tri_off(r, c + 2)], Tm[tri_off(r, c + 3)], th.y, tl.y);
-        split2(W[0], W[1], wh.x, wl.x);
-        split2(W[2], W[3], wh.y, wl.y);
-      }
-      f32x4 R = zero4();
-      const auto v4 = [](uint2 x) { return __builtin_bit_cast(s16x4, x); };
-      R = mma16(R, v4(th), v4(wh));
-      R = mma16(R, v4(th), v4(wl));
-      R = mma16(R, v4(tl), v4(wh));
-#pragma unroll
-      for (int jj = 0; jj < 4; ++jj) Tm[tri_off(16 * I + 4 * g + jj, 16 * J + li)] = -R[jj];
+      const double Glast = __shfl(G, kC - 1);
+      Gd[t] = G;
+      Bs[t] = uint32_t(t) < L ? bx : 0.f;
+      tile->beta[t] = Bs[t];
+      tile->gam[t] = expf(float(G));
+      tile->dec[t] = expf(float(Glast - G));
+      tile->G[t] = float(G);
+      if (vh + 1 < grp) load_scalars(hv + 1, gx, bx);
     }
     __syncthreads();
-  }
-
-  // T and Tb = T diag(beta), hi and lo, on and below the diagonal blocks: thread -> row tid / 4, columns
-  // 16 (tid % 4) .. + 15.
-  {
-    const int i = tid >> 2, j0 = (tid & 3) * 16;
-    if ((j0 >> 4) <= (i >> 4)) {
-      uint32_t th[8], tl[8], bh[8], bl[8];  // packed bf16 pairs, columns j0 + 2p, j0 + 2p + 1
 #pragma unroll
-      for (int p2 = 0; p2 < 8; ++p2) {
-        const int j = j0 + 2 * p2;
-        const float t0 = Tm[tri_off(i, j)], t1 = Tm[tri_off(i, j + 1)];
-        split2(t0, t1, th[p2], tl[p2]);
-        split2(t0 * Bs[j], t1 * Bs[j + 1], bh[p2], bl[p2]);
+    for (int u = 0; u < 3; ++u) {
+      const int b = w + 4 * u;
+      if (b < 10) {
+        const int I = (b >= 1) + (b >= 3) + (b >= 6), J = b - I * (I + 1) / 2;
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          const int i = 16 * I + 4 * g + jj, j = 16 * J + li, at = tri_off(i, j);
+          // The hardware exponential: its error (a few ulp) is far below the 2^-17 of the hi/lo split that carries E.
+          const float e = j <= i ? __expf(float(Gd[i] - Gd[j])) : 0.f;
+          Am[at] = j < i ? Bs[i] * e * kk[u][jj] : 0.f;
+          const float x = e * qk[u][jj];
+          const __bf16 h = (__bf16)x;
+          Pp[at] = h;
+          Pp[kTri + at] = (__bf16)(x - (float)h);
+        }
       }
-      const int at = tri_off(i, j0);
+    }
+    __syncthreads();
+    // P, hi and lo, to the tile: the packed bytes as they are, 16 bytes per thread and step.
+    for (int u = tid; u < 2 * kTri / 8; u += kThreads)
+      *reinterpret_cast<uint4*>(tile->p[0] + 8 * u) = *reinterpret_cast<const uint4*>(Pp + 8 * u);
+
+    // Diagonal blocks: thread -> column j of block bd; the column lives in registers through the substitution.
+    if (tid < kC) {
+      const int bd = tid >> 4, jl = tid & 15, b0 = 16 * bd;
+      float x[16];
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int q = 4 * h;
-        *reinterpret_cast<uint4*>(tile->t[0] + at + 8 * h) = uint4{th[q], th[q + 1], th[q + 2], th[q + 3]};
-        *reinterpret_cast<uint4*>(tile->t[1] + at + 8 * h) = uint4{tl[q], tl[q + 1], tl[q + 2], tl[q + 3]};
-        *reinterpret_cast<uint4*>(tile->tb[0] + at + 8 * h) = uint4{bh[q], bh[q + 1], bh[q + 2], bh[q + 3]};
-        *reinterpret_cast<uint4*>(tile->tb[1] + at + 8 * h) = uint4{bl[q], bl[q + 1], bl[q + 2], bl[q + 3]};
+      for (int il = 0; il < 16; ++il) {
+        float v = il == jl ? 1.f : 0.f;
+#pragma unroll
+        for (int kl = 0; kl < il; ++kl) v -= Am[tri_off(b0 + il, b0 + kl)] * x[kl];  // x[kl] = 0 for kl < jl
+        x[il] = il >= jl ? v : 0.f;
+      }
+#pragma unroll
+      for (int il = 0; il < 16; ++il) Tm[tri_off(b0 + il, b0 + jl)] = x[il];
+    }
+    __syncthreads();
+    // Off-diagonal blocks at distance d = I - J, one wave per block (wave w: I = d + w, J = w), on MFMA with split
+    // float32 operands:
+    //   W = sum_{J <= K < I} A_IK T_KJ    16 x 16 x 16d, k zero-padded to a multiple of 32
+    //   T_IJ = -T_II W                    16 x 16 x 16, with W's result tile as the B operand (k = W's rows)
+    for (int d = 1; d < 4; ++d) {
+      if (w < 4 - d) {
+        const int I = d + w, J = w;
+        f32x4 W = zero4();
+        for (int s = 0; s < (d + 1) / 2; ++s) {
+          const int k0 = 16 * J + 32 * s + 8 * g;
+          const bool in = k0 < 16 * I;  // whole groups of 8 columns are in or out
+          float x[8], y[8];
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            x[j] = in ? Am[tri_off(16 * I + li, k0 + j)] : 0.f;  // A rows 16 I + li, columns k
+            y[j] = in ? Tm[tri_off(k0 + j, 16 * J + li)] : 0.f;  // T rows k, column 16 J + li
+          }
+          W = mma3(W, split8(x), split8(y));
+        }
+        uint2 th, tl, wh, wl;  // T_II rows li, k = 4g + j, and W, as packed hi / lo pairs
+        {
+          const int r = 16 * I + li, c = 16 * I + 4 * g;
+          split2(Tm[tri_off(r, c)], Tm[tri_off(r, c + 1)], th.x, tl.x);
+          split2(Tm[tri_off(r, c + 2)], Tm[tri_off(r, c + 3)], th.y, tl.y);
+          split2(W[0], W[1], wh.x, wl.x);
+          split2(W[2], W[3], wh.y, wl.y);
+        }
+        f32x4 R = zero4();
+        const auto v4 = [](uint2 x) { return __builtin_bit_cast(s16x4, x); };
+        R = mma16(R, v4(th), v4(wh));
+        R = mma16(R, v4(th), v4(wl));
+        R = mma16(R, v4(tl), v4(wh));
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) Tm[tri_off(16 * I + 4 * g + jj, 16 * J + li)] = -R[jj];
+      }
+      __syncthreads();
+    }
+
+    // T and Tb = T diag(beta), hi and lo, on and below the diagonal blocks: thread -> row tid / 4, columns
+    // 16 (tid % 4) .. + 15.
+    {
+      const int i = tid >> 2, j0 = (tid & 3) * 16;
+      if ((j0 >> 4) <= (i >> 4)) {
+        uint32_t th[8], tl[8], bh[8], bl[8];  // packed bf16 pairs, columns j0 + 2p, j0 + 2p + 1
+#pragma unroll
+        for (int p2 = 0; p2 < 8; ++p2) {
+          const int j = j0 + 2 * p2;
+          const float t0 = Tm[tri_off(i, j)], t1 = Tm[tri_off(i, j + 1)];
+          split2(t0, t1, th[p2], tl[p2]);
+          split2(t0 * Bs[j], t1 * Bs[j + 1], bh[p2], bl[p2]);
+        }
+        const int at = tri_off(i, j0);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int q = 4 * h;
+          *reinterpret_cast<uint4*>(tile->t[0] + at + 8 * h) = uint4{th[q], th[q + 1], th[q + 2], th[q + 3]};
+          *reinterpret_cast<uint4*>(tile->t[1] + at + 8 * h) = uint4{tl[q], tl[q + 1], tl[q + 2], tl[q + 3]};
+          *reinterpret_cast<uint4*>(tile->tb[0] + at + 8 * h) = uint4{bh[q], bh[q + 1], bh[q + 2], bh[q + 3]};
+          *reinterpret_cast<uint4*>(tile->tb[1] + at + 8 * h) = uint4{bl[q], bl[q + 1], bl[q + 2], bl[q + 3]};
+        }
       }
     }
   }
@@ -270,7 +284,7 @@ __global__ __launch_bounds__(kThreads) void chunk_prep_kernel(ChunkArgs a) {
 }  // namespace
 
 hipError_t launch_chunk_prep(const ChunkArgs& a, hipStream_t s, bool fused_prologue) {
-  const int total = int(a.lay.NC) * a.Hv;
+  const int total = int(a.lay.NC) * a.Hk;  // one block per (chunk slot, key head)
   if (total == 0) return hipSuccess;
   if (fused_prologue)
     hipLaunchKernelGGL(chunk_prep_kernel<true>, dim3(total), dim3(kThreads), 0, s, a);
