@@ -1,7 +1,7 @@
-// Chunked design, kernel 1 (prep), one block per (chunk slot, key head): K K^T and Q K^T once, then for each value
-// head of the key head's group everything about the chunk that does not depend on the state, written once as
-// MFMA-ready operands (the Tile record, chunk_common.h: T, Tb and P as bf16 hi/lo pairs of their lower-triangular
-// blocks).
+// Chunked design, kernel 1 (prep), one block per (chunk slot, value head), or per (chunk slot, key head) when that
+// grid would not fit on the device at once: everything about the chunk that does not depend on the state, written
+// once as MFMA-ready operands (the Tile record, chunk_common.h: T, Tb and P as bf16 hi/lo pairs of their
+// lower-triangular blocks).
 //   G = cumsum of the log-decays (fp64, so G_i - G_j keeps its bits when |G| is large)
 //   A = strict_lower(diag(beta) (E * K K^T)),  T = (I + A)^-1,  Tb = T diag(beta)
 //   P = lower_incl(E * Q K^T),  E_ij = exp(G_i - G_j)
@@ -35,10 +35,13 @@ static_assert(kPoff + 2 * kTri * 2 <= kKQBytes, "A, T and P fit in the k/q stagi
 
 // kFused: the layer's prologue in front (qb_gdn_fwd_prologue). The block reads q_raw, k_raw, a and b in place of
 // q, k, g and beta and forms them as the separate prologue pass does, bit for bit (prologue_math.h; a row's sum of
-// squares is the same in-lane sum over 8 consecutive elements and DPP reduction over its 16 lanes). It writes q and k
-// of its key head and beta and the log-decay of each of its value heads.
+// squares is the same in-lane sum over 8 consecutive elements and DPP reduction over its 16 lanes). It writes beta and
+// the log-decay of each of its value heads, and the block of a key head's first value head writes q and k.
+//
+// hpb: value heads per block, 1 or the key head's whole group (Hv / Hk). A block forms K K^T and Q K^T once for its
+// heads and then works through them in turn.
 template <bool kFused>
-__global__ __launch_bounds__(kThreads) void chunk_prep_kernel(ChunkArgs a) {
+__global__ __launch_bounds__(kThreads) void chunk_prep_kernel(ChunkArgs a, int hpb) {
   __shared__ __align__(16) unsigned char smem[kKQBytes];
   __shared__ double Gd[kC];
   __shared__ float Bs[kC];
@@ -48,10 +51,10 @@ __global__ __launch_bounds__(kThreads) void chunk_prep_kernel(ChunkArgs a) {
   float* Tm = reinterpret_cast<float*>(smem + kToff);
   __bf16* Pp = reinterpret_cast<__bf16*>(smem + kPoff);  // hi; lo at + kTri
 
-  const int total = int(a.lay.NC) * a.Hk, grp = a.Hv / a.Hk;
+  const int units = a.Hv / hpb, total = int(a.lay.NC) * units, grp = a.Hv / a.Hk;
   const int wid = xcd_remap(blockIdx.x, total);
-  const int64_t slot = wid / a.Hk;
-  const int hk = wid % a.Hk;
+  const int64_t slot = wid / units;
+  const int hv0 = (wid % units) * hpb, hk = hv0 / grp;
   const SlotPos sp = slot_pos(a.tab, slot);
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 4, li = lane & 15;
 
@@ -79,7 +82,7 @@ __global__ __launch_bounds__(kThreads) void chunk_prep_kernel(ChunkArgs a) {
     }
   };
   float gx = 0.f, bx = 0.f;
-  if (tid < kC) load_scalars(hk * grp, gx, bx);
+  if (tid < kC) load_scalars(hv0, gx, bx);
   // The key head's K and Q rows, read once for every value head of its group; all issued before any is used.
   {
     const int sk = a.Hk * 128;
@@ -95,8 +98,9 @@ __global__ __launch_bounds__(kThreads) void chunk_prep_kernel(ChunkArgs a) {
       qv[q4] = buf_ld16(qr, uint32_t(t * sk + c8) * 2);
     }
     if constexpr (kFused) {
-      // Normalise each row (16 lanes of 8 elements) and write it; rows past the chunk's end are zeros and stay
-      // zeros.
+      // Normalise each row (16 lanes of 8 elements); rows past the chunk's end are zeros and stay zeros. The block
+      // of the group's first value head writes them.
+      const bool writer = hv0 % grp == 0;
       const auto ko = buffer_rsrc(a.pro.k + sp.tok * sk + hk * 128, bytes);
       const auto qo = buffer_rsrc(a.pro.q + sp.tok * sk + hk * 128, bytes);
       auto norm = [&](uint4& u, float s) {
@@ -113,8 +117,10 @@ __global__ __launch_bounds__(kThreads) void chunk_prep_kernel(ChunkArgs a) {
         const int e = tid + kThreads * q4, t = e >> 4, c8 = (e & 15) * 8;
         norm(kv[q4], a.pro.scale_k);
         norm(qv[q4], a.pro.scale_q);
-        buf_st16(ko, uint32_t(t * sk + c8) * 2, kv[q4]);
-        buf_st16(qo, uint32_t(t * sk + c8) * 2, qv[q4]);
+        if (writer) {
+          buf_st16(ko, uint32_t(t * sk + c8) * 2, kv[q4]);
+          buf_st16(qo, uint32_t(t * sk + c8) * 2, qv[q4]);
+        }
       }
     }
 #pragma unroll
@@ -145,8 +151,8 @@ __global__ __launch_bounds__(kThreads) void chunk_prep_kernel(ChunkArgs a) {
     }
   }
 
-  for (int vh = 0; vh < grp; ++vh) {
-    const int hv = hk * grp + vh;
+  for (int vh = 0; vh < hpb; ++vh) {
+    const int hv = hv0 + vh;
     Tile* tile = a.tiles + (slot * a.Hv + hv);
     // The thread's indices re-formed from an opaque copy of its id, so that the compiler does not keep the LDS
     // addresses of one head's inverse in registers for the next (they would take the registers of two more waves).
@@ -175,7 +181,7 @@ __global__ __launch_bounds__(kThreads) void chunk_prep_kernel(ChunkArgs a) {
       tile->gam[t] = expf(float(G));
       tile->dec[t] = expf(float(Glast - G));
       tile->G[t] = float(G);
-      if (vh + 1 < grp) load_scalars(hv + 1, gx, bx);
+      if (vh + 1 < hpb) load_scalars(hv + 1, gx, bx);
     }
     __syncthreads();
 #pragma unroll
@@ -284,12 +290,21 @@ __global__ __launch_bounds__(kThreads) void chunk_prep_kernel(ChunkArgs a) {
 }  // namespace
 
 hipError_t launch_chunk_prep(const ChunkArgs& a, hipStream_t s, bool fused_prologue) {
-  const int total = int(a.lay.NC) * a.Hk;  // one block per (chunk slot, key head)
-  if (total == 0) return hipSuccess;
+  if (a.lay.NC == 0) return hipSuccess;
+  // One block per (chunk slot, value head) while those blocks fit on the device at once (four per CU: 37 KB of LDS
+  // and at most 128 registers each), so that a short sequence's heads run side by side; past that, one per (chunk
+  // slot, key head), which reads the group's k and q rows and forms K K^T and Q K^T once for all its value heads and
+  // needs half (or a third) of the rounds.
+  int dev = 0, cus = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  if (e != hipSuccess) return e;
+  const int hpb = int64_t(a.lay.NC) * a.Hv <= int64_t(4) * cus ? 1 : a.Hv / a.Hk;
+  const dim3 grid(int(a.lay.NC) * (a.Hv / hpb));
   if (fused_prologue)
-    hipLaunchKernelGGL(chunk_prep_kernel<true>, dim3(total), dim3(kThreads), 0, s, a);
+    hipLaunchKernelGGL(chunk_prep_kernel<true>, grid, dim3(kThreads), 0, s, a, hpb);
   else
-    hipLaunchKernelGGL(chunk_prep_kernel<false>, dim3(total), dim3(kThreads), 0, s, a);
+    hipLaunchKernelGGL(chunk_prep_kernel<false>, grid, dim3(kThreads), 0, s, a, hpb);
   return hipGetLastError();
 }
 
