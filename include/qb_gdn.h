@@ -89,8 +89,10 @@ size_t qb_gdn_ckpt_bytes(const qb_gdn_desc* desc);
  * not need to survive between calls. 0 on an invalid desc. */
 size_t qb_gdn_workspace_bytes(const qb_gdn_desc* desc);
 
-/* The kernels a call launches, in order: their count is returned and their names written comma-separated into
- * names (cut to len; may be NULL). which: 0 for qb_gdn_fwd, 1 for qb_gdn_bwd. -1 on an invalid desc. */
+/* The main kernels a call launches, in order, as its trace events time them (a small follow-up pass, such as the
+ * chunked backward's dq/dk sum for short sequences, is timed with the kernel before it): their count is returned
+ * and their names written comma-separated into names (cut to len; may be NULL). which: 0 for qb_gdn_fwd, 1 for
+ * qb_gdn_bwd. -1 on an invalid desc. */
 int qb_gdn_launches(const qb_gdn_desc* desc, int which, char* names, int len);
 
 /* Forward. s0 may be NULL (zero initial state); s_out may be NULL; ckpt may be NULL when no backward follows. */

@@ -15,6 +15,13 @@ size_t dsend_bytes(const Problem& p) { return size_t(p.NC) * p.Hv * p.Dv * p.Dk 
 // The fused prologue backward's per-(chunk slot, value head) sums, after dSend.
 size_t gate_part_bytes(const Problem& p) { return (size_t(p.NC) * p.Hv * 2 * 4 + 255) & ~size_t(255); }
 
+// Short sequences: when the (chunk slot, value head) pairs fit one per CU of the 256-CU device (NC * Hv <= 256), the
+// gradient kernel takes each value head of a GQA group as a work item of its own, so that the group's heads run side
+// by side rather than in turn, and a second pass sums their dq and dk in order. Past that, its items already fill
+// the device and the heads run in turn with dq, dk summed in registers.
+bool split_grads(const Problem& p) { return p.Hv > p.Hk && int64_t(p.NC) * p.Hv <= 256; }
+size_t dqk_part_bytes(const Problem& p) { return split_grads(p) ? size_t(p.NC) * p.Hv * 2 * 64 * p.Dk * 4 : 0; }
+
 ChunkArgs base_args(const Problem& p) {
   ChunkArgs a{};
   a.lay = layout_of(p);
@@ -47,7 +54,7 @@ const char* chunk_supports(const Problem& p) {
 size_t chunk_ckpt_bytes(const Problem& p) { return layout_of(p).bytes(); }
 
 size_t chunk_workspace_bytes(const Problem& p) {
-  const size_t a = dsend_bytes(p) + gate_part_bytes(p), b = extras_bytes(p);
+  const size_t a = dsend_bytes(p) + gate_part_bytes(p) + dqk_part_bytes(p), b = extras_bytes(p);
   return a > b ? a : b;
 }
 
@@ -115,6 +122,8 @@ hipError_t bwd_impl(const Problem& p, const PrologueGradIn* pro, const BwdPtrs& 
   a.dbeta = b.dbeta;
   a.ds0 = b.ds0;
   a.dsend = static_cast<float*>(ws);
+  if (split_grads(p))
+    a.dqk_part = reinterpret_cast<float*>(static_cast<unsigned char*>(ws) + dsend_bytes(p) + gate_part_bytes(p));
   if (pro) {
     a.pro.q_raw = static_cast<const bf16_t*>(pro->q_raw), a.pro.k_raw = static_cast<const bf16_t*>(pro->k_raw);
     a.pro.a = static_cast<const bf16_t*>(pro->a), a.pro.b = static_cast<const bf16_t*>(pro->b);
@@ -129,6 +138,8 @@ hipError_t bwd_impl(const Problem& p, const PrologueGradIn* pro, const BwdPtrs& 
   if (e != hipSuccess) return e;
   tr.mark();
   e = launch_chunk_bwd_grads(a, p.out_bf16, s, pro != nullptr);
+  // Timed with the gradient kernel. With the prologue, the sum pass also does the normalisation's backward.
+  if (e == hipSuccess && a.dqk_part) e = launch_chunk_dqk_sum(a, p.out_bf16, s, pro != nullptr);
   tr.mark();
   if (e == hipSuccess && pro) e = launch_chunk_gate_sums(a, pro->da_log, pro->ddt_bias, s);
   // With g given as the factor, dL/dg at tiny or zero factors comes from an exact replay (chunk_dgfix.hip); chunks

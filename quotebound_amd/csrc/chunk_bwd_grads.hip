@@ -92,22 +92,25 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
   Row* x1cp = reinterpret_cast<Row*>(sf + ex1c);
   Row* tpos = reinterpret_cast<Row*>(sf + etq);
 
-  const int total = int(a.lay.NC) * a.Hk, grp = a.Hv / a.Hk;
+  // Split (a.dqk_part set): one work item per (chunk slot, key head, value head), whose dq and dk go to the partials
+  // for chunk_dqk_sum_kernel; otherwise one per (chunk slot, key head), the group's value heads in turn.
+  const int grp = a.Hv / a.Hk, hs = a.dqk_part ? grp : 1, total = int(a.lay.NC) * a.Hk * hs;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 4, li = lane & 15;
   const int pw = w & 3, hw = w >> 2;  // position tile, half
   const OutT* dy = static_cast<const OutT*>(a.dy);
   const int sk = a.Hk * Dk, sv = a.Hv * a.Dv;  // token strides of k/q/dq/dk and v/dy
-  // A work item: a chunk slot and key head. The grid is persistent: block b takes items b, b + gridDim.x, ..., and
+  // A work item: a chunk slot, key head and its value heads [e0, e0 + ne). The grid is persistent: block b takes items b, b + gridDim.x, ..., and
   // gridDim.x is a multiple of 8, so all of a block's items fall in its own XCD's range of xcd_remap.
   struct Item {
     int64_t slot, tok;
-    int hk, L;
+    int hk, L, e0, ne;
   };
   auto item_at = [&](int id) {
     const int wid = xcd_remap(id, total);
-    const int64_t slot = wid / a.Hk;
+    const int64_t slot = wid / (a.Hk * hs);
+    const int rem = wid % (a.Hk * hs);
     const SlotPos sp = slot_pos(a.tab, slot);
-    return Item{slot, sp.tok, wid % a.Hk, sp.L};
+    return Item{slot, sp.tok, rem / hs, sp.L, hs > 1 ? rem % hs : 0, hs > 1 ? 1 : grp};
   };
 
   // Global reads, kept in registers from issue to staging. A value head's tile (Tb and P rows hi and lo, thread ->
@@ -165,7 +168,7 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
   BlockIn nb;
   {
     const Item first = item_at(blockIdx.x);
-    load_head(ti, nb, first, first.hk * grp);
+    load_head(ti, nb, first, first.hk * grp + first.e0);
   }
   for (int id = blockIdx.x; id < total; id += gridDim.x) {
     const Item cur = item_at(id);
@@ -186,10 +189,10 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
 #pragma unroll
     for (int t = 0; t < 4; ++t) dQ[t] = zero4(), dK[t] = zero4();
     // (K K^T)[p][m], rows p = 16 pw + 4g + jj, columns m = 16 key_tile(pw, hw, mi) + li; zero above tile pw. The same
-    // for every value head of the group: formed in the first one's end phase.
+    // for every value head of the group: formed in the item's first one's end phase.
     f32x4 kk[2];
 
-    for (int e = 0; e < grp; ++e) {
+    for (int e = cur.e0; e < cur.e0 + cur.ne; ++e) {
       const int hv = hk * grp + e;
       const int64_t sh = slot * a.Hv + hv;
       const Tile* tl = a.tiles + sh;
@@ -199,11 +202,11 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
       // same, so the compiler's waits stay exact).
       Item nx = cur;
       int nhv = hv;
-      if (e + 1 < grp) {
+      if (e + 1 < cur.e0 + cur.ne) {
         nhv = hv + 1;
       } else if (id + int(gridDim.x) < total) {
         nx = item_at(id + gridDim.x);
-        nhv = nx.hk * grp;
+        nhv = nx.hk * grp + nx.e0;
       }
       __syncthreads();
       if (tid < kC) gam[tid] = ti.sc[0], dec[tid] = ti.sc[1], bet[tid] = ti.sc[2], Gf[tid] = ti.sc[3];
@@ -508,7 +511,7 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
           const float v = sum16(tq[jj]);
           tpos[hw][i0 + jj] = v;
         }
-        if (e == 0) {
+        if (e == cur.e0) {
 #pragma unroll
           for (int mi = 0; mi < 2; ++mi) {
             const int m = key_tile(pw, hw, mi);
@@ -661,6 +664,21 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
       }
     }
 
+    if (a.dqk_part) {  // the item's value head's dq and dk, float32, [64][128] each (rows past L unused)
+      int lt = tid;
+      asm volatile("" : "+v"(lt));
+      const int g = (lt >> 4) & 3, li = lt & 15, pw = (lt >> 6) & 3, hw = lt >> 8;
+      float* pq = a.dqk_part + (slot * a.Hv + hk * grp + cur.e0) * (2 * kC * Dk);
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          const int at = (16 * pw + 4 * g + jj) * Dk + 16 * (4 * hw + t) + li;
+          pq[at] = dQ[t][jj];
+          pq[kC * Dk + at] = dK[t][jj];
+        }
+      continue;
+    }
     if constexpr (kFused) {
       // dq, dk rounded to bf16 into rows [64][128] in the end phase's bytes (E5's reads of them done), then the
       // normalisation's backward row by row, 16 lanes of 8 elements per row as in the separate pass: the raw rows,
@@ -747,10 +765,94 @@ __global__ __launch_bounds__(256) void chunk_gate_sums_kernel(const float* part,
   if (lane == 0) da_log[h] = sa, ddt_bias[h] = sd;
 }
 
+// dq, dk [tokens, Hk, Dk] of the split gradient kernel: the sum over the key head's value heads, in order, of their
+// partials. Thread -> (chunk slot, key head, position, four columns); positions past the chunk's end write nothing.
+template <typename OutT>
+__global__ __launch_bounds__(256) void chunk_dqk_sum_kernel(ChunkArgs a) {
+  constexpr int Dk = 128;
+  const int grp = a.Hv / a.Hk;
+  const int64_t id = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  const int c4 = int(id & 31), t = int((id >> 5) & (kC - 1));
+  const int64_t sh = id >> 11;  // slot * Hk + hk
+  if (sh >= a.lay.NC * a.Hk) return;
+  const int64_t slot = sh / a.Hk;
+  const int hk = int(sh % a.Hk);
+  const SlotPos sp = slot_pos(a.tab, slot);
+  if (t >= sp.L) return;
+  float4 q = make_float4(0.f, 0.f, 0.f, 0.f), k = q;
+  for (int e = 0; e < grp; ++e) {
+    const float* pq = a.dqk_part + (slot * a.Hv + hk * grp + e) * (2 * kC * Dk) + t * Dk + 4 * c4;
+    const float4 x = *reinterpret_cast<const float4*>(pq), y = *reinterpret_cast<const float4*>(pq + kC * Dk);
+    q.x += x.x, q.y += x.y, q.z += x.z, q.w += x.w;
+    k.x += y.x, k.y += y.y, k.z += y.z, k.w += y.w;
+  }
+  const int64_t at = ((sp.tok + t) * a.Hk + hk) * Dk + 4 * c4;
+  OutT* dq = static_cast<OutT*>(a.dq) + at;
+  OutT* dk = static_cast<OutT*>(a.dk) + at;
+  IO<OutT>::st(dq, 0, q.x), IO<OutT>::st(dq, 1, q.y), IO<OutT>::st(dq, 2, q.z), IO<OutT>::st(dq, 3, q.w);
+  IO<OutT>::st(dk, 0, k.x), IO<OutT>::st(dk, 1, k.y), IO<OutT>::st(dk, 2, k.z), IO<OutT>::st(dk, 3, k.w);
+}
+
+// The same with the layer's prologue behind (qb_gdn_bwd_prologue): each summed dq and dk row rounded to bf16, as
+// the unfused backward stores it, then the q/k normalisation's backward as the separate pass forms it (16 lanes of
+// 8 elements per row, the row sums on the 16-lane DPP tree), written as dq_raw and dk_raw. Thread -> (chunk slot,
+// key head, position, q or k row, 8 columns).
+__global__ __launch_bounds__(256) void chunk_dqk_sum_prologue_kernel(ChunkArgs a) {
+  constexpr int Dk = 128;
+  const int grp = a.Hv / a.Hk;
+  const int64_t id = int64_t(blockIdx.x) * 256 + threadIdx.x, rid = id >> 4;
+  const int c8 = int(id & 15) * 8, isk = int(rid & 1), t = int((rid >> 1) & (kC - 1));
+  const int64_t sh = rid >> 7;  // slot * Hk + hk; a row's 16 lanes leave together
+  if (sh >= a.lay.NC * a.Hk) return;
+  const int64_t slot = sh / a.Hk;
+  const int hk = int(sh % a.Hk);
+  const SlotPos sp = slot_pos(a.tab, slot);
+  if (t >= sp.L) return;
+  float gg[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int e = 0; e < grp; ++e) {
+    const float* pq = a.dqk_part + (slot * a.Hv + hk * grp + e) * (2 * kC * Dk) + isk * kC * Dk + t * Dk + c8;
+    const float4 x0 = *reinterpret_cast<const float4*>(pq), x1 = *reinterpret_cast<const float4*>(pq + 4);
+    gg[0] += x0.x, gg[1] += x0.y, gg[2] += x0.z, gg[3] += x0.w;
+    gg[4] += x1.x, gg[5] += x1.y, gg[6] += x1.z, gg[7] += x1.w;
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) gg[j] = bf16_to_f32(f32_to_bf16(gg[j]));
+  const int64_t at = ((sp.tok + t) * a.Hk + hk) * Dk + c8;
+  const uint4 xr = *reinterpret_cast<const uint4*>((isk ? a.pro.k_raw : a.pro.q_raw) + at);
+  float x[8];
+  const uint32_t xw[4] = {xr.x, xr.y, xr.z, xr.w};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) x[2 * j] = __uint_as_float(xw[j] << 16), x[2 * j + 1] = __uint_as_float(xw[j] & 0xffff0000u);
+  float ss, gx;
+  norm_bwd_sums(x, gg, isk ? a.pro.scale_k : a.pro.scale_q, ss, gx);
+  norm_bwd_apply(x, gg, sum16(ss), sum16(gx), Dk);
+  *reinterpret_cast<uint4*>(static_cast<bf16_t*>(isk ? a.dk : a.dq) + at) =
+      uint4{f32x2_to_bf16x2(x[0], x[1]), f32x2_to_bf16x2(x[2], x[3]), f32x2_to_bf16x2(x[4], x[5]),
+            f32x2_to_bf16x2(x[6], x[7])};
+}
+
 }  // namespace
 
+hipError_t launch_chunk_dqk_sum(const ChunkArgs& a, bool out_bf16, hipStream_t s, bool fused_prologue) {
+  if (fused_prologue) {
+    if (!out_bf16) return hipErrorInvalidValue;
+    const int64_t threads = a.lay.NC * a.Hk * kC * 2 * 16;
+    if (threads == 0) return hipSuccess;
+    hipLaunchKernelGGL(chunk_dqk_sum_prologue_kernel, dim3(unsigned((threads + 255) / 256)), dim3(256), 0, s, a);
+    return hipGetLastError();
+  }
+  const int64_t threads = a.lay.NC * a.Hk * kC * 32;
+  if (threads == 0) return hipSuccess;
+  const dim3 grid(unsigned((threads + 255) / 256));
+  if (out_bf16)
+    hipLaunchKernelGGL(chunk_dqk_sum_kernel<bf16_t>, grid, dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL(chunk_dqk_sum_kernel<float>, grid, dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
 hipError_t launch_chunk_bwd_grads(const ChunkArgs& a, bool out_bf16, hipStream_t s, bool fused_prologue) {
-  const int total = int(a.lay.NC) * a.Hk;
+  const int total = int(a.lay.NC) * a.Hk * (a.dqk_part ? a.Hv / a.Hk : 1);
   if (total == 0) return hipSuccess;
   // One resident block per CU (the kernel's LDS allows no more), looping over its items; a multiple of 8 blocks, so
   // each block's items stay on its XCD.

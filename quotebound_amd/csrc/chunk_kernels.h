@@ -25,6 +25,7 @@ struct ChunkArgs {
   void* dbeta;
   float* ds0;
   float* dsend;  // workspace: cotangent of each chunk's end state
+  float* dqk_part;  // workspace, short sequences: per (chunk slot, value head) dq and dk [64][128] float32, or null
   ChunkLayout lay;
   int Hk, Hv, Dv, g_is_log;
   int nblk;  // Dv / 16 state-row blocks
@@ -55,6 +56,7 @@ struct ChunkArgs {
 hipError_t launch_chunk_prep(const ChunkArgs& a, hipStream_t s, bool fused_prologue = false);
 hipError_t launch_chunk_fwd(const ChunkArgs& a, bool out_bf16, hipStream_t s);
 hipError_t launch_chunk_bwd_state(const ChunkArgs& a, bool out_bf16, hipStream_t s);
+hipError_t launch_chunk_dqk_sum(const ChunkArgs& a, bool out_bf16, hipStream_t s, bool fused_prologue);
 hipError_t launch_chunk_bwd_grads(const ChunkArgs& a, bool out_bf16, hipStream_t s, bool fused_prologue = false);
 hipError_t launch_chunk_gate_sums(const ChunkArgs& a, float* da_log, float* ddt_bias, hipStream_t s);
 hipError_t launch_chunk_dgfix(const ChunkArgs& a, bool out_bf16, hipStream_t s);
