@@ -65,11 +65,11 @@ struct Scratch {
 };
 
 // The design the adapters run: the chunked one where the library supports the shape and T > 48, else the recurrent
-// one, which is the faster at a few dozen steps (4B layer shape, launches included: forward + backward 54.8 against
-// 59.7 us at T = 48, 66.5 against 60.0 us at T = 64; a one-token decode call about 6 us against 15 us).
+// one, which is the faster up to a few dozen steps (4B layer shape, launches included: forward + backward 43.7
+// against 47.0 us at T = 32, 53.0 against 47.4 us at T = 48; a one-token decode call about 6 us against 15 us).
 int pick_design(qb_gdn_desc d) {
   char err[16];
-  if (d.T <= 48) return QB_GDN_RECURRENT;
+  if (d.T <= 40) return QB_GDN_RECURRENT;
   d.design = QB_GDN_CHUNKED;
   if (qb_gdn_validate(&d, err, sizeof err) == 0) return QB_GDN_CHUNKED;
   return QB_GDN_RECURRENT;

@@ -19,9 +19,9 @@ from . import _lib
 
 DEFAULT_DESIGN = None  # the chunked design where the library supports the shape and T > SHORT_T, else recurrent
 # At most this many steps per sequence, the recurrent design is the faster one (4B layer shape, launches included):
-# forward + backward 54.8 against 59.7 us at T = 48, 66.5 against 60.0 us at T = 64; a one-token decode call takes
-# about 6 us with it and 15 us with the chunked design's two launches.
-SHORT_T = 48
+# forward + backward 43.7 against 47.0 us at T = 32, 53.0 against 47.4 us at T = 48 (crossing near T = 38); a
+# one-token decode call takes about 6 us with it and 15 us with the chunked design's two launches.
+SHORT_T = 40
 
 
 def _dev_ptr(t):
