@@ -71,7 +71,9 @@ __device__ __forceinline__ int key_tile(int pw, int hw, int mi) { return pw < 2 
 // beta are rounded to bf16 as the separate pass would read them, then turned into those of q_raw, k_raw, a and b with
 // the separate pass's arithmetic (prologue_math.h); the dA_log and ddt_bias terms are summed per (chunk, value head)
 // into a.pro.part, which chunk_gate_sums_kernel sums over chunks.
-template <typename OutT, bool kFused>
+// kSplit: short sequences, a.dqk_part set (a separate instantiation, so that the long-sequence kernel carries none of
+// its indexing).
+template <typename OutT, bool kFused, bool kSplit>
 __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) {
   constexpr int Dk = 128;
   constexpr bool kExactDy = std::is_same<OutT, bf16_t>::value;
@@ -92,9 +94,9 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
   Row* x1cp = reinterpret_cast<Row*>(sf + ex1c);
   Row* tpos = reinterpret_cast<Row*>(sf + etq);
 
-  // Split (a.dqk_part set): one work item per (chunk slot, key head, value head), whose dq and dk go to the partials
-  // for chunk_dqk_sum_kernel; otherwise one per (chunk slot, key head), the group's value heads in turn.
-  const int grp = a.Hv / a.Hk, hs = a.dqk_part ? grp : 1, total = int(a.lay.NC) * a.Hk * hs;
+  // kSplit: one work item per (chunk slot, key head, value head), whose dq and dk go to the partials for
+  // chunk_dqk_sum_kernel; otherwise one per (chunk slot, key head), the group's value heads in turn.
+  const int grp = a.Hv / a.Hk, hs = kSplit ? grp : 1, total = int(a.lay.NC) * a.Hk * hs;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 4, li = lane & 15;
   const int pw = w & 3, hw = w >> 2;  // position tile, half
   const OutT* dy = static_cast<const OutT*>(a.dy);
@@ -110,7 +112,7 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
     const int64_t slot = wid / (a.Hk * hs);
     const int rem = wid % (a.Hk * hs);
     const SlotPos sp = slot_pos(a.tab, slot);
-    return Item{slot, sp.tok, rem / hs, sp.L, hs > 1 ? rem % hs : 0, hs > 1 ? 1 : grp};
+    return Item{slot, sp.tok, rem / hs, sp.L, kSplit ? rem % hs : 0, kSplit ? 1 : grp};
   };
 
   // Global reads, kept in registers from issue to staging. A value head's tile (Tb and P rows hi and lo, thread ->
@@ -664,7 +666,7 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
       }
     }
 
-    if (a.dqk_part) {  // the item's value head's dq and dk, float32, [64][128] each (rows past L unused)
+    if constexpr (kSplit) {  // the item's value head's dq and dk, float32, [64][128] each (rows past L unused)
       int lt = tid;
       asm volatile("" : "+v"(lt));
       const int g = (lt >> 4) & 3, li = lt & 15, pw = (lt >> 6) & 3, hw = lt >> 8;
@@ -861,13 +863,23 @@ hipError_t launch_chunk_bwd_grads(const ChunkArgs& a, bool out_bf16, hipStream_t
   if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
   if (e != hipSuccess) return e;
   const int grid = total <= cus ? total : (cus >= 8 ? cus & ~7 : cus);
+  const bool split = a.dqk_part != nullptr;
   if (fused_prologue) {
     if (!out_bf16) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((chunk_bwd_grads_kernel<bf16_t, true>), dim3(grid), dim3(kThreads), 0, s, a);
+    if (split)
+      hipLaunchKernelGGL((chunk_bwd_grads_kernel<bf16_t, true, true>), dim3(grid), dim3(kThreads), 0, s, a);
+    else
+      hipLaunchKernelGGL((chunk_bwd_grads_kernel<bf16_t, true, false>), dim3(grid), dim3(kThreads), 0, s, a);
   } else if (out_bf16) {
-    hipLaunchKernelGGL((chunk_bwd_grads_kernel<bf16_t, false>), dim3(grid), dim3(kThreads), 0, s, a);
+    if (split)
+      hipLaunchKernelGGL((chunk_bwd_grads_kernel<bf16_t, false, true>), dim3(grid), dim3(kThreads), 0, s, a);
+    else
+      hipLaunchKernelGGL((chunk_bwd_grads_kernel<bf16_t, false, false>), dim3(grid), dim3(kThreads), 0, s, a);
   } else {
-    hipLaunchKernelGGL((chunk_bwd_grads_kernel<float, false>), dim3(grid), dim3(kThreads), 0, s, a);
+    if (split)
+      hipLaunchKernelGGL((chunk_bwd_grads_kernel<float, false, true>), dim3(grid), dim3(kThreads), 0, s, a);
+    else
+      hipLaunchKernelGGL((chunk_bwd_grads_kernel<float, false, false>), dim3(grid), dim3(kThreads), 0, s, a);
   }
   return hipGetLastError();
 }
