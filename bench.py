@@ -503,11 +503,11 @@ def run_t_sweep(torch, hip, lib, design, steps=10, warmup=2):
     """The reference bench's sweep (reference tests/bench_grad.cpp:38-68, 124-130): the recurrence at the 4B head
     shape (B=1, Hk=16, Hv=32, Dk=Dv=128) for T in 128, 512, 1024, 2048, forward and forward + backward, with each
     kernel's time (what dominates at short T)."""
-    from quotebound_amd.synthetic import Workload, make_inputs, to_device
+    from quotebound_amd.synthetic import make_inputs, to_device, workload
 
     out = {"unit": "ms (HIP events around the library's kernels)", "design": DESIGN_NAMES[design]}
     for T in (128, 512, 1024, 2048):
-        w = Workload(f"sweep_{T}", 1, T, 16, 32, 128, 128, seed=40 + T)
+        w = workload(f"qwen35_4b_t{T}")
         dev = to_device(make_inputs(w), "cuda")
         r, why = run_design(torch, hip, lib, w, dev, design, steps, warmup)
         if r is None:

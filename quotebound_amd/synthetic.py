@@ -118,8 +118,8 @@ def varlen_lengths(seed: int, n: int = 8, lo: int = 256, hi: int = 2048) -> list
 
 
 def workload(name: str) -> Workload:
-    """The named workloads: the tiny fp32 case, the Qwen3.5-4B and -9B layer shapes, the packed batch, and the 4B
-    shape with float32 activations."""
+    """The named workloads: the tiny fp32 case, the Qwen3.5-4B and -9B layer shapes, the packed batch, the 4B shape
+    with float32 activations, and qwen35_4b_t<T>, the 4B head shape at T tokens."""
     if name == "tiny":
         return Workload("tiny", 1, 64, 2, 2, 32, 32, dtype="f32", seed=0, clip_log_decay=None)
     if name == "qwen35_4b":
@@ -131,6 +131,9 @@ def workload(name: str) -> Workload:
         return Workload("qwen35_4b_varlen", 1, sum(lens), 16, 32, 128, 128, seed=3, seq_lens=lens)
     if name == "qwen35_4b_f32":  # the 4B layer shape with float32 activations, the reference op's own dtype
         return Workload("qwen35_4b_f32", 1, 4096, 16, 32, 128, 128, dtype="f32", seed=1)
+    if name.startswith("qwen35_4b_t") and name[11:].isdigit():  # the 4B head shape at T tokens (the T sweep)
+        T = int(name[11:])
+        return Workload(name, 1, T, 16, 32, 128, 128, seed=40 + T)
     raise KeyError(name)
 
 
