@@ -382,7 +382,11 @@ def run_lora_step(torch, steps=5, warmup=2):
     """One LoRA training step of the tiny Qwen3.5-architecture model (quotebound_amd.lora.Config: 8 layers 3
     DeltaNet : 1 attention, hidden 1024, bf16 base, rank 16 on q/k/v/o and the DeltaNet in/out projections) on 4
     sequences of 1024 random tokens with the loss on the last half: forward, adapter gradients, AdamW. Timed with
-    device synchronisations around `steps` steps, run eagerly and replayed from a captured HIP graph."""
+    device synchronisations around `steps` steps, run eagerly and replayed from a captured HIP graph, with the
+    DeltaNet layers' prologue fused into the recurrence (the default); `separate_prologue` replays the same step
+    with the prologue as its own passes, and `prologue_fusion_ms` is what the fusion saves per step."""
+    import dataclasses
+
     from quotebound_amd import lora
 
     cfg = lora.Config()
@@ -405,6 +409,19 @@ def run_lora_step(torch, steps=5, warmup=2):
         ms = (time.perf_counter() - t0) * 1e3 / steps
         out[mode] = {"ms_per_step": ms, "tokens_per_s": 4 * 1024 / (ms * 1e-3), "loss": float(loss)}
         del step
+    sep = dataclasses.replace(cfg, fused_prologue=False)
+    step = lora.GraphStep(w, ads, lora.AdamW(lr=1e-4), sep, batch, capture=True)
+    for _ in range(warmup):
+        loss, _ = step(*batch)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        loss, _ = step(*batch)
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    out["separate_prologue"] = {"graph_ms_per_step": ms, "loss": float(loss)}
+    out["prologue_fusion_ms"] = ms - out["graph"]["ms_per_step"]
+    del step
     return out
 
 

@@ -64,9 +64,10 @@ struct Scratch {
   Scratch& operator=(const Scratch&) = delete;
 };
 
-// The design the adapters run: the chunked one where the library supports the shape and T > 48, else the recurrent
+// The design the adapters run: the chunked one where the library supports the shape and T > 40, else the recurrent
 // one, which is the faster up to a few dozen steps (4B layer shape, launches included: forward + backward 43.7
-// against 47.0 us at T = 32, 53.0 against 47.4 us at T = 48; a one-token decode call about 6 us against 15 us).
+// against 47.0 us at T = 32, 53.0 against 47.4 us at T = 48, the two crossing near T = 38; a one-token decode call
+// about 6 us against 15 us).
 int pick_design(qb_gdn_desc d) {
   char err[16];
   if (d.T <= 40) return QB_GDN_RECURRENT;
@@ -156,6 +157,30 @@ void abi(int rc, const char* err) {
 
 const float* fp(const array& x) { return static_cast<const float*>(x.data()); }
 float* fp(array& x) { return static_cast<float*>(x.data()); }
+
+// The shapes of the prologue fused into the recurrence, checked against each other.
+Problem check_fused(const char* who, const array& q_raw, const array& k_raw, const array& v, const array& a,
+                    const array& b, const array& a_log, const array& dt_bias, const array& state) {
+  need(q_raw.ndim() == 4 && k_raw.shape() == q_raw.shape() && v.ndim() == 4 && a.ndim() == 3 && b.shape() == a.shape(),
+       who, "q_raw, k_raw must be [B, T, Hk, Dk], v [B, T, Hv, Dv] and a, b [B, T, Hv]", {&q_raw, &k_raw, &v, &a, &b});
+  const Problem p{q_raw.shape(0), q_raw.shape(1), q_raw.shape(2), q_raw.shape(3), v.shape(2), v.shape(3)};
+  need(v.shape(0) == p.B && v.shape(1) == p.T && a.shape() == Shape{p.B, p.T, p.Hv}, who,
+       "v, a, b must match q_raw in batch and time, with v's Hv heads", {&q_raw, &v, &a});
+  need(a_log.shape() == Shape{p.Hv} && dt_bias.shape() == Shape{p.Hv}, who, "a_log and dt_bias must be [Hv]",
+       {&a, &a_log, &dt_bias});
+  need(state.empty() || state.shape() == Shape{p.B, p.Hv, p.Dv, p.Dk}, who, "state must be [B, Hv, Dv, Dk] or empty",
+       {&v, &state});
+  need(act_dtype({&q_raw, &k_raw, &v, &a, &b}) == bfloat16, who, "the fused prologue takes bfloat16 activations",
+       {&q_raw, &v, &a});
+  return p;
+}
+
+qb_gdn_desc fused_desc(const Problem& p) {
+  qb_gdn_desc d = make_desc(p, bfloat16, false);
+  d.g_is_log = 1;  // the prologue emits the log-decay
+  d.design = QB_GDN_CHUNKED;
+  return d;
+}
 
 }  // namespace
 
@@ -354,6 +379,65 @@ EpilogueGrads deltanet_epilogue_vjp(const array& y, const array& z, const array&
   char err[512];
   abi(qb_gdn_epilogue_bwd(&d, yy.data(), zz.data(), fp(w), eps, go.data(), r.dy.data(), r.dz.data(), fp(r.dnorm_w),
                           ws.p, g_stream, err, sizeof err),
+      err);
+  return r;
+}
+
+PrologueRecurrence deltanet_prologue_recurrence(const array& q_raw, const array& k_raw, const array& v,
+                                                const array& a, const array& b, const array& a_log,
+                                                const array& dt_bias, const array& state) {
+  const Problem p = check_fused("deltanet prologue + recurrence", q_raw, k_raw, v, a, b, a_log, dt_bias, state);
+  const qb_gdn_desc d = fused_desc(p);
+  const array al = astype(a_log, float32), dt = astype(dt_bias, float32);
+  const array s0 = state.empty() ? array() : astype(state, float32);
+  PrologueRecurrence r{array(v.shape(), bfloat16),     array({p.B, p.Hv, p.Dv, p.Dk}, float32),
+                       array(q_raw.shape(), bfloat16), array(k_raw.shape(), bfloat16),
+                       array(a.shape(), bfloat16),     array(a.shape(), float32)};
+  Scratch ws(qb_gdn_workspace_bytes(&d));
+  char err[512];
+  abi(qb_gdn_fwd_prologue(&d, q_raw.data(), k_raw.data(), v.data(), a.data(), b.data(), fp(al), fp(dt), fp(s0),
+                          r.q.data(), r.k.data(), r.beta.data(), fp(r.log_decay), r.y.data(), fp(r.state), nullptr,
+                          ws.p, g_stream, err, sizeof err),
+      err);
+  return r;
+}
+
+PrologueRecurrenceGrads deltanet_prologue_recurrence_vjp(const array& q_raw, const array& k_raw, const array& v,
+                                                         const array& a, const array& b, const array& a_log,
+                                                         const array& dt_bias, const array& state, const array& dy,
+                                                         const array& dstate) {
+  const char* who = "deltanet prologue + recurrence backward";
+  const Problem p = check_fused(who, q_raw, k_raw, v, a, b, a_log, dt_bias, state);
+  need(dy.shape() == v.shape(), who, "dy must have v's shape", {&v, &dy});
+  need(dstate.empty() || dstate.shape() == Shape{p.B, p.Hv, p.Dv, p.Dk}, who,
+       "dstate must be [B, Hv, Dv, Dk] or empty", {&v, &dstate});
+  const qb_gdn_desc d = fused_desc(p);
+  const array al = astype(a_log, float32), dt = astype(dt_bias, float32);
+  const array s0 = state.empty() ? array() : astype(state, float32);
+  // The forward again, keeping the chunk-start states and the recurrence's inputs (as gated_delta_vjp rebuilds the
+  // states, src/delta_grad.cpp:172-181).
+  Scratch ckpt(qb_gdn_ckpt_bytes(&d));
+  array q(q_raw.shape(), bfloat16), k(k_raw.shape(), bfloat16), beta(a.shape(), bfloat16), ld(a.shape(), float32);
+  char err[512];
+  {
+    array y(v.shape(), bfloat16), s_out({p.B, p.Hv, p.Dv, p.Dk}, float32);
+    Scratch ws(qb_gdn_workspace_bytes(&d));
+    abi(qb_gdn_fwd_prologue(&d, q_raw.data(), k_raw.data(), v.data(), a.data(), b.data(), fp(al), fp(dt), fp(s0),
+                            q.data(), k.data(), beta.data(), fp(ld), y.data(), fp(s_out),
+                            static_cast<float*>(ckpt.p), ws.p, g_stream, err, sizeof err),
+        err);
+  }
+  const array dyi = astype(dy, bfloat16);
+  const array dsi = dstate.empty() ? array() : astype(dstate, float32);
+  PrologueRecurrenceGrads r{array(q_raw.shape(), bfloat16), array(k_raw.shape(), bfloat16),
+                            array(v.shape(), bfloat16),     array(a.shape(), bfloat16),
+                            array(b.shape(), bfloat16),     array({p.Hv}, float32),
+                            array({p.Hv}, float32),         array({p.B, p.Hv, p.Dv, p.Dk}, float32)};
+  Scratch ws(qb_gdn_workspace_bytes(&d));
+  abi(qb_gdn_bwd_prologue(&d, q_raw.data(), k_raw.data(), a.data(), b.data(), fp(al), fp(dt), q.data(), k.data(),
+                          v.data(), beta.data(), fp(ld), static_cast<const float*>(ckpt.p), dyi.data(), fp(dsi),
+                          r.dq_raw.data(), r.dk_raw.data(), r.dv.data(), r.da.data(), r.db.data(), fp(r.da_log),
+                          fp(r.ddt_bias), fp(r.dstate), ws.p, g_stream, err, sizeof err),
       err);
   return r;
 }

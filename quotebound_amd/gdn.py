@@ -230,6 +230,41 @@ class _GatedDelta(torch.autograd.Function):
                 ds0.to(sdt) if has_state else None, None, None)
 
 
+class _GatedDeltaPrologue(torch.autograd.Function):
+    """The layer's prologue and the trainable recurrence as one autograd node on the fused entry points
+    (qb_gdn_fwd_prologue, qb_gdn_bwd_prologue): neighbours.prologue followed by gated_delta_trainable(...,
+    log_decay=True), with the same results bit for bit (the gate parameters' cotangents up to float32 reassociation
+    of their sums over tokens), without the prologue's separate passes over q_raw and k_raw (reference
+    src/deltanet.cpp:94-100 feeding gated_delta at :111). The forward keeps its chunk-start states and the
+    recurrence's inputs q, k, beta, log_decay for the backward."""
+
+    @staticmethod
+    def forward(ctx, q_raw, k_raw, v, a, b, a_log, dt_bias, state):
+        y, s_out, ckpt, q, k, beta, log_decay = forward_prologue(q_raw, k_raw, v, a, b, a_log, dt_bias, state)
+        ctx.save_for_backward(q_raw, k_raw, a, b, a_log, dt_bias, q, k, v, beta, log_decay, ckpt)
+        ctx.meta = (state is not None, None if state is None else state.dtype, a_log.dtype, dt_bias.dtype)
+        return y, s_out
+
+    @staticmethod
+    def backward(ctx, dy, dstate):
+        q_raw, k_raw, a, b, a_log, dt_bias, q, k, v, beta, log_decay, ckpt = ctx.saved_tensors
+        has_state, sdt, adt, ddt = ctx.meta
+        if dy is None:
+            dy = torch.zeros(v.shape, dtype=torch.bfloat16, device=v.device)
+        dq_raw, dk_raw, dv, da, db, da_log, ddt_bias, ds0 = backward_prologue(
+            q_raw, k_raw, a, b, a_log, dt_bias, q, k, v, beta, log_decay, ckpt, dy.to(torch.bfloat16), dstate,
+            want_ds0=has_state)
+        return (dq_raw, dk_raw, dv, da, db, da_log.to(adt), ddt_bias.to(ddt), ds0.to(sdt) if has_state else None)
+
+
+def gated_delta_prologue(q_raw, k_raw, v, a, b, a_log, dt_bias, state=None):
+    """(y in bf16, new float32 state) of the layer's prologue then the trainable recurrence in one fused call:
+    q = rms_norm(q_raw) / Dk, k = rms_norm(k_raw) / sqrt(Dk), beta = sigmoid(b), log-decay = -exp(a_log) *
+    softplus(a + dt_bias), then gated_delta_trainable(q, k, v, log-decay, beta, state, log_decay=True). Autograd
+    runs the fused backward. The chunked design's shapes only: bf16 activations, Dk = 128, Dv a multiple of 32."""
+    return _GatedDeltaPrologue.apply(q_raw, k_raw, v, a, b, a_log, dt_bias, state)
+
+
 def gated_delta_trainable(q, k, v, g, beta, state, *, log_decay=False, design=DEFAULT_DESIGN):
     """(y, new_state) with gated_delta_vjp as the backward."""
     return _GatedDelta.apply(q, k, v, g, beta, state, log_decay, design)

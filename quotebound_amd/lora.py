@@ -46,6 +46,9 @@ class Config:
     lin_k_dim: int = 128
     lin_v_dim: int = 128
     conv_kernel: int = 4
+    # The DeltaNet layers' prologue fused into the recurrence's kernels (gdn.gated_delta_prologue) where the
+    # activations are bf16; else, and for float32 activations, the separate prologue pass then the recurrence.
+    fused_prologue: bool = True
 
     def is_linear(self, layer: int) -> bool:
         """Gated DeltaNet (else full attention): every fourth layer and the last are attention (tests/tiny.h:23)."""
@@ -246,7 +249,7 @@ def attention(x, w, p, ads, scale, cfg):
 
 def deltanet(x, w, p, ads, scale, cfg):
     """src/deltanet.cpp:63-124 without a cache, training form: projections, causal conv + SiLU, the library's
-    prologue, recurrence and gated RMSNorm, out_proj."""
+    prologue and recurrence (one fused call on bf16 activations), its gated RMSNorm, out_proj."""
     B, S, _ = x.shape
     Hk, Hv, Dk, Dv = cfg.lin_k_heads, cfg.lin_v_heads, cfg.lin_k_dim, cfg.lin_v_dim
     kd = Hk * Dk
@@ -259,8 +262,11 @@ def deltanet(x, w, p, ads, scale, cfg):
     q_raw = conv[..., :kd].reshape(B, S, Hk, Dk)
     k_raw = conv[..., kd:2 * kd].reshape(B, S, Hk, Dk)
     v = conv[..., 2 * kd:].reshape(B, S, Hv, Dv)
-    q, k, beta, log_decay = neighbours.prologue(q_raw, k_raw, g_in, b, w[a + "A_log"], w[a + "dt_bias"])
-    y, _ = gdn.gated_delta_trainable(q, k, v, log_decay, beta, None, log_decay=True)
+    if cfg.fused_prologue and x.dtype == torch.bfloat16:
+        y, _ = gdn.gated_delta_prologue(q_raw, k_raw, v, g_in, b, w[a + "A_log"], w[a + "dt_bias"], None)
+    else:
+        q, k, beta, log_decay = neighbours.prologue(q_raw, k_raw, g_in, b, w[a + "A_log"], w[a + "dt_bias"])
+        y, _ = gdn.gated_delta_trainable(q, k, v, log_decay, beta, None, log_decay=True)
     o = neighbours.epilogue(y, z, w[a + "norm.weight"], cfg.eps)
     return linear(o.reshape(B, S, Hv * Dv), w[a + "out_proj.weight"], ads.get(a + "out_proj"), scale)
 

@@ -1,6 +1,7 @@
 // Checks the C++ adapters of include/qb (gated_delta, gated_delta_trainable, gated_delta_vjp, gated_delta_rows)
-// against the oracle, and the neighbours' adapters (deltanet_prologue / _epilogue and their vjps) in float32
-// against a float64 statement of their formulas here,
+// against the oracle, the neighbours' adapters (deltanet_prologue / _epilogue and their vjps) in float32
+// against a float64 statement of their formulas here, and the prologue fused into the recurrence
+// (deltanet_prologue_recurrence and its vjp) against the separate steps it replaces, bit for bit,
 // the way the reference's tests check its entry points (tests/test_deltanet.cpp:25-154): seeded inputs, the
 // forward and every cotangent compared normwise, max|X - X_ref| / max|X_ref|. float32 outputs must be within 2e-3;
 // a bfloat16 output may in addition differ by half a bfloat16 ulp of each reference element (its own rounding).
@@ -14,6 +15,7 @@
 #include <vector>
 
 #include "../../oracle/gdn_ref.h"
+#include "qb_gdn.h"
 #include "qb/delta_grad.h"
 #include "qb/deltanet.h"
 #include "qb/neighbours.h"
@@ -258,6 +260,75 @@ void neighbours_case() {
   compare("dy", E.dy, dy, 1e-5), compare("dz", E.dz, dz, 1e-5), compare("dw", E.dnorm_w, dw, 1e-4);
 }
 
+void same(const char* what, const qb::array& a, const qb::array& b) {
+  const std::vector<float> x = fetch(a), y = fetch(b);
+  const bool ok = x.size() == y.size() && std::memcmp(x.data(), y.data(), x.size() * sizeof(float)) == 0;
+  std::printf("  %-8s bit-equal%s\n", what, ok ? "" : "  <-- FAIL");
+  failures += !ok;
+}
+
+// The prologue fused into the recurrence against the separate steps: deltanet_prologue, then the chunked forward
+// and backward through the C ABI with the log-decay (g_is_log = 1), then deltanet_prologue_vjp. Every output but
+// the summed gate-parameter cotangents must be the same bits; those two differ by float32 reassociation only.
+void fused_case() {
+  const int B = 2, T = 150, Hk = 2, Hv = 4, Dk = 128, Dv = 64;
+  std::printf("case prologue + recurrence: B=%d T=%d Hk=%d Hv=%d Dk=%d Dv=%d bf16, nonzero state\n", B, T, Hk, Hv, Dk,
+              Dv);
+  Rng r{31};
+  auto fill = [&](size_t n, double sc, double mean = 0.0) {
+    std::vector<float> x(n);
+    for (auto& e : x) e = float(mean + sc * r.normal());
+    return x;
+  };
+  const qb::Shape sqk{B, T, Hk, Dk}, sv{B, T, Hv, Dv}, sg{B, T, Hv}, ss{B, Hv, Dv, Dk};
+  const size_t nqk = size_t(B) * T * Hk * Dk, nv = size_t(B) * T * Hv * Dv, ng = size_t(B) * T * Hv,
+               ns = size_t(B) * Hv * Dv * Dk;
+  const qb::Dtype bf = qb::bfloat16, f = qb::float32;
+  const Tensor qr = make(fill(nqk, 1), sqk, bf), kr = make(fill(nqk, 1), sqk, bf), v = make(fill(nv, 1), sv, bf);
+  const Tensor a = make(fill(ng, 1), sg, bf), b = make(fill(ng, 1), sg, bf), dy = make(fill(nv, 1), sv, bf);
+  std::vector<float> alog(Hv);
+  for (auto& e : alog) e = float(std::log(1.0 + 15.0 * r.uniform()));
+  const Tensor al = make(alog, {Hv}, f), dt = make(fill(Hv, 0.5), {Hv}, f);
+  const Tensor s0 = make(fill(ns, 0.02), ss, f), dso = make(fill(ns, 1), ss, f);
+
+  std::printf(" deltanet_prologue_recurrence\n");
+  const qb::PrologueRecurrence F = qb::deltanet_prologue_recurrence(qr.dev, kr.dev, v.dev, a.dev, b.dev, al.dev,
+                                                                    dt.dev, s0.dev);
+  const qb::Prologue P = qb::deltanet_prologue(qr.dev, kr.dev, a.dev, b.dev, al.dev, dt.dev);
+  qb_gdn_desc d{};
+  d.B = B, d.T = T, d.Hk = Hk, d.Hv = Hv, d.Dk = Dk, d.Dv = Dv, d.chunk = 64, d.dtype = QB_DTYPE_BF16, d.g_is_log = 1;
+  d.design = QB_GDN_CHUNKED;
+  char err[512];
+  auto buf = [](size_t bytes) { return qb::array({int((bytes + 3) / 4) + 1}, qb::float32); };
+  qb::array ckpt = buf(qb_gdn_ckpt_bytes(&d)), ws = buf(qb_gdn_workspace_bytes(&d));
+  qb::array y(sv, bf), s_out(ss, f);
+  auto abi = [&](int rc) {
+    if (rc != 0) {
+      std::printf("  C ABI call failed: %s  <-- FAIL\n", err);
+      ++failures;
+    }
+  };
+  abi(qb_gdn_fwd(&d, P.q.data(), P.k.data(), v.dev.data(), static_cast<const float*>(P.log_decay.data()),
+                 P.beta.data(), static_cast<const float*>(s0.dev.data()), y.data(), static_cast<float*>(s_out.data()),
+                 static_cast<float*>(ckpt.data()), ws.data(), qb::stream(), err, sizeof err));
+  same("y", F.y, y), same("state", F.state, s_out), same("q", F.q, P.q), same("k", F.k, P.k);
+  same("beta", F.beta, P.beta), same("logdec", F.log_decay, P.log_decay);
+
+  std::printf(" deltanet_prologue_recurrence_vjp\n");
+  const qb::PrologueRecurrenceGrads G = qb::deltanet_prologue_recurrence_vjp(
+      qr.dev, kr.dev, v.dev, a.dev, b.dev, al.dev, dt.dev, s0.dev, dy.dev, dso.dev);
+  qb::array dq(sqk, bf), dk(sqk, bf), dv(sv, bf), dl(sg, f), dbeta(sg, bf), ds0(ss, f);
+  abi(qb_gdn_bwd(&d, P.q.data(), P.k.data(), v.dev.data(), static_cast<const float*>(P.log_decay.data()),
+                 P.beta.data(), static_cast<const float*>(ckpt.data()), dy.dev.data(),
+                 static_cast<const float*>(dso.dev.data()), dq.data(), dk.data(), dv.data(),
+                 static_cast<float*>(dl.data()), dbeta.data(), static_cast<float*>(ds0.data()), ws.data(), qb::stream(),
+                 err, sizeof err));
+  const qb::PrologueGrads S = qb::deltanet_prologue_vjp(qr.dev, kr.dev, a.dev, b.dev, al.dev, dt.dev, dq, dk, dbeta, dl);
+  same("dq_raw", G.dq_raw, S.dq_raw), same("dk_raw", G.dk_raw, S.dk_raw), same("dv", G.dv, dv);
+  same("da", G.da, S.da), same("db", G.db, S.db), same("dstate", G.dstate, ds0);
+  compare("dA_log", G.da_log, fetch(S.da_log), 1e-5), compare("ddt", G.ddt_bias, fetch(S.ddt_bias), 1e-5);
+}
+
 void expect_throw(const char* what, void (*fn)()) {
   try {
     fn();
@@ -274,6 +345,7 @@ int main() {
   run_case("chunked", 2, 150, 2, 4, 128, 64, qb::bfloat16, 11);
   run_case("recurrent", 1, 100, 2, 4, 64, 32, qb::float32, 12);
   neighbours_case();
+  fused_case();
   std::printf("errors\n");
   expect_throw("k shape", [] {
     const qb::array q = qb::array::zeros({1, 8, 2, 64}, qb::float32), k = qb::array::zeros({1, 8, 2, 32}, qb::float32);
@@ -291,6 +363,11 @@ int main() {
     const qb::array x = qb::array::zeros({1, 8, 2, 32}, qb::float32), a = qb::array::zeros({1, 8, 4}, qb::float32);
     const qb::array p = qb::array::zeros({4}, qb::float32);
     qb::deltanet_prologue(x, x, a, a, p, p);
+  });
+  expect_throw("fused prologue dtype", [] {
+    const qb::array x = qb::array::zeros({1, 8, 2, 128}, qb::float32), a = qb::array::zeros({1, 8, 4}, qb::float32);
+    const qb::array v = qb::array::zeros({1, 8, 4, 64}, qb::float32), p = qb::array::zeros({4}, qb::float32);
+    qb::deltanet_prologue_recurrence(x, x, v, a, a, p, p, qb::array());
   });
   expect_throw("epilogue weight", [] {
     const qb::array y = qb::array::zeros({1, 8, 4, 64}, qb::float32), w = qb::array::zeros({32}, qb::float32);

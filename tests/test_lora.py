@@ -230,16 +230,19 @@ def test_lora_step_workload_bf16(dev, oracle):
 
 @pytest.mark.gpu
 def test_lora_step_recurrence_layers_match_oracle(dev, oracle, monkeypatch):
-    """The chunked kernels inside the LoRA workload's bf16 step, held to the recurrence's own bar. Every DeltaNet
-    layer's call of the trainable recurrence is recorded: its bf16 inputs (q, k, v, beta; the float32 log-decay), its
-    output y and the cotangents the step's backward fed it (dy) and got from it (dq, dk, dv, dg, dbeta). The oracle
-    (float32) then runs each layer on exactly those inputs:
-      * the same kernels rerun on those inputs with float32 outputs within 1e-4 normwise (the split-bf16 products'
-        level; a kernel bug worth a fraction of a percent shows here, not under the whole-gradient noise bar);
-      * the step's own tensors equal to those float32 results rounded once to bf16 (dg, float32, bit-equal), and so
-        within 2e-3 of the oracle plus their own half-ulp, the rule of the layer-shape tests."""
+    """The chunked kernels inside the LoRA workload's bf16 step, held to the recurrence's own bar. The step runs each
+    DeltaNet layer's prologue and recurrence as one fused call (gdn.gated_delta_prologue); every such call is
+    recorded: its raw bf16 inputs (q_raw, k_raw, v, a, b) and gate parameters, its output y, and the cotangents the
+    step's backward fed it (dy) and got from it (dq_raw, dk_raw, dv, da, db). Per layer, with q, k, beta and the
+    log-decay from the separate prologue pass (bit-equal to what the fused kernel forms, tests/test_neighbours.py):
+      * the chunked kernels rerun on them with float32 outputs are within 1e-4 of the oracle (float32) normwise (the
+        split-bf16 products' level; a kernel bug worth a fraction of a percent shows here, not under the
+        whole-gradient noise bar);
+      * the step's y is that float32 y rounded once to bf16, and so within 2e-3 of the oracle plus its half-ulp;
+      * the step's cotangents are bit for bit those of the separate path: the chunked backward in bf16 (its dq, dk,
+        dv, dbeta the float32 results rounded once, dg bit-equal) followed by the prologue's backward."""
     from helpers import bf16_half_ulp
-    from quotebound_amd import _lib, gdn
+    from quotebound_amd import _lib, gdn, neighbours
     from quotebound_amd.synthetic import round_bf16
 
     cfg = lora.Config()
@@ -247,12 +250,12 @@ def test_lora_step_recurrence_layers_match_oracle(dev, oracle, monkeypatch):
     ads = lora.init_adapters(cfg, w, seed=32, b_std=0.05)
     tokens, positions, targets = lora.last_half_batch(4, 1024, cfg.vocab, seed=33)
     calls = []
-    real = gdn.gated_delta_trainable
+    real = gdn.gated_delta_prologue
 
-    def spy(q, k, v, g, beta, state, **kw):
-        assert state is None and kw.get("log_decay") is True
-        y, s = real(q, k, v, g, beta, state, **kw)
-        rec = {"in": [t.detach().clone() for t in (q, k, v, g, beta)], "y": y.detach().clone()}
+    def spy(q_raw, k_raw, v, a, b, a_log, dt_bias, state):
+        assert state is None
+        y, s = real(q_raw, k_raw, v, a, b, a_log, dt_bias, state)
+        rec = {"in": [t.detach().clone() for t in (q_raw, k_raw, v, a, b, a_log, dt_bias)], "y": y.detach().clone()}
 
         def keep(name):
             def hook(grad):
@@ -260,46 +263,74 @@ def test_lora_step_recurrence_layers_match_oracle(dev, oracle, monkeypatch):
             return hook
 
         y.register_hook(keep("dy"))
-        for name, t in zip(("dq", "dk", "dv", "dg", "dbeta"), (q, k, v, g, beta)):
-            t.register_hook(keep(name))
+        for name, t in zip(("dq_raw", "dk_raw", "dv", "da", "db"), (q_raw, k_raw, v, a, b)):
+            if t.requires_grad:  # a and b of the first layer depend on no adapter
+                t.register_hook(keep(name))
         calls.append(rec)
         return y, s
 
-    monkeypatch.setattr(lora.gdn, "gated_delta_trainable", spy)
+    monkeypatch.setattr(lora.gdn, "gated_delta_prologue", spy)
     lora.loss_and_grads(lora.to_device(w, "cuda", torch.bfloat16), lora.adapters_to(ads, "cuda"), tokens.cuda(),
                         positions.cuda(), targets.cuda(), cfg)
     torch.cuda.synchronize()
     assert len(calls) == sum(cfg.is_linear(i) for i in range(cfg.layers))
     names = ("y", "dq", "dk", "dv", "dg", "dbeta")
     for li, rec in enumerate(calls):
-        q, k, v, g, beta = rec["in"]
-        B, T, Hk, Dk = q.shape
-        Hv, Dv = v.shape[2], v.shape[3]
-        desc, _ = gdn._desc(q, v, torch.bfloat16, True, None, None, False)  # the step's own choice of design
-        assert desc.design == _lib.CHUNKED
+        q_raw, k_raw, v, a, b, a_log, dt_bias = rec["in"]
+        q, k, beta, g = neighbours.prologue_forward(q_raw, k_raw, a, b, a_log, dt_bias)
         host = {n: t.float().cpu().numpy() for n, t in zip(("q", "k", "v", "g", "beta"), (q, k, v, g, beta))}
         host["dy"] = rec["dy"].float().cpu().numpy()
         exp = oracle.fwd_bwd(host, dtype=np.float32)
         y32, _, ckpt = gdn.forward(q, k, v, g, beta, None, log_decay=True, design=_lib.CHUNKED, out_f32=True)
         g32 = gdn.backward(q, k, v, g, beta, ckpt, rec["dy"].float(), None, log_decay=True, design=_lib.CHUNKED,
                            want_ds0=False, out_f32=True)
+        g16 = gdn.backward(q, k, v, g, beta, ckpt, rec["dy"], None, log_decay=True, design=_lib.CHUNKED,
+                           want_ds0=False)
+        sep = neighbours.prologue_backward(q_raw, k_raw, a, b, a_log, dt_bias, g16[0], g16[1], g16[4], g16[3])
         torch.cuda.synchronize()
         f32 = {n: t.float().cpu().numpy() for n, t in zip(names, [y32] + list(g32[:5]))}
-        step = {n: rec[n].float().cpu().numpy() for n in names}
+        b16 = {n: t.float().cpu().numpy() for n, t in zip(names, [rec["y"]] + list(g16[:5]))}
         errs32 = {n: normwise(f32[n], exp[n]) for n in names}
-        errs = {n: normwise(step[n], exp[n]) for n in names}
+        errs = {n: normwise(b16[n], exp[n]) for n in names}
         print(f"layer call {li}: float32 outputs " + ", ".join(f"{n} {e:.1e}" for n, e in errs32.items())
-              + "; the step's own " + ", ".join(f"{n} {e:.1e}" for n, e in errs.items()))
+              + "; bf16 " + ", ".join(f"{n} {e:.1e}" for n, e in errs.items()))
         for n in names:
             assert errs32[n] <= 1e-4, (li, n, errs32)
             if n == "dg":  # float32 in the step too
-                assert np.array_equal(step[n], f32[n]), (li, n)
+                assert np.array_equal(b16[n], f32[n]), (li, n)
                 continue
-            # The step's bf16 tensors are the float32 results rounded once, and so within the criterion plus their
-            # own half-ulp of the oracle.
-            assert np.array_equal(step[n], round_bf16(f32[n])), (li, n)
-            slack = np.abs(step[n] - exp[n]) - bf16_half_ulp(np.maximum(np.abs(exp[n]), np.abs(f32[n])))
+            # The bf16 tensors are the float32 results rounded once, and so within the criterion plus their own
+            # half-ulp of the oracle.
+            assert np.array_equal(b16[n], round_bf16(f32[n])), (li, n)
+            slack = np.abs(b16[n] - exp[n]) - bf16_half_ulp(np.maximum(np.abs(exp[n]), np.abs(f32[n])))
             assert slack.max() <= 2e-3 * np.max(np.abs(exp[n])), (li, n)
+        # The step's own cotangents: those of the separate path, bit for bit.
+        assert all(n in rec for n in ("dq_raw", "dk_raw", "dv")), li
+        for n, want in zip(("dq_raw", "dk_raw", "dv", "da", "db"), (sep[0], sep[1], g16[2], sep[2], sep[3])):
+            if n in rec:
+                assert torch.equal(rec[n], want), (li, n)
+
+
+@pytest.mark.gpu
+def test_lora_step_fused_prologue_is_the_separate_path(dev):
+    """The DeltaNet layers' prologue fused into the recurrence's kernels (the default) against the separate prologue
+    pass followed by the recurrence, in the bf16 step: the loss, every adapter gradient and the gradient norm equal
+    bit for bit (only the frozen gate parameters' sums over tokens run in another order, and they feed nothing the
+    step trains)."""
+    import dataclasses
+
+    cfg = SMALL
+    w = lora.to_device(lora.init_weights(cfg, seed=51), "cuda", torch.bfloat16)
+    ads = lora.adapters_to(lora.init_adapters(cfg, lora.init_weights(cfg, seed=51), seed=52, b_std=0.05), "cuda")
+    tokens, positions, targets = (t.cuda() for t in lora.last_half_batch(2, 128, cfg.vocab, seed=53))
+    out = {}
+    for fused in (True, False):
+        c = dataclasses.replace(cfg, fused_prologue=fused)
+        out[fused] = lora.loss_and_grads(w, ads, tokens, positions, targets, c)
+    torch.cuda.synchronize()
+    (lf, gf, nf), (ls, gs, ns) = out[True], out[False]
+    assert torch.equal(lf, ls) and torch.equal(nf, ns)
+    assert len(gf) == len(gs) and all(torch.equal(a, b) for a, b in zip(gf, gs))
 
 
 @pytest.mark.gpu

@@ -431,3 +431,48 @@ def test_fused_prologue_backward_is_the_two_passes(dev, case):
     for name, got, ref, mag in (("da_log", fused[5], da_log, mag_a), ("ddt_bias", fused[6], ddt, mag_d)):
         err = ((got.double() - ref.double()).abs() / mag.clamp_min(1e-30)).max().item()
         assert err <= 1e-5, (name, err)
+
+
+@pytest.mark.gpu
+def test_fused_prologue_autograd_is_the_separate_ops(dev):
+    """gdn.gated_delta_prologue, the autograd op on the fused entry points, against neighbours.prologue followed by
+    gdn.gated_delta_trainable(log_decay=True) under torch autograd, with a nonzero initial state and cotangents on
+    y and the final state: y, the final state and the gradients of q_raw, k_raw, v, a, b and the state equal bit for
+    bit; those of a_log and dt_bias (sums over tokens in another fixed order) within 1e-5 relative to the sum of
+    their terms' magnitudes."""
+    torch = dev
+    from quotebound_amd import gdn, neighbours
+
+    B, T, Hk, Hv, Dk, Dv = 2, 150, 2, 4, 128, 64
+    rng = np.random.default_rng(91)
+    x = _prologue_inputs(rng, B, T, Hk, Hv, Dk, bf16=True)
+    x["v"] = nb.round_bf16(rng.standard_normal((B, T, Hv, Dv)))
+    d = _to_dev(torch, x, True, ("q_raw", "k_raw", "a", "b", "v"))
+    s0 = torch.tensor(rng.normal(0.0, 0.1, (B, Hv, Dv, Dk)).astype(np.float32)).cuda()
+    dy = torch.tensor(nb.round_bf16(rng.standard_normal((B, T, Hv, Dv)))).cuda().to(torch.bfloat16)
+    dso = torch.tensor(rng.normal(0.0, 0.1, (B, Hv, Dv, Dk)).astype(np.float32)).cuda()
+    names = ("q_raw", "k_raw", "v", "a", "b", "a_log", "dt_bias", "state")
+
+    def run(fused):
+        leaves = [d[n].detach().clone().requires_grad_() for n in names[:7]] + [s0.clone().requires_grad_()]
+        qr, kr, v, a, b, al, dt, st = leaves
+        if fused:
+            y, s = gdn.gated_delta_prologue(qr, kr, v, a, b, al, dt, st)
+        else:
+            q, k, beta, ld = neighbours.prologue(qr, kr, a, b, al, dt)
+            y, s = gdn.gated_delta_trainable(q, k, v, ld, beta, st, log_decay=True, design=2)
+        torch.autograd.backward([y, s], [dy, dso])
+        torch.cuda.synchronize()
+        return y.detach(), s.detach(), [t.grad for t in leaves]
+
+    yf, sf, gf = run(True)
+    ys, ss, gs = run(False)
+    bits = lambda t: t.view(torch.int16) if t.dtype == torch.bfloat16 else t.view(torch.int32)  # noqa: E731
+    assert torch.equal(bits(yf), bits(ys)) and torch.equal(bits(sf), bits(ss))
+    for name, a_, b_ in zip(names, gf, gs):
+        assert a_.dtype == b_.dtype and a_.shape == b_.shape, name
+        if name in ("a_log", "dt_bias"):
+            err = ((a_.double() - b_.double()).abs().max() / b_.double().abs().max().clamp_min(1e-30)).item()
+            assert err <= 1e-5, (name, err)
+        else:
+            assert torch.equal(bits(a_), bits(b_)), name
