@@ -89,8 +89,9 @@ size_t qb_gdn_ckpt_bytes(const qb_gdn_desc* desc);
  * not need to survive between calls. 0 on an invalid desc. */
 size_t qb_gdn_workspace_bytes(const qb_gdn_desc* desc);
 
-/* The main kernels a call launches, in order, as its trace events time them (a small follow-up pass, such as the
- * chunked backward's dq/dk sum for short sequences, is timed with the kernel before it): their count is returned
+/* The main kernels a call launches, in order, as its trace events time them (the small follow-up passes are timed
+ * with the kernel before them: the chunked backward's dq/dk sum for short sequences, its gate-parameter sums with the
+ * fused prologue, and its exact dL/dg replay where g is the decay factor): their count is returned
  * and their names written comma-separated into names (cut to len; may be NULL). which: 0 for qb_gdn_fwd, 1 for
  * qb_gdn_bwd. -1 on an invalid desc. */
 int qb_gdn_launches(const qb_gdn_desc* desc, int which, char* names, int len);
@@ -118,7 +119,7 @@ int qb_gdn_bwd(const qb_gdn_desc* desc, const void* q, const void* k, const void
 
 /* Size of the device array qb_gdn_bwd_static uses as its workspace, per GPU: 257 MiB, which holds the chunked
  * design's workspace (the chunk-end state cotangents and 8 bytes per chunk and value head) up to
- * NC * Hv * Dv * Dk = 2^26 (the 4B and 9B layer shapes at T = 4096 hold half that). */
+ * NC * Hv * Dv * Dk = 2^26 (the 4B layer shape at T = 4096 uses half of it, the 9B shape three quarters). */
 #define QB_GDN_STATIC_SCRATCH_BYTES (257u << 20)
 
 /* qb_gdn_bwd without a workspace argument, for callers that cannot allocate device memory (code under HIP graph
@@ -126,7 +127,9 @@ int qb_gdn_bwd(const qb_gdn_desc* desc, const void* q, const void* k, const void
  * a file-scope device array of QB_GDN_STATIC_SCRATCH_BYTES that each GPU the library runs on holds until the
  * process ends; a desc whose qb_gdn_workspace_bytes exceeds that is refused with -1 and the reason in err, before any
  * GPU work. It calls no hipMalloc, hipFree or allocating routine. The first call on a device looks up that device's
- * address of the array (with the device current). Every call on one GPU shares that GPU's array: calls that overlap
+ * address of the array (with the device current), which may load the library's device code: make that first call
+ * outside any graph capture. Later calls only launch kernels on the stream (no memset, no copy), so they may be
+ * captured into a HIP graph and replayed. Every call on one GPU shares that GPU's array: calls that overlap
  * on one GPU (on different streams, or unordered across host threads) race on it and must not be issued. Nothing in
  * the array needs to start at zero (the backward writes every byte of its workspace before reading it), and it keeps
  * the last call's contents. Otherwise as qb_gdn_bwd, with the same outputs bit for bit. */

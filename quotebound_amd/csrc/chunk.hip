@@ -15,11 +15,24 @@ size_t dsend_bytes(const Problem& p) { return size_t(p.NC) * p.Hv * p.Dv * p.Dk 
 // The fused prologue backward's per-(chunk slot, value head) sums, after dSend.
 size_t gate_part_bytes(const Problem& p) { return (size_t(p.NC) * p.Hv * 2 * 4 + 255) & ~size_t(255); }
 
-// Short sequences: when the (chunk slot, value head) pairs fit one per CU of the 256-CU device (NC * Hv <= 256), the
+// The current device's compute-unit count; 256 (MI355X) when it cannot be read, as with no device (host-only
+// sizing calls).
+int device_cus() {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) {
+    (void)hipGetLastError();
+    return 256;
+  }
+  return cus;
+}
+
+// Short sequences: when the (chunk slot, value head) pairs fit one per CU of the current device (NC * Hv <= CUs), the
 // gradient kernel takes each value head of a GQA group as a work item of its own, so that the group's heads run side
 // by side rather than in turn, and a second pass sums their dq and dk in order. Past that, its items already fill
-// the device and the heads run in turn with dq, dk summed in registers.
-bool split_grads(const Problem& p) { return p.Hv > p.Hk && int64_t(p.NC) * p.Hv <= 256; }
+// the device and the heads run in turn with dq, dk summed in registers. The workspace is sized by the same rule on
+// the device current at sizing time.
+bool split_grads(const Problem& p) { return p.Hv > p.Hk && int64_t(p.NC) * p.Hv <= device_cus(); }
 size_t dqk_part_bytes(const Problem& p) { return split_grads(p) ? size_t(p.NC) * p.Hv * 2 * 64 * p.Dk * 4 : 0; }
 
 ChunkArgs base_args(const Problem& p) {
@@ -138,13 +151,14 @@ hipError_t bwd_impl(const Problem& p, const PrologueGradIn* pro, const BwdPtrs& 
   if (e != hipSuccess) return e;
   tr.mark();
   e = launch_chunk_bwd_grads(a, p.out_bf16, s, pro != nullptr);
-  // Timed with the gradient kernel. With the prologue, the sum pass also does the normalisation's backward.
+  // The follow-up passes are timed with the gradient kernel. With the prologue, the sum pass also does the
+  // normalisation's backward.
   if (e == hipSuccess && a.dqk_part) e = launch_chunk_dqk_sum(a, p.out_bf16, s, pro != nullptr);
-  tr.mark();
   if (e == hipSuccess && pro) e = launch_chunk_gate_sums(a, pro->da_log, pro->ddt_bias, s);
   // With g given as the factor, dL/dg at tiny or zero factors comes from an exact replay (chunk_dgfix.hip); chunks
   // without one return at once.
   if (e == hipSuccess && !p.g_is_log) e = launch_chunk_dgfix(a, p.out_bf16, s);
+  tr.mark();
   return e;
 }
 

@@ -361,11 +361,13 @@ def test_random_shapes(torch_dev, oracle, seed):
 
 @pytest.mark.parametrize("design", DESIGNS, ids=DESIGN_IDS.get)
 @pytest.mark.parametrize("mode", ["factor", "log"])
-def test_zero_and_tiny_decays(torch_dev, oracle, design, mode):
+@pytest.mark.parametrize("crowded", [False, True], ids=["spread", "crowded"])
+def test_zero_and_tiny_decays(torch_dev, oracle, design, mode, crowded):
     """Decay factors of 0 (a log-decay of -inf) and tiny ones: at a chunk's first and last step, twice in a row,
     mid-chunk and at the sequence's last step, beside ordinary ones. Every output finite and within the bf16
     tolerance of the oracle. (The chunked design floors the log-decay at -150 and, with g given as the factor, takes
-    dL/dg at factors below 2^-10 from its exact replay of the chunk.)"""
+    dL/dg at factors below 2^-10 from its exact replay of the chunk, four flagged steps per replay.) crowded: seven
+    such factors in one (chunk, value head), its first and last steps among them, so that the replay runs twice."""
     torch = torch_dev
     from quotebound_amd.synthetic import round_bf16
 
@@ -376,6 +378,8 @@ def test_zero_and_tiny_decays(torch_dev, oracle, design, mode):
     g[0, 70, 1], g[0, 71, 1], g[0, 72, 1] = 1e-30, 2.0 ** -12, 2.0 ** -9
     g[0, 199, 2] = 0.0
     g[0, 128, 3] = 1e-42  # subnormal in float32
+    if crowded:  # chunk 1 (steps 64-127) of value head 2: zeros and tiny factors, first and last steps included
+        g[0, [64, 65, 80, 96, 111, 126, 127], 2] = [0.0, 1e-30, 2.0 ** -12, 0.0, 2.0 ** -11, 1e-38, 0.0]
     for n in ("q", "k", "v", "beta", "dy"):
         inp[n] = round_bf16(np.asarray(inp[n], np.float32))
     for n in ("s0", "ds_out"):

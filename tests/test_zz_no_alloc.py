@@ -82,3 +82,45 @@ def test_static_scratch_refuses_oversize(torch_dev):
     assert _lib.workspace_bytes(d) > _lib.STATIC_SCRATCH_BYTES
     with pytest.raises(RuntimeError, match="without allocation needs"):
         _lib.bwd_static(d, *([16] * 14), None)
+
+
+def test_static_scratch_backward_in_a_graph(torch_dev):
+    """qb_gdn_bwd_static captured into a HIP graph on a side stream (after its first call on the device, outside the
+    capture, as the header asks), replayed three times with eager work between the replays: every replay equals
+    qb_gdn_bwd with a caller-allocated workspace, bit for bit."""
+    torch = torch_dev
+    from quotebound_amd.synthetic import Workload
+
+    w = Workload("graph", 1, 700, 4, 8, 128, 128, seed=65, s0_std=0.02, ds_out=True, seq_lens=[300, 0, 400])
+    print(f"static-scratch backward in a graph: T={w.T} Hk={w.Hk} Hv={w.Hv} packed {w.seq_lens}", flush=True)
+    desc, hold, args, ws, outs, stream = _case(torch, w, _lib.CHUNKED)
+    p = lambda t: t.data_ptr()  # noqa: E731
+    names = ("dq", "dk", "dv", "dg", "dbeta", "ds0")
+    want, got = outs(), outs()
+    _lib.bwd(desc, *args, *[p(t) for t in want], ws.data_ptr(), stream)
+    _lib.bwd_static(desc, *args, *[p(t) for t in got], stream)  # the first call on the device, outside any capture
+    torch.cuda.synchronize()
+    for name, a, b in zip(names, want, got):
+        assert not torch.isnan(a).any(), name
+        assert torch.equal(a, b), name
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.graph(graph, stream=side):
+        _lib.bwd_static(desc, *args, *[p(t) for t in got], side.cuda_stream)
+    torch.cuda.synchronize()
+    again = outs()
+    for r in range(3):
+        for t in got:
+            t.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for name, a, b in zip(names, want, got):
+            assert torch.equal(a, b), f"replay {r} {name}: max |diff| {(a.float() - b.float()).abs().max().item()}"
+        # eager work between the replays: the allocating backward again, into other buffers
+        _lib.bwd(desc, *args, *[p(t) for t in again], ws.data_ptr(), stream)
+        torch.cuda.synchronize()
+        for name, a, b in zip(names, want, again):
+            assert torch.equal(a, b), f"eager after replay {r} {name}"
+    del graph, hold
