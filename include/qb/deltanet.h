@@ -18,7 +18,7 @@ std::pair<array, array> gated_delta(const array& q, const array& k, const array&
 // The forward keeping the state after every token: (y in q's dtype, states [B, T, Hv, Dv, Dk] float32, entry t
 // the state after token t). It replaces the reference's rows pass, one gated_delta call per token
 // (src/deltanet.cpp:101-117), whose states a draft decoder rolls back to (src/exact.cpp:152-162). It always runs
-// the recurrent design, so Dk must be a multiple of 32 of at most 256.
+// the recurrent design, so Dk must be a multiple of 32 of at most 4096.
 std::pair<array, array> gated_delta_rows(const array& q, const array& k, const array& v, const array& g,
                                          const array& beta, const array& state);
 

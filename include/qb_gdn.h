@@ -105,7 +105,7 @@ int qb_gdn_fwd(const qb_gdn_desc* desc, const void* q, const void* k, const void
  * the reference's rows pass, one gated_delta call per token keeping each step's state (src/deltanet.cpp:101-117;
  * RowStates, src/model.h:80-86; keep_rows, src/exact.cpp:152-162). row_states [tokens, Hv, Dv, Dk] float32, where
  * tokens is B*T (or the packed total): entry t is the state after token t. Always runs the recurrent design, whatever
- * desc->design says (the shape must suit it: Dk a multiple of 32 of at most 256), so no ckpt or workspace is taken. */
+ * desc->design says (the shape must suit it: Dk a multiple of 32 of at most 4096), so no ckpt or workspace is taken. */
 int qb_gdn_fwd_rows(const qb_gdn_desc* desc, const void* q, const void* k, const void* v, const float* g,
                     const void* beta, const float* s0, void* y, float* row_states, void* stream, char* err,
                     int errlen);

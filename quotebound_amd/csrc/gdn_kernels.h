@@ -72,6 +72,17 @@ extern const char* const kRecBwdLaunches;
 hipError_t rec_fwd(const Problem& p, const FwdPtrs& a, void* ws, hipStream_t s, Tracer& tr);
 hipError_t rec_bwd(const Problem& p, const BwdPtrs& a, void* ws, hipStream_t s, Tracer& tr);
 
+// Design 1 past Dk = 256 (rec_wide.hip): one wave per state row, rows per block for the forward and the backward
+// (the backward's is the row-block granularity of its partials), the backward's per-row scratch, and the kernels.
+int rec_wide_fwd_rows(int Dk);
+int rec_wide_bwd_rows(int Dk);
+size_t rec_wide_scratch_bytes(const Problem& p);
+template <typename InT, typename OutT>
+hipError_t rec_wide_fwd(const Problem& p, const FwdPtrs& ptrs, hipStream_t s);
+template <typename InT, typename OutT>
+hipError_t rec_wide_bwd(const Problem& p, const BwdPtrs& ptrs, float* dq_part, float* dk_part, float* dg_part,
+                        float* db_part, float* scratch, int nblk, hipStream_t s);
+
 // Design 2: chunkwise WY/UT form on MFMA.
 const char* chunk_supports(const Problem& p);
 size_t chunk_ckpt_bytes(const Problem& p);

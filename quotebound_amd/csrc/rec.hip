@@ -41,8 +41,9 @@ struct Layout {
   static constexpr int kRowsPerWave = 64 / LPR;
   static constexpr int kRows = kWaves * kRowsPerWave;
 };
-// Rows per block for a key width (the host side's view of the same layout): 16 up to Dk = 128, 8 past it.
-inline int rec_rows(int Dk) { return Dk <= 128 ? 16 : 8; }
+// Rows per block for a key width (the host side's view of the same layout, and the row-block granularity of the
+// backward's partials): 16 up to Dk = 128, 8 up to 256, then the wide kernels' (rec_wide.hip).
+inline int rec_rows(int Dk) { return Dk <= 128 ? 16 : Dk <= 256 ? 8 : rec_wide_bwd_rows(Dk); }
 
 // Sum over each group of LPR lanes; every lane of the group gets the same bits.
 template <int LPR>
@@ -590,6 +591,11 @@ hipError_t launch_fwd(const Problem& p, const FwdPtrs& ptrs, hipStream_t s, Trac
   a.tab = p.tab;
   const dim3 grid(a.total);
   tr.mark();
+  if (p.Dk > 256) {  // one wave per row (rec_wide.hip)
+    const hipError_t e = rec_wide_fwd<InT, OutT>(p, ptrs, s);
+    tr.mark();
+    return e;
+  }
   const bool rows = ptrs.rows != nullptr;
   const bool ok = with_width(p.Dk, [&](auto npt, auto lpr) {
     constexpr int NPT = decltype(npt)::value, LPR = decltype(lpr)::value;
@@ -605,14 +611,15 @@ hipError_t launch_fwd(const Problem& p, const FwdPtrs& ptrs, hipStream_t s, Trac
 }
 
 struct BwdWs {
-  float *dq_part, *dk_part, *dg_part, *db_part;
+  float *dq_part, *dk_part, *dg_part, *db_part, *scratch;
 };
 
+// The partials, then (past Dk = 256) the wide backward's per-row scratch.
 BwdWs carve(const Problem& p, void* ws) {
   const int64_t nblk = row_blocks(p);
   const int64_t big = p.BT * p.Hv * nblk * p.Dk, small = p.BT * p.Hv * nblk;
   float* f = static_cast<float*>(ws);
-  return BwdWs{f, f + big, f + 2 * big, f + 2 * big + small};
+  return BwdWs{f, f + big, f + 2 * big, f + 2 * big + small, f + 2 * big + 2 * small};
 }
 
 template <typename InT, typename OutT>
@@ -628,13 +635,18 @@ hipError_t launch_bwd(const Problem& p, const BwdPtrs& ptrs, void* ws, hipStream
   a.tab = p.tab;
   const dim3 grid(a.total);
   tr.mark();
-  const bool ok = with_width(p.Dk, [&](auto npt, auto lpr) {
-    constexpr int NPT = decltype(npt)::value, LPR = decltype(lpr)::value;
-    const dim3 block(Layout<NPT, LPR>::kThreads);
-    hipLaunchKernelGGL((rec_bwd_kernel<NPT, LPR, InT, OutT>), grid, block, 0, s, a);
-  });
-  if (!ok) return hipErrorInvalidValue;
-  hipError_t e = hipGetLastError();
+  hipError_t e = hipSuccess;
+  if (p.Dk > 256) {  // one wave per row (rec_wide.hip)
+    e = rec_wide_bwd<InT, OutT>(p, ptrs, w.dq_part, w.dk_part, w.dg_part, w.db_part, w.scratch, a.nblk, s);
+  } else {
+    const bool ok = with_width(p.Dk, [&](auto npt, auto lpr) {
+      constexpr int NPT = decltype(npt)::value, LPR = decltype(lpr)::value;
+      const dim3 block(Layout<NPT, LPR>::kThreads);
+      hipLaunchKernelGGL((rec_bwd_kernel<NPT, LPR, InT, OutT>), grid, block, 0, s, a);
+    });
+    if (!ok) return hipErrorInvalidValue;
+    e = hipGetLastError();
+  }
   if (e != hipSuccess) return e;
   tr.mark();
   if (p.BT == 0) {
@@ -652,8 +664,10 @@ hipError_t launch_bwd(const Problem& p, const BwdPtrs& ptrs, void* ws, hipStream
 
 }  // namespace
 
+// The reference's vjp takes Dk a multiple of 32 whose 2 * Dk * 4-byte row reduction fits its 32 KB of threadgroup
+// memory (src/delta_grad.cpp:159-170), so at most 4096.
 const char* rec_supports(const Problem& p) {
-  if (p.Dk % 32 || p.Dk > 256) return "the recurrent design needs Dk a multiple of 32 of at most 256";
+  if (p.Dk % 32 || p.Dk > 4096) return "the recurrent design needs Dk a multiple of 32 of at most 4096";
   return nullptr;
 }
 
@@ -664,7 +678,8 @@ size_t rec_ckpt_bytes(const Problem& p) {
 
 size_t rec_workspace_bytes(const Problem& p) {
   const size_t nblk = row_blocks(p);
-  return (2 * size_t(p.BT) * p.Hv * nblk * p.Dk + 2 * size_t(p.BT) * p.Hv * nblk) * sizeof(float);
+  const size_t parts = (2 * size_t(p.BT) * p.Hv * nblk * p.Dk + 2 * size_t(p.BT) * p.Hv * nblk) * sizeof(float);
+  return parts + (p.Dk > 256 ? rec_wide_scratch_bytes(p) : 0);
 }
 
 const char* const kRecFwdLaunches = "rec_fwd";

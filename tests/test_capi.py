@@ -62,10 +62,10 @@ def test_accepts_the_layer_shapes(lib):
         assert _lib.validate(d) is None
 
 
-@pytest.mark.parametrize("Dk", [32, 64, 96, 128, 160, 192, 224, 256])
-def test_recurrent_design_takes_every_key_width_to_256(lib, Dk):
-    """Every multiple of 32 up to 256, the range of the reference's own cases (reference tests/test_deltanet.cpp:154;
-    its vjp checks Dk % 32, src/delta_grad.cpp:164)."""
+@pytest.mark.parametrize("Dk", [32, 64, 96, 128, 160, 192, 224, 256, 288, 512, 1024, 2080, 4096])
+def test_recurrent_design_takes_every_key_width_to_4096(lib, Dk):
+    """Multiples of 32 up to 4096: the reference's own cases go to 256 (reference tests/test_deltanet.cpp:154) and its
+    vjp takes any multiple of 32 whose row reduction fits 32 KB of threadgroup memory (src/delta_grad.cpp:159-170)."""
     for dt in (_lib.F32, _lib.BF16):
         d, _ = desc(Dk=Dk, Dv=64, dtype=dt, design=_lib.RECURRENT)
         assert _lib.validate(d) is None
@@ -78,7 +78,7 @@ def test_recurrent_design_takes_every_key_width_to_256(lib, Dk):
     (dict(dtype=7), "dtype"),
     (dict(design=3), "design"),
     (dict(B=0), "positive"),
-    (dict(Dk=288), "recurrent design needs Dk a multiple of 32 of at most 256"),
+    (dict(Dk=4128, design=_lib.RECURRENT), "recurrent design needs Dk a multiple of 32 of at most 4096"),
     (dict(B=2, T=10, cu_seqlens=[0, 4, 10]), "B == 1"),
     (dict(T=10, cu_seqlens=[0, 4, 9]), "from 0 to T"),
     (dict(T=10, cu_seqlens=[0, 6, 4, 10]), "must not decrease"),
@@ -153,7 +153,7 @@ def test_neighbours_errors_before_any_gpu_work(lib):
 
 
 def test_fwd_rows_errors_before_any_gpu_work(lib):
-    d, _ = desc(Dk=288, Dv=64, design=_lib.CHUNKED)
+    d, _ = desc(Dk=4128, Dv=64, design=_lib.CHUNKED)
     with pytest.raises(RuntimeError, match="Dk"):
         _lib.fwd_rows(d, 16, 16, 16, 16, 16, None, 16, 16, None)
     d, _ = desc()

@@ -433,6 +433,38 @@ def test_recurrent_key_widths(torch_dev, oracle, Dk, bf16):
     assert_close(got, exp, BF16_TOL if bf16 else F32_TOL, label=f"Dk {Dk} {'bf16' if bf16 else 'f32'}")
 
 
+@pytest.mark.parametrize("Dk,Dv,lens", [
+    (288, 64, [70, 0, 131, 1]), (512, 64, [70, 0, 131, 1]), (1024, 32, [70, 0, 131, 1]),
+    (2080, 16, [70, 0, 40, 1]), (4096, 16, [70, 0, 40, 1])], ids=lambda x: str(x) if isinstance(x, int) else None)
+@pytest.mark.parametrize("bf16", [False, True], ids=["f32", "bf16"])
+def test_recurrent_wide_key_widths(torch_dev, oracle, Dk, Dv, lens, bf16):
+    """The recurrent design past Dk = 256, up to the 4096 the reference's vjp accepts (src/delta_grad.cpp:159-170):
+    one wave per state row (four, two or one rows per block by width). A packed batch with an empty sequence, a
+    nonzero initial state and a final-state cotangent, every output against the oracle, float32 at the reference's
+    1e-5."""
+    torch = torch_dev
+    from quotebound_amd.synthetic import round_bf16
+
+    Hk, Hv = 2, 4
+    print(f"recurrent design, Dk {Dk}, Dv {Dv}, packed {lens}, {'bf16' if bf16 else 'f32'}", flush=True)
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    inp = small_case(1, int(cu[-1]), Hk, Hv, Dk, Dv, seed=Dk)
+    r = np.random.default_rng(Dk)
+    inp["s0"] = r.normal(0.0, 0.1, (len(lens), Hv, Dv, Dk))
+    inp["ds_out"] = r.standard_normal((len(lens), Hv, Dv, Dk))
+    for n in ("q", "k", "v", "beta", "dy"):
+        x = np.asarray(inp[n], np.float32)
+        inp[n] = round_bf16(x) if bf16 else x
+    for n in ("g", "s0", "ds_out"):
+        inp[n] = np.asarray(inp[n], np.float32)
+    exp = oracle.fwd_bwd(inp, cu_seqlens=cu, dtype=np.float32)
+    d = host_to_dev(torch, inp, torch.bfloat16 if bf16 else torch.float32)
+    if bf16:
+        d["dy"] = d["dy"].float()
+    got = run(torch, d, _lib.RECURRENT, cu=cu, out_f32=bf16)
+    assert_close(got, exp, BF16_TOL if bf16 else F32_TOL, label=f"Dk {Dk} {'bf16' if bf16 else 'f32'}")
+
+
 @pytest.mark.parametrize("design", DESIGNS, ids=DESIGN_IDS.get)
 def test_deterministic(torch_dev, design):
     """Same inputs, same bits: every sum runs in a fixed order (the reference's resume bit-identity relies on it,
