@@ -5,14 +5,16 @@
 // end phase, as a value head's is during the previous head's.
 //
 // Per value head, with S0 the chunk's start state (checkpoint), dS its end-state cotangent (from the backward state
-// pass) and the chunk's tile (Tb, P, T, exp G, D from prep), the state rows are streamed in blocks of 32:
-//   KS = K S0^T, R = V - diag(exp G) KS, Delta = Tb R, KdS = K dS^T,
-//   dDelta = P^T dY + D KdS, dR = Tb^T dDelta                          (Tb = T diag(beta), D = diag(exp(G_63 - G)))
-//   dP^T += Delta dY^T, dTb^T += R dDelta^T, dQ_inter += dY S0, dK += -diag(exp G) dR S0 + D Delta dS
+// pass) and the chunk's tile (T, P, exp G, D, beta from prep), the state rows are streamed in blocks of 32:
+//   KS = K S0^T, R = V - diag(exp G) KS, Delta = T (diag(beta) R), KdS = K dS^T,
+//   dDelta = P^T dY + D KdS, dR' = T^T dDelta, dR = diag(beta) dR'     (D = diag(exp(G_63 - G)))
+//   dP^T += Delta dY^T, dT^T += (diag(beta) R) dDelta^T, dbeta += rowsum(R * dR'),
+//   dQ_inter += dY S0, dK += -diag(exp G) dR S0 + D Delta dS
 // then, once per value head, the 64 x 64 part:
 //   dQ += diag(exp G) dQ_inter + (dP * M) K,  dK += (dP * M)^T Q + (dKK + dKK^T) K
-//   dA = -T^T (dTb diag(beta)) T^T,  dKK = strict_lower(diag(beta) dA * E)
-//   dbeta_j = sum_i dTb_ij T_ij + sum_m dA_jm E_jm (K K^T)_jm,  dG from every exp(.) factor, dg = reverse cumsum
+//   dA = -T^T dT T^T,  dKK = strict_lower(diag(beta) dA * E)
+//   dbeta_j += sum_m dA_jm E_jm (K K^T)_jm,  dG from every exp(.) factor, dg = reverse cumsum
+// (dbeta's first term, sum_i dTb_ij T_ij with Tb = T diag(beta), equals sum_r R_jr (T^T dDelta)_jr.)
 // (tests/chunk_math.py restates these equations and checks them against the oracle.) Wave w owns positions
 // 16 (w % 4) .. + 15 and, within each product, the half w / 4 of the other index (state rows of a 32-row block,
 // key-position tiles, or 64 of the 128 columns). MFMA with split float32 operands as in the forward. Each
@@ -38,31 +40,31 @@ constexpr int kThreads = 512;
 constexpr int kLS = 144;  // S0, dS [32][128]
 constexpr int kLY = 48;   // dY [64][32]
 constexpr int kLP = 80;   // [32][64]
-constexpr int kLT = 80;   // Tb, P [64][64]
+constexpr int kLT = 80;   // T, P [64][64]
 constexpr int oS0h = 0, oS0l = oS0h + 32 * kLS, odSh = oS0l + 32 * kLS, odSl = odSh + 32 * kLS;
 constexpr int odYh = odSl + 32 * kLS, odYl = odYh + kC * kLY;
-constexpr int oRh = odYl + kC * kLY, oRl = oRh + 32 * kLP;        // R = V - diag(exp G) K S0^T
+constexpr int oRh = odYl + kC * kLY, oRl = oRh + 32 * kLP;        // diag(beta) R, R = V - diag(exp G) K S0^T
 constexpr int oDh = oRl + 32 * kLP, oDl = oDh + 32 * kLP;         // Delta
 constexpr int oDDh = oDl + 32 * kLP, oDDl = oDDh + 32 * kLP;      // D Delta
 constexpr int odDh = oDDl + 32 * kLP, odDl = odDh + 32 * kLP;     // dDelta
 constexpr int oGdRh = odDl + 32 * kLP, oGdRl = oGdRh + 32 * kLP;  // -diag(exp G) dR
 constexpr int kLoopBytes = (oGdRl + 32 * kLP) * 2;
-// End-phase region (aliases the block-loop region), bf16 element offsets: Q rows, then the value head's T, Z^T
-// (Z = dTb diag(beta) T^T) and dKK^T, each as hi and lo 64 x 64 matrices; then float32 per-position partial sums.
-// (K rows stay in their own array for the whole block; P * M and dTb diag(beta) reuse the Tb and P arrays.)
+// End-phase region (aliases the block-loop region), bf16 element offsets: Q rows, then P * M, Z^T (Z = dT T^T) and
+// dKK^T, each as hi and lo 64 x 64 matrices; then float32 per-position partial sums. (K rows stay in their own array
+// for the whole block and T in TL for the whole value head; dT reuses the P array.)
 constexpr int kLK = 144;
 constexpr int eQb = 0;
-constexpr int eTh = eQb + kC * kLK, eTl = eTh + kC * kLT;
-constexpr int eZh = eTl + kC * kLT, eZl = eZh + kC * kLT;
+constexpr int eMh = eQb + kC * kLK, eMl = eMh + kC * kLT;  // P * M
+constexpr int eZh = eMl + kC * kLT, eZl = eZh + kC * kLT;
 constexpr int eKh = eZl + kC * kLT, eKl = eKh + kC * kLT;
 constexpr int eF = (eKl + kC * kLT) / 2;  // first float32 offset
-constexpr int eX2r = eF, eX2c = eX2r + 2 * kC, edbT = eX2c + 4 * kC, edbA = edbT + 4 * kC;
+constexpr int eX2r = eF, eX2c = eX2r + 2 * kC, edbA = eX2c + 4 * kC;
 constexpr int ex1c = edbA + 2 * kC, etq = ex1c + 4 * kC;
 constexpr int kEndBytes = (etq + 2 * kC) * 4;
 constexpr int kSmemBytes = kLoopBytes > kEndBytes ? kLoopBytes : kEndBytes;
 
 // The key tile (16 positions j) that accumulator mi of the wave at position tile pw, half hw holds in dP^T and
-// dTb^T. Only tiles m <= pw carry work. For each pw the two halves together hold all four tiles; positions 0..31
+// dT^T. Only tiles m <= pw carry work. For each pw the two halves together hold all four tiles; positions 0..31
 // alternate the tiles between halves so each half works on one of the tiles 0..pw, positions 32..63 split them in
 // halves. The busiest wave of the phase that accumulates them then runs 5 products in place of 6.
 __device__ __forceinline__ int key_tile(int pw, int hw, int mi) { return pw < 2 ? hw + 2 * mi : 2 * hw + mi; }
@@ -79,17 +81,16 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
   constexpr bool kExactDy = std::is_same<OutT, bf16_t>::value;
   __shared__ __align__(16) unsigned char smem[kSmemBytes];
   __shared__ __align__(16) __bf16 Kres[kC * kLK];  // the chunk's K rows, for the whole block
-  // The value head's Tb and P (bf16 hi and lo, rows i, columns j), staged once per head: A operands of Tb rows
-  // directly, of Tb^T and P^T rows through the transposing read.
-  __shared__ __align__(16) __bf16 TbL[2][kC * kLT], PL[2][kC * kLT];
+  // The value head's T and P (bf16 hi and lo, rows i, columns j), staged once per head: A operands of T rows
+  // directly, of T^T and P^T rows through the transposing read.
+  __shared__ __align__(16) __bf16 TL[2][kC * kLT], PL[2][kC * kLT];
   __shared__ float gam[kC], dec[kC], bet[kC], Gf[kC];
-  __shared__ float gpos[2][kC], hpos[2][kC], red[kThreads / 64];
+  __shared__ float gpos[2][kC], hpos[2][kC], bpos[2][kC], red[kThreads / 64];
   __bf16* sb = reinterpret_cast<__bf16*>(smem);
   float* sf = reinterpret_cast<float*>(smem);
   typedef float Row[kC];
   Row* x2r = reinterpret_cast<Row*>(sf + eX2r);
   Row* x2c = reinterpret_cast<Row*>(sf + eX2c);
-  Row* dbTp = reinterpret_cast<Row*>(sf + edbT);
   Row* dbAp = reinterpret_cast<Row*>(sf + edbA);
   Row* x1cp = reinterpret_cast<Row*>(sf + ex1c);
   Row* tpos = reinterpret_cast<Row*>(sf + etq);
@@ -115,12 +116,12 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
     return Item{slot, sp.tok, rem / hs, sp.L, kSplit ? rem % hs : 0, kSplit ? 1 : grp};
   };
 
-  // Global reads, kept in registers from issue to staging. A value head's tile (Tb and P rows hi and lo, thread ->
+  // Global reads, kept in registers from issue to staging. A value head's tile (T and P rows hi and lo, thread ->
   // row lt / 8, columns 8 (lt % 8) .. + 7, zeros above the diagonal blocks; and the per-position scalars, thread lt <
   // 64) and one 32-row block of its state (S0 and dS rows, dY, v). dy and v go through buffer resources that end at
   // the chunk's last row, so rows past it read as zeros without a branch.
   struct TileIn {
-    bf16x8 tp[4];  // Tb hi, Tb lo, P hi, P lo
+    bf16x8 tp[4];  // T hi, T lo, P hi, P lo
     float sc[4];   // exp G, exp(G_63 - G), beta, G
   };
   struct BlockIn {
@@ -131,7 +132,7 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
   auto load_tile = [&](TileIn& ti, const Item& it, int hv, int lt) {
     const Tile* tl = a.tiles + it.slot * a.Hv + hv;
     if (lt < kC) ti.sc[0] = tl->gam[lt], ti.sc[1] = tl->dec[lt], ti.sc[2] = tl->beta[lt], ti.sc[3] = tl->G[lt];
-    const auto tr = buffer_rsrc(tl->tb[0], 4 * kTri * 2);  // tb[0], tb[1], p[0], p[1] are contiguous
+    const auto tr = buffer_rsrc(tl->t[0], 4 * kTri * 2);  // t[0], t[1], p[0], p[1] are contiguous
 #pragma unroll
     for (int q4 = 0; q4 < 4; ++q4) ti.tp[q4] = tri_ld8(tr, q4 * kTri, lt >> 3, (lt & 7) * 8);
   };
@@ -212,28 +213,24 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
       }
       __syncthreads();
       if (tid < kC) gam[tid] = ti.sc[0], dec[tid] = ti.sc[1], bet[tid] = ti.sc[2], Gf[tid] = ti.sc[3];
-      {  // Tb and P, hi and lo
+      {  // T and P, hi and lo
         const int lt8 = swz(tid >> 3, (tid & 7) * 8, kLT);
-        *reinterpret_cast<bf16x8*>(TbL[0] + lt8) = ti.tp[0];
-        *reinterpret_cast<bf16x8*>(TbL[1] + lt8) = ti.tp[1];
+        *reinterpret_cast<bf16x8*>(TL[0] + lt8) = ti.tp[0];
+        *reinterpret_cast<bf16x8*>(TL[1] + lt8) = ti.tp[1];
         *reinterpret_cast<bf16x8*>(PL[0] + lt8) = ti.tp[2];
         *reinterpret_cast<bf16x8*>(PL[1] + lt8) = ti.tp[3];
       }
-      f32x4 dPt[2], dTbt[2], dQi[4];  // dPt, dTbt: key tiles m = key_tile(pw, hw, mi); lane -> column i = ip, rows j
+      f32x4 dPt[2], dTt[2], dQi[4];  // dPt, dTt: key tiles m = key_tile(pw, hw, mi); lane -> column i = ip, rows j
 #pragma unroll
-      for (int t = 0; t < 2; ++t) dPt[t] = zero4(), dTbt[t] = zero4();
+      for (int t = 0; t < 2; ++t) dPt[t] = zero4(), dTt[t] = zero4();
 #pragma unroll
       for (int t = 0; t < 4; ++t) dQi[t] = zero4();
-      float gpart[4] = {0.f, 0.f, 0.f, 0.f}, hD[4] = {0.f, 0.f, 0.f, 0.f}, sds = 0.f;
+      float gpart[4] = {0.f, 0.f, 0.f, 0.f}, hD[4] = {0.f, 0.f, 0.f, 0.f}, bpart[4] = {0.f, 0.f, 0.f, 0.f}, sds = 0.f;
       __syncthreads();
 
-      // The end phase's inputs (T rows hi and lo, Q rows, as bf16 bits), loaded during the value head's last block
-      // into the registers the next block's reads would use: thread -> T row tid / 8, columns 8 (tid % 8) .. + 7
-      // (zeros above the diagonal blocks), and Q row e / 16, columns 8 (e % 16) .. + 7 for e = tid, tid + 512.
+      // The end phase's inputs (Q rows, as bf16 bits), loaded during the value head's last block into the registers
+      // the next block's reads would use: thread -> Q row e / 16, columns 8 (e % 16) .. + 7 for e = tid, tid + 512.
       auto load_end = [&](BlockIn& b, int lt) {
-        const auto trr = buffer_rsrc(tl->t[0], 2 * kTri * 2);
-        b.xs[0] = __builtin_bit_cast(float4, tri_ld8(trr, 0, lt >> 3, (lt & 7) * 8));
-        b.xs[1] = __builtin_bit_cast(float4, tri_ld8(trr, kTri, lt >> 3, (lt & 7) * 8));
 #pragma unroll
         for (int q2 = 0; q2 < 2; ++q2) {
           const int e = lt + kThreads * q2, t = e >> 4, c8 = (e & 15) * 8;
@@ -305,18 +302,19 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
           gks[jj] = gam[i0 + jj] * ks[jj];
           rv[jj] = vv[jj] - gks[jj];
         }
-        put4(sb + oRh, sb + oRl, swz(r, i0, kLP), rv[0], rv[1], rv[2], rv[3]);
+        put4(sb + oRh, sb + oRl, swz(r, i0, kLP), bet[i0] * rv[0], bet[i0 + 1] * rv[1], bet[i0 + 2] * rv[2],
+             bet[i0 + 3] * rv[3]);
         __syncthreads();
         if constexpr (more) load_rows(nb.ys, a.dsend, cur, hv, r0 + 32, lt);
 
-        // Phase 2: Delta = Tb R and dDelta = P^T dY + D KdS (rows: the wave's positions; lane: row r).
+        // Phase 2: Delta = T (diag(beta) R) and dDelta = P^T dY + D KdS (rows: the wave's positions; lane: row r).
         f32x4 dl = zero4(), dd;
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
-          if (s == 0 || pw >= 2) {  // Tb is zero above the diagonal blocks: rows 0..31 end at column 31
+          if (s == 0 || pw >= 2) {  // T is zero above the diagonal blocks: rows 0..31 end at column 31
             const int at = swz(r, 32 * s + 8 * g, kLP), atb = swz(ip, 32 * s + 8 * g, kLT);
-            const Split8 TbA{lds8(TbL[0] + atb), lds8(TbL[1] + atb)};
-            dl = mma3(dl, TbA, Split8{lds8(sb + oRh + at), lds8(sb + oRl + at)});
+            const Split8 TA{lds8(TL[0] + atb), lds8(TL[1] + atb)};
+            dl = mma3(dl, TA, Split8{lds8(sb + oRh + at), lds8(sb + oRl + at)});
           }
         }
 #pragma unroll
@@ -347,22 +345,25 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
         __syncthreads();
         if constexpr (more) load_dy_v(nb, cur, hv, r0 + 32, lt);
 
-        // Phase 3: dR = Tb^T dDelta; dP^T += Delta dY^T and dTb^T += R dDelta^T over this half's key tiles.
+        // Phase 3: dR = diag(beta) T^T dDelta (and dbeta's T part, R * (T^T dDelta) summed over the rows); dP^T +=
+        // Delta dY^T and dT^T += (diag(beta) R) dDelta^T over this half's key tiles.
         {
           f32x4 dr = zero4();
 #pragma unroll
           for (int s = 0; s < 2; ++s) {
-            if (32 * s + 31 >= 16 * pw) {  // Tb^T is zero below the diagonal
+            if (32 * s + 31 >= 16 * pw) {  // T^T is zero below the diagonal
               const int at = swz(r, 32 * s + 8 * g, kLP);
-              // Tb^T rows ip (k = j): Tb's rows 32s.., column ip.
-              const Split8 TbtA{lds_tr8s(TbL[0] + 32 * s * kLT + 16 * pw, kLT, lt),
-                                lds_tr8s(TbL[1] + 32 * s * kLT + 16 * pw, kLT, lt)};
-              dr = mma3(dr, TbtA, Split8{lds8(sb + odDh + at), lds8(sb + odDl + at)});
+              // T^T rows ip (k = j): T's rows 32s.., column ip.
+              const Split8 TtA{lds_tr8s(TL[0] + 32 * s * kLT + 16 * pw, kLT, lt),
+                               lds_tr8s(TL[1] + 32 * s * kLT + 16 * pw, kLT, lt)};
+              dr = mma3(dr, TtA, Split8{lds8(sb + odDh + at), lds8(sb + odDl + at)});
             }
           }
           float gdr[4];
 #pragma unroll
           for (int jj = 0; jj < 4; ++jj) {
+            bpart[jj] += rv[jj] * dr[jj];
+            dr[jj] *= bet[i0 + jj];
             gpart[jj] -= dr[jj] * gks[jj];
             gdr[jj] = -gam[i0 + jj] * dr[jj];
           }
@@ -375,14 +376,14 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
           for (int mi = 0; mi < 2; ++mi) {
             const int m = key_tile(pw, hw, mi);
             if (m <= pw) {
-              // Delta and R rows j of key tile m as A (m = j, k = r).
+              // Delta and diag(beta) R rows j of key tile m as A (m = j, k = r).
               const Split8 AD{lds_tr8s(sb + oDh + 16 * m, kLP, lt), lds_tr8s(sb + oDl + 16 * m, kLP, lt)};
               if constexpr (kExactDy)
                 dPt[mi] = mma2(dPt[mi], AD, dYo.hi);
               else
                 dPt[mi] = mma3(dPt[mi], AD, dYo);
               const Split8 AR{lds_tr8s(sb + oRh + 16 * m, kLP, lt), lds_tr8s(sb + oRl + 16 * m, kLP, lt)};
-              dTbt[mi] = mma3(dTbt[mi], AR, BdD);
+              dTt[mi] = mma3(dTt[mi], AR, BdD);
             }
           }
         }
@@ -417,8 +418,9 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
       const int i0 = 16 * pw + 4 * g;  // first of the lane's accumulator rows
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj) {
-        const float v = sum16(gpart[jj]), h = sum16(hD[jj]);
-        gpos[hw][i0 + jj] = v, hpos[hw][i0 + jj] = h;  // the 16 lanes of a row hold the same bits: no branch
+        const float v = sum16(gpart[jj]), h = sum16(hD[jj]), bt = sum16(bpart[jj]);
+        // the 16 lanes of a row hold the same bits: no branch
+        gpos[hw][i0 + jj] = v, hpos[hw][i0 + jj] = h, bpos[hw][i0 + jj] = bt;
       }
       {
         float v = sum16(sds);
@@ -427,15 +429,12 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
       }
       __syncthreads();
 
-      // E1: Q rows and T (hi, lo) into the end-phase region. Per lane, at i = ip and
-      // j = 16 key_tile(pw, hw, mi) + 4g + jj (dP and dTb masked to j <= i): the row and column sums of dP * P (the P
-      // factor's part of dG), P * M with M_ij = exp(G_i - G_j) over P's entries, and dTb diag(beta), both as hi and lo
-      // in place of Tb and P (each lane rewrites only the P entries it has just read).
+      // E1: Q rows into the end-phase region. Per lane, at i = ip and j = 16 key_tile(pw, hw, mi) + 4g + jj (dP and
+      // dT masked to j <= i): the row and column sums of dP * P (the P factor's part of dG), P * M with
+      // M_ij = exp(G_i - G_j) over P's entries into the end-phase region, and dT, both as hi and lo, dT in place of P
+      // (each lane rewrites only the P entries it has just read).
       {
         {
-          const int at = swz(lt >> 3, (lt & 7) * 8, kLT);
-          *reinterpret_cast<float4*>(sb + eTh + at) = nb.xs[0];
-          *reinterpret_cast<float4*>(sb + eTl + at) = nb.xs[1];
 #pragma unroll
           for (int q2 = 0; q2 < 2; ++q2) {
             const int e = lt + kThreads * q2;
@@ -465,9 +464,9 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
             x2c[pw][j] = col;
             // Where j > i, dp is zero and the exponent positive: clamped at 0 to keep the product finite.
             pm[jj] = dp * __expf(fminf(gi - Gf[j], 0.f));
-            db[jj] = (j <= ip ? dTbt[mi][jj] : 0.f) * bet[j];
+            db[jj] = j <= ip ? dTt[mi][jj] : 0.f;
           }
-          put4(TbL[0], TbL[1], at, pm[0], pm[1], pm[2], pm[3]);
+          put4(sb + eMh, sb + eMl, at, pm[0], pm[1], pm[2], pm[3]);
           put4(PL[0], PL[1], at, db[0], db[1], db[2], db[3]);
         }
         prow = swap32_sum(swap16_sum(prow));
@@ -480,25 +479,9 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
         asm volatile("" : "+v"(lq));
         load_tile(ti, nx, nhv, lq);
       }
-      // E2: the column sums of dTb * T (dbeta's T part); dQ += diag(exp G) dQ_inter and its dG term; K K^T (the first
-      // value head only, kept in registers); dQ += (P * M) K; dK += (P * M)^T Q; Z = dTb diag(beta) T^T, stored as Z^T.
+      // E2: dQ += diag(exp G) dQ_inter and its dG term; K K^T (the first value head only, kept in registers);
+      // dQ += (P * M) K; dK += (P * M)^T Q; Z = dT T^T, stored as Z^T.
       {
-#pragma unroll
-        for (int mi = 0; mi < 2; ++mi) {
-          const int j0 = 16 * key_tile(pw, hw, mi) + 4 * g, at = swz(ip, j0, kLT);
-          const uint2 th = *reinterpret_cast<const uint2*>(sb + eTh + at);
-          const uint2 tlo = *reinterpret_cast<const uint2*>(sb + eTl + at);
-          const uint32_t hw4[2] = {th.x, th.y}, lw4[2] = {tlo.x, tlo.y};
-#pragma unroll
-          for (int jj = 0; jj < 4; ++jj) {
-            const int j = j0 + jj;
-            const uint32_t hb = hw4[jj >> 1], lb = lw4[jj >> 1];
-            const float tv = jj & 1 ? __uint_as_float(hb & 0xffff0000u) + __uint_as_float(lb & 0xffff0000u)
-                                    : __uint_as_float(hb << 16) + __uint_as_float(lb << 16);
-            const float colb = sum16((j <= ip ? dTbt[mi][jj] : 0.f) * tv);
-            dbTp[pw][j] = colb;
-          }
-        }
         float tq[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int t = 0; t < 4; ++t)
@@ -530,14 +513,14 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
         for (int s = 0; s < 2; ++s) {
           if (s == 0 || pw >= 2) {
             const int at = swz(ip, 32 * s + 8 * g, kLT);
-            const Split8 Apm{lds8(TbL[0] + at), lds8(TbL[1] + at)};  // (P * M) rows i = ip, k = j
+            const Split8 Apm{lds8(sb + eMh + at), lds8(sb + eMl + at)};  // (P * M) rows i = ip, k = j
 #pragma unroll
             for (int t = 0; t < 4; ++t)
               dQ[t] = mma2(dQ[t], Apm, lds_tr8s(Kres + 32 * s * kLK + 16 * (4 * hw + t), kLK, lt));
           }
           if (s == 1 || pw < 2) {
-            const Split8 Apmt{lds_tr8s(TbL[0] + 32 * s * kLT + 16 * pw, kLT, lt),
-                              lds_tr8s(TbL[1] + 32 * s * kLT + 16 * pw, kLT, lt)};  // (P * M)^T rows j = ip, k = i
+            const Split8 Apmt{lds_tr8s(sb + eMh + 32 * s * kLT + 16 * pw, kLT, lt),
+                              lds_tr8s(sb + eMl + 32 * s * kLT + 16 * pw, kLT, lt)};  // (P * M)^T rows j = ip, k = i
 #pragma unroll
             for (int t = 0; t < 4; ++t)
               dK[t] = mma2(dK[t], Apmt, lds_tr8s(sb + eQb + 32 * s * kLK + 16 * (4 * hw + t), kLK, lt));
@@ -550,7 +533,7 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
 #pragma unroll
           for (int s = 0; s < 2; ++s) {
             const int aa = swz(ip, 32 * s + 8 * g, kLT), ab = swz(mr, 32 * s + 8 * g, kLT);
-            z = mma3(z, Split8{lds8(PL[0] + aa), lds8(PL[1] + aa)}, Split8{lds8(sb + eTh + ab), lds8(sb + eTl + ab)});
+            z = mma3(z, Split8{lds8(PL[0] + aa), lds8(PL[1] + aa)}, Split8{lds8(TL[0] + ab), lds8(TL[1] + ab)});
           }
           put4(sb + eZh, sb + eZl, swz(mr, i0, kLT), z[0], z[1], z[2], z[3]);
         }
@@ -566,8 +549,8 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
         Split8 AT[2];  // T^T rows p = ip, k = i
 #pragma unroll
         for (int s = 0; s < 2; ++s)
-          AT[s] = Split8{lds_tr8s(sb + eTh + 32 * s * kLT + 16 * pw, kLT, lt),
-                         lds_tr8s(sb + eTl + 32 * s * kLT + 16 * pw, kLT, lt)};
+          AT[s] = Split8{lds_tr8s(TL[0] + 32 * s * kLT + 16 * pw, kLT, lt),
+                         lds_tr8s(TL[1] + 32 * s * kLT + 16 * pw, kLT, lt)};
         float rowp[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int mi = 0; mi < 2; ++mi) {
@@ -644,7 +627,7 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
         if constexpr (kFused) {
           const int64_t g0 = tok * a.Hv + hv;
           const uint32_t gi = uint32_t(t * a.Hv);
-          const float dbT = dbTp[0][t] + dbTp[1][t] + dbTp[2][t] + dbTp[3][t];
+          const float dbT = bpos[0][t] + bpos[1][t];
           float pa = 0.f, pd = 0.f;
           if (t < L) {
             float da, db;
@@ -660,7 +643,7 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
           const int64_t g0 = tok * a.Hv + hv;
           const uint32_t gi = uint32_t(t * a.Hv);
           a.dg[g0 + gi] = a.g_is_log ? v : v / a.g[g0 + gi];
-          const float dbT = dbTp[0][t] + dbTp[1][t] + dbTp[2][t] + dbTp[3][t];
+          const float dbT = bpos[0][t] + bpos[1][t];
           IO<OutT>::st(static_cast<OutT*>(a.dbeta) + g0, gi, dbT + dbA);
         }
       }

@@ -4,11 +4,11 @@
 // state rows (or one state row and four consecutive columns):
 //   store dS (the gradient kernel needs it)
 //   dDelta^T = (dS K^T) D + dY^T P,  D = diag(exp(G_63 - G))      waves 0-3, positions 16w..16w+15: the chain
-//   dR^T = dDelta^T Tb;   dv = dR                                  waves 0-3
+//   dR^T = dDelta^T T diag(beta);   dv = dR                        waves 0-3
 //   X^T = Q^T (diag(exp G) dY)                                     waves 4-7, beside the chain (no dS in it)
 //   dS^T <- exp(G_63) dS^T + X^T - K^T (diag(exp G) dR)            waves 0-3, state columns 32w..32w+31
 // This is the adjoint of the forward state pass; together with the gradient kernel it reproduces the reference's
-// backward (src/delta_grad.cpp:14-18). dS0 is what remains after the first chunk. Tb and P come ready from the prep
+// backward (src/delta_grad.cpp:14-18). dS0 is what remains after the first chunk. T and P come ready from the prep
 // kernel, packed; the products that contract over their rows read them through the transposing LDS read (tri_tr8).
 // MFMA with split float32 operands as in the forward. Three barriers per chunk. Waves 4-7 load every input of the
 // next chunk (in the reverse sweep) in two groups, in windows where they would otherwise wait for the chain, and
@@ -40,9 +40,9 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_state_kernel(ChunkArgs a) 
   __shared__ __align__(16) __bf16 Qb[kC * kLK];                   // q rows
   __shared__ __align__(16) __bf16 dYm[2][kC * kLP], GdYm[2][kC * kLP];
   __shared__ __align__(16) __bf16 dDm[2][kC * kLP], GdRm[2][kC * kLP];
-  __shared__ __align__(16) __bf16 Tbp[kTriUnits * 8], Pp[kTriUnits * 8];  // packed Tb, P (hi then lo)
+  __shared__ __align__(16) __bf16 Tbp[kTriUnits * 8], Pp[kTriUnits * 8];  // packed T, P (hi then lo)
   __shared__ __align__(16) float Xs[16 * kLX];
-  __shared__ float Gs[2][2 * kC];  // exp G, then D, by chunk parity
+  __shared__ float Gs[2][3 * kC];  // exp G, D, beta, by chunk parity
 
   const int total = a.nblk * a.Hv * a.N;
   const StateItem item = state_item(a.tab, blockIdx.x, a.nblk, a.Hv, a.Hk, total);
@@ -64,16 +64,16 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_state_kernel(ChunkArgs a) 
 
   if (side) {
     // Waves 4-7. One chunk's inputs, loaded a chunk ahead: (a) k and q rows, staged while the chain computes dR;
-    // (b) dy, the packed Tb and P, and exp G, D, staged after the chain's last use of the previous ones. k, q, dy go
-    // through buffer resources that end at the sequence's last row, so rows past it read as zeros without a branch;
-    // units past the packed matrices read as zeros and land in padding.
+    // (b) dy, the packed T and P, and exp G, D, beta, staged after the chain's last use of the previous ones. k, q,
+    // dy go through buffer resources that end at the sequence's last row, so rows past it read as zeros without a
+    // branch; units past the packed matrices read as zeros and land in padding.
     struct GroupA {
       uint4 k[4], q[4];  // units u + 256 q4: row e / 16, columns 8 (e % 16) ..
     };
     struct GroupB {
       uint4 dy;           // row u / 4, state rows 4 (u % 4) .. + 3: raw bits (4 bf16 in .x, .y, or 4 float32)
-      uint4 tb[3], p[3];  // packed units u + 256 t
-      float gam, dec;     // of position lane (every wave loads all 64)
+      uint4 tb[3], p[3];    // packed T and P units u + 256 t
+      float gam, dec, bet;  // of position lane (every wave loads all 64)
     };
     auto load_a = [&](GroupA& f, int c) {
       const int64_t tok = sq.tok0 + int64_t(c) * kC;
@@ -103,13 +103,14 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_state_kernel(ChunkArgs a) 
       } else {
         f.dy = buf_ld16(yr, yo * 4);
       }
-      const auto tr = buffer_rsrc(tl->tb[0], 2 * kTri * 2), pr = buffer_rsrc(tl->p[0], 2 * kTri * 2);
+      const auto tr = buffer_rsrc(tl->t[0], 2 * kTri * 2), pr = buffer_rsrc(tl->p[0], 2 * kTri * 2);
 #pragma unroll
       for (int t = 0; t < 3; ++t) f.tb[t] = buf_ld16(tr, uint32_t(u + 256 * t) * 16);
 #pragma unroll
       for (int t = 0; t < 3; ++t) f.p[t] = buf_ld16(pr, uint32_t(u + 256 * t) * 16);
-      const auto gr = buffer_rsrc(tl->gam, 2 * kC * 4);  // gam, then dec
+      const auto gr = buffer_rsrc(tl->gam, 3 * kC * 4);  // gam, dec, beta
       f.gam = buf_ld4(gr, uint32_t(lane) * 4), f.dec = buf_ld4(gr, uint32_t(kC + lane) * 4);
+      f.bet = buf_ld4(gr, uint32_t(2 * kC + lane) * 4);
     };
     auto stage_a = [&](const GroupA& f, int b) {
 #pragma unroll
@@ -137,7 +138,7 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_state_kernel(ChunkArgs a) 
         *reinterpret_cast<uint4*>(Tbp + 8 * (u + 256 * t)) = f.tb[t];
         *reinterpret_cast<uint4*>(Pp + 8 * (u + 256 * t)) = f.p[t];
       }
-      if (u < kC) Gs[b][u] = f.gam, Gs[b][kC + u] = f.dec;
+      if (u < kC) Gs[b][u] = f.gam, Gs[b][kC + u] = f.dec, Gs[b][2 * kC + u] = f.bet;
     };
     // Per chunk c: X^T for it (its q and diag(exp G) dY were staged during chunk c + 1); the inputs of chunk c - 1,
     // loaded during chunk c + 1, to LDS; the loads of chunk c - 2 (clamped at 0: the last chunks load chunk 0 again
@@ -167,7 +168,7 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_state_kernel(ChunkArgs a) 
       load_b(nxt.b, cn);
       stage_a(cur.a, cs & 1);  // q's last readers (the X^T above) and k's (chunk c + 1) are a barrier back
       __syncthreads();
-      stage_b(cur.b, cs & 1);  // the chain's last readers of dY, Tb, P were before this barrier
+      stage_b(cur.b, cs & 1);  // the chain's last readers of dY, T, P were before this barrier
     };
     Group ga, gb;
     if (nch > 0) {
@@ -235,14 +236,14 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_state_kernel(ChunkArgs a) 
     }
     __syncthreads();
 
-    {  // dR^T = dDelta^T Tb: A = dDelta^T through the transposing read, B = Tb's column ip; dv = dR
+    {  // dR^T = dDelta^T T diag(beta): A = dDelta^T through the transposing read, B = T's column ip; dv = dR
       f32x4 d2[2];
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
         const Split8 A{lds_tr8s(dDm[0] + 32 * s * kLP, kLP, lane), lds_tr8s(dDm[1] + 32 * s * kLP, kLP, lane)};
         d2[s] = mma3(zero4(), A, Split8{tri_tr8(Tbp, 32 * s, wp, lane), tri_tr8(Tbp + kTri, 32 * s, wp, lane)});
       }
-      const f32x4 dr = d2[0] + d2[1];
+      const f32x4 dr = Gs[b][2 * kC + ip] * (d2[0] + d2[1]);
       // Positions past the chunk's end fall past the resource and are dropped.
       const auto vr = buffer_rsrc(dv + tok * sv + hv * a.Dv + row0, L * sv * uint32_t(sizeof(OutT)));
       BufIO<OutT>::st4(vr, uint32_t(ip * sv + 4 * g), dr);

@@ -15,11 +15,12 @@ constexpr int kC = kChunk;  // 64 positions per chunk
 constexpr int kPadB = 8;    // bf16 row padding in LDS (keeps 16-byte alignment, staggers banks)
 
 // Everything about a (chunk, value head) that does not depend on the state, as MFMA-ready bf16 hi/lo pairs:
-//   T = (I + A)^-1, A = strict_lower(diag(beta) (E * K K^T)), E_ij = exp(G_i - G_j),  Tb = T diag(beta)
+//   T = (I + A)^-1, A = strict_lower(diag(beta) (E * K K^T)), E_ij = exp(G_i - G_j)
 //   P = lower_incl(E * Q K^T)
 // and the per-position vectors. Positions past the chunk's end are padded (beta 0, log-decay 0, k = q = 0).
-// The three 64 x 64 matrices are lower triangular; each is stored as its ten 16 x 16 blocks on or below the
-// diagonal (tri_off), so the record holds no zero blocks.
+// Every step's delta_t of the chunk is T diag(beta) R; the readers apply beta to R's rows (and to the rows of dR in
+// the backward) rather than keep T diag(beta) as a third matrix. The two 64 x 64 matrices are lower triangular; each
+// is stored as its ten 16 x 16 blocks on or below the diagonal (tri_off), so the record holds no zero blocks.
 constexpr int kTri = 10 * 256;
 
 // Element offset of (i, j), j / 16 <= i / 16, in a lower-triangular 64 x 64 matrix stored as the blocks (I, J),
@@ -30,13 +31,12 @@ __host__ __device__ constexpr int tri_off(int i, int j) {
 }
 
 struct Tile {
-  bf16_t tb[2][kTri];  // Tb, hi and lo (row i, column j)
-  bf16_t p[2][kTri];   // P, hi and lo (row i: query, column j: key)
-  bf16_t t[2][kTri];   // T, hi and lo
+  bf16_t t[2][kTri];  // T, hi and lo (row i, column j)
+  bf16_t p[2][kTri];  // P, hi and lo (row i: query, column j: key)
+  float gam[kC];      // exp(G_i)
+  float dec[kC];      // exp(G_63 - G_i)
   float beta[kC];
-  float gam[kC];  // exp(G_i)
-  float dec[kC];  // exp(G_63 - G_i)
-  float G[kC];    // G_i = sum_{j <= i} a_j within the chunk
+  float G[kC];        // G_i = sum_{j <= i} a_j within the chunk
 };
 static_assert(sizeof(Tile) % 16 == 0, "Tile records stay 16-byte aligned");
 

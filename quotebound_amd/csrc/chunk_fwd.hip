@@ -4,19 +4,19 @@
 // product is formed transposed, so that a lane holds one position i and four consecutive state rows r (or one
 // state row and four consecutive columns):
 //   write S to LDS and to the chunk's checkpoint slot (the reference's ckpt, src/delta_grad.cpp:172-181)
-//   R^T = V^T - (S K^T) diag(exp G), and S Q^T                     waves 4-7, positions 16(w-4)..
-//   Delta^T = R^T Tb^T                                             waves 0-3, positions 16w..16w+15
+//   R^T = (V^T - (S K^T) diag(exp G)) diag(beta), and S Q^T        waves 4-7, positions 16(w-4)..
+//   Delta^T = R^T T^T                                              waves 0-3, positions 16w..16w+15
 //   S^T <- exp(G_63) S^T + K^T (D Delta),  D = diag(exp(G_63 - G)) waves 0-3, state columns 32w..32w+31
 //   Y^T = (S Q^T) diag(exp G) + Delta^T P^T                        waves 4-7: off the chain
 // Three barriers per chunk. Waves 0-3 carry the state and touch no global memory but the checkpoint stores.
 // Waves 4-7 read S from LDS once for both S K^T and S Q^T, and form y from LDS. Waves 8-11 load every input two chunks ahead, each wave load reading whole cache lines,
-// and stage them in LDS: the chain's k rows, packed Tb, v and exp G (two buffers, by chunk parity), the output
+// and stage them in LDS: the chain's k rows, packed T, v, exp G, D and beta (two buffers, by chunk parity), the output
 // group's q rows and packed P (one buffer each); K^T for the state update comes from the staged k rows through the
 // transposing read. The loads and the LDS writes are spread over the chain's phases and the work over two groups,
 // so that neither group, nor the CU's vector memory path or LDS, holds the chain at its barriers. Each group
 // runs a loop of its own, so that each loop holds only its own group's memory operations: the compiler's waits stay
 // exact and none covers a load issued for a later chunk. All products run on v_mfma_f32_16x16x32_bf16; float32
-// operands (S, R, Delta, Tb, P) are split into bf16 hi + lo pairs so the state keeps float32 accuracy, while k, q, v
+// operands (S, R, Delta, T, P) are split into bf16 hi + lo pairs so the state keeps float32 accuracy, while k, q, v
 // enter exactly.
 #include "chunk_common.h"
 #include "chunk_kernels.h"
@@ -29,7 +29,7 @@ constexpr int kThreads = 768;  // waves 0-3 the chain, 4-7 the output, 8-11 the 
 constexpr int kLS = 144;  // S [16][128]
 constexpr int kLK = 144;  // K [64][128]
 constexpr int kLP = 48;   // [64][16]: R, Delta, D Delta (positions as rows)
-constexpr int kTbUnits = 3 * 256;  // 16-byte units of a staged packed Tb (hi, lo: 640 used, the rest padding)
+constexpr int kTbUnits = 3 * 256;  // 16-byte units of a staged packed T (hi, lo: 640 used, the rest padding)
 
 __device__ __forceinline__ float bf16_lo(uint32_t x) { return __uint_as_float(x << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t x) { return __uint_as_float(x & 0xffff0000u); }
@@ -42,9 +42,9 @@ __global__ __launch_bounds__(kThreads) void chunk_fwd_kernel(ChunkArgs a) {
   __shared__ __align__(16) __bf16 Sm[2][16 * kLS];
   __shared__ __align__(16) __bf16 Rm[2][kC * kLP], Dm[2][kC * kLP], DDm[2][kC * kLP];
   __shared__ __align__(16) __bf16 Kb[2][kC * kLK];
-  __shared__ __align__(16) __bf16 Tbp[2][kTbUnits * 8];  // packed Tb (tri_off), hi then lo
+  __shared__ __align__(16) __bf16 Tbp[2][kTbUnits * 8];  // packed T (tri_off), hi then lo
   __shared__ __align__(16) bf16_t Vs[2][256 * 8];        // v [64][16] (units 128.. padding)
-  __shared__ __align__(16) float Gs[2][256];             // exp G [64], D [64] (the rest padding)
+  __shared__ __align__(16) float Gs[2][256];             // exp G [64], D [64], beta [64] (the rest padding)
   // The output group's operands, one buffer each: q rows (written after the chunk's S Q^T, read in the next) and
   // packed P (written after the previous chunk's y, read in this chunk's).
   __shared__ __align__(16) __bf16 Qb[kC * kLK];
@@ -67,21 +67,21 @@ __global__ __launch_bounds__(kThreads) void chunk_fwd_kernel(ChunkArgs a) {
   const int64_t srow = (int64_t(n) * a.Hv + hv) * a.Dv + row0 + li;  // the lane's state row
 
   // Waves 8-11 (the staging group) load each chunk's inputs two chunks ahead, in rows of 16-byte units that a wave
-  // reads whole (every cache line it touches in full), and stage them in LDS: k, packed Tb, v and the per-position
-  // vectors for the chain (two buffers, by chunk parity), q and packed P for waves 4-7 (the output group), which
-  // then read no global memory. k, q, v go through buffer resources that end at the sequence's last row, so rows
-  // past it read as zeros without a branch; units past the packed matrices, v or the two per-position vectors read
-  // as zeros, and the waves whose units are all past them (10 and 11) skip those LDS writes.
+  // reads whole (every cache line it touches in full), and stage them in LDS: k, packed T, v and the per-position
+  // vectors for the chain and the output group's R (two buffers, by chunk parity), q and packed P for waves 4-7 (the
+  // output group), which then read no global memory. k, q, v go through buffer resources that end at the sequence's
+  // last row, so rows past it read as zeros without a branch; units past the packed matrices, v or the three
+  // per-position vectors read as zeros, and the waves whose units are all past them skip those LDS writes.
   struct Stage {
     uint4 k[4];   // k units u + 256 q4: row e / 16, columns 8 (e % 16) ..
     uint4 q[4];   // q, the same units
-    uint4 tb[3];  // packed Tb units u + 256 t
+    uint4 tb[3];  // packed T units u + 256 t
     uint4 p[3];   // packed P units u + 256 t
     uint4 v;      // v unit u: row u / 2, state rows 8 (u % 2) ..
-    float gd;     // exp G_u (u < 64), D_(u - 64) (u < 128)
+    float gd;     // exp G_u (u < 64), D_(u - 64) (u < 128), beta_(u - 128) (u < 192)
   };
   // The loads in two parts, issued in two of the chain's phases so that the CU's vector memory path is not asked
-  // for a whole chunk's bytes at once: k and packed Tb, then q, packed P, v and the per-position vectors.
+  // for a whole chunk's bytes at once: k and packed T, then q, packed P, v and the per-position vectors.
   auto load1 = [&](Stage& st, int c) {
     const int64_t slot = sq.slot0 + c, tok = sq.tok0 + int64_t(c) * kC;
     const uint32_t L = uint32_t(min(kC, sq.len - c * kC));
@@ -92,7 +92,7 @@ __global__ __launch_bounds__(kThreads) void chunk_fwd_kernel(ChunkArgs a) {
       const int e = u + 256 * q4;
       st.k[q4] = buf_ld16(kr, uint32_t((e >> 4) * sk + (e & 15) * 8) * 2);
     }
-    const auto tr = buffer_rsrc(tl->tb[0], 2 * kTri * 2);
+    const auto tr = buffer_rsrc(tl->t[0], 2 * kTri * 2);
 #pragma unroll
     for (int t = 0; t < 3; ++t) st.tb[t] = buf_ld16(tr, uint32_t(u + 256 * t) * 16);
   };
@@ -106,7 +106,7 @@ __global__ __launch_bounds__(kThreads) void chunk_fwd_kernel(ChunkArgs a) {
       const int e = u + 256 * q4;
       st.q[q4] = buf_ld16(qr, uint32_t((e >> 4) * sk + (e & 15) * 8) * 2);
     }
-    const auto gr = buffer_rsrc(tl->gam, 2 * kC * 4);  // gam, then dec
+    const auto gr = buffer_rsrc(tl->gam, 3 * kC * 4);  // gam, dec, beta
     st.gd = buf_ld4(gr, uint32_t(u) * 4);
     const auto vr = buffer_rsrc(a.v + tok * sv + hv * a.Dv + row0, L * sv * 2);
     st.v = buf_ld16(vr, u < 128 ? uint32_t((u >> 1) * sv + 8 * (u & 1)) * 2 : 0x80000000u);
@@ -114,7 +114,7 @@ __global__ __launch_bounds__(kThreads) void chunk_fwd_kernel(ChunkArgs a) {
 #pragma unroll
     for (int t = 0; t < 3; ++t) st.p[t] = buf_ld16(pr, uint32_t(u + 256 * t) * 16);
   };
-  // k and packed Tb, then v, the per-position vectors and q: to buffer b of the chain and to Qb.
+  // k and packed T, then v, the per-position vectors and q: to buffer b of the chain and to Qb.
   auto stage1 = [&](const Stage& st, int b) {
 #pragma unroll
     for (int q4 = 0; q4 < 4; ++q4) {
@@ -131,10 +131,8 @@ __global__ __launch_bounds__(kThreads) void chunk_fwd_kernel(ChunkArgs a) {
       const int e = u + 256 * q4;
       *reinterpret_cast<uint4*>(Qb + swz(e >> 4, (e & 15) * 8, kLK)) = st.q[q4];
     }
-    if (w < 10) {  // units 128.. are padding
-      Gs[b][u] = st.gd;
-      *reinterpret_cast<uint4*>(Vs[b] + 8 * u) = st.v;
-    }
+    if (w < 11) Gs[b][u] = st.gd;                                // units 192.. are padding
+    if (w < 10) *reinterpret_cast<uint4*>(Vs[b] + 8 * u) = st.v;  // units 128.. are padding
   };
   auto stage_p = [&](const Stage& st) {
 #pragma unroll
@@ -147,7 +145,7 @@ __global__ __launch_bounds__(kThreads) void chunk_fwd_kernel(ChunkArgs a) {
   if (w >= 8) {
     // Two register sets take turns, cur holding chunk c (staged but for its P) and nxt chunk c + 1, and the LDS
     // writes go where the chain's phases leave the LDS least busy. After the chain's first barrier of chunk c:
-    // chunk c + 1's k and Tb to the chain's other LDS buffers (their last readers were chunk c - 1's), and the first
+    // chunk c + 1's k and T to the chain's other LDS buffers (their last readers were chunk c - 1's), and the first
     // part of chunk c + 2 into cur (two chunks ahead, which covers the memory latency). After the second: chunk c's
     // P to Pb (chunk c - 1's y is formed) and the second part of chunk c + 2. After the third: chunk c + 1's q to Qb
     // (chunk c's S Q^T is done), its v and per-position vectors.
@@ -186,7 +184,7 @@ __global__ __launch_bounds__(kThreads) void chunk_fwd_kernel(ChunkArgs a) {
       const int b = c & 1;
       __syncthreads();
       // S K^T and S Q^T at state rows 4g + jj, position ip, from one read of S (hi and lo); then
-      // R^T = V^T - (S K^T) diag(exp G), which the chain's next phase reads.
+      // R^T = (V^T - (S K^T) diag(exp G)) diag(beta), which the chain's next phase reads.
       f32x4 kh = zero4(), kl = zero4(), xh = zero4(), xl = zero4();
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
@@ -200,11 +198,12 @@ __global__ __launch_bounds__(kThreads) void chunk_fwd_kernel(ChunkArgs a) {
       }
       const float gam = Gs[b][ip];
       {
+        const float bet = Gs[b][2 * kC + ip];
         const uint2 v = *reinterpret_cast<const uint2*>(Vs[b] + 16 * ip + 4 * g);
         const f32x4 ks = kh + kl;
         const f32x4 r = {bf16_lo(v.x) - gam * ks[0], bf16_hi(v.x) - gam * ks[1], bf16_lo(v.y) - gam * ks[2],
                          bf16_hi(v.y) - gam * ks[3]};
-        put4(Rm[0], Rm[1], swz(ip, 4 * g, kLP), r);
+        put4(Rm[0], Rm[1], swz(ip, 4 * g, kLP), bet * r);
       }
       const f32x4 xs = xh + xl;
       __syncthreads();
@@ -257,7 +256,7 @@ __global__ __launch_bounds__(kThreads) void chunk_fwd_kernel(ChunkArgs a) {
     __syncthreads();  // S in LDS: the output group forms R from it
     __syncthreads();  // R in LDS
 
-    {  // Delta^T = R^T Tb^T: A = R^T through the transposing read, B = Tb rows ip from the packed copy
+    {  // Delta^T = R^T T^T (R with beta applied): A = R^T through the transposing read, B = T rows ip from the packed copy
       f32x4 d2[2];  // the two k steps in independent chains
 #pragma unroll
       for (int s = 0; s < 2; ++s) {

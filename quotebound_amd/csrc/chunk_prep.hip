@@ -1,11 +1,11 @@
 // Chunked design, kernel 1 (prep), one block per (chunk slot, value head), or per (chunk slot, key head) when that
 // grid would not fit on the device at once: everything about the chunk that does not depend on the state, written
-// once as MFMA-ready operands (the Tile record, chunk_common.h: T, Tb and P as bf16 hi/lo pairs of their
+// once as MFMA-ready operands (the Tile record, chunk_common.h: T and P as bf16 hi/lo pairs of their
 // lower-triangular blocks).
 //   G = cumsum of the log-decays (fp64, so G_i - G_j keeps its bits when |G| is large)
-//   A = strict_lower(diag(beta) (E * K K^T)),  T = (I + A)^-1,  Tb = T diag(beta)
+//   A = strict_lower(diag(beta) (E * K K^T)),  T = (I + A)^-1
 //   P = lower_incl(E * Q K^T),  E_ij = exp(G_i - G_j)
-// T is the UT transform of the chunk's delta rule: Delta = Tb (V - diag(exp G) K S0^T) gives every step's
+// T is the UT transform of the chunk's delta rule: Delta = T diag(beta) (V - diag(exp G) K S0^T) gives every step's
 // delta_t = beta_t (v_t - u_t) of the recurrence (reference src/delta_grad.cpp:14) at once. K K^T and Q K^T run on
 // MFMA (bf16 inputs are exact, fp32 accumulation); the inverse is blocked forward substitution in fp32: each 16 x 16
 // diagonal block by substitution with the column held in registers, then T_IJ = -T_II sum_K A_IK T_KJ by distance.
@@ -260,18 +260,15 @@ __global__ __launch_bounds__(kThreads) void chunk_prep_kernel(ChunkArgs a, int h
       __syncthreads();
     }
 
-    // T and Tb = T diag(beta), hi and lo, on and below the diagonal blocks: thread -> row tid / 4, columns
-    // 16 (tid % 4) .. + 15.
+    // T, hi and lo, on and below the diagonal blocks: thread -> row tid / 4, columns 16 (tid % 4) .. + 15.
     {
       const int i = tid >> 2, j0 = (tid & 3) * 16;
       if ((j0 >> 4) <= (i >> 4)) {
-        uint32_t th[8], tl[8], bh[8], bl[8];  // packed bf16 pairs, columns j0 + 2p, j0 + 2p + 1
+        uint32_t th[8], tl[8];  // packed bf16 pairs, columns j0 + 2p, j0 + 2p + 1
 #pragma unroll
         for (int p2 = 0; p2 < 8; ++p2) {
           const int j = j0 + 2 * p2;
-          const float t0 = Tm[tri_off(i, j)], t1 = Tm[tri_off(i, j + 1)];
-          split2(t0, t1, th[p2], tl[p2]);
-          split2(t0 * Bs[j], t1 * Bs[j + 1], bh[p2], bl[p2]);
+          split2(Tm[tri_off(i, j)], Tm[tri_off(i, j + 1)], th[p2], tl[p2]);
         }
         const int at = tri_off(i, j0);
 #pragma unroll
@@ -279,8 +276,6 @@ __global__ __launch_bounds__(kThreads) void chunk_prep_kernel(ChunkArgs a, int h
           const int q = 4 * h;
           *reinterpret_cast<uint4*>(tile->t[0] + at + 8 * h) = uint4{th[q], th[q + 1], th[q + 2], th[q + 3]};
           *reinterpret_cast<uint4*>(tile->t[1] + at + 8 * h) = uint4{tl[q], tl[q + 1], tl[q + 2], tl[q + 3]};
-          *reinterpret_cast<uint4*>(tile->tb[0] + at + 8 * h) = uint4{bh[q], bh[q + 1], bh[q + 2], bh[q + 3]};
-          *reinterpret_cast<uint4*>(tile->tb[1] + at + 8 * h) = uint4{bl[q], bl[q + 1], bl[q + 2], bl[q + 3]};
         }
       }
     }

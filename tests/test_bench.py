@@ -42,7 +42,10 @@ def test_gradient_kernel_bytes():
     s = bench._sizes(w, nc)
     assert amount == sum(s[n] for n in ("q", "k", "v", "dy", "g", "beta", "ckpt_read", "dq", "dk", "dg", "dbeta"))
     assert amount == 270_008_320
-    assert design == tiles + s["ckpt_read"] == 199_229_440
+    # one tile record per (chunk, value head): T and P as packed bf16 hi/lo blocks (4 x 2560 elements) and four
+    # 64-float vectors, 21,504 bytes
+    assert tiles == 64 * 32 * (4 * 2560 * 2 + 4 * 64 * 4) == 44_040_192
+    assert design == tiles + s["ckpt_read"] == 178_257_920
 
 
 def test_step_roofline_4b():
