@@ -384,7 +384,9 @@ def run_lora_step(torch, steps=5, warmup=2):
     sequences of 1024 random tokens with the loss on the last half: forward, adapter gradients, AdamW. Timed with
     device synchronisations around `steps` steps, run eagerly and replayed from a captured HIP graph, with the
     DeltaNet layers' prologue fused into the recurrence (the default); `separate_prologue` replays the same step
-    with the prologue as its own passes, and `prologue_fusion_ms` is what the fusion saves per step."""
+    with the prologue as its own passes, and `prologue_fusion_ms` is what the fusion saves per step.
+    `deltanet_path` times one DeltaNet layer's prologue and recurrence, forward and backward, at the layer's shape
+    (B=4, T=1024, Hk=4, Hv=8, Dk=Dv=128) both ways, events around back-to-back calls."""
     import dataclasses
 
     from quotebound_amd import lora
@@ -422,6 +424,12 @@ def run_lora_step(torch, steps=5, warmup=2):
     out["separate_prologue"] = {"graph_ms_per_step": ms, "loss": float(loss)}
     out["prologue_fusion_ms"] = ms - out["graph"]["ms_per_step"]
     del step
+    from quotebound_amd import _lib
+    from quotebound_amd.synthetic import Workload
+
+    lw = Workload("lora_deltanet_layer", 4, 1024, cfg.lin_k_heads, cfg.lin_v_heads, cfg.lin_k_dim, cfg.lin_v_dim)
+    out["deltanet_path"] = run_prologue_fusion(torch, _lib, lw, calls=20, warmup=warmup)
+    out["deltanet_path"]["layers_per_step"] = sum(cfg.is_linear(i) for i in range(cfg.layers))
     return out
 
 
