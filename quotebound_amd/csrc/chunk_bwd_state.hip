@@ -1,4 +1,4 @@
-// Chunked design, kernel 3: the backward state pass. One block (8 waves) per (sequence, value head, 16 state rows),
+// Chunked design, kernel 3: the backward state pass. One block (12 waves) per (sequence, value head, 16 state rows),
 // over the chunks in reverse. With dS the cotangent of the block's rows of the chunk's end state (ds_out for the
 // last chunk), per chunk, every product formed transposed so that a lane holds one position and four consecutive
 // state rows (or one state row and four consecutive columns):
@@ -10,11 +10,13 @@
 // This is the adjoint of the forward state pass; together with the gradient kernel it reproduces the reference's
 // backward (src/delta_grad.cpp:14-18). dS0 is what remains after the first chunk. T and P come ready from the prep
 // kernel, packed; the products that contract over their rows read them through the transposing LDS read (tri_tr8).
-// MFMA with split float32 operands as in the forward. Three barriers per chunk. Waves 4-7 load every input of the
-// next chunk (in the reverse sweep) in two groups, in windows where they would otherwise wait for the chain, and
-// stage them in LDS; waves 0-3 touch global memory only to store dS and dv. The two wave groups run loops of their
-// own, with the same barriers, so that each loop holds only its own group's memory operations and the compiler's
-// waits stay exact.
+// MFMA with split float32 operands as in the forward. Three barriers per chunk. The inputs of the next chunk (in the
+// reverse sweep) are loaded and staged in LDS beside the chain by two groups, one wave of each per SIMD: waves 4-7
+// the k and q rows (and X^T), waves 8-11 dy, the packed T and P and the per-position vectors; waves 0-3 touch global
+// memory only to store dS and dv. Each group's loads and LDS writes go in windows where it would otherwise wait for
+// the chain, and neither group's loads hold back the other's LDS writes. The three groups run loops of their own,
+// with the same barriers, so that each loop holds only its own group's memory operations and the compiler's waits
+// stay exact.
 #include <type_traits>
 
 #include "chunk_common.h"
@@ -23,7 +25,7 @@
 namespace qbgdn {
 namespace {
 
-constexpr int kThreads = 512;
+constexpr int kThreads = 768;  // waves 0-3 the chain, 4-7 k, q and X^T, 8-11 dy, T, P
 // Row pitches (elements) of the swz-placed LDS matrices: 16 x an odd number.
 constexpr int kLS = 144;  // dS [16][128]
 constexpr int kLK = 144;  // k, q rows [64][128]
@@ -52,9 +54,8 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_state_kernel(ChunkArgs a) 
   // The wave index, made visibly uniform so that its branches are scalar and buffer resources stay in scalar
   // registers.
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const bool side = w >= 4;
   const int wp = w & 3, ip = 16 * wp + li;  // position tile; the lane's position in products over positions
-  const int u = tid & 255;                   // waves 4-7: thread index within the loading group
+  const int u = tid & 255;                   // waves 4-11: thread index within the wave's group
   const Seq sq = seq_of(a.tab, n);
   const int nch = (sq.len + kC - 1) / kC;
   const OutT* dy = static_cast<const OutT*>(a.dy);
@@ -62,11 +63,11 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_state_kernel(ChunkArgs a) 
   const int sk = a.Hk * Dk, sv = a.Hv * a.Dv;
   const int64_t srow = (int64_t(n) * a.Hv + hv) * a.Dv + row0 + li;  // the lane's state row
 
-  if (side) {
-    // Waves 4-7. One chunk's inputs, loaded a chunk ahead: (a) k and q rows, staged while the chain computes dR;
-    // (b) dy, the packed T and P, and exp G, D, beta, staged after the chain's last use of the previous ones. k, q,
-    // dy go through buffer resources that end at the sequence's last row, so rows past it read as zeros without a
-    // branch; units past the packed matrices read as zeros and land in padding.
+  if (w >= 4) {
+    // Waves 4-11. One chunk's inputs, loaded a chunk ahead: (a) k and q rows (waves 4-7), staged while the chain
+    // computes dR; (b) dy, the packed T and P, and exp G, D, beta (waves 8-11), staged after the chain's last use of
+    // the previous ones. k, q, dy go through buffer resources that end at the sequence's last row, so rows past it
+    // read as zeros without a branch; units past the packed matrices read as zeros and land in padding.
     struct GroupA {
       uint4 k[4], q[4];  // units u + 256 q4: row e / 16, columns 8 (e % 16) ..
     };
@@ -140,51 +141,65 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_state_kernel(ChunkArgs a) 
       }
       if (u < kC) Gs[b][u] = f.gam, Gs[b][kC + u] = f.dec, Gs[b][2 * kC + u] = f.bet;
     };
-    // Per chunk c: X^T for it (its q and diag(exp G) dY were staged during chunk c + 1); the inputs of chunk c - 1,
-    // loaded during chunk c + 1, to LDS; the loads of chunk c - 2 (clamped at 0: the last chunks load chunk 0 again
-    // rather than branch). Two register sets in turn.
-    struct Group {
-      GroupA a;
-      GroupB b;
-    };
-    auto step = [&](int c, Group& cur, Group& nxt) {
-      const int cs = max(c - 1, 0), cn = max(c - 2, 0);
-      __syncthreads();
-      load_a(nxt.a, cn);
-      // X^T = Q^T (diag(exp G) dY) for state columns 32 wp + 16 t + 4g + jj, state row li: A = Q^T through the
-      // transposing read of the q rows, B = diag(exp G) dY through the transposing read.
+    // Per chunk c, with two register sets in turn: X^T for chunk c (its q and diag(exp G) dY were staged during
+    // chunk c + 1); the inputs of chunk c - 1, loaded during chunk c + 1, to LDS; the loads of chunk c - 2 (clamped
+    // at 0: the last chunks load chunk 0 again rather than branch).
+    if (w < 8) {
+      auto step = [&](int c, GroupA& cur, GroupA& nxt) {
+        const int cs = max(c - 1, 0), cn = max(c - 2, 0);
+        __syncthreads();
+        load_a(nxt, cn);
+        // X^T = Q^T (diag(exp G) dY) for state columns 32 wp + 16 t + 4g + jj, state row li: A = Q^T through the
+        // transposing read of the q rows, B = diag(exp G) dY through the transposing read.
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        f32x4 x2[2];
+        for (int t = 0; t < 2; ++t) {
+          f32x4 x2[2];
 #pragma unroll
-        for (int s = 0; s < 2; ++s) {
-          const bf16x8 aq = lds_tr8s(Qb + swz(32 * s, 32 * wp + 16 * t, kLK), kLK, lane);
-          x2[s] = mma2(zero4(), aq, Split8{lds_tr8s(GdYm[0] + 32 * s * kLP, kLP, lane),
-                                           lds_tr8s(GdYm[1] + 32 * s * kLP, kLP, lane)});
+          for (int s = 0; s < 2; ++s) {
+            const bf16x8 aq = lds_tr8s(Qb + swz(32 * s, 32 * wp + 16 * t, kLK), kLK, lane);
+            x2[s] = mma2(zero4(), aq, Split8{lds_tr8s(GdYm[0] + 32 * s * kLP, kLP, lane),
+                                             lds_tr8s(GdYm[1] + 32 * s * kLP, kLP, lane)});
+          }
+          *reinterpret_cast<f32x4*>(Xs + li * kLX + 32 * wp + 16 * t + 4 * g) = x2[0] + x2[1];
         }
-        *reinterpret_cast<f32x4*>(Xs + li * kLX + 32 * wp + 16 * t + 4 * g) = x2[0] + x2[1];
+        __syncthreads();
+        stage_a(cur, cs & 1);  // q's last readers (the X^T above) and k's (chunk c + 1) are a barrier back
+        __syncthreads();
+      };
+      GroupA ga, gb;
+      if (nch > 0) {
+        load_a(ga, nch - 1);
+        stage_a(ga, (nch - 1) & 1);
+        load_a(ga, max(nch - 2, 0));
       }
-      __syncthreads();
-      load_b(nxt.b, cn);
-      stage_a(cur.a, cs & 1);  // q's last readers (the X^T above) and k's (chunk c + 1) are a barrier back
-      __syncthreads();
-      stage_b(cur.b, cs & 1);  // the chain's last readers of dY, T, P were before this barrier
-    };
-    Group ga, gb;
-    if (nch > 0) {
-      load_a(ga.a, nch - 1);
-      load_b(ga.b, nch - 1);
-      stage_a(ga.a, (nch - 1) & 1);
-      stage_b(ga.b, (nch - 1) & 1);
-      load_a(ga.a, max(nch - 2, 0));
-      load_b(ga.b, max(nch - 2, 0));
+      int c = nch - 1;
+      for (; c >= 1; c -= 2) {
+        step(c, ga, gb);
+        step(c - 1, gb, ga);
+      }
+      if (c == 0) step(0, ga, gb);
+    } else {
+      auto step = [&](int c, GroupB& cur, GroupB& nxt) {
+        const int cs = max(c - 1, 0), cn = max(c - 2, 0);
+        __syncthreads();
+        __syncthreads();
+        load_b(nxt, cn);
+        __syncthreads();
+        stage_b(cur, cs & 1);  // the chain's last readers of dY, T, P and X^T's of diag(exp G) dY were before this barrier
+      };
+      GroupB ga, gb;
+      if (nch > 0) {
+        load_b(ga, nch - 1);
+        stage_b(ga, (nch - 1) & 1);
+        load_b(ga, max(nch - 2, 0));
+      }
+      int c = nch - 1;
+      for (; c >= 1; c -= 2) {
+        step(c, ga, gb);
+        step(c - 1, gb, ga);
+      }
+      if (c == 0) step(0, ga, gb);
     }
-    int c = nch - 1;
-    for (; c >= 1; c -= 2) {
-      step(c, ga, gb);
-      step(c - 1, gb, ga);
-    }
-    if (c == 0) step(0, ga, gb);
     return;
   }
 
