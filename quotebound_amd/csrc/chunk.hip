@@ -35,11 +35,15 @@ int device_cus() {
 bool split_grads(const Problem& p) { return p.Hv > p.Hk && int64_t(p.NC) * p.Hv <= device_cus(); }
 size_t dqk_part_bytes(const Problem& p) { return split_grads(p) ? size_t(p.NC) * p.Hv * 2 * 64 * p.Dk * 4 : 0; }
 
+// State rows per block of the state passes: 16, or 32 when the 16-row blocks (one resident per CU) would take more
+// than one round of the device, so that each block's per-chunk loads of k, q and the tile serve twice the rows.
+int state_rows(const Problem& p) { return int64_t(p.N) * p.Hv * (p.Dv / 16) > device_cus() ? 32 : 16; }
+
 ChunkArgs base_args(const Problem& p) {
   ChunkArgs a{};
   a.lay = layout_of(p);
   a.Hk = p.Hk, a.Hv = p.Hv, a.Dv = p.Dv, a.g_is_log = p.g_is_log;
-  a.nblk = p.Dv / 16;
+  a.nblk = p.Dv / state_rows(p);
   a.N = p.N;
   a.tab = p.tab;
   return a;

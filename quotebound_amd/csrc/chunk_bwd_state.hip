@@ -1,7 +1,8 @@
-// Chunked design, kernel 3: the backward state pass. One block (12 waves) per (sequence, value head, 16 state rows),
-// over the chunks in reverse. With dS the cotangent of the block's rows of the chunk's end state (ds_out for the
-// last chunk), per chunk, every product formed transposed so that a lane holds one position and four consecutive
-// state rows (or one state row and four consecutive columns):
+// Chunked design, kernel 3: the backward state pass. One block (12 waves) per (sequence, value head, kRows state
+// rows: 16, or 32 when the 16-row blocks would not all fit on the device at once), over the chunks in reverse. With
+// dS the cotangent of the block's rows of the chunk's end state (ds_out for the last chunk), per chunk, every product
+// formed transposed so that a lane holds one position and four consecutive state rows (or one state row and four
+// consecutive columns), for each 16-row tile of the block's rows:
 //   store dS (the gradient kernel needs it)
 //   dDelta^T = (dS K^T) D + dY^T P,  D = diag(exp(G_63 - G))      waves 0-3, positions 16w..16w+15: the chain
 //   dR^T = dDelta^T T diag(beta);   dv = dR                        waves 0-3
@@ -27,29 +28,34 @@ namespace {
 
 constexpr int kThreads = 768;  // waves 0-3 the chain, 4-7 k, q and X^T, 8-11 dy, T, P
 // Row pitches (elements) of the swz-placed LDS matrices: 16 x an odd number.
-constexpr int kLS = 144;  // dS [16][128]
+constexpr int kLS = 144;  // dS [kRows][128]
 constexpr int kLK = 144;  // k, q rows [64][128]
-constexpr int kLP = 48;   // [64][16]: dY, diag(exp G) dY, dDelta, -diag(exp G) dR (positions as rows)
-constexpr int kLX = 128 + 4;       // float32 X^T rows [16][..] (state row, then column)
+constexpr int kLX = 128 + 4;       // float32 X^T rows [kRows][..] (state row, then column)
 constexpr int kTriUnits = 3 * 256;  // 16-byte units of a staged packed matrix (hi, lo: 640 used, the rest padding)
+// dY, diag(exp G) dY, dDelta and -diag(exp G) dR ([64][kRows] each, positions as rows) side by side in one [64][kLW]
+// matrix, at columns 0, kRows, 2 kRows and 3 kRows: a view at a column offset that is a multiple of 16 is swz-placed
+// with the same pitch, so each keeps the conflict-free reads of a matrix of its own, without its own padding.
+template <int kRows>
+constexpr int kLW = kRows == 16 ? 80 : 144;
 
-template <typename OutT>
+template <typename OutT, int kRows>
 __global__ __launch_bounds__(kThreads) void chunk_bwd_state_kernel(ChunkArgs a) {
-  constexpr int Dk = 128;
+  constexpr int Dk = 128, kRT = kRows / 16, kLP = kLW<kRows>;
+  constexpr int oY = 0, oGY = kRows, odD = 2 * kRows, oGR = 3 * kRows;  // column offsets in Wm
+  static_assert(4 * kRows <= kLP, "dY, diag(exp G) dY, dDelta and -diag(exp G) dR side by side");
   constexpr bool kExactDy = std::is_same<OutT, bf16_t>::value;  // bf16 cotangents enter MFMA exactly
-  __shared__ __align__(16) __bf16 dSm[2][16 * kLS];               // dS rows, hi and lo
+  __shared__ __align__(16) __bf16 dSm[2][kRows * kLS];            // dS rows, hi and lo
   __shared__ __align__(16) __bf16 Kb[2][kC * kLK];                // k rows, by chunk parity
   __shared__ __align__(16) __bf16 Qb[kC * kLK];                   // q rows
-  __shared__ __align__(16) __bf16 dYm[2][kC * kLP], GdYm[2][kC * kLP];
-  __shared__ __align__(16) __bf16 dDm[2][kC * kLP], GdRm[2][kC * kLP];
+  __shared__ __align__(16) __bf16 Wm[2][kC * kLP];                // dY, diag(exp G) dY, dDelta, -diag(exp G) dR
   __shared__ __align__(16) __bf16 Tbp[kTriUnits * 8], Pp[kTriUnits * 8];  // packed T, P (hi then lo)
-  __shared__ __align__(16) float Xs[16 * kLX];
+  __shared__ __align__(16) float Xs[kRows * kLX];
   __shared__ float Gs[2][3 * kC];  // exp G, D, beta, by chunk parity
 
   const int total = a.nblk * a.Hv * a.N;
   const StateItem item = state_item(a.tab, blockIdx.x, a.nblk, a.Hv, a.Hk, total);
   const int blk = item.blk, hv = item.hv, n = item.n;
-  const int hk = hv / (a.Hv / a.Hk), row0 = 16 * blk;
+  const int hk = hv / (a.Hv / a.Hk), row0 = kRows * blk;
   const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, li = lane & 15;
   // The wave index, made visibly uniform so that its branches are scalar and buffer resources stay in scalar
   // registers.
@@ -61,7 +67,7 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_state_kernel(ChunkArgs a) 
   const OutT* dy = static_cast<const OutT*>(a.dy);
   OutT* dv = static_cast<OutT*>(a.dv);
   const int sk = a.Hk * Dk, sv = a.Hv * a.Dv;
-  const int64_t srow = (int64_t(n) * a.Hv + hv) * a.Dv + row0 + li;  // the lane's state row
+  const int64_t srow = (int64_t(n) * a.Hv + hv) * a.Dv + row0 + li;  // the lane's state row in the first row tile
 
   if (w >= 4) {
     // Waves 4-11. One chunk's inputs, loaded a chunk ahead: (a) k and q rows (waves 4-7), staged while the chain
@@ -72,7 +78,7 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_state_kernel(ChunkArgs a) 
       uint4 k[4], q[4];  // units u + 256 q4: row e / 16, columns 8 (e % 16) ..
     };
     struct GroupB {
-      uint4 dy;           // row u / 4, state rows 4 (u % 4) .. + 3: raw bits (4 bf16 in .x, .y, or 4 float32)
+      uint4 dy[kRT];        // row u / 4, state rows 16 rt + 4 (u % 4) .. + 3: raw bits (4 bf16 in .x, .y, or 4 float32)
       uint4 tb[3], p[3];    // packed T and P units u + 256 t
       float gam, dec, bet;  // of position lane (every wave loads all 64)
     };
@@ -97,12 +103,15 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_state_kernel(ChunkArgs a) 
       const uint32_t L = uint32_t(min(kC, sq.len - c * kC));
       const Tile* tl = a.tiles + ((sq.slot0 + c) * a.Hv + hv);
       const auto yr = buffer_rsrc(dy + tok * sv + hv * a.Dv + row0, L * sv * uint32_t(sizeof(OutT)));
-      const uint32_t yo = uint32_t((u >> 2) * sv + 4 * (u & 3));
-      if constexpr (kExactDy) {
-        const uint2 t2 = buf_ld8(yr, yo * 2);
-        f.dy = uint4{t2.x, t2.y, 0u, 0u};
-      } else {
-        f.dy = buf_ld16(yr, yo * 4);
+#pragma unroll
+      for (int rt = 0; rt < kRT; ++rt) {
+        const uint32_t yo = uint32_t((u >> 2) * sv + 16 * rt + 4 * (u & 3));
+        if constexpr (kExactDy) {
+          const uint2 t2 = buf_ld8(yr, yo * 2);
+          f.dy[rt] = uint4{t2.x, t2.y, 0u, 0u};
+        } else {
+          f.dy[rt] = buf_ld16(yr, yo * 4);
+        }
       }
       const auto tr = buffer_rsrc(tl->t[0], 2 * kTri * 2), pr = buffer_rsrc(tl->p[0], 2 * kTri * 2);
 #pragma unroll
@@ -125,15 +134,19 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_state_kernel(ChunkArgs a) 
       // dy's four values of row u / 4, as floats, and the same times exp G of that row (lane u / 4 of this wave
       // holds it).
       const int yt = u >> 2, yr4 = 4 * (u & 3);
-      float yv[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const uint32_t x = kExactDy ? (j & 1 ? (&f.dy.x)[j >> 1] & 0xffff0000u : (&f.dy.x)[j >> 1] << 16) : (&f.dy.x)[j];
-        yv[j] = __uint_as_float(x);
-      }
       const float gy = __shfl(f.gam, yt);
-      put4(dYm[0], dYm[1], swz(yt, yr4, kLP), yv[0], yv[1], yv[2], yv[3]);
-      put4(GdYm[0], GdYm[1], swz(yt, yr4, kLP), gy * yv[0], gy * yv[1], gy * yv[2], gy * yv[3]);
+#pragma unroll
+      for (int rt = 0; rt < kRT; ++rt) {
+        float yv[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint4& d = f.dy[rt];
+          const uint32_t x = kExactDy ? (j & 1 ? (&d.x)[j >> 1] & 0xffff0000u : (&d.x)[j >> 1] << 16) : (&d.x)[j];
+          yv[j] = __uint_as_float(x);
+        }
+        put4(Wm[0], Wm[1], swz(yt, oY + 16 * rt + yr4, kLP), yv[0], yv[1], yv[2], yv[3]);
+        put4(Wm[0], Wm[1], swz(yt, oGY + 16 * rt + yr4, kLP), gy * yv[0], gy * yv[1], gy * yv[2], gy * yv[3]);
+      }
 #pragma unroll
       for (int t = 0; t < 3; ++t) {
         *reinterpret_cast<uint4*>(Tbp + 8 * (u + 256 * t)) = f.tb[t];
@@ -149,18 +162,23 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_state_kernel(ChunkArgs a) 
         const int cs = max(c - 1, 0), cn = max(c - 2, 0);
         __syncthreads();
         load_a(nxt, cn);
-        // X^T = Q^T (diag(exp G) dY) for state columns 32 wp + 16 t + 4g + jj, state row li: A = Q^T through the
-        // transposing read of the q rows, B = diag(exp G) dY through the transposing read.
+        // X^T = Q^T (diag(exp G) dY) for state columns 32 wp + 16 t + 4g + jj, state row 16 rt + li: A = Q^T through
+        // the transposing read of the q rows, B = diag(exp G) dY through the transposing read.
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
-          f32x4 x2[2];
+          bf16x8 aq[2];
 #pragma unroll
-          for (int s = 0; s < 2; ++s) {
-            const bf16x8 aq = lds_tr8s(Qb + swz(32 * s, 32 * wp + 16 * t, kLK), kLK, lane);
-            x2[s] = mma2(zero4(), aq, Split8{lds_tr8s(GdYm[0] + 32 * s * kLP, kLP, lane),
-                                             lds_tr8s(GdYm[1] + 32 * s * kLP, kLP, lane)});
+          for (int s = 0; s < 2; ++s) aq[s] = lds_tr8s(Qb + swz(32 * s, 32 * wp + 16 * t, kLK), kLK, lane);
+#pragma unroll
+          for (int rt = 0; rt < kRT; ++rt) {
+            f32x4 x2[2];
+#pragma unroll
+            for (int s = 0; s < 2; ++s) {
+              const int o = 32 * s * kLP + oGY + 16 * rt;
+              x2[s] = mma2(zero4(), aq[s], Split8{lds_tr8s(Wm[0] + o, kLP, lane), lds_tr8s(Wm[1] + o, kLP, lane)});
+            }
+            *reinterpret_cast<f32x4*>(Xs + (16 * rt + li) * kLX + 32 * wp + 16 * t + 4 * g) = x2[0] + x2[1];
           }
-          *reinterpret_cast<f32x4*>(Xs + li * kLX + 32 * wp + 16 * t + 4 * g) = x2[0] + x2[1];
         }
         __syncthreads();
         stage_a(cur, cs & 1);  // q's last readers (the X^T above) and k's (chunk c + 1) are a barrier back
@@ -203,66 +221,92 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_state_kernel(ChunkArgs a) 
     return;
   }
 
-  // Waves 0-3: the recurrence. dS tile t holds dS[li][32 wp + 16 t + 4 g + jj]. (ds_out and ds0 need only 4-byte
-  // alignment: one element at a time.)
-  f32x4 dS[2] = {zero4(), zero4()};
+  // Waves 0-3: the recurrence. dS tile (rt, t) holds dS[16 rt + li][32 wp + 16 t + 4 g + jj]. (ds_out and ds0 need
+  // only 4-byte alignment: one element at a time.)
+  f32x4 dS[kRT][2];
+#pragma unroll
+  for (int rt = 0; rt < kRT; ++rt) dS[rt][0] = zero4(), dS[rt][1] = zero4();
   if (a.ds_out) {
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+    for (int rt = 0; rt < kRT; ++rt)
 #pragma unroll
-      for (int jj = 0; jj < 4; ++jj) dS[t][jj] = a.ds_out[srow * Dk + 32 * wp + 16 * t + 4 * g + jj];
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj)
+          dS[rt][t][jj] = a.ds_out[(srow + 16 * rt) * Dk + 32 * wp + 16 * t + 4 * g + jj];
   }
   for (int c = nch - 1; c >= 0; --c) {
     const int64_t slot = sq.slot0 + c, tok = sq.tok0 + int64_t(c) * kC;
     const uint32_t L = uint32_t(min(kC, sq.len - c * kC));
     const int b = c & 1;
     {  // dS to the workspace and, split, to LDS (its last readers are two barriers back)
-      const auto out = buffer_rsrc(a.dsend + ((slot * a.Hv + hv) * a.Dv + row0) * Dk, 16 * Dk * 4);
+      const auto out = buffer_rsrc(a.dsend + ((slot * a.Hv + hv) * a.Dv + row0) * Dk, kRows * Dk * 4);
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        const int col = 32 * wp + 16 * t + 4 * g;
-        put4(dSm[0], dSm[1], swz(li, col, kLS), dS[t]);
-        BufIO<float>::st4(out, uint32_t(li * Dk + col), dS[t]);
-      }
+      for (int rt = 0; rt < kRT; ++rt)
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          const int col = 32 * wp + 16 * t + 4 * g;
+          put4(dSm[0], dSm[1], swz(16 * rt + li, col, kLS), dS[rt][t]);
+          BufIO<float>::st4(out, uint32_t((16 * rt + li) * Dk + col), dS[rt][t]);
+        }
     }
     __syncthreads();
 
-    {  // dDelta^T at state rows 4g + jj, position ip = (dS K^T) D + dY^T P
-      f32x4 xh = zero4(), xl = zero4(), z = zero4();  // three independent chains
+    {  // dDelta^T at state rows 16 rt + 4g + jj, position ip = (dS K^T) D + dY^T P
+      f32x4 xh[kRT], xl[kRT], z[kRT];  // independent chains
+#pragma unroll
+      for (int rt = 0; rt < kRT; ++rt) xh[rt] = zero4(), xl[rt] = zero4(), z[rt] = zero4();
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        const int at = swz(li, 32 * s + 8 * g, kLS);
         const bf16x8 bk = lds8(Kb[b] + swz(ip, 32 * s + 8 * g, kLK));
-        xh = mma(xh, lds8(dSm[0] + at), bk);
-        xl = mma(xl, lds8(dSm[1] + at), bk);
+#pragma unroll
+        for (int rt = 0; rt < kRT; ++rt) {
+          const int at = swz(16 * rt + li, 32 * s + 8 * g, kLS);
+          xh[rt] = mma(xh[rt], lds8(dSm[0] + at), bk);
+          xl[rt] = mma(xl[rt], lds8(dSm[1] + at), bk);
+        }
       }
 #pragma unroll
       for (int s = 0; s < 2; ++s) {  // dY^T P: A = dY^T through the transposing read, B = P's column ip
         const Split8 B{tri_tr8(Pp, 32 * s, wp, lane), tri_tr8(Pp + kTri, 32 * s, wp, lane)};
-        if constexpr (kExactDy) {
-          z = mma2(z, lds_tr8s(dYm[0] + 32 * s * kLP, kLP, lane), B);
-        } else {
-          z = mma3(z, Split8{lds_tr8s(dYm[0] + 32 * s * kLP, kLP, lane), lds_tr8s(dYm[1] + 32 * s * kLP, kLP, lane)},
-                   B);
+#pragma unroll
+        for (int rt = 0; rt < kRT; ++rt) {
+          const int o = 32 * s * kLP + oY + 16 * rt;
+          if constexpr (kExactDy) {
+            z[rt] = mma2(z[rt], lds_tr8s(Wm[0] + o, kLP, lane), B);
+          } else {
+            z[rt] = mma3(z[rt], Split8{lds_tr8s(Wm[0] + o, kLP, lane), lds_tr8s(Wm[1] + o, kLP, lane)}, B);
+          }
         }
       }
-      const f32x4 dd = Gs[b][kC + ip] * (xh + xl) + z;
-      put4(dDm[0], dDm[1], swz(ip, 4 * g, kLP), dd);
+      const float dec = Gs[b][kC + ip];
+#pragma unroll
+      for (int rt = 0; rt < kRT; ++rt) {
+        const f32x4 dd = dec * (xh[rt] + xl[rt]) + z[rt];
+        put4(Wm[0], Wm[1], swz(ip, odD + 16 * rt + 4 * g, kLP), dd);
+      }
     }
     __syncthreads();
 
     {  // dR^T = dDelta^T T diag(beta): A = dDelta^T through the transposing read, B = T's column ip; dv = dR
-      f32x4 d2[2];
+      Split8 TB[2];
 #pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        const Split8 A{lds_tr8s(dDm[0] + 32 * s * kLP, kLP, lane), lds_tr8s(dDm[1] + 32 * s * kLP, kLP, lane)};
-        d2[s] = mma3(zero4(), A, Split8{tri_tr8(Tbp, 32 * s, wp, lane), tri_tr8(Tbp + kTri, 32 * s, wp, lane)});
-      }
-      const f32x4 dr = Gs[b][2 * kC + ip] * (d2[0] + d2[1]);
+      for (int s = 0; s < 2; ++s) TB[s] = Split8{tri_tr8(Tbp, 32 * s, wp, lane), tri_tr8(Tbp + kTri, 32 * s, wp, lane)};
+      const float bet = Gs[b][2 * kC + ip], ngam = -Gs[b][ip];
       // Positions past the chunk's end fall past the resource and are dropped.
       const auto vr = buffer_rsrc(dv + tok * sv + hv * a.Dv + row0, L * sv * uint32_t(sizeof(OutT)));
-      BufIO<OutT>::st4(vr, uint32_t(ip * sv + 4 * g), dr);
-      put4(GdRm[0], GdRm[1], swz(ip, 4 * g, kLP), -Gs[b][ip] * dr);
+#pragma unroll
+      for (int rt = 0; rt < kRT; ++rt) {
+        f32x4 d2[2];
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+          const int o = 32 * s * kLP + odD + 16 * rt;
+          d2[s] = mma3(zero4(), Split8{lds_tr8s(Wm[0] + o, kLP, lane), lds_tr8s(Wm[1] + o, kLP, lane)}, TB[s]);
+        }
+        const f32x4 dr = bet * (d2[0] + d2[1]);
+        BufIO<OutT>::st4(vr, uint32_t(ip * sv + 16 * rt + 4 * g), dr);
+        put4(Wm[0], Wm[1], swz(ip, oGR + 16 * rt + 4 * g, kLP), ngam * dr);
+      }
     }
     __syncthreads();
 
@@ -270,23 +314,33 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_state_kernel(ChunkArgs a) 
     // read, B = -diag(exp G) dR through the transposing read.
     const float glast = Gs[b][kC - 1];
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const f32x4 x = *reinterpret_cast<const f32x4*>(Xs + li * kLX + 32 * wp + 16 * t + 4 * g);
-      dS[t] = glast * dS[t] + x;
-    }
+    for (int rt = 0; rt < kRT; ++rt)
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const f32x4 x = *reinterpret_cast<const f32x4*>(Xs + (16 * rt + li) * kLX + 32 * wp + 16 * t + 4 * g);
+        dS[rt][t] = glast * dS[rt][t] + x;
+      }
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
-      const Split8 B{lds_tr8s(GdRm[0] + 32 * s * kLP, kLP, lane), lds_tr8s(GdRm[1] + 32 * s * kLP, kLP, lane)};
+      bf16x8 KA[2];
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
-        dS[t] = mma2(dS[t], lds_tr8s(Kb[b] + swz(32 * s, 32 * wp + 16 * t, kLK), kLK, lane), B);
+      for (int t = 0; t < 2; ++t) KA[t] = lds_tr8s(Kb[b] + swz(32 * s, 32 * wp + 16 * t, kLK), kLK, lane);
+#pragma unroll
+      for (int rt = 0; rt < kRT; ++rt) {
+        const int o = 32 * s * kLP + oGR + 16 * rt;
+        const Split8 B{lds_tr8s(Wm[0] + o, kLP, lane), lds_tr8s(Wm[1] + o, kLP, lane)};
+#pragma unroll
+        for (int t = 0; t < 2; ++t) dS[rt][t] = mma2(dS[rt][t], KA[t], B);
+      }
     }
   }
   if (a.ds0) {
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+    for (int rt = 0; rt < kRT; ++rt)
 #pragma unroll
-      for (int jj = 0; jj < 4; ++jj) a.ds0[srow * Dk + 32 * wp + 16 * t + 4 * g + jj] = dS[t][jj];
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) a.ds0[(srow + 16 * rt) * Dk + 32 * wp + 16 * t + 4 * g + jj] = dS[rt][t][jj];
   }
 }
 
@@ -294,10 +348,10 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_state_kernel(ChunkArgs a) 
 
 hipError_t launch_chunk_bwd_state(const ChunkArgs& a, bool out_bf16, hipStream_t s) {
   const int total = a.nblk * a.Hv * a.N;
-  if (out_bf16)
-    hipLaunchKernelGGL(chunk_bwd_state_kernel<bf16_t>, dim3(total), dim3(kThreads), 0, s, a);
-  else
-    hipLaunchKernelGGL(chunk_bwd_state_kernel<float>, dim3(total), dim3(kThreads), 0, s, a);
+  const bool r32 = a.Dv == 32 * a.nblk;  // 32 state rows per block (else 16)
+  void (*k)(ChunkArgs) = out_bf16 ? (r32 ? chunk_bwd_state_kernel<bf16_t, 32> : chunk_bwd_state_kernel<bf16_t, 16>)
+                                  : (r32 ? chunk_bwd_state_kernel<float, 32> : chunk_bwd_state_kernel<float, 16>);
+  hipLaunchKernelGGL(k, dim3(total), dim3(kThreads), 0, s, a);
   return hipGetLastError();
 }
 

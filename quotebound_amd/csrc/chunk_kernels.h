@@ -28,7 +28,7 @@ struct ChunkArgs {
   float* dqk_part;  // workspace, short sequences: per (chunk slot, value head) dq and dk [64][128] float32, or null
   ChunkLayout lay;
   int Hk, Hv, Dv, g_is_log;
-  int nblk;  // Dv / 16 state-row blocks
+  int nblk;  // state-row blocks of a head in the state passes: Dv / 16 or Dv / 32
   int N;     // sequences
   SeqTable tab;
   // The layer's prologue fused into chunk_prep (qb_gdn_fwd_prologue): the raw inputs, and the prologue's outputs,
