@@ -98,8 +98,9 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
   // kSplit: one work item per (chunk slot, key head, value head), whose dq and dk go to the partials for
   // chunk_dqk_sum_kernel; otherwise one per (chunk slot, key head), the group's value heads in turn.
   const int grp = a.Hv / a.Hk, hs = kSplit ? grp : 1, total = int(a.lay.NC) * a.Hk * hs;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 4, li = lane & 15;
-  const int pw = w & 3, hw = w >> 2;  // position tile, half
+  // Lane roles (position tile pw = w % 4, half hw = w / 4, lane group g, lane li) are derived where they are used, from
+  // an opaque copy of the thread index, so that their address expressions are not held across the loops.
+  const int tid = threadIdx.x;
   const OutT* dy = static_cast<const OutT*>(a.dy);
   const int sk = a.Hk * Dk, sv = a.Hv * a.Dv;  // token strides of k/q/dq/dk and v/dy
   // A work item: a chunk slot, key head and its value heads [e0, e0 + ne). The grid is persistent: block b takes items b, b + gridDim.x, ..., and
@@ -197,8 +198,6 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
 
     for (int e = cur.e0; e < cur.e0 + cur.ne; ++e) {
       const int hv = hk * grp + e;
-      const int64_t sh = slot * a.Hv + hv;
-      const Tile* tl = a.tiles + sh;
       // The head whose tile and first block the end phase reads ahead, in pieces at the starts of E2, E3 and E4
       // (beside their products, so that no phase issues them all): the next in the group, the next item's first,
       // or, for the block's last item, this head again (those reads are unused; they keep every path's loads the
