@@ -28,9 +28,17 @@ __device__ __forceinline__ f32x4 mma16(f32x4 c, s16x4 a, s16x4 b) {
 }
 
 // LDS: k and q rows while K K^T and Q K^T run; then, in the same bytes, A and T in float32 and P as bf16 hi/lo,
-// each as its ten lower-triangular blocks (tri_off). About 37 KB, so four blocks share a CU.
+// each as its ten lower-triangular blocks. About 37 KB, so four blocks share a CU. P is laid out as in the tile
+// (tri_off), to be copied out as it is; A and T, which stay in LDS, are padded (tri_pad): rows of 20 floats inside a
+// block, so that a row's 4 columns written from each of 16 lanes, and the 16 rows of a column read at once, fall on
+// distinct banks, and blocks 324 floats apart, so that the four diagonal blocks the substitution reads side by side
+// do too.
+constexpr int kLdPad = 20, kBlkPad = 16 * kLdPad + 4, kTriPad = 10 * kBlkPad;
+__device__ __forceinline__ int tri_pad(int i, int j) {
+  return ((i >> 4) * ((i >> 4) + 1) / 2 + (j >> 4)) * kBlkPad + (i & 15) * kLdPad + (j & 15);
+}
 constexpr int kKQBytes = 2 * kC * kLDK * 2;
-constexpr int kAoff = 0, kToff = kTri * 4, kPoff = 2 * kTri * 4;  // byte offsets of A, T, P (hi then lo)
+constexpr int kAoff = 0, kToff = kTriPad * 4, kPoff = 2 * kTriPad * 4;  // byte offsets of A, T, P (hi then lo)
 static_assert(kPoff + 2 * kTri * 2 <= kKQBytes, "A, T and P fit in the k/q staging bytes");
 
 // kFused: the layer's prologue in front (qb_gdn_fwd_prologue). The block reads q_raw, k_raw, a and b in place of
@@ -133,7 +141,8 @@ __global__ __launch_bounds__(kThreads) void chunk_prep_kernel(ChunkArgs a, int h
   __syncthreads();
 
   // The ten lower-triangular 16 x 16 blocks (I, J) of K K^T and Q K^T, block b = tri_off order, round-robin over the
-  // waves (three, three, two, two), on MFMA: lane -> column j = 16 J + li, rows i = 16 I + 4g + jj. They stay in
+  // waves (three, three, two, two), on MFMA, formed transposed (K_J K_I^T, K_J Q_I^T) so that a lane holds row
+  // i = 16 I + li, columns j = 16 J + 4g + jj: its four values of a row leave as one vector store. They stay in
   // registers for every value head of the group; A and P take the k and q rows' bytes once every wave is done.
   f32x4 kk[3], qk[3];
 #pragma unroll
@@ -144,9 +153,9 @@ __global__ __launch_bounds__(kThreads) void chunk_prep_kernel(ChunkArgs a, int h
     if (b < 10) {
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        const bf16x8 bk = lds8(Kb + (16 * J + li) * kLDK + 32 * s + 8 * g);
-        kk[u] = mma(kk[u], lds8(Kb + (16 * I + li) * kLDK + 32 * s + 8 * g), bk);
-        qk[u] = mma(qk[u], lds8(Qb + (16 * I + li) * kLDK + 32 * s + 8 * g), bk);
+        const bf16x8 ak = lds8(Kb + (16 * J + li) * kLDK + 32 * s + 8 * g);
+        kk[u] = mma(kk[u], ak, lds8(Kb + (16 * I + li) * kLDK + 32 * s + 8 * g));
+        qk[u] = mma(qk[u], ak, lds8(Qb + (16 * I + li) * kLDK + 32 * s + 8 * g));
       }
     }
   }
@@ -189,17 +198,23 @@ __global__ __launch_bounds__(kThreads) void chunk_prep_kernel(ChunkArgs a, int h
       const int b = w + 4 * u;
       if (b < 10) {
         const int I = (b >= 1) + (b >= 3) + (b >= 6), J = b - I * (I + 1) / 2;
+        const int i = 16 * I + li, j0 = 16 * J + 4 * g;
+        float av[4], pv[4];
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) {
-          const int i = 16 * I + 4 * g + jj, j = 16 * J + li, at = tri_off(i, j);
+          const int j = j0 + jj;
           // The hardware exponential: its error (a few ulp) is far below the 2^-17 of the hi/lo split that carries E.
           const float e = j <= i ? __expf(float(Gd[i] - Gd[j])) : 0.f;
-          Am[at] = j < i ? Bs[i] * e * kk[u][jj] : 0.f;
-          const float x = e * qk[u][jj];
-          const __bf16 h = (__bf16)x;
-          Pp[at] = h;
-          Pp[kTri + at] = (__bf16)(x - (float)h);
+          av[jj] = j < i ? Bs[i] * e * kk[u][jj] : 0.f;
+          pv[jj] = e * qk[u][jj];
         }
+        *reinterpret_cast<float4*>(Am + tri_pad(i, j0)) = float4{av[0], av[1], av[2], av[3]};
+        uint2 ph, pl;
+        split2(pv[0], pv[1], ph.x, pl.x);
+        split2(pv[2], pv[3], ph.y, pl.y);
+        const int at = tri_off(i, j0);
+        *reinterpret_cast<uint2*>(Pp + at) = ph;
+        *reinterpret_cast<uint2*>(Pp + kTri + at) = pl;
       }
     }
     __syncthreads();
@@ -215,11 +230,11 @@ __global__ __launch_bounds__(kThreads) void chunk_prep_kernel(ChunkArgs a, int h
       for (int il = 0; il < 16; ++il) {
         float v = il == jl ? 1.f : 0.f;
 #pragma unroll
-        for (int kl = 0; kl < il; ++kl) v -= Am[tri_off(b0 + il, b0 + kl)] * x[kl];  // x[kl] = 0 for kl < jl
+        for (int kl = 0; kl < il; ++kl) v -= Am[tri_pad(b0 + il, b0 + kl)] * x[kl];  // x[kl] = 0 for kl < jl
         x[il] = il >= jl ? v : 0.f;
       }
 #pragma unroll
-      for (int il = 0; il < 16; ++il) Tm[tri_off(b0 + il, b0 + jl)] = x[il];
+      for (int il = 0; il < 16; ++il) Tm[tri_pad(b0 + il, b0 + jl)] = x[il];
     }
     __syncthreads();
     // Off-diagonal blocks at distance d = I - J, one wave per block (wave w: I = d + w, J = w), on MFMA with split
@@ -236,16 +251,16 @@ __global__ __launch_bounds__(kThreads) void chunk_prep_kernel(ChunkArgs a, int h
           float x[8], y[8];
 #pragma unroll
           for (int j = 0; j < 8; ++j) {
-            x[j] = in ? Am[tri_off(16 * I + li, k0 + j)] : 0.f;  // A rows 16 I + li, columns k
-            y[j] = in ? Tm[tri_off(k0 + j, 16 * J + li)] : 0.f;  // T rows k, column 16 J + li
+            x[j] = in ? Am[tri_pad(16 * I + li, k0 + j)] : 0.f;  // A rows 16 I + li, columns k
+            y[j] = in ? Tm[tri_pad(k0 + j, 16 * J + li)] : 0.f;  // T rows k, column 16 J + li
           }
           W = mma3(W, split8(x), split8(y));
         }
         uint2 th, tl, wh, wl;  // T_II rows li, k = 4g + j, and W, as packed hi / lo pairs
         {
           const int r = 16 * I + li, c = 16 * I + 4 * g;
-          split2(Tm[tri_off(r, c)], Tm[tri_off(r, c + 1)], th.x, tl.x);
-          split2(Tm[tri_off(r, c + 2)], Tm[tri_off(r, c + 3)], th.y, tl.y);
+          split2(Tm[tri_pad(r, c)], Tm[tri_pad(r, c + 1)], th.x, tl.x);
+          split2(Tm[tri_pad(r, c + 2)], Tm[tri_pad(r, c + 3)], th.y, tl.y);
           split2(W[0], W[1], wh.x, wl.x);
           split2(W[2], W[3], wh.y, wl.y);
         }
@@ -255,7 +270,7 @@ __global__ __launch_bounds__(kThreads) void chunk_prep_kernel(ChunkArgs a, int h
         R = mma16(R, v4(th), v4(wl));
         R = mma16(R, v4(tl), v4(wh));
 #pragma unroll
-        for (int jj = 0; jj < 4; ++jj) Tm[tri_off(16 * I + 4 * g + jj, 16 * J + li)] = -R[jj];
+        for (int jj = 0; jj < 4; ++jj) Tm[tri_pad(16 * I + 4 * g + jj, 16 * J + li)] = -R[jj];
       }
       __syncthreads();
     }
@@ -268,7 +283,7 @@ __global__ __launch_bounds__(kThreads) void chunk_prep_kernel(ChunkArgs a, int h
 #pragma unroll
         for (int p2 = 0; p2 < 8; ++p2) {
           const int j = j0 + 2 * p2;
-          split2(Tm[tri_off(i, j)], Tm[tri_off(i, j + 1)], th[p2], tl[p2]);
+          split2(Tm[tri_pad(i, j)], Tm[tri_pad(i, j + 1)], th[p2], tl[p2]);
         }
         const int at = tri_off(i, j0);
 #pragma unroll
