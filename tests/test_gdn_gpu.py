@@ -465,26 +465,29 @@ def test_recurrent_wide_key_widths(torch_dev, oracle, Dk, Dv, lens, bf16):
     assert_close(got, exp, BF16_TOL if bf16 else F32_TOL, label=f"Dk {Dk} {'bf16' if bf16 else 'f32'}")
 
 
-@pytest.mark.parametrize("packed", [False, True], ids=["batch", "packed"])
-def test_state_rows_per_block_change_no_bits(torch_dev, oracle, packed):
+@pytest.mark.parametrize("lens,Dv", [(None, 128), ([70, 0, 100, 1], 128), ([40, 64, 10, 1], 64),
+                                     ([40, 64, 10, 1], 32)], ids=["batch", "packed", "packed_Dv64", "packed_Dv32"])
+def test_state_rows_per_block_change_no_bits(torch_dev, oracle, lens, Dv):
     """The chunked state passes take 32 state rows per block when their 16-row blocks would not all be resident at
     once (more than one per CU), else 16. Heads are independent, so the first two key heads of a problem that takes
-    32-row blocks (Hv = 48: 384 or 1,536 blocks of 16 rows) give the bits of the same heads run alone (Hv = 6: 48 or
-    192 blocks, 16 rows each), and the whole problem matches the oracle. Both sizes keep NC * Hv <= 256, so the
-    gradient kernel takes one work item per value head in both and sums dq, dk the same way."""
+    32-row blocks (Hv = 48: 384 to 1,536 blocks of 16 rows; with Dv = 32 a head is one 32-row block) give the bits of
+    the same heads run alone (Hv = 6: 48 to 192 blocks, 16 rows each), and the whole problem matches the oracle.
+    Both sizes keep NC * Hv <= 256, so the gradient kernel takes one work item per value head in both and sums dq, dk
+    the same way."""
     torch = torch_dev
     from quotebound_amd.synthetic import Workload, make_inputs, to_device
 
-    lens = [70, 0, 100, 1] if packed else None
-    w = Workload("rows", 1, sum(lens) if packed else 200, 16, 48, 128, 128, seed=41, s0_std=0.02, ds_out=True,
+    packed = lens is not None
+    w = Workload("rows", 1, sum(lens) if packed else 200, 16, 48, 128, Dv, seed=41, s0_std=0.02, ds_out=True,
                  seq_lens=lens)
+    assert w.n_states * w.Hv * Dv // 16 > 256 >= w.n_states * 6 * Dv // 16  # 32-row blocks in full, 16 in the slice
     inp = make_inputs(w)
     cu = w.cu_seqlens
     d = to_device(inp)
     d = dict(d, dy=d["dy"].float())
     full = run(torch, d, _lib.CHUNKED, cu=cu, out_f32=True)
     exp = oracle.fwd_bwd(inp.f32, cu_seqlens=cu, dtype=np.float32)
-    assert_close(full, exp, BF16_TOL, label=f"rows packed={packed}")
+    assert_close(full, exp, BF16_TOL, label=f"rows packed={packed} Dv={Dv}")
     sub = {n: d[n][:, :, :2].contiguous() for n in ("q", "k")}
     sub.update({n: d[n][:, :, :6].contiguous() for n in ("v", "g", "beta", "dy")})
     sub.update({n: d[n][:, :6].contiguous() for n in ("s0", "ds_out")})
