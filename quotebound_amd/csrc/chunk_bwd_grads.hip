@@ -103,8 +103,9 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_grads_kernel(ChunkArgs a) 
   const int tid = threadIdx.x;
   const OutT* dy = static_cast<const OutT*>(a.dy);
   const int sk = a.Hk * Dk, sv = a.Hv * a.Dv;  // token strides of k/q/dq/dk and v/dy
-  // A work item: a chunk slot, key head and its value heads [e0, e0 + ne). The grid is persistent: block b takes items b, b + gridDim.x, ..., and
-  // gridDim.x is a multiple of 8, so all of a block's items fall in its own XCD's range of xcd_remap.
+  // A work item: a chunk slot, key head and its value heads [e0, e0 + ne). The grid is persistent: block b takes items
+  // b, b + gridDim.x, ..., and gridDim.x is a multiple of 8, so all of a block's items fall in its own XCD's range of
+  // xcd_remap.
   struct Item {
     int64_t slot, tok;
     int hk, L, e0, ne;

@@ -203,7 +203,8 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_state_kernel(ChunkArgs a) 
         __syncthreads();
         load_b(nxt, cn);
         __syncthreads();
-        stage_b(cur, cs & 1);  // the chain's last readers of dY, T, P and X^T's of diag(exp G) dY were before this barrier
+        // The chain's last readers of dY, T and P, and X^T's of diag(exp G) dY, were before this barrier.
+        stage_b(cur, cs & 1);
       };
       GroupB ga, gb;
       if (nch > 0) {

@@ -10,15 +10,15 @@
 //   S^T <- exp(G_63) S^T + K^T (D Delta),  D = diag(exp(G_63 - G)) waves 0-3, state columns 32w..32w+31
 //   Y^T = (S Q^T) diag(exp G) + Delta^T P^T                        waves 4-7: off the chain
 // Three barriers per chunk. Waves 0-3 carry the state and touch no global memory but the checkpoint stores.
-// Waves 4-7 read S from LDS once for both S K^T and S Q^T, and form y from LDS. Waves 8-11 load every input two chunks ahead, each wave load reading whole cache lines,
-// and stage them in LDS: the chain's k rows, packed T, v, exp G, D and beta (two buffers, by chunk parity), the output
-// group's q rows and packed P (one buffer each); K^T for the state update comes from the staged k rows through the
-// transposing read. The loads and the LDS writes are spread over the chain's phases and the work over two groups,
-// so that neither group, nor the CU's vector memory path or LDS, holds the chain at its barriers. Each group
-// runs a loop of its own, so that each loop holds only its own group's memory operations: the compiler's waits stay
-// exact and none covers a load issued for a later chunk. All products run on v_mfma_f32_16x16x32_bf16; float32
-// operands (S, R, Delta, T, P) are split into bf16 hi + lo pairs so the state keeps float32 accuracy, while k, q, v
-// enter exactly.
+// Waves 4-7 read S from LDS once for both S K^T and S Q^T, and form y from LDS. Waves 8-11 load every input two
+// chunks ahead, each wave load reading whole cache lines, and stage them in LDS: the chain's k rows, packed T, v,
+// exp G, D and beta (two buffers, by chunk parity), the output group's q rows and packed P (one buffer each); K^T for
+// the state update comes from the staged k rows through the transposing read. The loads and the LDS writes are
+// spread over the chain's phases and the work over two groups, so that neither group, nor the CU's vector memory
+// path or LDS, holds the chain at its barriers. Each group runs a loop of its own, so that each loop holds only its
+// own group's memory operations: the compiler's waits stay exact and none covers a load issued for a later chunk.
+// All products run on v_mfma_f32_16x16x32_bf16; float32 operands (S, R, Delta, T, P) are split into bf16 hi + lo
+// pairs so the state keeps float32 accuracy, while k, q, v enter exactly.
 #include "chunk_common.h"
 #include "chunk_kernels.h"
 
@@ -289,7 +289,9 @@ __global__ __launch_bounds__(kThreads) void chunk_fwd_kernel(ChunkArgs a) {
     __syncthreads();  // S in LDS: the output group forms R from it
     __syncthreads();  // R in LDS
 
-    {  // Delta^T = R^T T^T (R with beta applied): A = R^T through the transposing read, B = T rows ip from the packed copy
+    // Delta^T = R^T T^T (R with beta applied): A = R^T through the transposing read, B = T rows ip from the packed
+    // copy.
+    {
       Split8 TB[2];
 #pragma unroll
       for (int s = 0; s < 2; ++s) {

@@ -97,7 +97,8 @@ __global__ __launch_bounds__(kThreads) void chunk_prep_kernel(ChunkArgs a, int h
     const uint32_t bytes = L * uint32_t(sk) * 2u;
     const bf16_t* kb = kFused ? a.pro.k_raw : a.k;
     const bf16_t* qb = kFused ? a.pro.q_raw : a.q;
-    const auto kr = buffer_rsrc(kb + sp.tok * sk + hk * 128, bytes), qr = buffer_rsrc(qb + sp.tok * sk + hk * 128, bytes);
+    const auto kr = buffer_rsrc(kb + sp.tok * sk + hk * 128, bytes);
+    const auto qr = buffer_rsrc(qb + sp.tok * sk + hk * 128, bytes);
     uint4 kv[4], qv[4];
 #pragma unroll
     for (int q4 = 0; q4 < 4; ++q4) {
@@ -115,7 +116,8 @@ __global__ __launch_bounds__(kThreads) void chunk_prep_kernel(ChunkArgs a, int h
         float x[8];
         const uint32_t w4[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
-        for (int j = 0; j < 4; ++j) x[2 * j] = __uint_as_float(w4[j] << 16), x[2 * j + 1] = __uint_as_float(w4[j] & 0xffff0000u);
+        for (int j = 0; j < 4; ++j)
+          x[2 * j] = __uint_as_float(w4[j] << 16), x[2 * j + 1] = __uint_as_float(w4[j] & 0xffff0000u);
         norm_row8<bf16_t>(x, sum16(sumsq8(x)), 128, s);
         u = uint4{f32x2_to_bf16x2(x[0], x[1]), f32x2_to_bf16x2(x[2], x[3]), f32x2_to_bf16x2(x[4], x[5]),
                   f32x2_to_bf16x2(x[6], x[7])};
