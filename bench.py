@@ -240,10 +240,12 @@ def run_design(torch, hip, lib, w, dev, design, steps, warmup):
             "tiles_bytes": tiles}, None
 
 
-def run_decode(torch, lib, w, design, calls=200, warmup=20):
+def run_decode(torch, lib, w, design, calls=200, warmup=20, graph_calls=64, replays=10):
     """The inference step: one-token forward calls at the workload's head shape, each carrying the state to the
-    next (the reference's decode, src/deltanet.cpp:101-120), timed back to back on the host clock (launch included).
-    Returns microseconds per call, or None when the design rejects the shape."""
+    next (the reference's decode, src/deltanet.cpp:101-120). Returns microseconds per call, or None when the design
+    rejects the shape: "host", the calls timed back to back on the host clock (launch included), and "graph", the
+    same calls captured into a HIP graph and replayed, timed with events (the GPU's time per call, as a serving loop
+    that replays captured steps sees it)."""
     from quotebound_amd.synthetic import Workload, make_inputs, to_device
 
     dw = Workload("decode", w.B, 1, w.Hk, w.Hv, w.Dk, w.Dv, seed=5, s0_std=0.02)
@@ -255,22 +257,37 @@ def run_decode(torch, lib, w, design, calls=200, warmup=20):
     y = torch.empty_like(dev["v"])
     states = [dev["s0"].clone(), torch.empty_like(dev["s0"])]
     ws = torch.empty(max(lib.workspace_bytes(desc), 1), dtype=torch.uint8, device="cuda")
-    stream = torch.cuda.current_stream().cuda_stream
+    side = torch.cuda.Stream()
     p = lambda t: None if t is None else t.data_ptr()  # noqa: E731
 
     def call(i):
         lib.fwd(desc, p(dev["q"]), p(dev["k"]), p(dev["v"]), p(dev["g"]), p(dev["beta"]), p(states[i & 1]), p(y),
-                p(states[(i + 1) & 1]), None, p(ws), stream)
+                p(states[(i + 1) & 1]), None, p(ws), side.cuda_stream)
 
-    for i in range(warmup):
-        call(i)
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for i in range(calls):
-        call(i)
+    with torch.cuda.stream(side):
+        for i in range(warmup):
+            call(i)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(calls):
+            call(i)
+        torch.cuda.synchronize()
+        host = (time.perf_counter() - t0) * 1e6 / calls
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        for i in range(graph_calls):
+            call(i)
+    graph.replay()
     torch.cuda.synchronize()
-    del keep
-    return (time.perf_counter() - t0) * 1e6 / calls
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(replays):
+        graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    del graph, keep
+    return {"host": host, "graph": e0.elapsed_time(e1) * 1e3 / (replays * graph_calls)}
 
 
 def run_neighbours(torch, lib, w, calls=50, warmup=5):
@@ -610,7 +627,7 @@ def main():
             out["workloads"][name] = summary
         best = lib.CHUNKED if head["design"] == "chunked" else lib.RECURRENT
         out["t_sweep"] = run_t_sweep(torch, hip, lib, best)
-        out["decode"] = {"unit": "us per one-token call (state carried, host clock, launch included)",
+        out["decode"] = {"unit": "us per one-token call (state carried): host clock with launch, and graph replay",
                          "config": f"B={w.B} Hk={w.Hk} Hv={w.Hv} Dk={w.Dk} Dv={w.Dv}, {w.dtype} I/O, fp32 state"}
         for d in designs:
             out["decode"][DESIGN_NAMES[d]] = run_decode(torch, lib, w, d)

@@ -11,6 +11,8 @@
 // products taken on the previous state, so one reduction latency per step sits on the dependency chain:
 //   a = S_prev k, b = S_prev q;  u = g a;  delta = beta (v - u);  y = g b + delta (k.q);  S = g S_prev + delta k^T
 // The chunk-start states (the reference's ckpt, src/delta_grad.cpp:172-181) are written as the forward passes them.
+// A call of one token per sequence that keeps neither checkpoints nor per-token states (decode) runs the same step
+// in rec_step_kernel, which reads its inputs straight into registers instead of staging a chunk.
 //
 // The forward also keeps e = v - u per token and state row after the checkpoints in ckpt (4 bytes per token and row).
 //
@@ -251,6 +253,69 @@ __global__ __launch_bounds__((Layout<NPT, LPR>::kThreads)) void rec_fwd_kernel(R
         if (a.e_res) a.e_res[at] = ye.y;
       }
     }
+  }
+  if (a.p.s_out && live) {
+#pragma unroll
+    for (int i = 0; i < NPT; ++i) a.p.s_out[srow + col_of<NPT, LPR>(cl, i)] = s[i];
+  }
+}
+
+// The one-token step (decode, reference src/deltanet.cpp:101-120): every sequence of the call has at most one token,
+// and neither checkpoints nor per-token states are asked for. The same work items, lanes and arithmetic as
+// rec_fwd_kernel's step, so the same bits, but every input goes straight from memory into the registers of the lanes
+// that use it (a lane's k and q columns, its row's v, the head's decay factor and beta), issued together with the
+// state's loads: no LDS staging, no barrier, and one memory round trip before the step.
+template <int NPT, int LPR, typename InT, typename OutT>
+__global__ __launch_bounds__((Layout<NPT, LPR>::kThreads)) void rec_step_kernel(RecFwdArgs a) {
+  using Lay = Layout<NPT, LPR>;
+  constexpr int Dk = LPR * NPT;
+  const Item it = item_of(a.tab, a.nblk, a.Hv, a.Hk, a.total);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int cl = lane % LPR, rl = (tid >> 6) * Lay::kRowsPerWave + lane / LPR;
+  const int row = it.blk * Lay::kRows + rl;
+  const bool live = row < a.Dv;
+  const int hv = it.hv, hk = hv / (a.Hv / a.Hk);
+  const Seq sq = seq_of(a.tab, it.n);
+  const int64_t SS = int64_t(a.Dv) * Dk;
+  const int64_t srow = (int64_t(it.n) * a.Hv + hv) * SS + int64_t(row) * Dk;
+
+  float s[NPT];
+#pragma unroll
+  for (int i = 0; i < NPT; ++i) s[i] = (live && a.p.s0) ? a.p.s0[srow + col_of<NPT, LPR>(cl, i)] : 0.f;
+  if (sq.len > 0) {  // uniform over the block; an empty sequence keeps its state
+    const InT* q = static_cast<const InT*>(a.p.q);
+    const InT* k = static_cast<const InT*>(a.p.k);
+    const InT* v = static_cast<const InT*>(a.p.v);
+    const int64_t kb = (sq.tok0 * a.Hk + hk) * Dk, hb = sq.tok0 * a.Hv + hv;
+    float kk[NPT], qq[NPT];
+#pragma unroll
+    for (int i = 0; i < NPT; ++i) {
+      kk[i] = IO<InT>::ld(k, kb + col_of<NPT, LPR>(cl, i));
+      qq[i] = IO<InT>::ld(q, kb + col_of<NPT, LPR>(cl, i));
+    }
+    const float gv = a.p.g[hb];
+    const float gt = a.g_is_log ? expf(gv) : gv;
+    const float bt = IO<InT>::ld(static_cast<const InT*>(a.p.beta), hb);
+    const float vv = live ? IO<InT>::ld(v, hb * a.Dv + row) : 0.f;
+    float kq = 0.f;
+#pragma unroll
+    for (int i = 0; i < NPT; ++i) kq += kk[i] * qq[i];
+    kq = sum_lanes<LPR>(kq);
+    float pa = 0.f, pb = 0.f;
+#pragma unroll
+    for (int i = 0; i < NPT; ++i) pa = fmaf(s[i], kk[i], pa), pb = fmaf(s[i], qq[i], pb);
+    if constexpr (LPR == 32) {
+      sum32_pair(pa, pb);
+    } else {
+      pa = sum_lanes<LPR>(pa);
+      pb = sum_lanes<LPR>(pb);
+    }
+    const float e = fmaf(-gt, pa, vv);
+    const float d = bt * e;
+    const float yv = fmaf(gt, pb, d * kq);
+#pragma unroll
+    for (int i = 0; i < NPT; ++i) s[i] = fmaf(gt, s[i], d * kk[i]);
+    if (live && cl == 0) IO<OutT>::st(static_cast<OutT*>(a.p.y), hb * a.Dv + row, yv);
   }
   if (a.p.s_out && live) {
 #pragma unroll
@@ -597,10 +662,15 @@ hipError_t launch_fwd(const Problem& p, const FwdPtrs& ptrs, hipStream_t s, Trac
     return e;
   }
   const bool rows = ptrs.rows != nullptr;
+  // One token or none per sequence (batch mode with T = 1; packed, where every sequence that is not empty has one
+  // chunk slot per token), with nothing to keep but y and the final state: the one-token step.
+  const bool one = (p.tab.n == 0 ? p.T <= 1 : p.NC == p.BT) && !ptrs.ckpt && !rows;
   const bool ok = with_width(p.Dk, [&](auto npt, auto lpr) {
     constexpr int NPT = decltype(npt)::value, LPR = decltype(lpr)::value;
     const dim3 block(Layout<NPT, LPR>::kThreads);
-    if (rows)
+    if (one)
+      hipLaunchKernelGGL((rec_step_kernel<NPT, LPR, InT, OutT>), grid, block, 0, s, a);
+    else if (rows)
       hipLaunchKernelGGL((rec_fwd_kernel<NPT, LPR, InT, OutT, true>), grid, block, 0, s, a);
     else
       hipLaunchKernelGGL((rec_fwd_kernel<NPT, LPR, InT, OutT, false>), grid, block, 0, s, a);

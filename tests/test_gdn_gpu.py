@@ -258,6 +258,38 @@ def test_row_states(torch_dev, oracle, packed):
         assert np.array_equal(state[0].cpu().numpy(), rows[0, t]), t
 
 
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+def test_one_token_steps_match_rows(torch_dev, dtype):
+    """One-token calls without checkpoints run a kernel of their own (rec_step_kernel), which must give the bits of
+    the multi-token forward: from the state the rows pass kept after token t - 1 (S0 for t = 0), one call on token t
+    gives that pass's state after token t and its y at t, bit for bit, in batch mode and as packed one-token
+    sequences beside an empty one (whose state passes through unchanged)."""
+    torch = torch_dev
+    from quotebound_amd import gdn
+    from quotebound_amd.synthetic import Workload, make_inputs, to_device
+
+    w = Workload("one_token", 2, 9, 2, 4, 128, 128, dtype=dtype, seed=67, s0_std=0.02)
+    print(f"one-token steps: {dtype} Dk={w.Dk} Dv={w.Dv} B={w.B} T={w.T}", flush=True)
+    d = to_device(make_inputs(w))
+    y, rows = gdn.forward_rows(d["q"], d["k"], d["v"], d["g"], d["beta"], d["s0"], log_decay=True)
+    rows = rows.reshape(w.B, w.T, *rows.shape[-3:])
+    step = lambda sl, state, cu=None, src=d: gdn.forward(  # noqa: E731
+        src["q"][:, sl], src["k"][:, sl], src["v"][:, sl], src["g"][:, sl], src["beta"][:, sl], state,
+        log_decay=True, design=_lib.RECURRENT, cu_seqlens=cu, save_ckpt=False)[:2]
+    for t in range(w.T):
+        before = d["s0"] if t == 0 else rows[:, t - 1].contiguous()
+        y_t, s_t = step(slice(t, t + 1), before)
+        assert torch.equal(s_t, rows[:, t]), t
+        assert torch.equal(y_t[:, 0], y[:, t]), t
+        # The same tokens as packed sequences of lengths 1, 0, 1.
+        packed = {n: d[n][:, t].unsqueeze(0) for n in ("q", "k", "v", "g", "beta")}
+        keep = rows[0, 0].unsqueeze(0)
+        y_p, s_p = step(slice(0, 2), torch.cat([before[:1], keep, before[1:]]), cu=[0, 1, 1, 2], src=packed)
+        assert torch.equal(s_p[0], rows[0, t]) and torch.equal(s_p[2], rows[1, t]), t
+        assert torch.equal(s_p[1], keep[0]), t
+        assert torch.equal(y_p[0], y[:, t]), t
+
+
 @pytest.mark.parametrize("design", DESIGNS, ids=DESIGN_IDS.get)
 @pytest.mark.parametrize("case", ["empty_sequences", "max_sequences"])
 def test_packed_edge_cases(torch_dev, oracle, design, case):
