@@ -575,6 +575,9 @@ def main():
     ap.add_argument("--prologue-fusion", action="store_true",
                     help="time only the layer with its prologue, fused and as four separate entry points, at the "
                          "named workload's shape, and print that object (for kernel traces)")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="time only the one-token inference step at the named workload's head shape, and print that "
+                         "object (for kernel traces)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the recurrence shards "
@@ -596,6 +599,9 @@ def main():
         return
     designs = [lib.RECURRENT, lib.CHUNKED] if args.design == "auto" else [int(args.design)]
     w = workload(args.workload)
+    if args.decode_only:
+        print(json.dumps({DESIGN_NAMES[d]: run_decode(torch, lib, w, d, calls=args.steps) for d in designs}))
+        return
     head, inp = measure_workload(torch, hip, lib, w, designs, args.steps, args.warmup)
     if head is None:
         print(json.dumps({"metric": METRIC, "error": inp}))
