@@ -2,7 +2,8 @@
 
 One step = one forward (qb_gdn_fwd, writing the 64-token checkpoints) and one backward (qb_gdn_bwd) over the
 workload's tokens, inputs resident in HBM before the timed region. value = tokens / (wall time per step), the best
-design's, timed with nothing between the kernels. Each kernel's duration comes from a second run of as many steps
+design's, timed with nothing between the kernels, after PREWARM_MS of the same step untimed (the device's clocks
+settle over about 100 ms of load after idling) and the --warmup steps. Each kernel's duration comes from a second run of as many steps
 with HIP events the library records on its launch stream around each kernel (the descriptor's trace_events);
 the roofline object is for the kernel with the most time per step, its algorithmic work per launch
 divided by its mean duration. A kernel's algorithmic bytes are the compulsory tensors it reads or writes in the
@@ -16,8 +17,8 @@ reference op (workloads, each with its own rooflines; float32 runs on the recurr
 bench's T sweep at the 4B head shape (t_sweep), the one-token inference step (decode), the layer's pointwise
 neighbours and the LoRA training step; --path-only leaves those out.
 
-python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--design auto|1|2] [--workload qwen35_4b] [--no-cpu]
-                [--copy-probe-mib N] [--path-only] [--prologue-fusion]
+python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--prewarm-ms 150] [--design auto|1|2] [--workload qwen35_4b]
+                [--no-cpu] [--copy-probe-mib N] [--path-only] [--prologue-fusion] [--decode-only]
 
 roofline.traffic is the dominant kernel's HBM bytes per launch as rocprofv3 counted them (FETCH_SIZE + WRITE_SIZE,
 each scaled by what the counter reads for a plain device copy of known size), read from profiles/traffic.json
@@ -38,6 +39,11 @@ sys.path.insert(0, ROOT)
 METRIC = "Gated DeltaNet fwd+bwd tokens/s per layer @4B shape; % HBM/MFMA roofline"
 HBM_PEAK_GBS = 8000.0      # MI355X HBM3E, published
 FP32_PEAK_TFLOPS = 157.3   # MI355X FP32 vector, published
+# The device's clocks take about 100 ms of sustained load to settle after it has idled: after one second idle, 20
+# steps at the 4B shape behind 5 warm-up steps averaged 447 us, behind 150 further ms of the same step 388 us. Each
+# design's timing therefore starts with this much wall time of its own step, untimed, before the warm-up steps
+# (--prewarm-ms; 0 turns it off).
+PREWARM_MS = 150.0
 BF16_MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense BF16 MFMA, published
 
 
@@ -144,7 +150,8 @@ def roofline_of(kind, amount, ms):
 
 
 def run_design(torch, hip, lib, w, dev, design, steps, warmup):
-    """Times `steps` fwd+bwd steps after `warmup`, then runs as many with the library's trace events for each
+    """Times `steps` fwd+bwd steps after PREWARM_MS of untimed steps and `warmup` more, then runs as many with the
+    library's trace events for each
     kernel's duration, then as many again with the caches flushed before the forward and before the backward;
     returns wall ms/step (of the uninstrumented steps), per-kernel mean ms, and the cold-cache step and kernels."""
     B, T, Hk, Hv, Dk, Dv = w.B, w.T, w.Hk, w.Hv, w.Dk, w.Dv
@@ -190,6 +197,11 @@ def run_design(torch, hip, lib, w, dev, design, steps, warmup):
         if i is not None:
             del keep1, keep2
 
+    t0 = time.perf_counter()
+    while (time.perf_counter() - t0) * 1e3 < PREWARM_MS:  # the clocks' settling time, untimed
+        for _ in range(4):
+            step()
+        torch.cuda.synchronize()
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
@@ -561,6 +573,7 @@ def run_t_sweep(torch, hip, lib, design, steps=10, warmup=2):
 
 
 def main():
+    global PREWARM_MS
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
@@ -575,10 +588,14 @@ def main():
     ap.add_argument("--prologue-fusion", action="store_true",
                     help="time only the layer with its prologue, fused and as four separate entry points, at the "
                          "named workload's shape, and print that object (for kernel traces)")
+    ap.add_argument("--prewarm-ms", type=float, default=PREWARM_MS,
+                    help="wall time of each design's own step run untimed before its warm-up steps, for the device's "
+                         "clocks to settle (0: none)")
     ap.add_argument("--decode-only", action="store_true",
                     help="time only the one-token inference step at the named workload's head shape, and print that "
                          "object (for kernel traces)")
     args = ap.parse_args()
+    PREWARM_MS = args.prewarm_ms
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the recurrence shards "
               "by key-head groups with no exchange, so per-GPU work is the one-GPU run at Hk/N, Hv/N).",
@@ -613,6 +630,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "prewarm_ms": PREWARM_MS,
         "ms_per_step": head["ms_per_step"],
         "higher_is_better": True,
         "scaling": "weak",
