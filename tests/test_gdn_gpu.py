@@ -259,16 +259,18 @@ def test_row_states(torch_dev, oracle, packed):
 
 
 @pytest.mark.parametrize("dtype", ["bf16", "f32"])
-def test_one_token_steps_match_rows(torch_dev, dtype):
+@pytest.mark.parametrize("Dk,Dv", [(128, 128), (64, 48), (256, 40), (96, 32)])
+def test_one_token_steps_match_rows(torch_dev, dtype, Dk, Dv):
     """One-token calls without checkpoints run a kernel of their own (rec_step_kernel), which must give the bits of
     the multi-token forward: from the state the rows pass kept after token t - 1 (S0 for t = 0), one call on token t
     gives that pass's state after token t and its y at t, bit for bit, in batch mode and as packed one-token
-    sequences beside an empty one (whose state passes through unchanged)."""
+    sequences beside an empty one (whose state passes through unchanged). Every lane layout (16 or 32 lanes per row,
+    4 to 8 columns per lane, contiguous or in runs of four) and a last row block that Dv only partly fills."""
     torch = torch_dev
     from quotebound_amd import gdn
     from quotebound_amd.synthetic import Workload, make_inputs, to_device
 
-    w = Workload("one_token", 2, 9, 2, 4, 128, 128, dtype=dtype, seed=67, s0_std=0.02)
+    w = Workload("one_token", 2, 9, 2, 4, Dk, Dv, dtype=dtype, seed=67, s0_std=0.02)
     print(f"one-token steps: {dtype} Dk={w.Dk} Dv={w.Dv} B={w.B} T={w.T}", flush=True)
     d = to_device(make_inputs(w))
     y, rows = gdn.forward_rows(d["q"], d["k"], d["v"], d["g"], d["beta"], d["s0"], log_decay=True)
