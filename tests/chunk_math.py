@@ -21,27 +21,35 @@ from __future__ import annotations
 
 import numpy as np
 
+# The matrix product every equation below uses: numpy's own (float64 inputs give float64 products), or a replacement
+# with the same signature, such as an emulation of the kernels' MFMA arithmetic on float32 inputs.
+MM = None
+
+
+def mm(x, y):
+    return x @ y if MM is None else MM(x, y)
+
 
 def prep(K, beta, a):
     C = K.shape[0]
     G = np.cumsum(a)
     E = np.exp(G[:, None] - G[None, :])
-    KK = K @ K.T
+    KK = mm(K, K.T)
     A = np.tril(beta[:, None] * E * KK, -1)
-    T = np.linalg.inv(np.eye(C) + A)
+    T = np.linalg.inv(np.eye(C, dtype=A.dtype) + A)
     return G, E, KK, A, T, T * beta[None, :]
 
 
 def chunk_fwd(K, Q, V, beta, a, S0):
     G, E, KK, A, T, Tb = prep(K, beta, a)
     gam = np.exp(G)
-    KS = K @ S0.T
+    KS = mm(K, S0.T)
     R = V - gam[:, None] * KS
-    Delta = Tb @ R
-    P = np.tril(E * (Q @ K.T))
-    Y = gam[:, None] * (Q @ S0.T) + P @ Delta
+    Delta = mm(Tb, R)
+    P = np.tril(E * mm(Q, K.T))
+    Y = gam[:, None] * mm(Q, S0.T) + mm(P, Delta)
     D = np.exp(G[-1] - G)
-    S1 = gam[-1] * S0 + (Delta * D[:, None]).T @ K
+    S1 = gam[-1] * S0 + mm((Delta * D[:, None]).T, K)
     return Y, S1
 
 
@@ -51,31 +59,31 @@ def chunk_bwd(K, Q, V, beta, a, S0, dY, dS1):
     gam = np.exp(G)
     D = np.exp(G[-1] - G)
     M = np.tril(E)
-    QK = Q @ K.T
+    QK = mm(Q, K.T)
     P = M * QK
-    KS = K @ S0.T
-    QS = Q @ S0.T
+    KS = mm(K, S0.T)
+    QS = mm(Q, S0.T)
     R = V - gam[:, None] * KS
-    Delta = Tb @ R
+    Delta = mm(Tb, R)
     # state pass
-    KdS = K @ dS1.T
-    dDelta = P.T @ dY + D[:, None] * KdS
-    dR = Tb.T @ dDelta
+    KdS = mm(K, dS1.T)
+    dDelta = mm(P.T, dY) + D[:, None] * KdS
+    dR = mm(Tb.T, dDelta)
     dV = dR
-    dS0 = gam[-1] * dS1 + (gam[:, None] * dY).T @ Q - (gam[:, None] * dR).T @ K
+    dS0 = gam[-1] * dS1 + mm((gam[:, None] * dY).T, Q) - mm((gam[:, None] * dR).T, K)
     # gradients
-    dP = np.tril(dY @ Delta.T)
-    dQ = gam[:, None] * (dY @ S0) + (dP * M) @ K
-    dK = -gam[:, None] * (dR @ S0) + D[:, None] * (Delta @ dS1) + (dP * M).T @ Q
-    dTb = np.tril(dDelta @ R.T)
+    dP = np.tril(mm(dY, Delta.T))
+    dQ = gam[:, None] * mm(dY, S0) + mm(dP * M, K)
+    dK = -gam[:, None] * mm(dR, S0) + D[:, None] * mm(Delta, dS1) + mm((dP * M).T, Q)
+    dTb = np.tril(mm(dDelta, R.T))
     dT = dTb * beta[None, :]
     dbeta = (dTb * T).sum(0)
-    dA = np.tril(-T.T @ dT @ T.T, -1)
+    dA = np.tril(-mm(mm(T.T, dT), T.T), -1)
     Gm = E * KK  # A = diag(beta) Gm (strict lower)
     dbeta += (dA * Gm).sum(1)
     dGm = beta[:, None] * dA
     dKK = dGm * E
-    dK += (dKK + dKK.T) @ K
+    dK += mm(dKK + dKK.T, K)
     dG = np.zeros_like(a)
     # exp(G_i - G_j) factors: A (via Gm), P (via M)
     for X in (dGm * Gm, dP * P):
@@ -105,14 +113,14 @@ def gated_delta_chunked(q, k, v, a, beta, s0, dy, ds_out, C=64):
 
     def chunk(x, b, h, c):
         t0, t1 = c * C, min(T, c * C + C)
-        out = np.zeros((C,) + x.shape[3:]) if x.ndim == 4 else np.zeros(C)
+        out = np.zeros((C,) + x.shape[3:], x.dtype) if x.ndim == 4 else np.zeros(C, x.dtype)
         out[: t1 - t0] = x[b, t0:t1, h]
         return out
 
     for b in range(B):
         for hv in range(Hv):
             hk = hv // grp
-            S = np.zeros((Dv, Dk)) if s0 is None else s0[b, hv].copy()
+            S = np.zeros((Dv, Dk), q.dtype) if s0 is None else s0[b, hv].copy()
             starts = []
             for c in range(nch):
                 starts.append(S)
@@ -121,7 +129,7 @@ def gated_delta_chunked(q, k, v, a, beta, s0, dy, ds_out, C=64):
                 t0, t1 = c * C, min(T, c * C + C)
                 y[b, t0:t1, hv] = Y[: t1 - t0]
             s_out[b, hv] = S
-            dS = np.zeros((Dv, Dk)) if ds_out is None else ds_out[b, hv].copy()
+            dS = np.zeros((Dv, Dk), q.dtype) if ds_out is None else ds_out[b, hv].copy()
             for c in reversed(range(nch)):
                 out = chunk_bwd(chunk(k, b, hk, c), chunk(q, b, hk, c), chunk(v, b, hv, c), chunk(beta, b, hv, c),
                                 chunk(a, b, hv, c), starts[c], chunk(dy, b, hv, c), dS)
