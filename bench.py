@@ -179,7 +179,7 @@ def run_design(torch, hip, lib, w, dev, design, steps, warmup):
     nf, nb = len(fnames) + 1, len(bnames) + 1
     evs = [[hip.event() for _ in range(nf + nb)] for _ in range(steps)]
 
-    def step(i=None, flush=None):
+    def step(i=None, flush=None, st=stream):
         if i is not None:
             keep1 = lib.set_trace(desc_f, evs[i][:nf])
             keep2 = lib.set_trace(desc_b, evs[i][nf:])
@@ -189,11 +189,11 @@ def run_design(torch, hip, lib, w, dev, design, steps, warmup):
         if flush is not None:
             flush.sum()
         lib.fwd(desc_f, p(dev["q"]), p(dev["k"]), p(dev["v"]), p(dev["g"]), p(dev["beta"]), p(dev["s0"]), p(y),
-                p(s_out), p(ckpt), p(ws), stream)
+                p(s_out), p(ckpt), p(ws), st)
         if flush is not None:
             flush.sum()
         lib.bwd(desc_b, p(dev["q"]), p(dev["k"]), p(dev["v"]), p(dev["g"]), p(dev["beta"]), p(ckpt), p(dev["dy"]),
-                p(dev["ds_out"]), p(dq), p(dk), p(dv), p(dg), p(dbeta), p(ds0), p(ws), stream)
+                p(dev["ds_out"]), p(dq), p(dk), p(dv), p(dg), p(dbeta), p(ds0), p(ws), st)
         if i is not None:
             del keep1, keep2
 
@@ -210,6 +210,24 @@ def run_design(torch, hip, lib, w, dev, design, steps, warmup):
         step()
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3 / steps
+    # The same steps captured once into a HIP graph and replayed, timed with events: the GPU's time per step without
+    # the host's launches (what a caller that replays captured steps sees; at short sequences the host's launch rate,
+    # not the GPU, sets the wall time above).
+    side = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        for _ in range(steps):
+            step(st=side.cuda_stream)
+    graph.replay()
+    torch.cuda.synchronize()
+    g0, g1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    g0.record()
+    for _ in range(3):
+        graph.replay()
+    g1.record()
+    torch.cuda.synchronize()
+    graph_ms = g0.elapsed_time(g1) / (3 * steps)
+    del graph
     for i in range(steps):  # the same steps again with an event before and after each kernel, for their durations
         step(i)
     torch.cuda.synchronize()
@@ -246,7 +264,8 @@ def run_design(torch, hip, lib, w, dev, design, steps, warmup):
     kernels = {n: sum(v) / len(v) for n, v in per.items()}
     nc = lib.num_chunks(desc_f)
     tiles = lib.ckpt_bytes(desc_f) - nc * Hv * Dv * Dk * 4
-    return {"ms_per_step": wall_ms, "fwd_ms": fwd_ms, "bwd_ms": bwd_ms, "kernels_ms": kernels,
+    return {"ms_per_step": wall_ms, "graph_ms_per_step": graph_ms, "fwd_ms": fwd_ms, "bwd_ms": bwd_ms,
+            "kernels_ms": kernels,
             "cold_caches": {"ms_per_step": cold_ms, "kernels_ms": {n: sum(v) / len(v) for n, v in cold.items()}},
             "nc": nc,
             "tiles_bytes": tiles}, None
@@ -559,7 +578,9 @@ def run_t_sweep(torch, hip, lib, design, steps=10, warmup=2):
     kernel's time (what dominates at short T)."""
     from quotebound_amd.synthetic import make_inputs, to_device, workload
 
-    out = {"unit": "ms (HIP events around the library's kernels)", "design": DESIGN_NAMES[design]}
+    out = {"unit": "ms: fwd_ms from HIP events around the forward's kernels, fwd_bwd_ms per step on the host clock "
+                   "(launches from Python included), fwd_bwd_graph_ms per step from a replayed HIP graph",
+           "design": DESIGN_NAMES[design]}
     for T in (128, 512, 1024, 2048):
         w = workload(f"qwen35_4b_t{T}")
         dev = to_device(make_inputs(w), "cuda")
@@ -568,6 +589,7 @@ def run_t_sweep(torch, hip, lib, design, steps=10, warmup=2):
             out[str(T)] = {"unavailable": why}
             continue
         out[str(T)] = {"fwd_ms": r["fwd_ms"], "fwd_bwd_ms": r["ms_per_step"],
+                       "fwd_bwd_graph_ms": r["graph_ms_per_step"],
                        "tokens_per_s": T / (r["ms_per_step"] * 1e-3), "kernels_ms": r["kernels_ms"]}
     return out
 
