@@ -571,6 +571,65 @@ def test_deterministic(torch_dev, design):
 
 
 @pytest.mark.parametrize("design", DESIGNS, ids=DESIGN_IDS.get)
+def test_forward_backward_in_a_graph(torch_dev, design):
+    """qb_gdn_fwd then qb_gdn_bwd captured into one HIP graph on a side stream (buffers allocated outside the
+    capture; the calls issue no allocation and no memset), replayed three times with eager calls of the same pair
+    between the replays and every output poisoned before each replay: every replay equals the eager pair, bit for
+    bit, for a packed batch with an empty sequence, an initial state and a final-state cotangent."""
+    torch = torch_dev
+    from quotebound_amd.synthetic import Workload, make_inputs, to_device
+
+    w = Workload("graph", 1, 700, 4, 8, 128, 128, seed=71, s0_std=0.02, ds_out=True, seq_lens=[300, 0, 400])
+    print(f"fwd+bwd in a graph: T={w.T} Hk={w.Hk} Hv={w.Hv} packed {w.seq_lens} design {design}", flush=True)
+    d = to_device(make_inputs(w))
+    desc_f, keep_f = _lib.make_desc(w.B, w.T, w.Hk, w.Hv, w.Dk, w.Dv, design=design, cu_seqlens=w.cu_seqlens)
+    desc_b, keep_b = _lib.make_desc(w.B, w.T, w.Hk, w.Hv, w.Dk, w.Dv, design=design, cu_seqlens=w.cu_seqlens)
+    N = w.n_states
+    ckpt = torch.empty(_lib.ckpt_bytes(desc_f) // 4, device="cuda")
+    ws = torch.empty(max(_lib.workspace_bytes(desc_f), 1), dtype=torch.uint8, device="cuda")
+
+    def outs():
+        return [torch.empty_like(d["v"]), torch.empty(N, w.Hv, w.Dv, w.Dk, device="cuda"), torch.empty_like(d["q"]),
+                torch.empty_like(d["k"]), torch.empty_like(d["v"]), torch.empty_like(d["g"]),
+                torch.empty_like(d["beta"]), torch.empty(N, w.Hv, w.Dv, w.Dk, device="cuda")]
+
+    p = lambda t: t.data_ptr()  # noqa: E731
+
+    def pair(o, stream):
+        y, s_out, dq, dk, dv, dg, dbeta, ds0 = o
+        _lib.fwd(desc_f, p(d["q"]), p(d["k"]), p(d["v"]), p(d["g"]), p(d["beta"]), p(d["s0"]), p(y), p(s_out),
+                 p(ckpt), p(ws), stream)
+        _lib.bwd(desc_b, p(d["q"]), p(d["k"]), p(d["v"]), p(d["g"]), p(d["beta"]), p(ckpt), p(d["dy"]),
+                 p(d["ds_out"]), p(dq), p(dk), p(dv), p(dg), p(dbeta), p(ds0), p(ws), stream)
+
+    names = ("y", "s_out", "dq", "dk", "dv", "dg", "dbeta", "ds0")
+    want, got, again = outs(), outs(), outs()
+    pair(want, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    for name, t in zip(names, want):
+        assert not torch.isnan(t.float()).any(), name
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.graph(graph, stream=side):
+        pair(got, side.cuda_stream)
+    torch.cuda.synchronize()
+    for r in range(3):
+        for t in got + [ckpt]:
+            t.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for name, a, b in zip(names, want, got):
+            assert torch.equal(a, b), f"replay {r} {name}: max |diff| {(a.float() - b.float()).abs().max().item()}"
+        pair(again, torch.cuda.current_stream().cuda_stream)  # eager work between the replays
+        torch.cuda.synchronize()
+        for name, a, b in zip(names, want, again):
+            assert torch.equal(a, b), f"eager after replay {r} {name}"
+    del graph, keep_f, keep_b
+
+
+@pytest.mark.parametrize("design", DESIGNS, ids=DESIGN_IDS.get)
 def test_trainable_autograd_matches_vjp(torch_dev, design):
     """gated_delta_trainable under torch autograd gives gated_delta_vjp's cotangents (reference
     src/delta_grad.cpp:201-212), with the decay factor as input as the reference's gated_delta takes it."""
